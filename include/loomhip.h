@@ -1,0 +1,169 @@
+/*
+ * loomhip.h -- C ABI of libloomhip, the MI355X (gfx950) backend for Loom's
+ * quantized MoE forward.
+ *
+ * Every entry point is plain C: pointers, sizes and ints, no HIP or torch
+ * types.  It is what a `-Dgpu=hip` arm of src/compute/backend.zig binds
+ * through @cImport (the shim is shown in INTEGRATION.md), and what the Python
+ * harness binds through ctypes.
+ *
+ * Two families:
+ *   - seam calls (host slices in, host slices out, synchronous), one per
+ *     backend.zig name they replace; they return LOOMHIP_OK when the device
+ *     did the work and LOOMHIP_DECLINED / an error otherwise, in which case
+ *     the caller runs its own CPU path, exactly as the reference's GPU
+ *     backends fall back (src/vulkan/backend.zig:365-378) or decline
+ *     (src/compute/backend.zig:75-96);
+ *   - device-resident calls (suffix _dev): every tensor pointer is a device
+ *     pointer in the device weight layout, work is stream-ordered on the
+ *     given stream (NULL = the library's compute stream) and nothing is
+ *     copied to or from the host.  These are the hot path.
+ *
+ * Numerics: LOOMHIP_NUM_CPU_PARITY (default) quantizes activations to int8
+ * exactly as the reference CPU path does (src/gguf/ggml.zig:776-800,
+ * 1077-1098), runs exact integer block dots and reproduces the f32 tail and
+ * the block summation order, so matvec/matmul are bit-identical to the
+ * reference's CPU kernels.
+ */
+#ifndef LOOMHIP_H
+#define LOOMHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define LOOMHIP_OK 0
+#define LOOMHIP_DECLINED 1  /* shape/type not served: caller runs its own path */
+#define LOOMHIP_ERR_ARG -1  /* invalid argument (message in loomhip_last_error) */
+#define LOOMHIP_ERR_HIP -2  /* HIP runtime error */
+#define LOOMHIP_ERR_INIT -3 /* no device / not initialised */
+
+/* GGML type tags (src/gguf/ggml.zig:23-47) */
+#define LOOMHIP_F32 0
+#define LOOMHIP_F16 1
+#define LOOMHIP_Q4_0 2
+#define LOOMHIP_Q8_0 8
+#define LOOMHIP_Q4_K 12
+#define LOOMHIP_Q6_K 14
+
+/* gating (src/gguf/moe.zig:36-44) */
+#define LOOMHIP_GATING_SOFTMAX 1
+#define LOOMHIP_GATING_SIGMOID 2
+#define LOOMHIP_GATING_SOFTMAX_TOPK 3
+
+/* MoE combine order */
+#define LOOMHIP_COMBINE_SELECTION 0 /* out = sum over slots in selection order
+                                       (llama.zig moeRun 1363-1398) */
+#define LOOMHIP_COMBINE_EXPERT_ASC 1 /* out += per expert in ascending id order
+                                        (llama.zig moeBatchUnion 1844-1903) */
+
+/* ---- lifecycle ------------------------------------------------------------ */
+
+/* Replaces backend.parallelBegin's device bring-up (src/vulkan/backend.zig:
+ * 185-229): selects the device, creates the compute and expert-copy streams. */
+int loomhip_init(int device);
+void loomhip_shutdown(void);
+/* Diagnostic for the last failed call (backend.arenaError, backend.zig:118). */
+const char *loomhip_last_error(void);
+/* Launches submitted since the last call, then reset (backend.takeCmdBufCount,
+ * src/compute/backend.zig:112-116).  Tests assert it moved to prove the
+ * device path ran. */
+uint64_t loomhip_take_launch_count(void);
+/* Library version string. */
+const char *loomhip_version(void);
+
+/* ---- weight residency ---------------------------------------------------- */
+
+/* Bytes of one [rows][cols] plane of type t in the device layout: Q4_K keeps
+ * GGML's 144-byte blocks; Q6_K, Q8_0 and Q4_0 are split per plane into
+ * structure-of-arrays (quants, then high bits / scales, then f16 d) so every
+ * load is 16-byte aligned.  Same byte count as GGML's, no padding inside a
+ * plane. */
+size_t loomhip_plane_bytes(int t, size_t rows, size_t cols);
+/* GGML bytes of the same plane (src/gguf/ggml.zig:103 rowBytes * rows). */
+size_t loomhip_ggml_bytes(int t, size_t rows, size_t cols);
+
+/* Pointer-keyed upload of an immutable host tensor of `planes` stacked
+ * [rows][cols] planes (replaces the Vulkan weightBuffer cache,
+ * src/vulkan/backend.zig:244-261; a length mismatch on a known pointer
+ * re-uploads).  Returns LOOMHIP_OK and the device pointer in *dev_out. */
+int loomhip_register_weights(int t, const void *host, size_t rows, size_t cols, size_t planes,
+                             void **dev_out);
+/* Drop every cached upload (tests recycle host addresses,
+ * src/vulkan/backend.zig:159-172). */
+void loomhip_clear_weight_cache(void);
+/* Bytes currently resident through the cache (backend.materializeArenas). */
+size_t loomhip_resident_bytes(void);
+
+/* Convert `planes` GGML planes at src (device memory) into the device layout
+ * at dst (device memory, loomhip_plane_bytes * planes). */
+int loomhip_repack_dev(int t, void *dst, const void *src, size_t rows, size_t cols, size_t planes,
+                       void *stream);
+/* Fill `planes` device-layout planes with seeded synthetic blocks whose
+ * dequantized values have roughly the given standard deviation (bench input
+ * generator; deterministic in seed). */
+int loomhip_synth_weights_dev(int t, void *dst, size_t rows, size_t cols, size_t planes,
+                              uint64_t seed, float stddev, void *stream);
+
+/* ---- seam calls: host in, host out (src/compute/backend.zig:56-63) ------- */
+
+/* backend.matvec (src/gguf/ggml.zig:602): out[rows] = W[rows][cols] . x */
+int loomhip_matvec(int t, float *out, const uint8_t *w, const float *x, size_t rows, size_t cols);
+/* backend.matmul (src/gguf/ggml.zig:504): out[n][rows], bit-identical to n
+ * matvecs. */
+int loomhip_matmul(int t, float *out, const uint8_t *w, const float *xs, size_t n, size_t rows,
+                   size_t cols);
+/* backend.dequantRow (src/gguf/ggml.zig:1739): bit-exact f32 row r. */
+int loomhip_dequant_row(int t, float *out, const uint8_t *w, size_t r, size_t cols);
+/* backend.moeRoute (src/compute/cpu.zig:86; src/vulkan/backend.zig:437):
+ * scores, top-k with lowest-index ties, gates from unbiased scores, renorm
+ * with the f16-min clamp, scale. */
+int loomhip_moe_route(const float *logits, const float *bias, size_t n_expert, size_t n_used,
+                      int gating, int weights_norm, float weights_scale, uint32_t *ids_out,
+                      float *gates_out);
+/* backend.moeFfnBlockRouted (src/compute/cpu.zig:68; metal 1505; vulkan
+ * 455-551) generalised to n_tok tokens: router logits in, the routed experts'
+ * gate/up/SwiGLU/down and gated combine out.  gate/up/down are whole 3D
+ * tensors in GGML layout ([n_expert][ffn][dim] and [n_expert][dim][ffn]).
+ * combine = LOOMHIP_COMBINE_*.  out is [n_tok][dim] (overwritten for
+ * SELECTION, accumulated into for EXPERT_ASC). */
+int loomhip_moe_ffn_routed(const float *normed, size_t n_tok, size_t dim, const float *logits,
+                           const float *sel_bias, size_t n_expert, size_t n_used, int gating,
+                           int weights_norm, float weights_scale, int gate_t, const void *gate_w,
+                           int up_t, const void *up_w, int down_t, const void *down_w, size_t ffn,
+                           int combine, float *out);
+
+/* ---- device-resident hot path ------------------------------------------- */
+
+/* out[n][rows] = W . x_k for n activation vectors x[n][cols] (device f32). */
+int loomhip_matvec_dev(int t, float *out, const void *w, const float *x, size_t n, size_t rows,
+                       size_t cols, void *stream);
+int loomhip_dequant_dev(int t, float *out, const void *w, size_t rows, size_t cols, void *stream);
+
+/* One MoE layer on device for n_tok tokens: router GEMV (f32 [n_expert][dim],
+ * plus optional logit bias), route, bucketing, grouped gate/up+SwiGLU, down,
+ * combine.  ids_out/gates_out ([n_tok][n_used]) are optional device outputs.
+ * Weights are device-layout planes, one per expert, contiguous per tensor. */
+typedef struct {
+    size_t dim, ffn, n_expert, n_used;
+    int gating, weights_norm;
+    float weights_scale;
+    const float *router;      /* [n_expert][dim] f32 */
+    const float *router_bias; /* [n_expert] logit bias or NULL */
+    const float *sel_bias;    /* [n_expert] selection-only bias or NULL */
+    int gate_t, up_t, down_t;
+    const void *gate, *up, *down; /* device-layout, plane per expert */
+} loomhip_moe_layer;
+
+int loomhip_moe_layer_dev(const loomhip_moe_layer *L, const float *normed, size_t n_tok,
+                          int combine, float *out, uint32_t *ids_out, float *gates_out,
+                          void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,129 @@
+"""loom_amd -- MI355X (gfx950) backend for Loom's quantized MoE forward.
+
+The product is ``libloomhip.so`` (hand-written HIP kernels behind the C ABI of
+``include/loomhip.h``).  This package loads it with ctypes and mirrors the
+reference's compute-backend seam (``src/compute/backend.zig``) in
+``loom_amd.backend``.  There is no CPU fallback: if the shared library is
+missing, importing the bindings raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "libloomhip.so")
+HEADER = os.path.join(ROOT, "include", "loomhip.h")
+
+OK, DECLINED, ERR_ARG, ERR_HIP, ERR_INIT = 0, 1, -1, -2, -3
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+GATING_SOFTMAX, GATING_SIGMOID, GATING_SOFTMAX_TOPK = 1, 2, 3
+COMBINE_SELECTION, COMBINE_EXPERT_ASC = 0, 1
+
+
+class LoomHipError(RuntimeError):
+    pass
+
+
+class MoeLayerDesc(C.Structure):
+    """Mirror of ``loomhip_moe_layer`` in include/loomhip.h."""
+
+    _fields_ = [
+        ("dim", C.c_size_t),
+        ("ffn", C.c_size_t),
+        ("n_expert", C.c_size_t),
+        ("n_used", C.c_size_t),
+        ("gating", C.c_int),
+        ("weights_norm", C.c_int),
+        ("weights_scale", C.c_float),
+        ("router", C.c_void_p),
+        ("router_bias", C.c_void_p),
+        ("sel_bias", C.c_void_p),
+        ("gate_t", C.c_int),
+        ("up_t", C.c_int),
+        ("down_t", C.c_int),
+        ("gate", C.c_void_p),
+        ("up", C.c_void_p),
+        ("down", C.c_void_p),
+    ]
+
+
+def header_symbols() -> list[str]:
+    """Every function name declared in include/loomhip.h."""
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(loomhip_[a-z0-9_]+)\s*\(", text)))
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load libloomhip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise LoomHipError(
+            f"{LIB_PATH} is missing: build it with `python -m loom_amd.build` "
+            "(there is no CPU fallback)")
+    L = C.CDLL(LIB_PATH)
+    vp, sz, i, f = C.c_void_p, C.c_size_t, C.c_int, C.c_float
+    u64 = C.c_uint64
+    sig = {
+        "loomhip_init": (i, [i]),
+        "loomhip_shutdown": (None, []),
+        "loomhip_last_error": (C.c_char_p, []),
+        "loomhip_take_launch_count": (u64, []),
+        "loomhip_version": (C.c_char_p, []),
+        "loomhip_plane_bytes": (sz, [i, sz, sz]),
+        "loomhip_ggml_bytes": (sz, [i, sz, sz]),
+        "loomhip_register_weights": (i, [i, vp, sz, sz, sz, C.POINTER(vp)]),
+        "loomhip_clear_weight_cache": (None, []),
+        "loomhip_resident_bytes": (sz, []),
+        "loomhip_repack_dev": (i, [i, vp, vp, sz, sz, sz, vp]),
+        "loomhip_synth_weights_dev": (i, [i, vp, sz, sz, sz, u64, f, vp]),
+        "loomhip_matvec": (i, [i, vp, vp, vp, sz, sz]),
+        "loomhip_matmul": (i, [i, vp, vp, vp, sz, sz, sz]),
+        "loomhip_dequant_row": (i, [i, vp, vp, sz, sz]),
+        "loomhip_moe_route": (i, [vp, vp, sz, sz, i, i, f, vp, vp]),
+        "loomhip_moe_ffn_routed": (i, [vp, sz, sz, vp, vp, sz, sz, i, i, f, i, vp, i, vp, i, vp,
+                                       sz, i, vp]),
+        "loomhip_matvec_dev": (i, [i, vp, vp, vp, sz, sz, sz, vp]),
+        "loomhip_dequant_dev": (i, [i, vp, vp, sz, sz, vp]),
+        "loomhip_moe_layer_dev": (i, [C.POINTER(MoeLayerDesc), vp, sz, i, vp, vp, vp, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return lib().loomhip_last_error().decode()
+
+
+def check(rc: int, what: str = "") -> int:
+    """Raise on errors; return rc (OK or DECLINED)."""
+    if rc < 0:
+        raise LoomHipError(f"{what}: {last_error()} (rc={rc})")
+    return rc
+
+
+def init(device: int = 0) -> None:
+    check(lib().loomhip_init(device), "loomhip_init")
+
+
+def take_launch_count() -> int:
+    return int(lib().loomhip_take_launch_count())
+
+
+def plane_bytes(t: int, rows: int, cols: int) -> int:
+    return int(lib().loomhip_plane_bytes(t, rows, cols))
+
+
+def ggml_bytes(t: int, rows: int, cols: int) -> int:
+    return int(lib().loomhip_ggml_bytes(t, rows, cols))

@@ -1,0 +1,216 @@
+"""Host mirror of Loom's compute-backend seam (src/compute/backend.zig) over
+libloomhip.
+
+Names, argument meaning and decline behaviour follow the reference:
+
+* ``matvec`` / ``matmul`` / ``dequantRow`` fill ``out`` and return True when the
+  device served the call; False means "declined" (type or shape not served),
+  and the caller runs its own CPU path -- the reference's GPU backends fall
+  back to ``cpu.matvec`` the same way (src/vulkan/backend.zig:365-378).
+* ``moeRoute`` / ``moeFfnBlockRouted`` return a bool like the reference
+  (src/compute/cpu.zig:68,86): False means declined before anything ran.
+* Hard errors (device faults, bad arguments) raise ``LoomHipError``.
+
+Host arrays are numpy; the ``*_dev`` helpers take torch device tensors and
+run on torch's current stream, so they order with torch's own allocations.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import (COMBINE_EXPERT_ASC, COMBINE_SELECTION, DECLINED, F32, GATING_SIGMOID,
+               GATING_SOFTMAX, OK, MoeLayerDesc, check, lib, take_launch_count)
+
+MAX_BATCH = 256  # tokens per grouped MoE launch (the reference caps batching at 8)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+@dataclass
+class WeightRef:
+    """src/compute/cpu.zig:21 WeightRef: a GGML-typed tensor's raw bytes."""
+
+    ty: int
+    data: np.ndarray  # uint8
+
+
+@dataclass
+class RoutedCfg:
+    """src/compute/cpu.zig:61 RoutedCfg."""
+
+    n_expert: int
+    n_used: int
+    gating_sigmoid: bool
+    weights_norm: bool
+    weights_scale: float
+
+
+def parallelBegin(n: int = 0, device: int = 0) -> None:
+    """Device bring-up (the GPU backends do theirs in parallelBegin)."""
+    from . import init
+
+    init(device)
+
+
+def parallelEnd() -> None:
+    pass
+
+
+def takeCmdBufCount() -> int:
+    """Launches since the last call (src/compute/backend.zig:112-116)."""
+    return take_launch_count()
+
+
+def _served(rc: int, what: str) -> bool:
+    return check(rc, what) == OK
+
+
+def matvec(t: int, out: np.ndarray, data: np.ndarray, x: np.ndarray, rows: int, cols: int) -> bool:
+    assert out.dtype == np.float32 and out.size >= rows and x.size >= cols
+    x = np.ascontiguousarray(x, np.float32)
+    return _served(lib().loomhip_matvec(t, _p(out), _p(data), _p(x), rows, cols), "matvec")
+
+
+def matmul(t: int, out: np.ndarray, data: np.ndarray, xs: np.ndarray, n: int, rows: int,
+           cols: int) -> bool:
+    assert out.dtype == np.float32 and out.size >= n * rows and xs.size >= n * cols
+    xs = np.ascontiguousarray(xs, np.float32)
+    return _served(lib().loomhip_matmul(t, _p(out), _p(data), _p(xs), n, rows, cols), "matmul")
+
+
+def dequantRow(t: int, out: np.ndarray, data: np.ndarray, r: int, cols: int) -> bool:
+    assert out.dtype == np.float32 and out.size >= cols
+    return _served(lib().loomhip_dequant_row(t, _p(out), _p(data), r, cols), "dequantRow")
+
+
+def moeRoute(logits: np.ndarray, bias, ids_out: np.ndarray, gates_out: np.ndarray,
+             gating_sigmoid: bool, weights_norm: bool, weights_scale: float) -> bool:
+    """src/compute/cpu.zig:86 / src/vulkan/backend.zig:437."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    assert ids_out.dtype == np.uint32 and gates_out.dtype == np.float32
+    if ids_out.size != gates_out.size:
+        return False
+    rc = lib().loomhip_moe_route(_p(logits), _p(b), logits.size, ids_out.size,
+                                 GATING_SIGMOID if gating_sigmoid else GATING_SOFTMAX,
+                                 int(weights_norm), weights_scale, _p(ids_out), _p(gates_out))
+    return _served(rc, "moeRoute")
+
+
+def moeFfnBlockRouted(normed: np.ndarray, logits: np.ndarray, bias, gate_w: WeightRef,
+                      up_w: WeightRef, down_w: WeightRef, shexp, ffn: int, shexp_ffn: int,
+                      cfg: RoutedCfg, out: np.ndarray, n_tok: int = 1,
+                      combine: int = COMBINE_SELECTION) -> bool:
+    """src/compute/cpu.zig:68 moeFfnBlockRouted, generalised to n_tok tokens.
+
+    ``normed`` is [n_tok][dim], ``logits`` [n_tok][n_expert]; ``out`` [n_tok][dim]
+    receives the gated sum (SELECTION) or has it added (EXPERT_ASC).  A shared
+    expert is declined (no config on this path has one)."""
+    if shexp is not None:
+        return False
+    normed = np.ascontiguousarray(normed, np.float32)
+    logits = np.ascontiguousarray(logits, np.float32)
+    dim = normed.size // n_tok
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    rc = lib().loomhip_moe_ffn_routed(
+        _p(normed), n_tok, dim, _p(logits), _p(b), cfg.n_expert, cfg.n_used,
+        GATING_SIGMOID if cfg.gating_sigmoid else GATING_SOFTMAX, int(cfg.weights_norm),
+        cfg.weights_scale, gate_w.ty, _p(gate_w.data), up_w.ty, _p(up_w.data), down_w.ty,
+        _p(down_w.data), ffn, combine, _p(out))
+    return _served(rc, "moeFfnBlockRouted")
+
+
+def registerWeights(t: int, host: np.ndarray, rows: int, cols: int, planes: int = 1) -> int:
+    """Pointer-keyed upload; returns the device address."""
+    dev = C.c_void_p()
+    check(lib().loomhip_register_weights(t, _p(host), rows, cols, planes, C.byref(dev)),
+          "register_weights")
+    return dev.value
+
+
+def clearWeightCache() -> None:
+    lib().loomhip_clear_weight_cache()
+
+
+# ---- device-resident helpers (torch tensors as HBM buffers) ------------------
+
+
+def _stream():
+    import torch
+
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def plane_bytes(t: int, rows: int, cols: int) -> int:
+    return int(lib().loomhip_plane_bytes(t, rows, cols))
+
+
+def synth_weights_dev(t: int, rows: int, cols: int, planes: int, seed: int, stddev: float,
+                      device="cuda"):
+    """Allocate and fill `planes` device-layout planes (bench input generator)."""
+    import torch
+
+    buf = torch.empty(plane_bytes(t, rows, cols) * planes, dtype=torch.uint8, device=device)
+    check(lib().loomhip_synth_weights_dev(t, _ptr(buf), rows, cols, planes, seed, stddev,
+                                          _stream()), "synth_weights_dev")
+    return buf
+
+
+def repack_dev(t: int, ggml_bytes_dev, rows: int, cols: int, planes: int):
+    """GGML bytes (device uint8 tensor) -> device layout."""
+    import torch
+
+    out = torch.empty(plane_bytes(t, rows, cols) * planes, dtype=torch.uint8,
+                      device=ggml_bytes_dev.device)
+    check(lib().loomhip_repack_dev(t, _ptr(out), _ptr(ggml_bytes_dev), rows, cols, planes,
+                                   _stream()), "repack_dev")
+    return out
+
+
+def matvec_dev(t: int, out, w, x, n: int, rows: int, cols: int) -> int:
+    return check(lib().loomhip_matvec_dev(t, _ptr(out), _ptr(w), _ptr(x), n, rows, cols,
+                                          _stream()), "matvec_dev")
+
+
+def dequant_dev(t: int, out, w, rows: int, cols: int) -> int:
+    return check(lib().loomhip_dequant_dev(t, _ptr(out), _ptr(w), rows, cols, _stream()),
+                 "dequant_dev")
+
+
+class MoeLayer:
+    """Device-resident MoE layer (weights are torch uint8 tensors in the
+    device layout, one plane per expert)."""
+
+    def __init__(self, dim, ffn, n_expert, n_used, router, gate, up, down, gate_t, up_t, down_t,
+                 router_bias=None, sel_bias=None, gating=GATING_SOFTMAX, weights_norm=True,
+                 weights_scale=1.0):
+        self.keep = (router, gate, up, down, router_bias, sel_bias)
+        self.desc = MoeLayerDesc(dim, ffn, n_expert, n_used, gating, int(weights_norm),
+                                 weights_scale, router.data_ptr(),
+                                 None if router_bias is None else router_bias.data_ptr(),
+                                 None if sel_bias is None else sel_bias.data_ptr(), gate_t, up_t,
+                                 down_t, gate.data_ptr(), up.data_ptr(), down.data_ptr())
+        self.dim, self.ffn, self.n_expert, self.n_used = dim, ffn, n_expert, n_used
+
+    def __call__(self, normed, out, combine=COMBINE_SELECTION, ids=None, gates=None) -> int:
+        n = normed.shape[0]
+        return check(lib().loomhip_moe_layer_dev(C.byref(self.desc), _ptr(normed), n, combine,
+                                                 _ptr(out), _ptr(ids), _ptr(gates), _stream()),
+                     "moe_layer_dev")
+
+
+__all__ = [
+    "COMBINE_EXPERT_ASC", "COMBINE_SELECTION", "DECLINED", "F32", "MAX_BATCH", "MoeLayer",
+    "RoutedCfg", "WeightRef", "clearWeightCache", "dequantRow", "matmul", "matvec", "moeFfnBlockRouted",
+    "moeRoute", "parallelBegin", "parallelEnd", "registerWeights", "takeCmdBufCount",
+]

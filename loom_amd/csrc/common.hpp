@@ -1,0 +1,138 @@
+// common.hpp -- shared definitions for libloomhip (gfx950, wave64).
+//
+// Device weight layout (per [rows][cols] plane, U = rows * blocks_per_row):
+//   Q4_K: GGML's native 144-byte blocks (16-byte aligned already).
+//   Q6_K: ql[U][128] | qh[U][64] | scales[U][16] | d[U] (f16, padded to 16 B)
+//   Q8_0: qs[U][32] | d[U] (f16, padded to 16 B)
+//   Q4_0: qs[U][16] | d[U] (f16, padded to 16 B)
+// GGML's 210/34/18-byte blocks are only 2-byte aligned; splitting them per
+// plane keeps the byte count and makes every lane's load an aligned 16 bytes.
+//
+// Quantized activations (the reference's XBlock / XBlockK,
+// src/gguf/ggml.zig:738-770), per activation vector of `cols` values:
+//   q: int8[cols]; d: f32[cols / QB]; s: i32[cols / 16] (K) or [cols / 32]
+// with QB = 256 for the K-quants (quantizeX256) and 32 for Q4_0/Q8_0
+// (quantizeX).  Vector v lives at q + v*cols, d + v*(cols/QB), s + v*ns.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define LH_F32 0
+#define LH_F16 1
+#define LH_Q4_0 2
+#define LH_Q8_0 8
+#define LH_Q4_K 12
+#define LH_Q6_K 14
+
+namespace lh {
+
+__host__ __device__ inline constexpr int block_elems(int t) {
+    return (t == LH_Q4_0 || t == LH_Q8_0) ? 32 : (t == LH_Q4_K || t == LH_Q6_K) ? 256 : 1;
+}
+__host__ __device__ inline constexpr int block_bytes(int t) {
+    return t == LH_Q4_0 ? 18 : t == LH_Q8_0 ? 34 : t == LH_Q4_K ? 144 : t == LH_Q6_K ? 210
+           : t == LH_F16 ? 2 : 4;
+}
+__host__ __device__ inline constexpr size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
+
+// Bytes of one plane in the device layout.
+__host__ __device__ inline size_t plane_bytes(int t, size_t rows, size_t cols) {
+    size_t U = rows * (cols / block_elems(t));
+    switch (t) {
+    case LH_Q4_K:
+        return U * 144;
+    case LH_Q6_K:
+        return U * 208 + align16(U * 2);
+    case LH_Q8_0:
+        return U * 32 + align16(U * 2);
+    case LH_Q4_0:
+        return U * 16 + align16(U * 2);
+    case LH_F16:
+        return rows * cols * 2;
+    default:
+        return rows * cols * 4;
+    }
+}
+__host__ __device__ inline size_t ggml_bytes(int t, size_t rows, size_t cols) {
+    return rows * (cols / block_elems(t)) * block_bytes(t);
+}
+
+// Activation block width used by the weight type's int8 kernel.
+__host__ __device__ inline constexpr int act_block(int t) {
+    return (t == LH_Q4_K || t == LH_Q6_K) ? 256 : 32;
+}
+// i32 sums per activation vector: per 16 for K-quants, per 32 otherwise.
+__host__ __device__ inline size_t act_sums(int t, size_t cols) {
+    return (t == LH_Q4_K || t == LH_Q6_K) ? cols / 16 : cols / 32;
+}
+
+// ---- device helpers -------------------------------------------------------
+
+__device__ inline float half_bits_to_float(uint32_t bits16) {
+    __half_raw r;
+    r.x = (unsigned short)(bits16 & 0xffff);
+    return __half2float(__half(r));
+}
+
+// Round half away from zero, saturate at +-127, non-finite -> 0
+// (src/gguf/ggml.zig:1067-1073 toI8Saturating).
+__device__ inline int to_i8_sat(float v) {
+    if (!__builtin_isfinite(v))
+        return 0;
+    float r = __builtin_roundf(v);
+    if (r >= 127.0f)
+        return 127;
+    if (r <= -127.0f)
+        return -127;
+    return (int)r;
+}
+
+__device__ inline int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// DPP reductions inside groups of 2, 4 and 8 lanes (quad_perm xor1/xor2 and
+// row_half_mirror).  Integer sums, so the order does not matter.
+__device__ inline int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+__device__ inline int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+__device__ inline int dpp_hmirror(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false); }
+
+template <int LANES>
+__device__ inline int group_sum(int v) {
+    if constexpr (LANES >= 2)
+        v += dpp_xor1(v);
+    if constexpr (LANES >= 4)
+        v += dpp_xor2(v);
+    if constexpr (LANES >= 8)
+        v += dpp_hmirror(v);
+    return v;
+}
+
+__device__ inline float wave_max(float v) {
+    for (int o = 32; o >= 1; o >>= 1)
+        v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// sdot4 over the four dwords of two 16-byte vectors.
+__device__ inline int dot16(const int4 &w, const int4 &x, int acc) {
+    acc = sdot4(w.x, x.x, acc);
+    acc = sdot4(w.y, x.y, acc);
+    acc = sdot4(w.z, x.z, acc);
+    acc = sdot4(w.w, x.w, acc);
+    return acc;
+}
+
+__device__ inline int4 and4(const int4 &a, int m) { return make_int4(a.x & m, a.y & m, a.z & m, a.w & m); }
+__device__ inline int4 shr4(const int4 &a, int s) {
+    return make_int4((int)((unsigned)a.x >> s), (int)((unsigned)a.y >> s), (int)((unsigned)a.z >> s),
+                     (int)((unsigned)a.w >> s));
+}
+
+__device__ inline uint32_t byte_of(const uint4 &v, int i) {
+    uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
+    return (w >> (8 * (i & 3))) & 0xff;
+}
+
+} // namespace lh

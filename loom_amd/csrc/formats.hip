@@ -1,0 +1,294 @@
+// formats.hip -- activation quantizers, exact dequant, GGML->device repack and
+// the synthetic weight generator.
+#include "kernels.hpp"
+
+namespace lh {
+
+// ---- activation quantizers ------------------------------------------------
+
+// quantizeX256 (src/gguf/ggml.zig:776-800): one wave per 256-value block.
+// Lane l holds values 4l..4l+3; amax is an exact max (order-free), the
+// per-16 sums are integer.
+__global__ __launch_bounds__(64) void quant_x256_kernel(const float *__restrict__ x, int cols,
+                                                        int x_stride, int8_t *__restrict__ q,
+                                                        float *__restrict__ d,
+                                                        int32_t *__restrict__ s) {
+    const int b = blockIdx.x, v = blockIdx.y, lane = threadIdx.x;
+    const int nb = cols / 256;
+    const float4 xv = *(const float4 *)(x + (size_t)v * x_stride + b * 256 + 4 * lane);
+    float a = 0.0f;
+    if (__builtin_isfinite(xv.x)) a = fmaxf(a, fabsf(xv.x));
+    if (__builtin_isfinite(xv.y)) a = fmaxf(a, fabsf(xv.y));
+    if (__builtin_isfinite(xv.z)) a = fmaxf(a, fabsf(xv.z));
+    if (__builtin_isfinite(xv.w)) a = fmaxf(a, fabsf(xv.w));
+    const float amax = wave_max(a);
+    const float dd = amax / 127.0f;
+    const float inv = (dd != 0.0f && __builtin_isfinite(dd)) ? 1.0f / dd : 0.0f;
+    const int q0 = to_i8_sat(xv.x * inv), q1 = to_i8_sat(xv.y * inv);
+    const int q2 = to_i8_sat(xv.z * inv), q3 = to_i8_sat(xv.w * inv);
+    const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                            ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+    *(uint32_t *)(q + (size_t)v * cols + b * 256 + 4 * lane) = packed;
+    const int sum16 = group_sum<4>(q0 + q1 + q2 + q3);
+    if ((lane & 3) == 0)
+        s[(size_t)v * (cols / 16) + b * 16 + lane / 4] = sum16;
+    if (lane == 0)
+        d[(size_t)v * nb + b] = __builtin_isfinite(dd) ? dd : 0.0f;
+}
+
+// quantizeX (src/gguf/ggml.zig:1077-1098): 32-value blocks, eight lanes per
+// block (4 values each), eight blocks per wave.
+__global__ __launch_bounds__(64) void quant_x32_kernel(const float *__restrict__ x, int cols,
+                                                       int x_stride, int8_t *__restrict__ q,
+                                                       float *__restrict__ d,
+                                                       int32_t *__restrict__ s) {
+    const int v = blockIdx.y, lane = threadIdx.x;
+    const int nb = cols / 32;
+    const int blk = blockIdx.x * 8 + lane / 8;
+    const bool live = blk < nb;
+    const int bc = live ? blk : nb - 1; // clamp: idle lanes read a valid block
+    const float4 xv = *(const float4 *)(x + (size_t)v * x_stride + bc * 32 + 4 * (lane & 7));
+    float a = 0.0f;
+    if (__builtin_isfinite(xv.x)) a = fmaxf(a, fabsf(xv.x));
+    if (__builtin_isfinite(xv.y)) a = fmaxf(a, fabsf(xv.y));
+    if (__builtin_isfinite(xv.z)) a = fmaxf(a, fabsf(xv.z));
+    if (__builtin_isfinite(xv.w)) a = fmaxf(a, fabsf(xv.w));
+    a = fmaxf(a, __shfl_xor(a, 1, 64));
+    a = fmaxf(a, __shfl_xor(a, 2, 64));
+    a = fmaxf(a, __shfl_xor(a, 4, 64));
+    const float dd = a / 127.0f;
+    const float inv = (dd != 0.0f && __builtin_isfinite(dd)) ? 1.0f / dd : 0.0f;
+    const int q0 = to_i8_sat(xv.x * inv), q1 = to_i8_sat(xv.y * inv);
+    const int q2 = to_i8_sat(xv.z * inv), q3 = to_i8_sat(xv.w * inv);
+    const int sum = group_sum<8>(q0 + q1 + q2 + q3);
+    if (live) {
+        const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                                ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+        *(uint32_t *)(q + (size_t)v * cols + blk * 32 + 4 * (lane & 7)) = packed;
+        if ((lane & 7) == 0) {
+            s[(size_t)v * nb + blk] = sum;
+            d[(size_t)v * nb + blk] = __builtin_isfinite(dd) ? dd : 0.0f;
+        }
+    }
+}
+
+void launch_quant_act(int wtype, const float *x, int cols, int x_stride, int nvec, QAct qa,
+                      hipStream_t st) {
+    if (act_block(wtype) == 256) {
+        hipLaunchKernelGGL(quant_x256_kernel, dim3(cols / 256, nvec), dim3(64), 0, st, x, cols,
+                           x_stride, qa.q, qa.d, qa.s);
+    } else {
+        const int nb = cols / 32;
+        hipLaunchKernelGGL(quant_x32_kernel, dim3((nb + 7) / 8, nvec), dim3(64), 0, st, x, cols,
+                           x_stride, qa.q, qa.d, qa.s);
+    }
+    note_launch();
+}
+
+// ---- exact dequant from the device layout ---------------------------------
+// One thread per value; f32 arithmetic in the reference's two-rounding form
+// (src/gguf/ggml.zig:1342-1374, 1420-1471, 1834-1849).
+
+__global__ void dequant_kernel(int t, const uint8_t *__restrict__ w, size_t rows, size_t cols,
+                               float *__restrict__ out) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * cols)
+        return;
+    const size_t r = idx / cols, c = idx % cols;
+    const int be = block_elems(t);
+    const size_t nb = cols / be;
+    const size_t unit = r * nb + c / be;
+    const size_t U = rows * nb;
+    const int e = (int)(c % be);
+    float val = 0.0f;
+    if (t == LH_Q4_K) {
+        const uint8_t *blk = w + unit * 144;
+        const float d = half_bits_to_float(blk[0] | (blk[1] << 8));
+        const float dmin = half_bits_to_float(blk[2] | (blk[3] << 8));
+        const uint8_t *s = blk + 4;
+        const int g = e / 32, l = e % 32;
+        int sc, m;
+        if (g < 4) {
+            sc = s[g] & 63;
+            m = s[g + 4] & 63;
+        } else {
+            sc = (s[g + 4] & 0xF) | ((s[g - 4] >> 6) << 4);
+            m = (s[g + 4] >> 4) | ((s[g] >> 6) << 4);
+        }
+        const uint8_t byte = blk[16 + 32 * (g / 2) + l];
+        const int qv = (g & 1) ? (byte >> 4) : (byte & 0xF);
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        val = d1 * (float)qv - m1;
+    } else if (t == LH_Q6_K) {
+        const uint8_t *ql = w + unit * 128, *qh = w + U * 128 + unit * 64;
+        const int8_t *sc = (const int8_t *)(w + U * 192 + unit * 16);
+        const uint16_t *dp = (const uint16_t *)(w + U * 208);
+        const float d = half_bits_to_float(dp[unit]);
+        const int h = e / 128, r128 = e % 128, quarter = r128 / 32, l = r128 % 32;
+        const uint8_t qlb = ql[64 * h + l + ((quarter & 1) ? 32 : 0)];
+        const uint8_t qhb = qh[32 * h + l];
+        const int nib = (quarter < 2) ? (qlb & 0xF) : (qlb >> 4);
+        const int qv = nib | (((qhb >> (2 * quarter)) & 3) << 4);
+        const float s = d * (float)sc[8 * h + l / 16 + 2 * quarter];
+        val = s * ((float)qv - 32.0f);
+    } else if (t == LH_Q8_0) {
+        const int8_t *qs = (const int8_t *)(w + unit * 32);
+        const uint16_t *dp = (const uint16_t *)(w + U * 32);
+        val = (float)qs[e] * half_bits_to_float(dp[unit]);
+    } else if (t == LH_Q4_0) {
+        const uint8_t *qs = w + unit * 16;
+        const uint16_t *dp = (const uint16_t *)(w + U * 16);
+        const int nib = e < 16 ? (qs[e] & 0xF) : (qs[e - 16] >> 4);
+        val = (float)(nib - 8) * half_bits_to_float(dp[unit]);
+    } else if (t == LH_F16) {
+        val = half_bits_to_float(((const uint16_t *)w)[idx]);
+    } else {
+        val = ((const float *)w)[idx];
+    }
+    out[idx] = val;
+}
+
+void launch_dequant(int t, const void *w, size_t rows, size_t cols, float *out, hipStream_t st) {
+    const size_t n = rows * cols;
+    hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, t,
+                       (const uint8_t *)w, rows, cols, out);
+    note_launch();
+}
+
+// ---- GGML -> device layout -------------------------------------------------
+// One thread per block; planes are independent.
+
+__global__ void repack_kernel(int t, const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                              size_t U, size_t src_plane, size_t dst_plane, size_t planes) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= U * planes)
+        return;
+    const size_t p = idx / U, u = idx % U;
+    const uint8_t *s = src + p * src_plane + u * block_bytes(t);
+    uint8_t *d = dst + p * dst_plane;
+    if (t == LH_Q6_K) {
+        for (int i = 0; i < 128; i++) d[u * 128 + i] = s[i];
+        for (int i = 0; i < 64; i++) d[U * 128 + u * 64 + i] = s[128 + i];
+        for (int i = 0; i < 16; i++) d[U * 192 + u * 16 + i] = s[192 + i];
+        d[U * 208 + 2 * u] = s[208];
+        d[U * 208 + 2 * u + 1] = s[209];
+    } else if (t == LH_Q8_0) {
+        for (int i = 0; i < 32; i++) d[u * 32 + i] = s[2 + i];
+        d[U * 32 + 2 * u] = s[0];
+        d[U * 32 + 2 * u + 1] = s[1];
+    } else if (t == LH_Q4_0) {
+        for (int i = 0; i < 16; i++) d[u * 16 + i] = s[2 + i];
+        d[U * 16 + 2 * u] = s[0];
+        d[U * 16 + 2 * u + 1] = s[1];
+    }
+}
+
+void launch_repack(int t, const void *src, void *dst, size_t rows, size_t cols, size_t planes,
+                   hipStream_t st) {
+    const size_t U = rows * (cols / block_elems(t));
+    const size_t sp = ggml_bytes(t, rows, cols), dp = plane_bytes(t, rows, cols);
+    if (t == LH_Q4_K || t == LH_F32 || t == LH_F16) {
+        (void)hipMemcpyAsync(dst, src, sp * planes, hipMemcpyDeviceToDevice, st);
+        return;
+    }
+    const size_t n = U * planes;
+    hipLaunchKernelGGL(repack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, t,
+                       (const uint8_t *)src, (uint8_t *)dst, U, sp, dp, planes);
+    note_launch();
+}
+
+// ---- synthetic weights ------------------------------------------------------
+// Counter-based hash per (seed, plane, unit, word): deterministic and
+// independent of launch shape.
+
+__device__ inline uint32_t mix32(uint64_t x) {
+    x ^= x >> 33;
+    x *= 0xff51afd7ed558ccdull;
+    x ^= x >> 33;
+    x *= 0xc4ceb9fe1a85ec53ull;
+    x ^= x >> 33;
+    return (uint32_t)x;
+}
+
+__device__ inline uint16_t f2h_bits(float f) {
+    __half h = __float2half(f);
+    return __half_raw(h).x;
+}
+
+__global__ void synth_kernel(int t, uint8_t *__restrict__ dst, size_t U, size_t plane_b,
+                             size_t planes, uint64_t seed, float stddev) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= U * planes)
+        return;
+    const size_t p = idx / U, u = idx % U;
+    uint8_t *d = dst + p * plane_b;
+    const uint64_t key = (seed * 0x9E3779B97F4A7C15ull) ^ (idx * 0xD1B54A32D192ED03ull);
+    auto word = [&](int i) { return mix32(key + (uint64_t)i * 0x632BE59BD9B4E019ull); };
+    if (t == LH_Q4_K) {
+        // value = d*sc*q - dmin*m with q uniform 0..15: std ~ d*sc*4.6
+        uint8_t *blk = d + u * 144;
+        const float dd = stddev / (4.6f * 52.0f);
+        const uint16_t hd = f2h_bits(dd), hm = f2h_bits(dd * 7.5f);
+        blk[0] = hd & 0xff; blk[1] = hd >> 8; blk[2] = hm & 0xff; blk[3] = hm >> 8;
+        const uint32_t r0 = word(0), r1 = word(1), r2 = word(2);
+        for (int j = 0; j < 12; j++) {
+            const uint32_t r = j < 4 ? r0 : j < 8 ? r1 : r2;
+            blk[4 + j] = (uint8_t)(0x28 | ((r >> (8 * (j & 3))) & 0xD7)); // scales 40..63, mins alike
+        }
+        for (int i = 0; i < 32; i++) {
+            const uint32_t r = word(3 + i);
+            blk[16 + 4 * i] = r & 0xff; blk[17 + 4 * i] = (r >> 8) & 0xff;
+            blk[18 + 4 * i] = (r >> 16) & 0xff; blk[19 + 4 * i] = r >> 24;
+        }
+    } else if (t == LH_Q6_K) {
+        for (int i = 0; i < 32; i++) {
+            const uint32_t r = word(i);
+            for (int k = 0; k < 4; k++) d[u * 128 + 4 * i + k] = (r >> (8 * k)) & 0xff;
+        }
+        for (int i = 0; i < 16; i++) {
+            const uint32_t r = word(32 + i);
+            for (int k = 0; k < 4; k++) d[U * 128 + u * 64 + 4 * i + k] = (r >> (8 * k)) & 0xff;
+        }
+        for (int i = 0; i < 4; i++) {
+            const uint32_t r = word(48 + i);
+            for (int k = 0; k < 4; k++) { // signed scales with |sc| in 64..127
+                const uint8_t b = (r >> (8 * k)) & 0xff;
+                const int v = 64 + (b & 63);
+                d[U * 192 + u * 16 + 4 * i + k] = (uint8_t)(int8_t)((b & 0x80) ? -v : v);
+            }
+        }
+        const uint16_t hd = f2h_bits(stddev / (18.5f * 96.0f));
+        d[U * 208 + 2 * u] = hd & 0xff;
+        d[U * 208 + 2 * u + 1] = hd >> 8;
+    } else if (t == LH_Q8_0) {
+        for (int i = 0; i < 8; i++) {
+            const uint32_t r = word(i);
+            for (int k = 0; k < 4; k++) {
+                int8_t v = (int8_t)((r >> (8 * k)) & 0xff);
+                d[u * 32 + 4 * i + k] = (uint8_t)(v == -128 ? -127 : v);
+            }
+        }
+        const uint16_t hd = f2h_bits(stddev / 73.0f);
+        d[U * 32 + 2 * u] = hd & 0xff;
+        d[U * 32 + 2 * u + 1] = hd >> 8;
+    } else if (t == LH_Q4_0) {
+        for (int i = 0; i < 4; i++) {
+            const uint32_t r = word(i);
+            for (int k = 0; k < 4; k++) d[u * 16 + 4 * i + k] = (r >> (8 * k)) & 0xff;
+        }
+        const uint16_t hd = f2h_bits(stddev / 4.6f);
+        d[U * 16 + 2 * u] = hd & 0xff;
+        d[U * 16 + 2 * u + 1] = hd >> 8;
+    }
+}
+
+void launch_synth(int t, void *dst, size_t rows, size_t cols, size_t planes, uint64_t seed,
+                  float stddev, hipStream_t st) {
+    const size_t U = rows * (cols / block_elems(t));
+    const size_t n = U * planes;
+    hipLaunchKernelGGL(synth_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, t,
+                       (uint8_t *)dst, U, plane_bytes(t, rows, cols), planes, seed, stddev);
+    note_launch();
+}
+
+} // namespace lh

@@ -1,0 +1,86 @@
+// kernels.hpp -- launch interfaces shared by the kernel files and the host
+// runtime of libloomhip.
+#pragma once
+
+#include "common.hpp"
+
+namespace lh {
+
+// Quantized activation vectors (see common.hpp for the layout).
+struct QAct {
+    int8_t *q;
+    float *d;
+    int32_t *s;
+};
+
+// One work group of the grouped matvec: `n` activation vectors (pairs
+// [first, first+n) of the pair table) against weight plane `plane`.
+struct DmmvGroup {
+    int plane;
+    int first;
+    int n;
+};
+
+struct DmmvParams {
+    const uint8_t *w;  // weight planes (device layout)
+    const uint8_t *w2; // second matrix sharing the activations (fused up), or null
+    size_t plane_bytes;
+    int rows, cols;
+    const int8_t *xq; // quantized activations
+    const float *xd;
+    const int32_t *xs;
+    const int *pair_src; // activation vector index of each pair
+    const int *pair_dst; // output index of each pair
+    const DmmvGroup *groups;
+    const int *n_groups_dev; // device-side group count, or null
+    int n_groups;            // host-side group count (upper bound when n_groups_dev set)
+    float *out;              // out[dst * out_stride + row]
+    int out_stride;
+    int rpw; // rows per wave
+};
+
+void note_launch();
+
+void launch_quant_act(int wtype, const float *x, int cols, int x_stride, int nvec, QAct qa,
+                      hipStream_t st);
+void launch_dequant(int t, const void *w, size_t rows, size_t cols, float *out, hipStream_t st);
+void launch_repack(int t, const void *src, void *dst, size_t rows, size_t cols, size_t planes,
+                   hipStream_t st);
+void launch_synth(int t, void *dst, size_t rows, size_t cols, size_t planes, uint64_t seed,
+                  float stddev, hipStream_t st);
+
+// Grouped int8-activation matvec (bit-identical to the reference CPU kernels).
+// nt = max pairs per group (1, 2, 4 or 8); fused = SwiGLU(gate, up) epilogue.
+bool dmmv_supported(int t, int cols);
+// Returns false (launching nothing) when the partials would not fit in LDS.
+bool launch_dmmv(int t, int nt, bool fused, const DmmvParams &p, hipStream_t st);
+// Rows per wave chosen for a launch of `rows` rows x `groups` groups.
+int dmmv_pick_rpw(int t, int cols, int rows, int groups, int nt, bool fused);
+size_t dmmv_lds_bytes(int t, int cols, int nt, bool fused, int rpw);
+constexpr size_t DMMV_LDS_BUDGET = 48 * 1024;
+
+// f32 router GEMV in dotF32 order (src/gguf/ggml.zig:198-217), plus optional
+// logit bias: logits[v][e] for n vectors.
+void launch_router_gemv(const float *w, const float *bias, const float *x, int n_expert, int dim,
+                        int n, float *logits, hipStream_t st);
+// Route n tokens (src/gguf/moe.zig:106-158).
+void launch_route(const float *logits, const float *sel_bias, int n_expert, int n_used, int gating,
+                  int weights_norm, float weights_scale, int n, uint32_t *ids, float *gates,
+                  hipStream_t st);
+
+// Token -> expert bucketing: pairs sorted by (expert, token), groups of at
+// most `nt` pairs per expert, pair_of[t][s] = pair index of token t slot s.
+struct MoeBuckets {
+    int *pair_tok;    // [n*k]
+    int *pair_of;     // [n*k]
+    int *iota;        // [n*k] identity
+    DmmvGroup *groups; // [max_groups]
+    int *n_groups;    // [1]
+};
+int moe_max_groups(int n, int k, int n_expert, int nt);
+void launch_bucket(const uint32_t *ids, int n, int k, int n_expert, int nt, MoeBuckets b,
+                   hipStream_t st);
+void launch_combine(const float *y, const float *gates, const uint32_t *ids, const int *pair_of,
+                    int n, int k, int dim, int mode, float *out, hipStream_t st);
+
+} // namespace lh

@@ -1,0 +1,256 @@
+// moe_host.hip -- host orchestration of the MoE layer: route -> bucket ->
+// quantize -> fused gate/up+SwiGLU -> quantize -> down -> combine, all
+// stream-ordered with no host round trip (the one-submission shape of
+// src/vulkan/backend.zig:455-551, generalised to n tokens with the grouped
+// expert kernels).
+#include "runtime.hpp"
+
+namespace lh {
+
+static Scratch g_moe;   // per-call workspace
+static Scratch g_stage; // seam-call staging
+
+void moe_release_scratch() {
+    g_moe.release();
+    g_stage.release();
+}
+
+struct MoeRun {
+    size_t dim, ffn, E, k;
+    int gating, weights_norm;
+    float weights_scale;
+    const float *router, *router_bias, *sel_bias; // router null: logits given
+    int gate_t, up_t, down_t;
+    const void *gate, *up, *down;
+};
+
+static int moe_check(const MoeRun &m, size_t n) {
+    if (n == 0 || n > 256)
+        return fail(LOOMHIP_DECLINED, "moe: %zu tokens (1..256 served)", n);
+    if (m.E == 0 || m.E > 256 || m.k == 0 || m.k > 16 || m.k > m.E)
+        return fail(LOOMHIP_DECLINED, "moe: %zu experts / top-%zu not served", m.E, m.k);
+    if (m.gate_t != m.up_t)
+        return fail(LOOMHIP_DECLINED, "moe: gate/up types differ (%d, %d)", m.gate_t, m.up_t);
+    if (!dmmv_supported(m.gate_t, (int)m.dim) || !dmmv_supported(m.down_t, (int)m.ffn))
+        return fail(LOOMHIP_DECLINED, "moe: shapes dim %zu / ffn %zu not served for types %d/%d",
+                    m.dim, m.ffn, m.gate_t, m.down_t);
+    if (m.dim % 32 || m.ffn % 32)
+        return fail(LOOMHIP_DECLINED, "moe: dims must be multiples of 32");
+    return LOOMHIP_OK;
+}
+
+static size_t qbytes(size_t nvec, size_t cols) {
+    return align16(nvec * cols) + align16(nvec * (cols / 32) * 4) + align16(nvec * (cols / 16) * 4);
+}
+
+static QAct qview(char *base, size_t nvec, size_t cols) {
+    QAct q;
+    q.q = (int8_t *)base;
+    q.d = (float *)(base + align16(nvec * cols));
+    q.s = (int32_t *)((char *)q.d + align16(nvec * (cols / 32) * 4));
+    return q;
+}
+
+static int moe_nt(size_t n, size_t k, size_t E) {
+    if (n == 1)
+        return 1;
+    const size_t per = (n * k + E - 1) / E;
+    return per >= 4 ? 8 : per >= 2 ? 4 : 2;
+}
+
+// normed/logits/out are device pointers; logits may be null when m.router is set.
+static int moe_run(const MoeRun &m, const float *normed, const float *logits_in, size_t n,
+                   int combine, float *out, uint32_t *ids_out, float *gates_out, hipStream_t st) {
+    if (int rc = moe_check(m, n))
+        return rc;
+    const size_t P = n * m.k;
+    const int nt = moe_nt(n, m.k, m.E);
+    const int maxg = moe_max_groups((int)n, (int)m.k, (int)m.E, nt);
+    // workspace layout
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = off;
+        off += align16(bytes);
+        return o;
+    };
+    const size_t o_qx = take(qbytes(n, m.dim));
+    const size_t o_log = take(n * m.E * 4);
+    const size_t o_ids = take(P * 4), o_gates = take(P * 4);
+    const size_t o_ptok = take(P * 4), o_pof = take(P * 4), o_iota = take(P * 4);
+    const size_t o_groups = take(maxg * sizeof(DmmvGroup)), o_ng = take(16);
+    const size_t o_act = take(P * m.ffn * 4);
+    const size_t o_qa = take(qbytes(P, m.ffn));
+    const size_t o_y = take(P * m.dim * 4);
+    if (int rc = g_moe.reserve(off))
+        return rc;
+    char *base = (char *)g_moe.ptr;
+    const QAct qx = qview(base + o_qx, n, m.dim);
+    const QAct qa = qview(base + o_qa, P, m.ffn);
+    float *logits = logits_in ? (float *)logits_in : (float *)(base + o_log);
+    uint32_t *ids = ids_out ? ids_out : (uint32_t *)(base + o_ids);
+    float *gates = gates_out ? gates_out : (float *)(base + o_gates);
+    MoeBuckets b;
+    b.pair_tok = (int *)(base + o_ptok);
+    b.pair_of = (int *)(base + o_pof);
+    b.iota = (int *)(base + o_iota);
+    b.groups = (DmmvGroup *)(base + o_groups);
+    b.n_groups = (int *)(base + o_ng);
+    float *act = (float *)(base + o_act);
+    float *y = (float *)(base + o_y);
+
+    if (m.router)
+        launch_router_gemv(m.router, m.router_bias, normed, (int)m.E, (int)m.dim, (int)n, logits, st);
+    launch_route(logits, m.sel_bias, (int)m.E, (int)m.k, m.gating, m.weights_norm, m.weights_scale,
+                 (int)n, ids, gates, st);
+    launch_bucket(ids, (int)n, (int)m.k, (int)m.E, nt, b, st);
+    launch_quant_act(m.gate_t, normed, (int)m.dim, (int)m.dim, (int)n, qx, st);
+
+    const int exp_groups = (int)(P < (size_t)maxg ? P : (size_t)maxg);
+    DmmvParams gu{};
+    gu.w = (const uint8_t *)m.gate;
+    gu.w2 = (const uint8_t *)m.up;
+    gu.plane_bytes = plane_bytes(m.gate_t, m.ffn, m.dim);
+    gu.rows = (int)m.ffn;
+    gu.cols = (int)m.dim;
+    gu.xq = qx.q;
+    gu.xd = qx.d;
+    gu.xs = qx.s;
+    gu.pair_src = b.pair_tok;
+    gu.pair_dst = b.iota;
+    gu.groups = b.groups;
+    gu.n_groups_dev = b.n_groups;
+    gu.n_groups = maxg;
+    gu.out = act;
+    gu.out_stride = (int)m.ffn;
+    gu.rpw = dmmv_pick_rpw(m.gate_t, (int)m.dim, (int)m.ffn, exp_groups, nt, true);
+    if (!launch_dmmv(m.gate_t, nt, true, gu, st))
+        return fail(LOOMHIP_ERR_ARG, "moe: gate/up partials exceed LDS");
+
+    launch_quant_act(m.down_t, act, (int)m.ffn, (int)m.ffn, (int)P, qa, st);
+
+    DmmvParams dn{};
+    dn.w = (const uint8_t *)m.down;
+    dn.w2 = nullptr;
+    dn.plane_bytes = plane_bytes(m.down_t, m.dim, m.ffn);
+    dn.rows = (int)m.dim;
+    dn.cols = (int)m.ffn;
+    dn.xq = qa.q;
+    dn.xd = qa.d;
+    dn.xs = qa.s;
+    dn.pair_src = b.iota;
+    dn.pair_dst = b.iota;
+    dn.groups = b.groups;
+    dn.n_groups_dev = b.n_groups;
+    dn.n_groups = maxg;
+    dn.out = y;
+    dn.out_stride = (int)m.dim;
+    dn.rpw = dmmv_pick_rpw(m.down_t, (int)m.ffn, (int)m.dim, exp_groups, nt, false);
+    if (!launch_dmmv(m.down_t, nt, false, dn, st))
+        return fail(LOOMHIP_ERR_ARG, "moe: down partials exceed LDS");
+
+    launch_combine(y, gates, ids, b.pair_of, (int)n, (int)m.k, (int)m.dim, combine, out, st);
+    return LOOMHIP_OK;
+}
+
+} // namespace lh
+
+using namespace lh;
+
+extern "C" {
+
+int loomhip_moe_layer_dev(const loomhip_moe_layer *L, const float *normed, size_t n_tok,
+                          int combine, float *out, uint32_t *ids_out, float *gates_out,
+                          void *stream) {
+    if (int rc = require_ready())
+        return rc;
+    if (!L || !normed || !out || !L->router)
+        return fail(LOOMHIP_ERR_ARG, "moe_layer_dev: null argument");
+    MoeRun m{L->dim, L->ffn, L->n_expert, L->n_used, L->gating, L->weights_norm, L->weights_scale,
+             L->router, L->router_bias, L->sel_bias, L->gate_t, L->up_t, L->down_t, L->gate,
+             L->up, L->down};
+    return moe_run(m, normed, nullptr, n_tok, combine, out, ids_out, gates_out, stream_of(stream));
+}
+
+int loomhip_moe_route(const float *logits, const float *bias, size_t n_expert, size_t n_used,
+                      int gating, int weights_norm, float weights_scale, uint32_t *ids_out,
+                      float *gates_out) {
+    if (int rc = require_ready())
+        return rc;
+    if (n_expert == 0 || n_expert > 256 || n_used == 0 || n_used > 16 || n_used > n_expert)
+        return fail(LOOMHIP_DECLINED, "moe_route: %zu experts / top-%zu not served", n_expert, n_used);
+    const size_t need = 2 * n_expert * 4 + 2 * 64;
+    if (int rc = g_stage.reserve(need))
+        return rc;
+    char *base = (char *)g_stage.ptr;
+    float *dl = (float *)base, *db = (float *)(base + n_expert * 4);
+    uint32_t *di = (uint32_t *)(base + 2 * n_expert * 4);
+    float *dg = (float *)(base + 2 * n_expert * 4 + 64);
+    hipStream_t st = g_ctx.compute;
+    hipError_t e = hipMemcpyAsync(dl, logits, n_expert * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess && bias)
+        e = hipMemcpyAsync(db, bias, n_expert * 4, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess)
+        return hip_fail(e, "moe_route staging");
+    launch_route(dl, bias ? db : nullptr, (int)n_expert, (int)n_used, gating, weights_norm,
+                 weights_scale, 1, di, dg, st);
+    e = hipMemcpyAsync(ids_out, di, n_used * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(gates_out, dg, n_used * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(st);
+    if (e != hipSuccess)
+        return hip_fail(e, "moe_route readback");
+    return LOOMHIP_OK;
+}
+
+int loomhip_moe_ffn_routed(const float *normed, size_t n_tok, size_t dim, const float *logits,
+                           const float *sel_bias, size_t n_expert, size_t n_used, int gating,
+                           int weights_norm, float weights_scale, int gate_t, const void *gate_w,
+                           int up_t, const void *up_w, int down_t, const void *down_w, size_t ffn,
+                           int combine, float *out) {
+    if (int rc = require_ready())
+        return rc;
+    if (!normed || !logits || !gate_w || !up_w || !down_w || !out)
+        return fail(LOOMHIP_ERR_ARG, "moe_ffn_routed: null argument");
+    MoeRun m{dim, ffn, n_expert, n_used, gating, weights_norm, weights_scale, nullptr, nullptr,
+             nullptr, gate_t, up_t, down_t, nullptr, nullptr, nullptr};
+    // Decline before touching the device (src/vulkan/backend.zig:462-489).
+    if (int rc = moe_check(m, n_tok))
+        return rc;
+    void *dg, *du, *dd;
+    int rc;
+    if ((rc = upload_weights(gate_t, gate_w, ffn, dim, n_expert, &dg)) ||
+        (rc = upload_weights(up_t, up_w, ffn, dim, n_expert, &du)) ||
+        (rc = upload_weights(down_t, down_w, dim, ffn, n_expert, &dd)))
+        return rc;
+    m.gate = dg;
+    m.up = du;
+    m.down = dd;
+    const size_t nb = align16(n_tok * dim * 4), lb = align16(n_tok * n_expert * 4);
+    if ((rc = g_stage.reserve(2 * nb + 2 * lb)))
+        return rc;
+    char *base = (char *)g_stage.ptr;
+    float *dn = (float *)base, *dout = (float *)(base + nb), *dl = (float *)(base + 2 * nb);
+    float *dsb = (float *)(base + 2 * nb + lb);
+    hipStream_t st = g_ctx.compute;
+    hipError_t e = hipMemcpyAsync(dn, normed, n_tok * dim * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(dl, logits, n_tok * n_expert * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess && sel_bias)
+        e = hipMemcpyAsync(dsb, sel_bias, n_expert * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess && combine == LOOMHIP_COMBINE_EXPERT_ASC)
+        e = hipMemcpyAsync(dout, out, n_tok * dim * 4, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess)
+        return hip_fail(e, "moe_ffn_routed staging");
+    m.sel_bias = sel_bias ? dsb : nullptr;
+    if ((rc = moe_run(m, dn, dl, n_tok, combine, dout, nullptr, nullptr, st)))
+        return rc;
+    e = hipMemcpyAsync(out, dout, n_tok * dim * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(st);
+    if (e != hipSuccess)
+        return hip_fail(e, "moe_ffn_routed readback");
+    return LOOMHIP_OK;
+}
+
+} // extern "C"

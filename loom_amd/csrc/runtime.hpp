@@ -1,0 +1,51 @@
+// runtime.hpp -- host-side context of libloomhip.
+#pragma once
+
+#include "../../include/loomhip.h"
+#include "kernels.hpp"
+
+#include <unordered_map>
+
+namespace lh {
+
+constexpr int IOTA_LEN = 1 << 16; // identity pair table (max pairs / vectors per launch)
+
+// Grow-only device buffer.  Reallocation synchronises the compute stream.
+struct Scratch {
+    void *ptr = nullptr;
+    size_t cap = 0;
+    int reserve(size_t bytes);
+    void release() {
+        if (ptr)
+            (void)hipFree(ptr);
+        ptr = nullptr;
+        cap = 0;
+    }
+};
+
+struct Ctx {
+    bool ready = false;
+    int device = -1;
+    hipStream_t compute = nullptr; // kernels
+    hipStream_t copy = nullptr;    // expert-cache host->HBM copies
+    const int *iota = nullptr;
+    Scratch act;    // quantized activations for dense matvecs
+    Scratch xstage; // seam-call staging
+    Scratch ostage;
+    std::unordered_map<int, void *> dense_tables;
+};
+
+extern Ctx g_ctx;
+
+int fail(int code, const char *fmt, ...);
+int hip_fail(hipError_t e, const char *what);
+int require_ready();
+hipStream_t stream_of(void *s);
+int upload_weights(int t, const void *host, size_t rows, size_t cols, size_t planes, void **dev);
+void clear_weight_cache();
+int matvec_dev_impl(int t, float *out, const void *w, const float *x, size_t n, size_t rows,
+                    size_t cols, hipStream_t st);
+int pick_nt(int n);
+void moe_release_scratch();
+
+} // namespace lh

@@ -1,0 +1,137 @@
+"""GPU parity of routing and the whole MoE layer against the CPU oracle
+(llama.moeLayer/moeRun at one token, moeBatchUnion for batches).  Runs on the
+MI355X box only."""
+import numpy as np
+import pytest
+
+import npref
+
+pytestmark = pytest.mark.gpu
+
+Q4_K, Q6_K, F32 = 12, 14, 0
+
+
+@pytest.fixture(scope="module")
+def be(oracle):
+    import loom_amd
+    from loom_amd import backend
+
+    loom_amd.init(0)
+    backend.clearWeightCache()
+    yield backend
+    backend.clearWeightCache()
+
+
+def _maxrel(got, want):
+    return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+@pytest.mark.parametrize("gating,norm,scale,bias", [
+    ("softmax", True, 1.0, False), ("sigmoid", True, 1.0, True), ("sigmoid", True, 1.0, False),
+    ("softmax", False, 2.5, False), ("sigmoid", False, 1.0, True),
+])
+def test_route_matches_oracle(be, oracle, gating, norm, scale, bias):
+    # src/vulkan/backend.zig:1242-1295: identical ids, gates within 1e-5
+    for n_expert, n_used, seed in ((64, 6, 1), (128, 8, 2), (256, 8, 3), (8, 2, 4)):
+        rng = np.random.default_rng(seed)
+        logits = ((rng.random(n_expert) - 0.5) * 4).astype(np.float32)
+        logits[5] = logits[7]  # a deliberate tie: lowest index must win
+        b = ((rng.random(n_expert) - 0.5) * 0.5).astype(np.float32) if bias else None
+        ids = np.empty(n_used, np.uint32)
+        gates = np.empty(n_used, np.float32)
+        assert be.moeRoute(logits, b, ids, gates, gating == "sigmoid", norm, scale)
+        g = oracle.GATING_SIGMOID if gating == "sigmoid" else oracle.GATING_SOFTMAX
+        wid, wg = oracle.route(logits, n_used, g, norm, scale, b)
+        assert np.array_equal(ids, wid)
+        assert np.all(np.abs(gates - wg) <= 1e-6)
+
+
+def test_route_kats_on_device(be, oracle):
+    # src/gguf/moe.zig:210-223
+    ids = np.empty(2, np.uint32)
+    gates = np.empty(2, np.float32)
+    assert be.moeRoute(np.array([0, 1, 2, 3], np.float32), np.array([10, 0, 0, 0], np.float32),
+                       ids, gates, True, False, 1.0)
+    assert list(ids) == [0, 3]
+    assert abs(gates[0] - 0.5) < 1e-6 and abs(gates[1] - 1 / (1 + np.exp(-3.0))) < 1e-6
+    # src/gguf/moe.zig:260-267
+    assert be.moeRoute(np.array([1, 2, 3, 4], np.float32), None, ids, gates, False, True, 2.5)
+    assert abs(gates.sum() - 2.5) < 1e-5
+
+
+def make_layer(oracle, dim, ffn, n_expert, n_used, seed, gate_t=Q4_K, down_t=Q6_K,
+               router_bias=False):
+    rng = np.random.default_rng(seed)
+    gate = npref.pinned_scale_blocks(gate_t, ffn, dim, rng, planes=n_expert)
+    up = npref.pinned_scale_blocks(gate_t, ffn, dim, rng, planes=n_expert)
+    down = npref.pinned_scale_blocks(down_t, dim, ffn, rng, planes=n_expert)
+    router = oracle.normal(n_expert * dim, seed + 1, 0.0, 1.0 / np.sqrt(dim)).reshape(n_expert, dim)
+    rb = None
+    if router_bias:  # Zipf(1.1) popularity as a logit bias (config 3)
+        ranks = rng.permutation(n_expert) + 1
+        rb = (np.log(1.0 / ranks ** 1.1) - np.log(1.0 / ranks ** 1.1).mean()).astype(np.float32)
+    return oracle.MoeWeights(dim, ffn, n_expert, n_used, router, gate, up, down, gate_t, gate_t,
+                             down_t, router_bias=rb)
+
+
+@pytest.mark.parametrize("dim,ffn,E,k", [(512, 256, 16, 4), (2048, 768, 128, 8)])
+def test_moe_ffn_routed_single_token(be, oracle, dim, ffn, E, k):
+    from loom_amd.backend import RoutedCfg, WeightRef
+
+    w = make_layer(oracle, dim, ffn, E, k, seed=dim + E)
+    normed = oracle.normal(dim, 99, 0.0, 1.0)
+    logits = oracle.matvec(F32, w.router.view(np.uint8).ravel(), normed, E, dim)
+    out = np.empty(dim, np.float32)
+    be.takeCmdBufCount()
+    ok = be.moeFfnBlockRouted(normed, logits, None, WeightRef(w.gate_t, w.gate),
+                              WeightRef(w.up_t, w.up), WeightRef(w.down_t, w.down), None, ffn, 0,
+                              RoutedCfg(E, k, False, True, 1.0), out)
+    assert ok
+    assert be.takeCmdBufCount() >= 6
+    want, ids, gates = oracle.moe_layer_token(w, normed)
+    assert _maxrel(out, want) <= 2e-3, _maxrel(out, want)
+
+
+def _dev_layer(be, w):
+    import torch
+
+    def dev(t, raw, rows, cols):
+        return be.repack_dev(t, torch.from_numpy(raw).cuda(), rows, cols, w.n_expert)
+
+    router = torch.from_numpy(w.router).cuda()
+    rb = None if w.router_bias is None else torch.from_numpy(w.router_bias).cuda()
+    return be.MoeLayer(w.dim, w.ffn, w.n_expert, w.n_used, router,
+                       dev(w.gate_t, w.gate, w.ffn, w.dim), dev(w.up_t, w.up, w.ffn, w.dim),
+                       dev(w.down_t, w.down, w.dim, w.ffn), w.gate_t, w.up_t, w.down_t,
+                       router_bias=rb)
+
+
+@pytest.mark.parametrize("n", [1, 8, 32, 128])
+def test_moe_layer_dev_matches_oracle(be, oracle, n):
+    """Config-3 shape: hidden 2048, 128 experts top-8, ffn 768, Q4_K gate/up,
+    Q6_K down, f32 router with a Zipf(1.1) logit bias."""
+    import torch
+
+    w = make_layer(oracle, 2048, 768, 128, 8, seed=3, router_bias=True)
+    layer = _dev_layer(be, w)
+    xs = np.stack([oracle.normal(2048, 500 + i, 0.0, 1.0) for i in range(n)])
+    normed = torch.from_numpy(xs).cuda()
+    ids = torch.empty((n, 8), dtype=torch.int32, device="cuda")
+    gates = torch.empty((n, 8), dtype=torch.float32, device="cuda")
+    if n == 1:
+        out = torch.empty((1, 2048), dtype=torch.float32, device="cuda")
+        layer(normed, out, combine=be.COMBINE_SELECTION, ids=ids, gates=gates)
+        want, wid, wg = oracle.moe_layer_token(w, xs[0])
+        want = want[None]
+        wid, wg = wid[None], wg[None]
+    else:
+        resid = np.stack([oracle.normal(2048, 900 + i, 0.0, 1.0) for i in range(n)])
+        out = torch.from_numpy(resid.copy()).cuda()
+        layer(normed, out, combine=be.COMBINE_EXPERT_ASC, ids=ids, gates=gates)
+        want, wid, wg = oracle.moe_batch_union(w, xs, resid)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy().astype(np.uint32), wid)
+    assert np.all(np.abs(gates.cpu().numpy() - wg) <= 1e-6)
+    got = out.cpu().numpy()
+    for i in range(n):
+        assert _maxrel(got[i], want[i]) <= 2e-3, (i, _maxrel(got[i], want[i]))
