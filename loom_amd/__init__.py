@@ -68,6 +68,14 @@ def lib() -> C.CDLL:
         raise LoomHipError(
             f"{LIB_PATH} is missing: build it with `python -m loom_amd.build` "
             "(there is no CPU fallback)")
+    # torch ships its own libamdhip64.so.7.  Loading torch first makes
+    # libloomhip bind to that same runtime (the SONAMEs match), so torch's
+    # device buffers and streams and ours live in one HIP runtime; loading
+    # ours first would map a second runtime from /opt/rocm.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = C.CDLL(LIB_PATH)
     vp, sz, i, f = C.c_void_p, C.c_size_t, C.c_int, C.c_float
     u64 = C.c_uint64

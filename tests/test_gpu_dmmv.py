@@ -26,6 +26,16 @@ def be(oracle):
     backend.clearWeightCache()
 
 
+@pytest.fixture(autouse=True)
+def fresh_weight_cache(be):
+    # The device weight cache is keyed by host address; numpy recycles
+    # addresses between tests, so stale weights would be served (the
+    # reference's tests clear their cache for the same reason,
+    # src/vulkan/backend.zig:159-172).
+    be.clearWeightCache()
+    yield
+
+
 def _bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 

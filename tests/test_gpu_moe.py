@@ -22,6 +22,16 @@ def be(oracle):
     backend.clearWeightCache()
 
 
+@pytest.fixture(autouse=True)
+def fresh_weight_cache(be):
+    # The device weight cache is keyed by host address; numpy recycles
+    # addresses between tests, so stale weights would be served (the
+    # reference's tests clear their cache for the same reason,
+    # src/vulkan/backend.zig:159-172).
+    be.clearWeightCache()
+    yield
+
+
 def _maxrel(got, want):
     return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
 
