@@ -73,6 +73,17 @@ const char *loomhip_last_error(void);
  * src/compute/backend.zig:112-116).  Tests assert it moved to prove the
  * device path ran. */
 uint64_t loomhip_take_launch_count(void);
+/* Kernel timing with HIP events recorded on the launching stream around
+ * every launch of the tagged kernels (the reference's LOOM_VK_KERNEL_PROF
+ * timestamps, src/vulkan/device.zig:158-167,245-252).  Enabling resets the
+ * totals; launches inside a stream capture are not timed. */
+#define LOOMHIP_KT_GATE_UP 0 /* grouped gate/up + SwiGLU expert kernel */
+#define LOOMHIP_KT_DOWN 1    /* grouped down expert kernel */
+#define LOOMHIP_KT_DENSE 2   /* dense dequant-fused matvec */
+#define LOOMHIP_KT_COUNT 3
+void loomhip_profile_kernels(int enable);
+/* Waits for the recorded events; total milliseconds and launch count of tag. */
+int loomhip_kernel_time(int tag, double *total_ms, uint64_t *launches);
 /* Library version string. */
 const char *loomhip_version(void);
 
@@ -103,9 +114,10 @@ size_t loomhip_resident_bytes(void);
  * at dst (device memory, loomhip_plane_bytes * planes). */
 int loomhip_repack_dev(int t, void *dst, const void *src, size_t rows, size_t cols, size_t planes,
                        void *stream);
-/* Fill `planes` device-layout planes with seeded synthetic blocks whose
- * dequantized values have roughly the given standard deviation (bench input
- * generator; deterministic in seed). */
+/* Fill `planes` planes in GGML layout (loomhip_ggml_bytes each) with seeded
+ * synthetic blocks whose dequantized values have roughly the given standard
+ * deviation: the bench's input generator, deterministic in seed.  Feed the
+ * bytes to loomhip_repack_dev for the device layout. */
 int loomhip_synth_weights_dev(int t, void *dst, size_t rows, size_t cols, size_t planes,
                               uint64_t seed, float stddev, void *stream);
 

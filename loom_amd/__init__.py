@@ -21,6 +21,8 @@ OK, DECLINED, ERR_ARG, ERR_HIP, ERR_INIT = 0, 1, -1, -2, -3
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
 GATING_SOFTMAX, GATING_SIGMOID, GATING_SOFTMAX_TOPK = 1, 2, 3
 COMBINE_SELECTION, COMBINE_EXPERT_ASC = 0, 1
+KT_GATE_UP, KT_DOWN, KT_DENSE = 0, 1, 2
+KT_NAMES = {KT_GATE_UP: "gate_up", KT_DOWN: "down", KT_DENSE: "dense"}
 
 
 class LoomHipError(RuntimeError):
@@ -85,6 +87,8 @@ def lib() -> C.CDLL:
         "loomhip_last_error": (C.c_char_p, []),
         "loomhip_take_launch_count": (u64, []),
         "loomhip_version": (C.c_char_p, []),
+        "loomhip_profile_kernels": (None, [i]),
+        "loomhip_kernel_time": (i, [i, C.POINTER(C.c_double), C.POINTER(u64)]),
         "loomhip_plane_bytes": (sz, [i, sz, sz]),
         "loomhip_ggml_bytes": (sz, [i, sz, sz]),
         "loomhip_register_weights": (i, [i, vp, sz, sz, sz, C.POINTER(vp)]),

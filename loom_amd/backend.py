@@ -126,6 +126,32 @@ def moeFfnBlockRouted(normed: np.ndarray, logits: np.ndarray, bias, gate_w: Weig
     return _served(rc, "moeFfnBlockRouted")
 
 
+def profileKernels(enable: bool) -> None:
+    """Record HIP events around every grouped-expert / dense matvec launch
+    (resets the totals)."""
+    lib().loomhip_profile_kernels(int(enable))
+
+
+_KERNEL_SYMBOLS = {
+    "gate_up": "dmmv_kernel<Q4_K|Q6_K|..., NT, FUSED=true> (grouped gate/up + SwiGLU)",
+    "down": "dmmv_kernel<..., NT, FUSED=false> (grouped down)",
+    "dense": "dmmv_kernel<..., NT, false> (dense matvec)",
+}
+
+
+def kernelStats() -> dict:
+    """{name: {"ms": total, "count": launches, "name": kernel}} for tags with launches."""
+    from . import KT_NAMES
+
+    out = {}
+    for tag, name in KT_NAMES.items():
+        ms, n = C.c_double(), C.c_uint64()
+        check(lib().loomhip_kernel_time(tag, C.byref(ms), C.byref(n)), "kernel_time")
+        if n.value:
+            out[name] = {"ms": ms.value, "count": n.value, "name": _KERNEL_SYMBOLS[name]}
+    return out
+
+
 def registerWeights(t: int, host: np.ndarray, rows: int, cols: int, planes: int = 1) -> int:
     """Pointer-keyed upload; returns the device address."""
     dev = C.c_void_p()
@@ -155,12 +181,16 @@ def plane_bytes(t: int, rows: int, cols: int) -> int:
     return int(lib().loomhip_plane_bytes(t, rows, cols))
 
 
-def synth_weights_dev(t: int, rows: int, cols: int, planes: int, seed: int, stddev: float,
-                      device="cuda"):
-    """Allocate and fill `planes` device-layout planes (bench input generator)."""
+def synth_ggml_dev(t: int, rows: int, cols: int, planes: int, seed: int, stddev: float,
+                   device="cuda"):
+    """Allocate and fill `planes` GGML-layout planes with seeded synthetic
+    blocks (bench input generator); ``repack_dev`` turns them into the device
+    layout."""
     import torch
 
-    buf = torch.empty(plane_bytes(t, rows, cols) * planes, dtype=torch.uint8, device=device)
+    from . import ggml_bytes
+
+    buf = torch.empty(ggml_bytes(t, rows, cols) * planes, dtype=torch.uint8, device=device)
     check(lib().loomhip_synth_weights_dev(t, _ptr(buf), rows, cols, planes, seed, stddev,
                                           _stream()), "synth_weights_dev")
     return buf

@@ -215,18 +215,25 @@ __device__ inline uint16_t f2h_bits(float f) {
     return __half_raw(h).x;
 }
 
+// Blocks are written in GGML layout (the bytes a GGUF file holds); callers
+// repack them into the device layout.
 __global__ void synth_kernel(int t, uint8_t *__restrict__ dst, size_t U, size_t plane_b,
                              size_t planes, uint64_t seed, float stddev) {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= U * planes)
         return;
     const size_t p = idx / U, u = idx % U;
-    uint8_t *d = dst + p * plane_b;
+    uint8_t *blk = dst + p * plane_b + u * block_bytes(t);
     const uint64_t key = (seed * 0x9E3779B97F4A7C15ull) ^ (idx * 0xD1B54A32D192ED03ull);
     auto word = [&](int i) { return mix32(key + (uint64_t)i * 0x632BE59BD9B4E019ull); };
+    auto put4 = [&](int off, uint32_t r) {
+        blk[off] = r & 0xff;
+        blk[off + 1] = (r >> 8) & 0xff;
+        blk[off + 2] = (r >> 16) & 0xff;
+        blk[off + 3] = r >> 24;
+    };
     if (t == LH_Q4_K) {
         // value = d*sc*q - dmin*m with q uniform 0..15: std ~ d*sc*4.6
-        uint8_t *blk = d + u * 144;
         const float dd = stddev / (4.6f * 52.0f);
         const uint16_t hd = f2h_bits(dd), hm = f2h_bits(dd * 7.5f);
         blk[0] = hd & 0xff; blk[1] = hd >> 8; blk[2] = hm & 0xff; blk[3] = hm >> 8;
@@ -235,50 +242,42 @@ __global__ void synth_kernel(int t, uint8_t *__restrict__ dst, size_t U, size_t 
             const uint32_t r = j < 4 ? r0 : j < 8 ? r1 : r2;
             blk[4 + j] = (uint8_t)(0x28 | ((r >> (8 * (j & 3))) & 0xD7)); // scales 40..63, mins alike
         }
-        for (int i = 0; i < 32; i++) {
-            const uint32_t r = word(3 + i);
-            blk[16 + 4 * i] = r & 0xff; blk[17 + 4 * i] = (r >> 8) & 0xff;
-            blk[18 + 4 * i] = (r >> 16) & 0xff; blk[19 + 4 * i] = r >> 24;
-        }
+        for (int i = 0; i < 32; i++)
+            put4(16 + 4 * i, word(3 + i));
     } else if (t == LH_Q6_K) {
-        for (int i = 0; i < 32; i++) {
-            const uint32_t r = word(i);
-            for (int k = 0; k < 4; k++) d[u * 128 + 4 * i + k] = (r >> (8 * k)) & 0xff;
-        }
-        for (int i = 0; i < 16; i++) {
-            const uint32_t r = word(32 + i);
-            for (int k = 0; k < 4; k++) d[U * 128 + u * 64 + 4 * i + k] = (r >> (8 * k)) & 0xff;
-        }
+        for (int i = 0; i < 48; i++) // ql[128] then qh[64]
+            put4(4 * i, word(i));
         for (int i = 0; i < 4; i++) {
             const uint32_t r = word(48 + i);
             for (int k = 0; k < 4; k++) { // signed scales with |sc| in 64..127
                 const uint8_t b = (r >> (8 * k)) & 0xff;
                 const int v = 64 + (b & 63);
-                d[U * 192 + u * 16 + 4 * i + k] = (uint8_t)(int8_t)((b & 0x80) ? -v : v);
+                blk[192 + 4 * i + k] = (uint8_t)(int8_t)((b & 0x80) ? -v : v);
             }
         }
         const uint16_t hd = f2h_bits(stddev / (18.5f * 96.0f));
-        d[U * 208 + 2 * u] = hd & 0xff;
-        d[U * 208 + 2 * u + 1] = hd >> 8;
+        blk[208] = hd & 0xff;
+        blk[209] = hd >> 8;
     } else if (t == LH_Q8_0) {
+        const uint16_t hd = f2h_bits(stddev / 73.0f);
+        blk[0] = hd & 0xff;
+        blk[1] = hd >> 8;
         for (int i = 0; i < 8; i++) {
             const uint32_t r = word(i);
             for (int k = 0; k < 4; k++) {
-                int8_t v = (int8_t)((r >> (8 * k)) & 0xff);
-                d[u * 32 + 4 * i + k] = (uint8_t)(v == -128 ? -127 : v);
+                const int8_t v = (int8_t)((r >> (8 * k)) & 0xff);
+                blk[2 + 4 * i + k] = (uint8_t)(v == -128 ? -127 : v);
             }
         }
-        const uint16_t hd = f2h_bits(stddev / 73.0f);
-        d[U * 32 + 2 * u] = hd & 0xff;
-        d[U * 32 + 2 * u + 1] = hd >> 8;
     } else if (t == LH_Q4_0) {
+        const uint16_t hd = f2h_bits(stddev / 4.6f);
+        blk[0] = hd & 0xff;
+        blk[1] = hd >> 8;
         for (int i = 0; i < 4; i++) {
             const uint32_t r = word(i);
-            for (int k = 0; k < 4; k++) d[u * 16 + 4 * i + k] = (r >> (8 * k)) & 0xff;
+            for (int k = 0; k < 4; k++)
+                blk[2 + 4 * i + k] = (r >> (8 * k)) & 0xff;
         }
-        const uint16_t hd = f2h_bits(stddev / 4.6f);
-        d[U * 16 + 2 * u] = hd & 0xff;
-        d[U * 16 + 2 * u + 1] = hd >> 8;
     }
 }
 
@@ -287,7 +286,7 @@ void launch_synth(int t, void *dst, size_t rows, size_t cols, size_t planes, uin
     const size_t U = rows * (cols / block_elems(t));
     const size_t n = U * planes;
     hipLaunchKernelGGL(synth_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, t,
-                       (uint8_t *)dst, U, plane_bytes(t, rows, cols), planes, seed, stddev);
+                       (uint8_t *)dst, U, ggml_bytes(t, rows, cols), planes, seed, stddev);
     note_launch();
 }
 

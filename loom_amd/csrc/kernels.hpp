@@ -40,6 +40,9 @@ struct DmmvParams {
 };
 
 void note_launch();
+// Event timing around tagged launches (LOOMHIP_KT_*); -1 when disabled.
+int prof_begin(int tag, hipStream_t st);
+void prof_end(int handle, hipStream_t st);
 
 void launch_quant_act(int wtype, const float *x, int cols, int x_stride, int nvec, QAct qa,
                       hipStream_t st);

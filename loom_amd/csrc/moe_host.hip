@@ -123,7 +123,10 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     gu.out = act;
     gu.out_stride = (int)m.ffn;
     gu.rpw = dmmv_pick_rpw(m.gate_t, (int)m.dim, (int)m.ffn, exp_groups, nt, true);
-    if (!launch_dmmv(m.gate_t, nt, true, gu, st))
+    int ph = prof_begin(LOOMHIP_KT_GATE_UP, st);
+    bool launched = launch_dmmv(m.gate_t, nt, true, gu, st);
+    prof_end(ph, st);
+    if (!launched)
         return fail(LOOMHIP_ERR_ARG, "moe: gate/up partials exceed LDS");
 
     launch_quant_act(m.down_t, act, (int)m.ffn, (int)m.ffn, (int)P, qa, st);
@@ -145,7 +148,10 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     dn.out = y;
     dn.out_stride = (int)m.dim;
     dn.rpw = dmmv_pick_rpw(m.down_t, (int)m.ffn, (int)m.dim, exp_groups, nt, false);
-    if (!launch_dmmv(m.down_t, nt, false, dn, st))
+    ph = prof_begin(LOOMHIP_KT_DOWN, st);
+    launched = launch_dmmv(m.down_t, nt, false, dn, st);
+    prof_end(ph, st);
+    if (!launched)
         return fail(LOOMHIP_ERR_ARG, "moe: down partials exceed LDS");
 
     launch_combine(y, gates, ids, b.pair_of, (int)n, (int)m.k, (int)m.dim, combine, out, st);

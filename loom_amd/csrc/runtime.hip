@@ -10,6 +10,7 @@
 #include <cstring>
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 namespace lh {
 
@@ -18,6 +19,61 @@ static thread_local char g_err[512] = "";
 Ctx g_ctx;
 
 void note_launch() { g_launches.fetch_add(1, std::memory_order_relaxed); }
+
+// ---- kernel timing -------------------------------------------------------------
+struct ProfRec {
+    hipEvent_t a, b;
+    int tag;
+};
+static bool g_prof = false;
+static std::vector<ProfRec> g_prof_recs;
+static std::vector<hipEvent_t> g_prof_pool;
+static double g_prof_ms[LOOMHIP_KT_COUNT];
+static uint64_t g_prof_n[LOOMHIP_KT_COUNT];
+
+static hipEvent_t prof_event() {
+    if (!g_prof_pool.empty()) {
+        hipEvent_t e = g_prof_pool.back();
+        g_prof_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess)
+        return nullptr;
+    return e;
+}
+
+int prof_begin(int tag, hipStream_t st) {
+    if (!g_prof || tag < 0 || tag >= LOOMHIP_KT_COUNT)
+        return -1;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+        return -1;
+    ProfRec r{prof_event(), prof_event(), tag};
+    if (!r.a || !r.b || hipEventRecord(r.a, st) != hipSuccess)
+        return -1;
+    g_prof_recs.push_back(r);
+    return (int)g_prof_recs.size() - 1;
+}
+
+void prof_end(int handle, hipStream_t st) {
+    if (handle < 0 || handle >= (int)g_prof_recs.size())
+        return;
+    (void)hipEventRecord(g_prof_recs[handle].b, st);
+}
+
+static void prof_drain() {
+    for (auto &r : g_prof_recs) {
+        float ms = 0.0f;
+        if (hipEventSynchronize(r.b) == hipSuccess && hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
+            g_prof_ms[r.tag] += ms;
+            g_prof_n[r.tag] += 1;
+        }
+        g_prof_pool.push_back(r.a);
+        g_prof_pool.push_back(r.b);
+    }
+    g_prof_recs.clear();
+}
 
 int fail(int code, const char *fmt, ...) {
     va_list ap;
@@ -191,7 +247,10 @@ int matvec_dev_impl(int t, float *out, const void *w, const float *x, size_t n, 
     p.out = out;
     p.out_stride = (int)rows;
     p.rpw = dmmv_pick_rpw(t, (int)cols, (int)rows, ng, nt, false);
-    if (!launch_dmmv(t, nt, false, p, st))
+    const int ph = prof_begin(LOOMHIP_KT_DENSE, st);
+    const bool launched = launch_dmmv(t, nt, false, p, st);
+    prof_end(ph, st);
+    if (!launched)
         return fail(LOOMHIP_DECLINED, "dmmv: partials exceed LDS for %zu columns", cols);
     return LOOMHIP_OK;
 }
@@ -257,6 +316,11 @@ void loomhip_shutdown(void) {
     g_ctx.xstage.release();
     g_ctx.ostage.release();
     moe_release_scratch();
+    prof_drain();
+    for (hipEvent_t e : g_prof_pool)
+        (void)hipEventDestroy(e);
+    g_prof_pool.clear();
+    g_prof = false;
     (void)hipFree((void *)g_ctx.iota);
     (void)hipStreamDestroy(g_ctx.compute);
     (void)hipStreamDestroy(g_ctx.copy);
@@ -264,6 +328,24 @@ void loomhip_shutdown(void) {
 }
 
 const char *loomhip_last_error(void) { return g_err; }
+
+void loomhip_profile_kernels(int enable) {
+    prof_drain();
+    for (int i = 0; i < LOOMHIP_KT_COUNT; i++) {
+        g_prof_ms[i] = 0.0;
+        g_prof_n[i] = 0;
+    }
+    g_prof = enable != 0;
+}
+
+int loomhip_kernel_time(int tag, double *total_ms, uint64_t *launches) {
+    if (tag < 0 || tag >= LOOMHIP_KT_COUNT || !total_ms || !launches)
+        return fail(LOOMHIP_ERR_ARG, "kernel_time: bad tag %d", tag);
+    prof_drain();
+    *total_ms = g_prof_ms[tag];
+    *launches = g_prof_n[tag];
+    return LOOMHIP_OK;
+}
 
 uint64_t loomhip_take_launch_count(void) { return g_launches.exchange(0); }
 
