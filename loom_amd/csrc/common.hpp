@@ -109,9 +109,30 @@ __device__ inline int group_sum(int v) {
     return v;
 }
 
+// DPP move of a float (disabled rows keep `old`).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ inline float dpp_f(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL,
+                                                      ROW_MASK, 0xF, false));
+}
+
+// Wave-wide max, returned uniformly: quad xor 1 and 2, half-row and row
+// mirrors, then row_bcast 15 / 31 carry the row maxima up to lane 63.
 __device__ inline float wave_max(float v) {
-    for (int o = 32; o >= 1; o >>= 1)
-        v = fmaxf(v, __shfl_xor(v, o, 64));
+    v = fmaxf(v, dpp_f<0xB1>(v, v));
+    v = fmaxf(v, dpp_f<0x4E>(v, v));
+    v = fmaxf(v, dpp_f<0x141>(v, v));
+    v = fmaxf(v, dpp_f<0x140>(v, v));
+    v = fmaxf(v, dpp_f<0x142, 0xA>(v, v));
+    v = fmaxf(v, dpp_f<0x143, 0xC>(v, v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Max over aligned groups of 8 lanes, in every lane of the group.
+__device__ inline float group8_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v, v));
+    v = fmaxf(v, dpp_f<0x4E>(v, v));
+    v = fmaxf(v, dpp_f<0x141>(v, v));
     return v;
 }
 

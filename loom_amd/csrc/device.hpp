@@ -1,0 +1,354 @@
+// device.hpp -- device-side helpers shared by the kernel files: the int8
+// activation quantizers (one wave per item) and the completion counters that
+// let the last workgroup of a set run an epilogue.
+#pragma once
+
+#include "kernels.hpp"
+
+namespace lh {
+
+constexpr int MAX_E = 256, MAX_K = 16, MAX_TOK = 256; // routing limits
+
+// ---- wave-level int8 activation quantizers ------------------------------------
+
+// Four consecutive floats; COHERENT reads them through relaxed agent-scope
+// atomic loads (values written by other work groups of the same launch).
+template <bool COHERENT = false>
+__device__ inline float4 load4(const float *x) {
+    if constexpr (COHERENT) {
+        float4 v;
+        v.x = __hip_atomic_load(const_cast<float *>(x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v.y = __hip_atomic_load(const_cast<float *>(x + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v.z = __hip_atomic_load(const_cast<float *>(x + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v.w = __hip_atomic_load(const_cast<float *>(x + 3), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return v;
+    } else {
+        return *(const float4 *)x;
+    }
+}
+
+// quantizeX256 (src/gguf/ggml.zig:776-800) of one 256-value block by one
+// wave whose values 4l..4l+3 are already in lane l: amax is an exact max
+// (order-free), the per-16 sums are integer.
+__device__ inline void quant256_regs(const float4 xv, int8_t *__restrict__ q,
+                                     float *__restrict__ d, int32_t *__restrict__ s) {
+    const int lane = threadIdx.x & 63;
+    float a = 0.0f;
+    if (__builtin_isfinite(xv.x)) a = fmaxf(a, fabsf(xv.x));
+    if (__builtin_isfinite(xv.y)) a = fmaxf(a, fabsf(xv.y));
+    if (__builtin_isfinite(xv.z)) a = fmaxf(a, fabsf(xv.z));
+    if (__builtin_isfinite(xv.w)) a = fmaxf(a, fabsf(xv.w));
+    const float amax = wave_max(a);
+    const float dd = amax / 127.0f;
+    const float inv = (dd != 0.0f && __builtin_isfinite(dd)) ? 1.0f / dd : 0.0f;
+    const int q0 = to_i8_sat(xv.x * inv), q1 = to_i8_sat(xv.y * inv);
+    const int q2 = to_i8_sat(xv.z * inv), q3 = to_i8_sat(xv.w * inv);
+    const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                            ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+    *(uint32_t *)(q + 4 * lane) = packed;
+    const int sum16 = group_sum<4>(q0 + q1 + q2 + q3);
+    if ((lane & 3) == 0)
+        s[lane / 4] = sum16;
+    if (lane == 0)
+        *d = __builtin_isfinite(dd) ? dd : 0.0f;
+}
+
+template <bool COHERENT = false>
+__device__ inline void quant_block256_wave(const float *__restrict__ x, int8_t *__restrict__ q,
+                                           float *__restrict__ d, int32_t *__restrict__ s) {
+    quant256_regs(load4<COHERENT>(x + 4 * (threadIdx.x & 63)), q, d, s);
+}
+
+// Lane l's four values of the quantizeX item starting at block b0.
+__device__ inline const float *blocks32_src(const float *x, int nb, int b0) {
+    const int lane = threadIdx.x & 63;
+    const int blk = b0 + lane / 8;
+    const int bc = blk < nb ? blk : nb - 1; // idle lanes read a valid block
+    return x + bc * 32 + 4 * (lane & 7);
+}
+
+// quantizeX (src/gguf/ggml.zig:1077-1098) of up to eight 32-value blocks
+// [b0, b0+8) of one vector by one wave, eight lanes per block, values
+// already in the lanes (lane l holds values 4(l%8).. of block b0 + l/8).
+__device__ inline void quant32x8_regs(const float4 xv, int nb, int b0, int8_t *__restrict__ q,
+                                      float *__restrict__ d, int32_t *__restrict__ s) {
+    const int lane = threadIdx.x & 63;
+    const int blk = b0 + lane / 8;
+    const bool live = blk < nb;
+    float a = 0.0f;
+    if (__builtin_isfinite(xv.x)) a = fmaxf(a, fabsf(xv.x));
+    if (__builtin_isfinite(xv.y)) a = fmaxf(a, fabsf(xv.y));
+    if (__builtin_isfinite(xv.z)) a = fmaxf(a, fabsf(xv.z));
+    if (__builtin_isfinite(xv.w)) a = fmaxf(a, fabsf(xv.w));
+    a = group8_max(a);
+    const float dd = a / 127.0f;
+    const float inv = (dd != 0.0f && __builtin_isfinite(dd)) ? 1.0f / dd : 0.0f;
+    const int q0 = to_i8_sat(xv.x * inv), q1 = to_i8_sat(xv.y * inv);
+    const int q2 = to_i8_sat(xv.z * inv), q3 = to_i8_sat(xv.w * inv);
+    const int sum = group_sum<8>(q0 + q1 + q2 + q3);
+    if (live) {
+        const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                                ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+        *(uint32_t *)(q + blk * 32 + 4 * (lane & 7)) = packed;
+        if ((lane & 7) == 0) {
+            s[blk] = sum;
+            d[blk] = __builtin_isfinite(dd) ? dd : 0.0f;
+        }
+    }
+}
+
+template <bool COHERENT = false>
+__device__ inline void quant_blocks32_wave(const float *__restrict__ x, int nb, int b0,
+                                           int8_t *__restrict__ q, float *__restrict__ d,
+                                           int32_t *__restrict__ s) {
+    quant32x8_regs(load4<COHERENT>(blocks32_src(x, nb, b0)), nb, b0, q, d, s);
+}
+
+// Work items of quantizing one vector of `cols` values for weight type wt:
+// one 256-block (K-quants) or eight 32-blocks per item.
+__host__ __device__ inline int quant_items(int wt, int cols) {
+    return act_block(wt) == 256 ? cols / 256 : (cols / 32 + 7) / 8;
+}
+
+// Quantize item `it` of vector v (x at x + v*x_stride) into qa.  COHERENT
+// reads x through ld_dev (x was written by other workgroups of this launch).
+template <bool COHERENT = false>
+__device__ inline void quant_item_wave(int wt, const float *x, int cols, int v, int it, QAct qa) {
+    if (act_block(wt) == 256) {
+        const int nb = cols / 256;
+        quant_block256_wave<COHERENT>(x + it * 256, qa.q + (size_t)v * cols + it * 256,
+                            qa.d + (size_t)v * nb + it, qa.s + (size_t)v * (cols / 16) + it * 16);
+    } else {
+        const int nb = cols / 32;
+        quant_blocks32_wave<COHERENT>(x, nb, it * 8, qa.q + (size_t)v * cols, qa.d + (size_t)v * nb,
+                            qa.s + (size_t)v * nb);
+    }
+}
+
+// LDS-only barrier: waits for this wave's LDS traffic, not for its global
+// loads, so weight loads issued before it stay in flight.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0); vmcnt and expcnt left open
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// ---- completion counters ----------------------------------------------------------
+// Offsets (ints) inside the library's zero-initialised sync buffer.  Every
+// counter is reset to zero by the arrival that completes it, so the buffer
+// is all zeros between launches.
+constexpr int SYNC_GATE_CHUNK = 0;   // [MAX_TOK / GT_TOK]
+constexpr int SYNC_GATE_FINAL = 128; // [1]
+//
+// Data handed from one workgroup to another inside a launch travels through
+// relaxed agent-scope atomic stores and loads (st_dev / ld_dev), which are
+// coherent per location across the chip's XCDs (each XCD has its own L2).
+// An agent-scope fence would instead write back the whole L2 of the XCD,
+// which costs far more than the data (about 0.7 us per workgroup, serialised
+// per XCD).  Ordering: each arriving workgroup waits until all its stores
+// are acknowledged (s_waitcnt 0) before the counter increment, and the last
+// arrival issues its loads only after reading the counter.
+
+__device__ inline void st_dev(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_dev(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float ld_dev(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint32_t ld_dev(const uint32_t *p) {
+    return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline bool last_arrival(int *counter, int target) {
+    __shared__ int s_last;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0); // this thread's stores are acknowledged
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == target - 1;
+        if (s_last) // every arrival is in: reset for the next launch
+            __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return s_last;
+}
+
+// ---- routing ------------------------------------------------------------------------
+
+// LDS scratch of the routing helpers: per-wave copies of the scores and
+// selection keys (so no wave waits for another), and the slot table.
+template <int NW>
+struct __align__(16) RouteLds {
+    float sc[NW][MAX_E];
+    unsigned long long key[NW][MAX_E];
+    int id[MAX_K];
+    float gate[MAX_K];
+};
+
+// Sequential f32 sum of lane s's value over s < K, uniform in every lane.
+__device__ inline float slot_sum(float v, int K) {
+    float sum = 0.0f;
+    for (int s = 0; s < K; s++)
+        sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), s));
+    return sum;
+}
+
+// Order-preserving map of an f32 onto u32 (larger value -> larger key).
+__device__ inline uint32_t ordered_u32(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Sequential sum of v[0..E) in LDS (the reference's softmax sum order); the
+// reads of each 32-value batch are issued before its adds.
+__device__ inline float lds_seq_sum(const float *v, int E) {
+    float sum = 0.0f;
+    for (int e0 = 0; e0 < E; e0 += 32) {
+        float4 r[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            r[q] = *(const float4 *)(v + e0 + 4 * q);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int e = e0 + 4 * q;
+            if (e + 0 < E) sum = sum + r[q].x;
+            if (e + 1 < E) sum = sum + r[q].y;
+            if (e + 2 < E) sum = sum + r[q].z;
+            if (e + 3 < E) sum = sum + r[q].w;
+        }
+    }
+    return sum;
+}
+
+// Routing of one token (src/gguf/moe.zig:106-158) by NW cooperating waves
+// (threads [0, 64*NW) of the work group): scores (softmax / sigmoid / raw for
+// softmax_topk), then the k rounds of argmax with strict '>' over the unused
+// experts (lowest index wins ties; a round that finds nothing above -inf
+// picks expert 0), with gates from the unbiased scores.
+//
+// The k rounds pick experts in the order (selection value descending, index
+// ascending) among values above -inf, so an expert's slot is its rank in
+// that order.  With key = (ordered value << 32) | ~index every key is
+// distinct and rank = #{keys greater}; each lane ranks its experts against
+// all keys in LDS.  Every wave computes the scores and keys on its own (no
+// cross-wave wait); the experts to rank are split over the waves.  On return
+// (after a barrier) L.id[s] / L.gate[s] hold slot s's expert and unbiased
+// score for s < K; route_gates then applies the gate post-processing.
+// COHERENT reads the logits through ld_dev (written by other work groups of
+// the same launch).
+template <int NW, bool COHERENT>
+__device__ inline void route_select(const float *lg, const float *sel_bias, int E, int K,
+                                    int gating, RouteLds<NW> &L) {
+    constexpr int NI = MAX_E / 64;
+    // w indexes this wave's copies inside L: with NW == 1 the caller hands
+    // each wave its own RouteLds<1>, so the index is 0
+    const int lane = threadIdx.x & 63, w = NW == 1 ? 0 : threadIdx.x >> 6;
+    float sv[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int e = lane + 64 * i;
+        sv[i] = e < E ? (COHERENT ? ld_dev(lg + e) : lg[e]) : -INFINITY;
+    }
+    if (gating == 2) { // sigmoid (tensor.zig:34-36)
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            sv[i] = 1.0f / (1.0f + expf(-sv[i]));
+    } else if (gating != 3) { // softmax (tensor.zig:18-28): max, exp, sequential sum, * (1/sum)
+        float m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            m = fmaxf(m, sv[i]);
+        m = wave_max(m);
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            sv[i] = expf(sv[i] - m);
+            L.sc[w][lane + 64 * i] = sv[i];
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        const float inv = 1.0f / lds_seq_sum(L.sc[w], E); // same value in every lane
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            sv[i] = sv[i] * inv;
+    }
+    unsigned long long key[NI];
+    int valid_n = 0;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int e = lane + 64 * i;
+        const float c = e < E ? (sel_bias ? sv[i] + sel_bias[e] : sv[i]) : -INFINITY;
+        const bool valid = c > -INFINITY; // NaN and -inf never win a strict '>'
+        key[i] = valid ? ((unsigned long long)ordered_u32(c) << 32) | (0xFFFFFFFFu - (uint32_t)e)
+                       : 0ull;
+        valid_n += __popcll(__ballot(valid));
+        L.key[w][e] = key[i];
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    // wave w ranks experts lane + 64*i for i = w, w + NW, ...
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        if (i % NW != w || 64 * i >= E)
+            continue;
+        int rank = 0;
+        const unsigned long long ki = key[i];
+        for (int j0 = 0; j0 < E; j0 += 16) {
+            ulonglong2 kk[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                kk[q] = *(const ulonglong2 *)(&L.key[w][j0 + 2 * q]);
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                rank += (kk[q].x > ki) + (kk[q].y > ki);
+        }
+        const int e = lane + 64 * i;
+        if (ki != 0ull && rank < K) {
+            L.id[rank] = e;
+            L.gate[rank] = sv[i];
+        }
+    }
+    // rounds that found nothing above -inf pick expert 0 (its unbiased score)
+    const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[0]), 0));
+    if (w == 0 && lane >= valid_n && lane < K) {
+        L.id[lane] = 0;
+        L.gate[lane] = s0;
+    }
+    if constexpr (NW == 1) {
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    } else {
+        __syncthreads();
+    }
+}
+
+// Gate post-processing in slot order (moe.zig:143-157): softmax over the k
+// for softmax_topk, renorm with the f16-min clamp, scale.  Called by one
+// wave after route_select; lane s < K returns slot s's final gate.
+template <int NW>
+__device__ inline float route_gates(const RouteLds<NW> &L, int K, int gating, int weights_norm,
+                                    float weights_scale) {
+    const int lane = threadIdx.x & 63;
+    float g = lane < K ? L.gate[lane] : 0.0f;
+    if (gating == 3) {
+        float m = -INFINITY;
+        for (int s = 0; s < K; s++)
+            m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), s)));
+        g = expf(g - m);
+        const float inv = 1.0f / slot_sum(g, K);
+        g = g * inv;
+    }
+    if (weights_norm) {
+        const float denom = fmaxf(slot_sum(g, K), 6.103515625e-5f);
+        g = g / denom;
+    }
+    if (weights_scale != 1.0f)
+        g = g * weights_scale;
+    return g;
+}
+
+} // namespace lh

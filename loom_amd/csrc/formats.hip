@@ -1,87 +1,20 @@
 // formats.hip -- activation quantizers, exact dequant, GGML->device repack and
 // the synthetic weight generator.
-#include "kernels.hpp"
+#include "device.hpp"
 
 namespace lh {
 
-// ---- activation quantizers ------------------------------------------------
+// ---- activation quantizers (one wave per item, device.hpp) -----------------------
 
-// quantizeX256 (src/gguf/ggml.zig:776-800): one wave per 256-value block.
-// Lane l holds values 4l..4l+3; amax is an exact max (order-free), the
-// per-16 sums are integer.
-__global__ __launch_bounds__(64) void quant_x256_kernel(const float *__restrict__ x, int cols,
-                                                        int x_stride, int8_t *__restrict__ q,
-                                                        float *__restrict__ d,
-                                                        int32_t *__restrict__ s) {
-    const int b = blockIdx.x, v = blockIdx.y, lane = threadIdx.x;
-    const int nb = cols / 256;
-    const float4 xv = *(const float4 *)(x + (size_t)v * x_stride + b * 256 + 4 * lane);
-    float a = 0.0f;
-    if (__builtin_isfinite(xv.x)) a = fmaxf(a, fabsf(xv.x));
-    if (__builtin_isfinite(xv.y)) a = fmaxf(a, fabsf(xv.y));
-    if (__builtin_isfinite(xv.z)) a = fmaxf(a, fabsf(xv.z));
-    if (__builtin_isfinite(xv.w)) a = fmaxf(a, fabsf(xv.w));
-    const float amax = wave_max(a);
-    const float dd = amax / 127.0f;
-    const float inv = (dd != 0.0f && __builtin_isfinite(dd)) ? 1.0f / dd : 0.0f;
-    const int q0 = to_i8_sat(xv.x * inv), q1 = to_i8_sat(xv.y * inv);
-    const int q2 = to_i8_sat(xv.z * inv), q3 = to_i8_sat(xv.w * inv);
-    const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-                            ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
-    *(uint32_t *)(q + (size_t)v * cols + b * 256 + 4 * lane) = packed;
-    const int sum16 = group_sum<4>(q0 + q1 + q2 + q3);
-    if ((lane & 3) == 0)
-        s[(size_t)v * (cols / 16) + b * 16 + lane / 4] = sum16;
-    if (lane == 0)
-        d[(size_t)v * nb + b] = __builtin_isfinite(dd) ? dd : 0.0f;
-}
-
-// quantizeX (src/gguf/ggml.zig:1077-1098): 32-value blocks, eight lanes per
-// block (4 values each), eight blocks per wave.
-__global__ __launch_bounds__(64) void quant_x32_kernel(const float *__restrict__ x, int cols,
-                                                       int x_stride, int8_t *__restrict__ q,
-                                                       float *__restrict__ d,
-                                                       int32_t *__restrict__ s) {
-    const int v = blockIdx.y, lane = threadIdx.x;
-    const int nb = cols / 32;
-    const int blk = blockIdx.x * 8 + lane / 8;
-    const bool live = blk < nb;
-    const int bc = live ? blk : nb - 1; // clamp: idle lanes read a valid block
-    const float4 xv = *(const float4 *)(x + (size_t)v * x_stride + bc * 32 + 4 * (lane & 7));
-    float a = 0.0f;
-    if (__builtin_isfinite(xv.x)) a = fmaxf(a, fabsf(xv.x));
-    if (__builtin_isfinite(xv.y)) a = fmaxf(a, fabsf(xv.y));
-    if (__builtin_isfinite(xv.z)) a = fmaxf(a, fabsf(xv.z));
-    if (__builtin_isfinite(xv.w)) a = fmaxf(a, fabsf(xv.w));
-    a = fmaxf(a, __shfl_xor(a, 1, 64));
-    a = fmaxf(a, __shfl_xor(a, 2, 64));
-    a = fmaxf(a, __shfl_xor(a, 4, 64));
-    const float dd = a / 127.0f;
-    const float inv = (dd != 0.0f && __builtin_isfinite(dd)) ? 1.0f / dd : 0.0f;
-    const int q0 = to_i8_sat(xv.x * inv), q1 = to_i8_sat(xv.y * inv);
-    const int q2 = to_i8_sat(xv.z * inv), q3 = to_i8_sat(xv.w * inv);
-    const int sum = group_sum<8>(q0 + q1 + q2 + q3);
-    if (live) {
-        const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-                                ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
-        *(uint32_t *)(q + (size_t)v * cols + blk * 32 + 4 * (lane & 7)) = packed;
-        if ((lane & 7) == 0) {
-            s[(size_t)v * nb + blk] = sum;
-            d[(size_t)v * nb + blk] = __builtin_isfinite(dd) ? dd : 0.0f;
-        }
-    }
+__global__ __launch_bounds__(64) void quant_act_kernel(int wt, const float *__restrict__ x,
+                                                       int cols, int x_stride, QAct qa) {
+    quant_item_wave(wt, x + (size_t)blockIdx.y * x_stride, cols, blockIdx.y, blockIdx.x, qa);
 }
 
 void launch_quant_act(int wtype, const float *x, int cols, int x_stride, int nvec, QAct qa,
                       hipStream_t st) {
-    if (act_block(wtype) == 256) {
-        hipLaunchKernelGGL(quant_x256_kernel, dim3(cols / 256, nvec), dim3(64), 0, st, x, cols,
-                           x_stride, qa.q, qa.d, qa.s);
-    } else {
-        const int nb = cols / 32;
-        hipLaunchKernelGGL(quant_x32_kernel, dim3((nb + 7) / 8, nvec), dim3(64), 0, st, x, cols,
-                           x_stride, qa.q, qa.d, qa.s);
-    }
+    hipLaunchKernelGGL(quant_act_kernel, dim3(quant_items(wtype, cols), nvec), dim3(64), 0, st,
+                       wtype, x, cols, x_stride, qa);
     note_launch();
 }
 

@@ -62,14 +62,10 @@ int dmmv_pick_rpw(int t, int cols, int rows, int groups, int nt, bool fused);
 size_t dmmv_lds_bytes(int t, int cols, int nt, bool fused, int rpw);
 constexpr size_t DMMV_LDS_BUDGET = 48 * 1024;
 
-// f32 router GEMV in dotF32 order (src/gguf/ggml.zig:198-217), plus optional
-// logit bias: logits[v][e] for n vectors.
+// f32 GEMV in dotF32 order (src/gguf/ggml.zig:198-217), plus optional bias:
+// out[v][r] for n vectors.
 void launch_router_gemv(const float *w, const float *bias, const float *x, int n_expert, int dim,
                         int n, float *logits, hipStream_t st);
-// Route n tokens (src/gguf/moe.zig:106-158).
-void launch_route(const float *logits, const float *sel_bias, int n_expert, int n_used, int gating,
-                  int weights_norm, float weights_scale, int n, uint32_t *ids, float *gates,
-                  hipStream_t st);
 
 // Token -> expert bucketing: pairs sorted by (expert, token), groups of at
 // most `nt` pairs per expert, pair_of[t][s] = pair index of token t slot s.
@@ -78,12 +74,60 @@ struct MoeBuckets {
     int *pair_of;     // [n*k]
     int *iota;        // [n*k] identity
     DmmvGroup *groups; // [max_groups]
-    int *n_groups;    // [1]
+    int *n_groups;    // [1]; null = route only, no bucketing
 };
 int moe_max_groups(int n, int k, int n_expert, int nt);
-void launch_bucket(const uint32_t *ids, int n, int k, int n_expert, int nt, MoeBuckets b,
-                   hipStream_t st);
+
+// The gate kernel: router GEMV (router != null) or given logits, routing
+// (src/gguf/moe.zig:106-158), bucketing, and quantization of x for weight
+// type qt (0 = none), in one launch.
+struct GateParams {
+    const float *router, *router_bias, *sel_bias, *x, *logits_in;
+    int n, dim, n_expert, k, gating, weights_norm;
+    float weights_scale;
+    float *logits;
+    uint32_t *ids;
+    float *gates;
+    int qt;
+    QAct qx;
+    MoeBuckets b;
+    int nt;
+    int *sync;
+    int chain; // 1: route + bucket after the GEMV (last-arrival chain); 0: GEMV + quantize only
+    // set by launch_gate
+    int n_chunks, wgs_per_chunk, gemv_wgs, quant_wgs;
+};
+bool gate_supported(int n, int n_expert, int k);
+void launch_gate(GateParams p, hipStream_t st);
+
+// Decode path (few tokens): gate/up with an in-kernel routing prologue per
+// (token, slot) pair, then down + gated combine per token.  No bucketing and
+// no communication between work groups.
+struct DecodeParams {
+    const float *logits, *sel_bias; // router logits [n][n_expert] (bias included)
+    int n_expert, k, gating, weights_norm;
+    float weights_scale;
+    uint32_t *ids; // [n][k] written by the gate/up kernel
+    float *gates;
+    const uint8_t *gate, *up, *down; // device-layout planes, one per expert
+    size_t gu_plane, dn_plane;
+    int dim, ffn, down_t;
+    const int8_t *xq; // quantized x [n][dim]
+    const float *xd;
+    const int32_t *xs;
+    float *act; // [n*k][ffn]
+    float *out; // [n][dim]
+    int mode;   // 0 selection-order combine (overwrite), 1 ascending expert (accumulate)
+    int rpw_gu, rpw_dn;
+};
+size_t decode_down_lds(int down_t, int ffn, int k, int rpw);
+size_t decode_gateup_lds(int gate_t, int dim, int rpw);
+bool launch_moe_decode(int gate_t, int down_t, const DecodeParams &p, int n, hipStream_t st,
+                       int prof_gu, int prof_dn);
 void launch_combine(const float *y, const float *gates, const uint32_t *ids, const int *pair_of,
                     int n, int k, int dim, int mode, float *out, hipStream_t st);
+
+// Sync-buffer size (ints): the gate kernel's completion counters.
+constexpr int SYNC_INTS = 1024;
 
 } // namespace lh

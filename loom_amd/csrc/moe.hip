@@ -1,59 +1,107 @@
-// moe.hip -- router GEMV, routing, token->expert bucketing and the gated
-// combine of the MoE layer (src/gguf/moe.zig:106-158; src/gguf/llama.zig
-// moeLayer 1262-1272, moeRun 1307-1419, moeBatchUnion 1828-1903).
-#include "kernels.hpp"
+// moe.hip -- the gate kernel of the MoE layer: router GEMV, routing,
+// token->expert bucketing and int8 quantization of the layer input in one
+// launch (src/gguf/moe.zig:106-158; src/gguf/llama.zig moeLayer 1262-1272,
+// moeRun 1307-1419, moeBatchUnion 1828-1903).
+//
+// Work split.  Workgroups [0, gemv_wgs) each own up to GT_ROWS router rows
+// (one half-wave per row) for one chunk of GT_TOK tokens; workgroups
+// [gemv_wgs, +quant_wgs) quantize the input for the expert kernels.  The
+// last workgroup to finish a token chunk routes that chunk (one wave per
+// token), and the last router of all chunks buckets every (token, slot) pair
+// by expert.  "Last" is decided by self-resetting completion counters with
+// agent-scope fences on both sides; nothing ever waits on another workgroup.
+#include "device.hpp"
 
 namespace lh {
 
-// ---- router GEMV in the reference's dotF32 order --------------------------
-// dotF32 (src/gguf/ggml.zig:198-217) keeps 4 x 8 f32 accumulators: lane
-// L = 8v + l of a half-wave accumulates a[32t + L] * b[32t + L] over t in
-// sequence; then per l, ((acc[0][l] + acc[1][l]) + acc[2][l]) + acc[3][l];
-// then the eight lanes in order; then the scalar tail.  A half-wave per
-// (row, 4 tokens) reproduces that exactly.
-constexpr int RG_TOK = 4;
+// ---- the gate kernel ------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void router_gemv_kernel(const float *__restrict__ w,
-                                                          const float *__restrict__ bias,
-                                                          const float *__restrict__ x, int n_expert,
-                                                          int dim, int n, float *__restrict__ logits) {
-    __shared__ float part[8][RG_TOK][32];
-    const int hw = threadIdx.x >> 5, L = threadIdx.x & 31;
-    const int e = blockIdx.x * 8 + hw;
-    const int t0 = blockIdx.y * RG_TOK;
-    const int ec = e < n_expert ? e : n_expert - 1;
-    const float *row = w + (size_t)ec * dim;
-    float acc[RG_TOK];
+constexpr int GT_THREADS = 256;
+constexpr int GT_ROWS = GT_THREADS / 32; // router rows per workgroup (a half-wave each)
+constexpr int GT_TOK = 4;                // tokens per chunk = tokens per half-wave pass
+constexpr int GT_UNROLL = 64; // router elements in flight per lane
+constexpr int GT_COLS = 32 * GT_UNROLL; // columns per staged chunk
+
+// Router GEMV for up to GT_TOK tokens in dotF32 order (src/gguf/ggml.zig:
+// 198-217): lane L of a half-wave accumulates row[32i + L] * x[32i + L] over
+// i in sequence (acc0..acc3 x 8 lanes), then per l: ((acc0 + acc1) + acc2) +
+// acc3, the eight lanes in order, and the scalar tail.  Every half-wave owns
+// one row (e < n_expert: valid); the whole work group calls this.  A chunk of
+// GT_COLS columns is processed at a time: the half-wave's row loads (64 per
+// lane) are issued together, and the tokens' matching x columns are staged
+// in LDS (xs, [GT_TOK][GT_COLS]) by the whole work group.
+__device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int nt, int hw, int L,
+                            float (*part)[GT_TOK][32], float *xs) {
+    const int dim = p.dim;
+    const float *row = p.router + (size_t)(valid ? e : 0) * dim;
+    float acc[GT_TOK];
 #pragma unroll
-    for (int k = 0; k < RG_TOK; k++)
+    for (int k = 0; k < GT_TOK; k++)
         acc[k] = 0.0f;
     const int main_end = dim / 32 * 32;
-    for (int i = 0; i < main_end; i += 32) {
-        const float a = row[i + L];
+    for (int c0 = 0; c0 < main_end; c0 += GT_COLS) {
+        const int ccols = (main_end - c0) < GT_COLS ? (main_end - c0) : GT_COLS;
+        const int cnt = ccols / 32;
+        // the tokens' x columns are requested first, then the row, so one
+        // round trip covers both; the barriers below wait on LDS only
+        constexpr int XPT = GT_TOK * GT_COLS / 4 / GT_THREADS;
+        float4 xv[XPT];
 #pragma unroll
-        for (int k = 0; k < RG_TOK; k++) {
-            const int t = t0 + k < n ? t0 + k : n - 1;
-            const float p = a * x[(size_t)t * dim + i + L];
-            acc[k] = acc[k] + p;
+        for (int q = 0; q < XPT; q++) {
+            const int idx = 4 * ((int)threadIdx.x + q * GT_THREADS);
+            const int k = idx / ccols, col = idx % ccols;
+            xv[q] = k < nt ? *(const float4 *)(p.x + (size_t)(t0 + k) * dim + c0 + col)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-    }
-    // leftover whole 8-chunks go to accumulator 0 (lanes 0..7)
-    for (int i = main_end; i + 8 <= dim; i += 8) {
-        if (L < 8) {
-            const float a = row[i + L];
+        float wv[GT_UNROLL];
 #pragma unroll
-            for (int k = 0; k < RG_TOK; k++) {
-                const int t = t0 + k < n ? t0 + k : n - 1;
-                const float p = a * x[(size_t)t * dim + i + L];
-                acc[k] = acc[k] + p;
+        for (int u = 0; u < GT_UNROLL; u++)
+            wv[u] = (valid && u < cnt) ? row[c0 + 32 * u + L] : 0.0f;
+        if (c0 > 0)
+            lds_barrier(); // the previous chunk's readers are done with xs
+#pragma unroll
+        for (int q = 0; q < XPT; q++) {
+            const int idx = 4 * ((int)threadIdx.x + q * GT_THREADS);
+            const int k = idx / ccols, col = idx % ccols;
+            if (k < nt)
+                *(float4 *)(xs + k * GT_COLS + col) = xv[q];
+        }
+        lds_barrier();
+#pragma unroll
+        for (int k = 0; k < GT_TOK; k++) {
+            if (k < nt) {
+#pragma unroll
+                for (int u = 0; u < GT_UNROLL; u++) {
+                    if (u < cnt) {
+                        const float pr = wv[u] * xs[k * GT_COLS + 32 * u + L];
+                        acc[k] = acc[k] + pr;
+                    }
+                }
             }
         }
     }
+    if (!valid)
+        return;
+    int i = main_end;
+    // leftover whole 8-chunks go to accumulator 0 (lanes 0..7)
+    for (; i + 8 <= dim; i += 8) {
+        if (L < 8) {
+            const float a = row[i + L];
 #pragma unroll
-    for (int k = 0; k < RG_TOK; k++)
+            for (int k = 0; k < GT_TOK; k++)
+                if (k < nt) {
+                    const float pr = a * p.x[(size_t)(t0 + k) * dim + i + L];
+                    acc[k] = acc[k] + pr;
+                }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < GT_TOK; k++)
         part[hw][k][L] = acc[k];
-    __syncthreads();
-    if (L < RG_TOK && e < n_expert && t0 + L < n) {
+    // the reduction below reads only this half-wave's lanes
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    if (L < nt) {
         const int k = L, t = t0 + k;
         float s = -0.0f;
         for (int l = 0; l < 8; l++) {
@@ -61,221 +109,152 @@ __global__ __launch_bounds__(256) void router_gemv_kernel(const float *__restric
                                part[hw][k][24 + l];
             s = s + lane;
         }
-        for (int i = dim / 8 * 8; i < dim; i++) {
-            const float p = row[i] * x[(size_t)t * dim + i];
-            s = s + p;
+        for (int j = dim / 8 * 8; j < dim; j++) {
+            const float pr = row[j] * p.x[(size_t)t * dim + j];
+            s = s + pr;
         }
-        if (bias)
-            s = s + bias[e];
-        logits[(size_t)t * n_expert + e] = s;
+        if (p.router_bias)
+            s = s + p.router_bias[e];
+        float *dst = p.logits + (size_t)t * p.n_expert + e;
+        if (p.chain)
+            st_dev(dst, s); // read by the chunk's router in this launch
+        else
+            *dst = s;
     }
 }
 
-void launch_router_gemv(const float *w, const float *bias, const float *x, int n_expert, int dim,
-                        int n, float *logits, hipStream_t st) {
-    dim3 grid((n_expert + 7) / 8, (n + RG_TOK - 1) / RG_TOK);
-    hipLaunchKernelGGL(router_gemv_kernel, grid, dim3(256), 0, st, w, bias, x, n_expert, dim, n,
-                       logits);
-    note_launch();
+// Route one token with one wave and publish ids (read by the bucketing work
+// group of this launch) and gates.
+__device__ void route_token_wave(const GateParams &p, int t, RouteLds<1> &L) {
+    const int lane = threadIdx.x & 63;
+    const int E = p.n_expert, K = p.k;
+    if (p.logits_in)
+        route_select<1, false>(p.logits_in + (size_t)t * E, p.sel_bias, E, K, p.gating, L);
+    else
+        route_select<1, true>(p.logits + (size_t)t * E, p.sel_bias, E, K, p.gating, L);
+    const float g = route_gates<1>(L, K, p.gating, p.weights_norm, p.weights_scale);
+    if (lane < K) {
+        st_dev(p.ids + (size_t)t * K + lane, (uint32_t)L.id[lane]); // read by the bucketing work group
+        p.gates[(size_t)t * K + lane] = g;
+    }
 }
 
-// ---- route: one wave per token ------------------------------------------------
-constexpr int MAX_E = 256, MAX_K = 16;
-
-__global__ __launch_bounds__(64) void route_kernel(const float *__restrict__ logits,
-                                                   const float *__restrict__ sel_bias, int n_expert,
-                                                   int n_used, int gating, int weights_norm,
-                                                   float weights_scale, uint32_t *__restrict__ ids,
-                                                   float *__restrict__ gates) {
-    __shared__ float sc[MAX_E];
-    __shared__ float gsel[MAX_K];
-    __shared__ int isel[MAX_K];
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const float *lg = logits + (size_t)t * n_expert;
-    // scores (moe.zig:110-120)
-    if (gating == 2) { // sigmoid
-        for (int e = lane; e < n_expert; e += 64)
-            sc[e] = 1.0f / (1.0f + expf(-lg[e]));
-    } else if (gating == 3) { // softmax_topk: raw logits
-        for (int e = lane; e < n_expert; e += 64)
-            sc[e] = lg[e];
-    } else { // softmax (tensor.zig:18-28): max, exp, sequential sum, * (1/sum)
-        float m = -INFINITY;
-        for (int e = lane; e < n_expert; e += 64)
-            m = fmaxf(m, lg[e]);
-        m = wave_max(m);
-        for (int e = lane; e < n_expert; e += 64)
-            sc[e] = expf(lg[e] - m);
-        __syncthreads();
-        float inv = 0.0f;
-        if (lane == 0) {
-            float sum = 0.0f;
-            for (int e = 0; e < n_expert; e++)
-                sum = sum + sc[e];
-            inv = 1.0f / sum;
-        }
-        inv = __shfl(inv, 0, 64);
-        __syncthreads();
-        for (int e = lane; e < n_expert; e += 64)
-            sc[e] = sc[e] * inv;
+// Exclusive block scan of one int per thread (GT_THREADS threads).
+__device__ int block_excl_scan(int v, int *total) {
+    __shared__ int wsum[GT_THREADS / 64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int inc = v;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(inc, o, 64);
+        if (lane >= o)
+            inc += y;
+    }
+    if (lane == 63)
+        wsum[w] = inc;
+    __syncthreads();
+    int base = 0, tot = 0;
+    for (int i = 0; i < GT_THREADS / 64; i++) {
+        if (i < w)
+            base += wsum[i];
+        tot += wsum[i];
     }
     __syncthreads();
-    // k rounds of argmax over unused experts, strict '>' (lowest index wins
-    // ties), selection on scores + bias, gates from unbiased scores.
-    float ch[MAX_E / 64];
-    bool used[MAX_E / 64];
-#pragma unroll
-    for (int i = 0; i < MAX_E / 64; i++) {
-        const int e = lane + 64 * i;
-        ch[i] = e < n_expert ? (sel_bias ? sc[e] + sel_bias[e] : sc[e]) : -INFINITY;
-        used[i] = e >= n_expert;
-    }
-    for (int s = 0; s < n_used; s++) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int i = 0; i < MAX_E / 64; i++)
-            if (!used[i] && ch[i] > bv) {
-                bv = ch[i];
-                bi = lane + 64 * i;
-            }
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        const int best = (bi == 0x7fffffff) ? 0 : bi; // nothing beat -inf: index 0
-#pragma unroll
-        for (int i = 0; i < MAX_E / 64; i++)
-            if (lane + 64 * i == best)
-                used[i] = true;
-        if (lane == 0) {
-            isel[s] = best;
-            gsel[s] = sc[best];
-        }
-    }
-    __syncthreads();
-    if (lane == 0) {
-        float g[MAX_K];
-        for (int s = 0; s < n_used; s++)
-            g[s] = gsel[s];
-        if (gating == 3) { // softmax over the selected k
-            float m = -INFINITY;
-            for (int s = 0; s < n_used; s++)
-                m = fmaxf(m, g[s]);
-            float sum = 0.0f;
-            for (int s = 0; s < n_used; s++) {
-                g[s] = expf(g[s] - m);
-                sum = sum + g[s];
-            }
-            const float inv = 1.0f / sum;
-            for (int s = 0; s < n_used; s++)
-                g[s] = g[s] * inv;
-        }
-        if (weights_norm) {
-            float sum = 0.0f;
-            for (int s = 0; s < n_used; s++)
-                sum = sum + g[s];
-            const float denom = fmaxf(sum, 6.103515625e-5f);
-            for (int s = 0; s < n_used; s++)
-                g[s] = g[s] / denom;
-        }
-        if (weights_scale != 1.0f)
-            for (int s = 0; s < n_used; s++)
-                g[s] = g[s] * weights_scale;
-        for (int s = 0; s < n_used; s++) {
-            ids[(size_t)t * n_used + s] = (uint32_t)isel[s];
-            gates[(size_t)t * n_used + s] = g[s];
-        }
-    }
+    *total = tot;
+    return base + inc - v;
 }
 
-void launch_route(const float *logits, const float *sel_bias, int n_expert, int n_used, int gating,
-                  int weights_norm, float weights_scale, int n, uint32_t *ids, float *gates,
-                  hipStream_t st) {
-    hipLaunchKernelGGL(route_kernel, dim3(n), dim3(64), 0, st, logits, sel_bias, n_expert, n_used,
-                       gating, weights_norm, weights_scale, ids, gates);
-    note_launch();
-}
-
-// ---- bucketing: one work group --------------------------------------------------
-// Per expert a token bitmask (order-free atomicOr); an expert's pairs are
-// ranked by token index via popcounts, so the pair order is (expert, token)
-// and deterministic.
-constexpr int BK_MAX_TOK = 256;
-
-int moe_max_groups(int n, int k, int n_expert, int nt) {
-    const int P = n * k;
-    const int bound = P / nt + (P < n_expert ? P : n_expert);
-    return bound < P ? bound : P;
-}
-
-__global__ __launch_bounds__(256) void bucket_kernel(const uint32_t *__restrict__ ids, int n, int k,
-                                                     int n_expert, int nt, MoeBuckets b) {
-    __shared__ uint32_t mask[MAX_E][BK_MAX_TOK / 32];
-    __shared__ int cnt[MAX_E], off[MAX_E], goff[MAX_E];
-    const int tid = threadIdx.x;
+// Token -> expert bucketing by the whole workgroup: pairs sorted by
+// (expert, token), groups of at most nt pairs per expert, pair_of[t][s] =
+// pair index of token t slot s.  Per expert a token bitmask (order-free
+// atomicOr) ranks an expert's pairs by token index via popcounts, so the
+// order is deterministic.
+__device__ void bucket_block(const GateParams &p) {
+    __shared__ uint32_t mask[MAX_E][MAX_TOK / 32];
+    __shared__ int off[MAX_E];
+    const int tid = threadIdx.x, n = p.n, K = p.k, E = p.n_expert, nt = p.nt;
     const int W = (n + 31) / 32;
-    for (int i = tid; i < n_expert * W; i += blockDim.x)
+    for (int i = tid; i < E * W; i += GT_THREADS)
         mask[i / W][i % W] = 0;
     __syncthreads();
-    const int P = n * k;
-    for (int p = tid; p < P; p += blockDim.x) {
-        const int t = p / k, e = (int)ids[p];
+    const int P = n * K;
+    for (int q = tid; q < P; q += GT_THREADS) {
+        const int t = q / K, e = min((int)ld_dev(p.ids + q), E - 1);
         atomicOr(&mask[e][t >> 5], 1u << (t & 31));
     }
     __syncthreads();
-    for (int e = tid; e < n_expert; e += blockDim.x) {
-        int c = 0;
+    int c = 0;
+    if (tid < E)
         for (int w = 0; w < W; w++)
-            c += __popc(mask[e][w]);
-        cnt[e] = c;
-    }
+            c += __popc(mask[tid][w]);
+    int tot = 0, gtot = 0;
+    const int o = block_excl_scan(c, &tot);
+    const int ng = (c + nt - 1) / nt;
+    const int go = block_excl_scan(ng, &gtot);
+    if (tid < E)
+        off[tid] = o;
+    if (tid == 0)
+        *p.b.n_groups = gtot;
     __syncthreads();
-    if (tid == 0) { // exclusive scans over <= 256 experts
-        int o = 0, go = 0;
-        for (int e = 0; e < n_expert; e++) {
-            off[e] = o;
-            goff[e] = go;
-            o += cnt[e];
-            go += (cnt[e] + nt - 1) / nt;
-        }
-        *b.n_groups = go;
-    }
-    __syncthreads();
-    for (int p = tid; p < P; p += blockDim.x) {
-        const int t = p / k, e = (int)ids[p];
+    for (int q = tid; q < P; q += GT_THREADS) {
+        const int t = q / K, e = min((int)ld_dev(p.ids + q), E - 1);
         int rank = 0;
         for (int w = 0; w < (t >> 5); w++)
             rank += __popc(mask[e][w]);
         rank += __popc(mask[e][t >> 5] & ((1u << (t & 31)) - 1u));
         const int pos = off[e] + rank;
-        b.pair_tok[pos] = t;
-        b.pair_of[p] = pos;
-        b.iota[p] = p;
+        p.b.pair_tok[pos] = t;
+        p.b.pair_of[q] = pos;
+        p.b.iota[q] = q;
     }
-    for (int e = tid; e < n_expert; e += blockDim.x) {
-        const int c = cnt[e];
+    if (tid < E)
         for (int gi = 0; gi * nt < c; gi++) {
             DmmvGroup g;
-            g.plane = e;
-            g.first = off[e] + gi * nt;
+            g.plane = tid;
+            g.first = o + gi * nt;
             g.n = (c - gi * nt) < nt ? (c - gi * nt) : nt;
-            b.groups[goff[e] + gi] = g;
+            p.b.groups[go + gi] = g;
         }
+}
+
+__global__ __launch_bounds__(GT_THREADS) void moe_gate_kernel(GateParams p) {
+    __shared__ float part[GT_ROWS][GT_TOK][32];
+    __shared__ RouteLds<1> sc[GT_THREADS / 64];
+    __shared__ __align__(16) float xs[GT_TOK * GT_COLS];
+    const int bid = blockIdx.x;
+    const int wave = threadIdx.x >> 6;
+
+    if (bid >= p.gemv_wgs) {
+        // input quantization for the expert kernels: one item per wave
+        const int per_vec = quant_items(p.qt, p.dim);
+        const int item = (bid - p.gemv_wgs) * (GT_THREADS / 64) + wave;
+        if (item < per_vec * p.n) {
+            const int v = item / per_vec, it = item % per_vec;
+            quant_item_wave(p.qt, p.x + (size_t)v * p.dim, p.dim, v, it, p.qx);
+        }
+        if (p.chain && last_arrival(p.sync + SYNC_GATE_FINAL, p.n_chunks + p.quant_wgs) &&
+            p.b.n_groups)
+            bucket_block(p);
+        return;
     }
+
+    const int chunk = bid / p.wgs_per_chunk, sub = bid % p.wgs_per_chunk;
+    const int t0 = chunk * GT_TOK;
+    const int nt = (p.n - t0) < GT_TOK ? (p.n - t0) : GT_TOK;
+    if (p.router) {
+        const int hw = threadIdx.x >> 5, L = threadIdx.x & 31;
+        const int e = sub * GT_ROWS + hw;
+        router_rows(p, e, e < p.n_expert, t0, nt, hw, L, part, xs);
+    }
+    if (!p.chain || !last_arrival(p.sync + SYNC_GATE_CHUNK + chunk, p.wgs_per_chunk))
+        return;
+    // last workgroup of this chunk: route its tokens, one wave each
+    if (wave < nt)
+        route_token_wave(p, t0 + wave, sc[wave]);
+    if (last_arrival(p.sync + SYNC_GATE_FINAL, p.n_chunks + p.quant_wgs) && p.b.n_groups)
+        bucket_block(p);
 }
 
-void launch_bucket(const uint32_t *ids, int n, int k, int n_expert, int nt, MoeBuckets b,
-                   hipStream_t st) {
-    hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(256), 0, st, ids, n, k, n_expert, nt, b);
-    note_launch();
-}
-
-// ---- combine ----------------------------------------------------------------------
+// ---- gated combine (batched path) --------------------------------------------------
 // mode 0 (moeRun): out = ((0 + g0*y0) + g1*y1) + ... in selection order.
 // mode 1 (moeBatchUnion): out += g*y per expert in ascending expert id.
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ y,
@@ -290,8 +269,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     if (mode == 0) {
         float acc = 0.0f;
         for (int s = 0; s < k; s++) {
-            const float p = gates[base + s] * y[(size_t)pair_of[base + s] * dim + i];
-            acc = acc + p;
+            const float pr = gates[base + s] * y[(size_t)pair_of[base + s] * dim + i];
+            acc = acc + pr;
         }
         out[(size_t)t * dim + i] = acc;
     } else {
@@ -308,8 +287,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
             }
             if (bs < 0)
                 break;
-            const float p = gates[base + bs] * y[(size_t)pair_of[base + bs] * dim + i];
-            acc = acc + p;
+            const float pr = gates[base + bs] * y[(size_t)pair_of[base + bs] * dim + i];
+            acc = acc + pr;
             prev = be;
         }
         out[(size_t)t * dim + i] = acc;
@@ -320,6 +299,56 @@ void launch_combine(const float *y, const float *gates, const uint32_t *ids, con
                     int n, int k, int dim, int mode, float *out, hipStream_t st) {
     hipLaunchKernelGGL(combine_kernel, dim3((dim + 255) / 256, n), dim3(256), 0, st, y, gates, ids,
                        pair_of, k, dim, mode, out);
+    note_launch();
+}
+
+int moe_max_groups(int n, int k, int n_expert, int nt) {
+    const int P = n * k;
+    const int bound = P / nt + (P < n_expert ? P : n_expert);
+    return bound < P ? bound : P;
+}
+
+bool gate_supported(int n, int n_expert, int k) {
+    return n >= 1 && n <= MAX_TOK && n_expert >= 1 && n_expert <= MAX_E && k >= 1 && k <= MAX_K &&
+           k <= n_expert;
+}
+
+void launch_gate(GateParams p, hipStream_t st) {
+    p.n_chunks = (p.n + GT_TOK - 1) / GT_TOK;
+    p.wgs_per_chunk = p.router ? (p.n_expert + GT_ROWS - 1) / GT_ROWS : 1;
+    p.gemv_wgs = p.n_chunks * p.wgs_per_chunk;
+    p.quant_wgs = p.qt ? (quant_items(p.qt, p.dim) * p.n + GT_THREADS / 64 - 1) / (GT_THREADS / 64) : 0;
+    hipLaunchKernelGGL(moe_gate_kernel, dim3(p.gemv_wgs + p.quant_wgs), dim3(GT_THREADS), 0, st, p);
+    note_launch();
+}
+
+// ---- f32 GEMV for the dense seam (F32 matvec), same dotF32 order ---------------
+// One half-wave per (row, up to GT_TOK vectors); no routing.
+__global__ __launch_bounds__(GT_THREADS) void f32_gemv_kernel(GateParams p) {
+    __shared__ float part[GT_ROWS][GT_TOK][32];
+    __shared__ __align__(16) float xs[GT_TOK * GT_COLS];
+    const int chunk = blockIdx.x / p.wgs_per_chunk, sub = blockIdx.x % p.wgs_per_chunk;
+    const int t0 = chunk * GT_TOK;
+    const int nt = (p.n - t0) < GT_TOK ? (p.n - t0) : GT_TOK;
+    const int hw = threadIdx.x >> 5, L = threadIdx.x & 31;
+    const int e = sub * GT_ROWS + hw;
+    router_rows(p, e, e < p.n_expert, t0, nt, hw, L, part, xs);
+}
+
+void launch_router_gemv(const float *w, const float *bias, const float *x, int n_expert, int dim,
+                        int n, float *logits, hipStream_t st) {
+    GateParams p{};
+    p.router = w;
+    p.router_bias = bias;
+    p.x = x;
+    p.n = n;
+    p.dim = dim;
+    p.n_expert = n_expert;
+    p.logits = logits;
+    p.n_chunks = (n + GT_TOK - 1) / GT_TOK;
+    p.wgs_per_chunk = (n_expert + GT_ROWS - 1) / GT_ROWS;
+    hipLaunchKernelGGL(f32_gemv_kernel, dim3(p.n_chunks * p.wgs_per_chunk), dim3(GT_THREADS), 0, st,
+                       p);
     note_launch();
 }
 

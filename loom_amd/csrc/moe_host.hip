@@ -25,10 +25,9 @@ struct MoeRun {
 };
 
 static int moe_check(const MoeRun &m, size_t n) {
-    if (n == 0 || n > 256)
-        return fail(LOOMHIP_DECLINED, "moe: %zu tokens (1..256 served)", n);
-    if (m.E == 0 || m.E > 256 || m.k == 0 || m.k > 16 || m.k > m.E)
-        return fail(LOOMHIP_DECLINED, "moe: %zu experts / top-%zu not served", m.E, m.k);
+    if (!gate_supported((int)n, (int)m.E, (int)m.k))
+        return fail(LOOMHIP_DECLINED, "moe: %zu tokens / %zu experts / top-%zu not served "
+                    "(1..256 tokens, <= 256 experts, top-k <= 16)", n, m.E, m.k);
     if (m.gate_t != m.up_t)
         return fail(LOOMHIP_DECLINED, "moe: gate/up types differ (%d, %d)", m.gate_t, m.up_t);
     if (!dmmv_supported(m.gate_t, (int)m.dim) || !dmmv_supported(m.down_t, (int)m.ffn))
@@ -58,12 +57,29 @@ static int moe_nt(size_t n, size_t k, size_t E) {
     return per >= 4 ? 8 : per >= 2 ? 4 : 2;
 }
 
+constexpr size_t DECODE_MAX_TOK = 4; // decode path up to this many tokens
+
 // normed/logits/out are device pointers; logits may be null when m.router is set.
+//
+// Decode path (n <= DECODE_MAX_TOK), three launches, no bucketing:
+//   gate     router GEMV + quantize x
+//   gate/up  one work group per (token, slot, row tile): routes its token,
+//            then fused gate/up + SwiGLU of the slot's expert
+//   down     one work group per (token, row tile): quantizes the token's k
+//            activations in LDS, down for every slot, gated combine
+// Batched path, five launches, experts grouped so each weight row is read
+// once per group of tokens:
+//   gate     router GEMV + route + bucket + quantize x (last-arrival chain)
+//   gate/up  grouped fused gate/up + SwiGLU
+//   quant    int8 quantization of the activations
+//   down     grouped down
+//   combine  gated combine per token
 static int moe_run(const MoeRun &m, const float *normed, const float *logits_in, size_t n,
                    int combine, float *out, uint32_t *ids_out, float *gates_out, hipStream_t st) {
     if (int rc = moe_check(m, n))
         return rc;
     const size_t P = n * m.k;
+    const bool decode = n <= DECODE_MAX_TOK;
     const int nt = moe_nt(n, m.k, m.E);
     const int maxg = moe_max_groups((int)n, (int)m.k, (int)m.E, nt);
     // workspace layout
@@ -79,31 +95,91 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     const size_t o_ptok = take(P * 4), o_pof = take(P * 4), o_iota = take(P * 4);
     const size_t o_groups = take(maxg * sizeof(DmmvGroup)), o_ng = take(16);
     const size_t o_act = take(P * m.ffn * 4);
-    const size_t o_qa = take(qbytes(P, m.ffn));
-    const size_t o_y = take(P * m.dim * 4);
+    const size_t o_qa = take(decode ? 0 : qbytes(P, m.ffn));
+    const size_t o_y = take(decode ? 0 : P * m.dim * 4);
     if (int rc = g_moe.reserve(off))
         return rc;
     char *base = (char *)g_moe.ptr;
     const QAct qx = qview(base + o_qx, n, m.dim);
-    const QAct qa = qview(base + o_qa, P, m.ffn);
-    float *logits = logits_in ? (float *)logits_in : (float *)(base + o_log);
     uint32_t *ids = ids_out ? ids_out : (uint32_t *)(base + o_ids);
     float *gates = gates_out ? gates_out : (float *)(base + o_gates);
+    float *logits = (float *)(base + o_log);
+    float *act = (float *)(base + o_act);
+
+    GateParams gp{};
+    gp.router = m.router;
+    gp.router_bias = m.router_bias;
+    gp.sel_bias = m.sel_bias;
+    gp.x = normed;
+    gp.logits_in = m.router ? nullptr : logits_in;
+    gp.n = (int)n;
+    gp.dim = (int)m.dim;
+    gp.n_expert = (int)m.E;
+    gp.k = (int)m.k;
+    gp.gating = m.gating;
+    gp.weights_norm = m.weights_norm;
+    gp.weights_scale = m.weights_scale;
+    gp.logits = logits;
+    gp.ids = ids;
+    gp.gates = gates;
+    gp.qt = m.gate_t;
+    gp.qx = qx;
+    gp.nt = nt;
+    gp.sync = g_ctx.sync;
+
+    if (decode) {
+        DecodeParams dp{};
+        dp.logits = m.router ? logits : logits_in;
+        dp.sel_bias = m.sel_bias;
+        dp.n_expert = (int)m.E;
+        dp.k = (int)m.k;
+        dp.gating = m.gating;
+        dp.weights_norm = m.weights_norm;
+        dp.weights_scale = m.weights_scale;
+        dp.ids = ids;
+        dp.gates = gates;
+        dp.gate = (const uint8_t *)m.gate;
+        dp.up = (const uint8_t *)m.up;
+        dp.down = (const uint8_t *)m.down;
+        dp.gu_plane = plane_bytes(m.gate_t, m.ffn, m.dim);
+        dp.dn_plane = plane_bytes(m.down_t, m.dim, m.ffn);
+        dp.dim = (int)m.dim;
+        dp.ffn = (int)m.ffn;
+        dp.down_t = m.down_t;
+        dp.xq = qx.q;
+        dp.xd = qx.d;
+        dp.xs = qx.s;
+        dp.act = act;
+        dp.out = out;
+        dp.mode = combine;
+        dp.rpw_gu = dmmv_pick_rpw(m.gate_t, (int)m.dim, (int)m.ffn, (int)P, 1, true);
+        int rpw = 2;
+        while (rpw < 8 && ((int)m.dim / (8 * rpw)) * (int)n >= 512)
+            rpw *= 2;
+        while (rpw > 1 && decode_down_lds(m.down_t, (int)m.ffn, (int)m.k, rpw) > 48 * 1024)
+            rpw /= 2;
+        dp.rpw_dn = rpw;
+        if (decode_down_lds(m.down_t, (int)m.ffn, (int)m.k, rpw) > 64 * 1024)
+            return fail(LOOMHIP_DECLINED, "moe: ffn %zu x top-%zu exceeds the decode LDS budget",
+                        m.ffn, m.k);
+        gp.chain = 0;
+        launch_gate(gp, st);
+        if (!launch_moe_decode(m.gate_t, m.down_t, dp, (int)n, st, LOOMHIP_KT_GATE_UP, LOOMHIP_KT_DOWN))
+            return fail(LOOMHIP_ERR_ARG, "moe: decode kernels declined the shape");
+        return LOOMHIP_OK;
+    }
+
+    const QAct qa = qview(base + o_qa, P, m.ffn);
     MoeBuckets b;
     b.pair_tok = (int *)(base + o_ptok);
     b.pair_of = (int *)(base + o_pof);
     b.iota = (int *)(base + o_iota);
     b.groups = (DmmvGroup *)(base + o_groups);
     b.n_groups = (int *)(base + o_ng);
-    float *act = (float *)(base + o_act);
     float *y = (float *)(base + o_y);
-
-    if (m.router)
-        launch_router_gemv(m.router, m.router_bias, normed, (int)m.E, (int)m.dim, (int)n, logits, st);
-    launch_route(logits, m.sel_bias, (int)m.E, (int)m.k, m.gating, m.weights_norm, m.weights_scale,
-                 (int)n, ids, gates, st);
-    launch_bucket(ids, (int)n, (int)m.k, (int)m.E, nt, b, st);
-    launch_quant_act(m.gate_t, normed, (int)m.dim, (int)m.dim, (int)n, qx, st);
+    gp.b = b;
+    gp.chain = 1;
+    launch_gate(gp, st);
 
     const int exp_groups = (int)(P < (size_t)maxg ? P : (size_t)maxg);
     DmmvParams gu{};
@@ -182,7 +258,7 @@ int loomhip_moe_route(const float *logits, const float *bias, size_t n_expert, s
                       float *gates_out) {
     if (int rc = require_ready())
         return rc;
-    if (n_expert == 0 || n_expert > 256 || n_used == 0 || n_used > 16 || n_used > n_expert)
+    if (!gate_supported(1, (int)n_expert, (int)n_used))
         return fail(LOOMHIP_DECLINED, "moe_route: %zu experts / top-%zu not served", n_expert, n_used);
     const size_t need = 2 * n_expert * 4 + 2 * 64;
     if (int rc = g_stage.reserve(need))
@@ -197,8 +273,23 @@ int loomhip_moe_route(const float *logits, const float *bias, size_t n_expert, s
         e = hipMemcpyAsync(db, bias, n_expert * 4, hipMemcpyHostToDevice, st);
     if (e != hipSuccess)
         return hip_fail(e, "moe_route staging");
-    launch_route(dl, bias ? db : nullptr, (int)n_expert, (int)n_used, gating, weights_norm,
-                 weights_scale, 1, di, dg, st);
+    GateParams gp{};
+    gp.sel_bias = bias ? db : nullptr;
+    gp.logits_in = dl;
+    gp.n = 1;
+    gp.dim = 0;
+    gp.n_expert = (int)n_expert;
+    gp.k = (int)n_used;
+    gp.gating = gating;
+    gp.weights_norm = weights_norm;
+    gp.weights_scale = weights_scale;
+    gp.ids = di;
+    gp.gates = dg;
+    gp.qt = 0;
+    gp.nt = 1;
+    gp.sync = g_ctx.sync;
+    gp.chain = 1;
+    launch_gate(gp, st);
     e = hipMemcpyAsync(ids_out, di, n_used * 4, hipMemcpyDeviceToHost, st);
     if (e == hipSuccess)
         e = hipMemcpyAsync(gates_out, dg, n_used * 4, hipMemcpyDeviceToHost, st);

@@ -299,6 +299,12 @@ int loomhip_init(int device) {
     if (e != hipSuccess)
         return hip_fail(e, "iota upload");
     g_ctx.iota = (const int *)d;
+    void *sy = nullptr;
+    if ((e = hipMalloc(&sy, sizeof(int) * SYNC_INTS)) != hipSuccess)
+        return hip_fail(e, "hipMalloc sync");
+    if ((e = hipMemset(sy, 0, sizeof(int) * SYNC_INTS)) != hipSuccess)
+        return hip_fail(e, "hipMemset sync");
+    g_ctx.sync = (int *)sy;
     g_ctx.device = device;
     g_ctx.ready = true;
     return LOOMHIP_OK;
@@ -322,6 +328,8 @@ void loomhip_shutdown(void) {
     g_prof_pool.clear();
     g_prof = false;
     (void)hipFree((void *)g_ctx.iota);
+    (void)hipFree(g_ctx.sync);
+    g_ctx.sync = nullptr;
     (void)hipStreamDestroy(g_ctx.compute);
     (void)hipStreamDestroy(g_ctx.copy);
     g_ctx.ready = false;

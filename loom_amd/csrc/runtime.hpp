@@ -29,6 +29,7 @@ struct Ctx {
     hipStream_t compute = nullptr; // kernels
     hipStream_t copy = nullptr;    // expert-cache host->HBM copies
     const int *iota = nullptr;
+    int *sync = nullptr; // SYNC_INTS zero-initialised completion counters
     Scratch act;    // quantized activations for dense matvecs
     Scratch xstage; // seam-call staging
     Scratch ostage;

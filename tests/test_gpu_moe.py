@@ -97,7 +97,7 @@ def test_moe_ffn_routed_single_token(be, oracle, dim, ffn, E, k):
                               WeightRef(w.up_t, w.up), WeightRef(w.down_t, w.down), None, ffn, 0,
                               RoutedCfg(E, k, False, True, 1.0), out)
     assert ok
-    assert be.takeCmdBufCount() >= 6
+    assert be.takeCmdBufCount() >= 3  # gate, gate/up, down ran on the device
     want, ids, gates = oracle.moe_layer_token(w, normed)
     assert _maxrel(out, want) <= 2e-3, _maxrel(out, want)
 
@@ -116,7 +116,7 @@ def _dev_layer(be, w):
                        router_bias=rb)
 
 
-@pytest.mark.parametrize("n", [1, 8, 32, 128])
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 8, 32, 128])
 def test_moe_layer_dev_matches_oracle(be, oracle, n):
     """Config-3 shape: hidden 2048, 128 experts top-8, ffn 768, Q4_K gate/up,
     Q6_K down, f32 router with a Zipf(1.1) logit bias."""
