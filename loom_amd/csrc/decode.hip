@@ -16,12 +16,15 @@
 
 namespace lh {
 
+constexpr int GU_MAXIT = 4; // weight rows per lane requested at once in the gate/up kernel
+
 template <int T>
 __global__ __launch_bounds__(256) void moe_gateup_decode_kernel(DecodeParams p) {
     using F = Fmt<T>;
     constexpr int LPB = F::LPB, BPI = 64 / LPB;
     extern __shared__ float lds[];
     __shared__ RouteLds<WAVES> rl;
+    __shared__ int s_redo;
     const int K = p.k;
     const int t = blockIdx.y / K, s = blockIdx.y % K;
     const int rows = p.ffn, cols = p.dim, nb = cols / F::BE;
@@ -37,49 +40,80 @@ __global__ __launch_bounds__(256) void moe_gateup_decode_kernel(DecodeParams p) 
     const bool active = wide || grp < RPI * nb;
     const int nit = (rpw + RPI - 1) / RPI;
     const size_t lds_mat = (size_t)TR * nb;
+    const bool exact = route_is_exact(p.gating, p.sel_bias);
+    const float *lg = p.logits + (size_t)t * p.n_expert;
 
     // the first column chunk's activations load while the waves route
-    typename F::X xr = F::load_x(p.xq, p.xd, p.xs, cols, t, wide ? grp : grp % nb, j);
-    route_select<WAVES, false>(p.logits + (size_t)t * p.n_expert, p.sel_bias, p.n_expert, K,
-                               p.gating, rl);
-    const int e = min(max(rl.id[s], 0), p.n_expert - 1); // never address past the tensor
-    const uint8_t *wb = p.gate + (size_t)e * p.gu_plane;
-    const uint8_t *wb2 = p.up + (size_t)e * p.gu_plane;
-    for (int c = 0; c < C; c++) {
-        const int b = wide ? c * BPI + grp : (grp % nb);
-        if (c > 0)
-            xr = F::load_x(p.xq, p.xd, p.xs, cols, t, b, j);
-#pragma unroll 4
-        for (int it = 0; it < nit; it++) {
-            const int rw = it * RPI + ro;
-            const int rl_ = wave * rpw + rw;
-            const int row = row0 + rl_;
-            const bool valid = active && rw < rpw && row < rows;
-            const size_t unit = (size_t)(valid ? row : 0) * nb + b;
-            const typename F::W w = F::load_w(wb, U, unit, j);
-            const typename F::W w2 = F::load_w(wb2, U, unit, j);
-            int is, ms;
-            F::dot(w, xr, j, is, ms);
-            is = group_sum<LPB>(is);
-            ms = group_sum<LPB>(ms);
-            if (valid && j == 0)
-                lds[(size_t)rl_ * nb + b] = F::tail(w, xr, is, ms);
-            F::dot(w2, xr, j, is, ms);
-            is = group_sum<LPB>(is);
-            ms = group_sum<LPB>(ms);
-            if (valid && j == 0)
-                lds[lds_mat + (size_t)rl_ * nb + b] = F::tail(w2, xr, is, ms);
+    const typename F::X x0 = F::load_x(p.xq, p.xd, p.xs, cols, t, wide ? grp : grp % nb, j);
+    route_rank<WAVES, false>(lg, p.sel_bias, p.n_expert, K, p.gating, rl);
+    float g = 0.0f;
+    for (int pass = 0; pass < 2; pass++) {
+        const int e = min(max(rl.id[s], 0), p.n_expert - 1); // never address past the tensor
+        const uint8_t *wb = p.gate + (size_t)e * p.gu_plane;
+        const uint8_t *wb2 = p.up + (size_t)e * p.gu_plane;
+        for (int c = 0; c < C; c++) {
+            const int b = wide ? c * BPI + grp : (grp % nb);
+            const typename F::X xr = c == 0 ? x0 : F::load_x(p.xq, p.xd, p.xs, cols, t, b, j);
+            for (int it0 = 0; it0 < nit; it0 += GU_MAXIT) {
+                typename F::W w[GU_MAXIT], w2[GU_MAXIT];
+                int rlv[GU_MAXIT];
+                bool valid[GU_MAXIT];
+#pragma unroll
+                for (int u = 0; u < GU_MAXIT; u++) {
+                    const int rw = (it0 + u) * RPI + ro;
+                    rlv[u] = wave * rpw + rw;
+                    const int row = row0 + rlv[u];
+                    valid[u] = active && it0 + u < nit && rw < rpw && row < rows;
+                    const size_t unit = (size_t)(valid[u] ? row : 0) * nb + b;
+                    w[u] = F::load_w(wb, U, unit, j);
+                    w2[u] = F::load_w(wb2, U, unit, j);
+                }
+                if (pass == 0 && c == 0 && it0 == 0 && wave == 0) {
+                    // settle the routing (sum, tie check, gates) while the rows load
+                    bool redo;
+                    g = route_finish<WAVES>(rl, p.n_expert, K, p.gating, exact, p.weights_norm,
+                                            p.weights_scale, redo);
+                    if (lane == 0)
+                        s_redo = redo;
+                }
+#pragma unroll
+                for (int u = 0; u < GU_MAXIT; u++) {
+                    if (it0 + u < nit) {
+                        int is, ms;
+                        F::dot(w[u], xr, j, is, ms);
+                        is = group_sum<LPB>(is);
+                        ms = group_sum<LPB>(ms);
+                        if (valid[u] && j == 0)
+                            lds[(size_t)rlv[u] * nb + b] = F::tail(w[u], xr, is, ms);
+                        F::dot(w2[u], xr, j, is, ms);
+                        is = group_sum<LPB>(is);
+                        ms = group_sum<LPB>(ms);
+                        if (valid[u] && j == 0)
+                            lds[lds_mat + (size_t)rlv[u] * nb + b] = F::tail(w2[u], xr, is, ms);
+                    }
+                }
+            }
         }
+        __syncthreads();
+        if (pass == 1 || !s_redo)
+            break;
+        // two experts tied on the final score: route exactly, and redo the
+        // tile only if this slot's expert changed
+        if (wave == 0) {
+            route_exact_wave<WAVES, false>(lg, p.sel_bias, p.n_expert, K, p.gating, rl);
+            bool again;
+            g = route_finish<WAVES>(rl, p.n_expert, K, p.gating, true, p.weights_norm,
+                                    p.weights_scale, again);
+        }
+        __syncthreads();
+        if (min(max(rl.id[s], 0), p.n_expert - 1) == e)
+            break;
     }
-    if (s == 0 && blockIdx.x == 0 && wave == 0) {
+    if (s == 0 && blockIdx.x == 0 && wave == 0 && lane < K) {
         // one work group per token publishes the routing for the down kernel
-        const float g = route_gates<WAVES>(rl, K, p.gating, p.weights_norm, p.weights_scale);
-        if (lane < K) {
-            p.ids[(size_t)t * K + lane] = (uint32_t)rl.id[lane];
-            p.gates[(size_t)t * K + lane] = g;
-        }
+        p.ids[(size_t)t * K + lane] = (uint32_t)rl.id[lane];
+        p.gates[(size_t)t * K + lane] = g;
     }
-    __syncthreads();
     for (int r = threadIdx.x; r < TR; r += blockDim.x) {
         const int row = row0 + r;
         if (row < rows)
@@ -178,11 +212,62 @@ __global__ __launch_bounds__(256) void moe_down_decode_kernel(DecodeParams p) {
                 w[u] = F::load_w(p.down + (size_t)s_ids[sl] * p.dn_plane, U, unit, j);
             }
             if (!quantized) {
-                // 3. quantize from registers while the weights are in flight
+                // 3. quantize from registers while the weights are in flight,
+                // phase by phase over the items so their chains interleave
+                float a[DN_QB], dd[DN_QB], inv[DN_QB];
+                int sum[DN_QB];
+                uint32_t packed[DN_QB];
 #pragma unroll
                 for (int i = 0; i < DN_QB; i++) {
-                    const int it = wave + WAVES * i;
-                    quantize(it < items ? it : items - 1, av[i]);
+                    float m = 0.0f;
+                    if (__builtin_isfinite(av[i].x)) m = fmaxf(m, fabsf(av[i].x));
+                    if (__builtin_isfinite(av[i].y)) m = fmaxf(m, fabsf(av[i].y));
+                    if (__builtin_isfinite(av[i].z)) m = fmaxf(m, fabsf(av[i].z));
+                    if (__builtin_isfinite(av[i].w)) m = fmaxf(m, fabsf(av[i].w));
+                    a[i] = m;
+                }
+#pragma unroll
+                for (int i = 0; i < DN_QB; i++)
+                    a[i] = k256 ? wave_max(a[i]) : group8_max(a[i]);
+#pragma unroll
+                for (int i = 0; i < DN_QB; i++)
+                    dd[i] = a[i] / 127.0f;
+#pragma unroll
+                for (int i = 0; i < DN_QB; i++)
+                    inv[i] = (dd[i] != 0.0f && __builtin_isfinite(dd[i])) ? 1.0f / dd[i] : 0.0f;
+#pragma unroll
+                for (int i = 0; i < DN_QB; i++) {
+                    const int q0 = to_i8_sat(av[i].x * inv[i]), q1 = to_i8_sat(av[i].y * inv[i]);
+                    const int q2 = to_i8_sat(av[i].z * inv[i]), q3 = to_i8_sat(av[i].w * inv[i]);
+                    packed[i] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                                ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+                    sum[i] = q0 + q1 + q2 + q3;
+                }
+#pragma unroll
+                for (int i = 0; i < DN_QB; i++)
+                    sum[i] = k256 ? group_sum<4>(sum[i]) : group_sum<8>(sum[i]);
+#pragma unroll
+                for (int i = 0; i < DN_QB; i++) {
+                    // items past the end repeat the last one (same values, same place)
+                    const int it = min(wave + WAVES * i, items - 1);
+                    const int v_ = it / per, item = it % per;
+                    const float dv = __builtin_isfinite(dd[i]) ? dd[i] : 0.0f;
+                    if constexpr (k256) {
+                        *(uint32_t *)(qq + (size_t)v_ * cols + item * 256 + 4 * lane) = packed[i];
+                        if ((lane & 3) == 0)
+                            qs[(size_t)v_ * (cols / 16) + item * 16 + lane / 4] = sum[i];
+                        if (lane == 0)
+                            qd[(size_t)v_ * (cols / 256) + item] = dv;
+                    } else {
+                        const int blk = item * 8 + lane / 8;
+                        if (blk < cols / 32) {
+                            *(uint32_t *)(qq + (size_t)v_ * cols + blk * 32 + 4 * (lane & 7)) = packed[i];
+                            if ((lane & 7) == 0) {
+                                qs[(size_t)v_ * (cols / 32) + blk] = sum[i];
+                                qd[(size_t)v_ * (cols / 32) + blk] = dv;
+                            }
+                        }
+                    }
                 }
                 lds_barrier();
                 quantized = true;

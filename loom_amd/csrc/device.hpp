@@ -180,18 +180,36 @@ __device__ inline bool last_arrival(int *counter, int target) {
 
 // ---- routing ------------------------------------------------------------------------
 
-// LDS scratch of the routing helpers: per-wave copies of the scores and
-// selection keys (so no wave waits for another), and the slot table.
+// ---- routing (src/gguf/moe.zig:106-158) ----------------------------------------------
+//
+// The reference picks k experts by k rounds of argmax with strict '>' over
+// the unused experts' selection values (scores + selection bias): lowest
+// index wins ties, and a round that finds nothing above -inf picks expert 0.
+// That is the order (value descending, index ascending) over values above
+// -inf, so an expert's slot is its rank in that order.  With
+// key = (ordered value << 32) | ~index every key is distinct and
+// rank = #{keys greater}.
+//
+// For softmax gating without a selection bias the ranks are taken on the
+// exp values e = exp(l - max) before the sequential sum: scores p = e * inv
+// are a non-decreasing function of e, so the order can only differ where
+// two different e round to the same p.  route_finish checks exactly that
+// (adjacent ranks 0..k with equal p) once the sum is known, off the critical
+// path, and asks for route_exact when it happens; ids stay bit-exact.
+
 template <int NW>
 struct __align__(16) RouteLds {
-    float sc[NW][MAX_E];
-    unsigned long long key[NW][MAX_E];
-    int id[MAX_K];
-    float gate[MAX_K];
+    unsigned long long key[NW][MAX_E]; // per-wave copy of the selection keys
+    int prank[NW][MAX_E];              // partial ranks (NW > 1)
+    float sc[MAX_E];                   // softmax exp values, for the sequential sum
+    int id[MAX_K + 1];                 // slot -> expert (slot k: the next one)
+    float val[MAX_K + 1];              // slot -> unbiased score (softmax: exp value)
+    int n_valid;
+    int redo; // set by the caller when route_finish asks for route_exact_wave
 };
 
 // Sequential f32 sum of lane s's value over s < K, uniform in every lane.
-__device__ inline float slot_sum(float v, int K) {
+__device__ __forceinline__ float slot_sum(float v, int K) {
     float sum = 0.0f;
     for (int s = 0; s < K; s++)
         sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), s));
@@ -199,14 +217,18 @@ __device__ inline float slot_sum(float v, int K) {
 }
 
 // Order-preserving map of an f32 onto u32 (larger value -> larger key).
-__device__ inline uint32_t ordered_u32(float f) {
+__device__ __forceinline__ uint32_t ordered_u32(float f) {
     const uint32_t b = __float_as_uint(f);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+__device__ __forceinline__ unsigned long long route_key(float c, int e, bool valid) {
+    return valid ? ((unsigned long long)ordered_u32(c) << 32) | (0xFFFFFFFFu - (uint32_t)e) : 0ull;
+}
+
 // Sequential sum of v[0..E) in LDS (the reference's softmax sum order); the
 // reads of each 32-value batch are issued before its adds.
-__device__ inline float lds_seq_sum(const float *v, int E) {
+__device__ __forceinline__ float lds_seq_sum(const float *v, int E) {
     float sum = 0.0f;
     for (int e0 = 0; e0 < E; e0 += 32) {
         float4 r[8];
@@ -225,29 +247,91 @@ __device__ inline float lds_seq_sum(const float *v, int E) {
     return sum;
 }
 
-// Routing of one token (src/gguf/moe.zig:106-158) by NW cooperating waves
-// (threads [0, 64*NW) of the work group): scores (softmax / sigmoid / raw for
-// softmax_topk), then the k rounds of argmax with strict '>' over the unused
-// experts (lowest index wins ties; a round that finds nothing above -inf
-// picks expert 0), with gates from the unbiased scores.
-//
-// The k rounds pick experts in the order (selection value descending, index
-// ascending) among values above -inf, so an expert's slot is its rank in
-// that order.  With key = (ordered value << 32) | ~index every key is
-// distinct and rank = #{keys greater}; each lane ranks its experts against
-// all keys in LDS.  Every wave computes the scores and keys on its own (no
-// cross-wave wait); the experts to rank are split over the waves.  On return
-// (after a barrier) L.id[s] / L.gate[s] hold slot s's expert and unbiased
-// score for s < K; route_gates then applies the gate post-processing.
-// COHERENT reads the logits through ld_dev (written by other work groups of
-// the same launch).
-template <int NW, bool COHERENT>
-__device__ inline void route_select(const float *lg, const float *sel_bias, int E, int K,
-                                    int gating, RouteLds<NW> &L) {
+// #{keys in [j0, j1) of kl greater than ki}
+__device__ __forceinline__ int count_greater(const unsigned long long *kl, int j0, int j1,
+                                    unsigned long long ki) {
+    int rank = 0;
+    for (int j = j0; j < j1; j += 16) {
+        ulonglong2 kk[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            kk[q] = *(const ulonglong2 *)(kl + j + 2 * q);
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            rank += (kk[q].x > ki) + (kk[q].y > ki);
+    }
+    return rank;
+}
+
+// Rank the experts' keys (key[i] for expert lane + 64i) and write the slot
+// table.  SINGLE: one wave does it all (index 0 of L's per-wave arrays);
+// otherwise NW waves split the comparisons, each holding every expert's key.
+// Ends with the participating waves seeing L.id / L.val / L.n_valid.
+template <int NW, bool SINGLE>
+__device__ __forceinline__ void route_slots(const unsigned long long (&key)[MAX_E / 64],
+                                   const float (&val)[MAX_E / 64], int valid_n, int E, int K,
+                                   RouteLds<NW> &L) {
     constexpr int NI = MAX_E / 64;
-    // w indexes this wave's copies inside L: with NW == 1 the caller hands
-    // each wave its own RouteLds<1>, so the index is 0
-    const int lane = threadIdx.x & 63, w = NW == 1 ? 0 : threadIdx.x >> 6;
+    constexpr bool ONE = SINGLE || NW == 1;
+    const int lane = threadIdx.x & 63, w = ONE ? 0 : threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        L.key[w][lane + 64 * i] = key[i];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const int Epad = (E + 15) & ~15; // keys past E are 0 and never count
+    const int ch = ONE ? Epad : (((Epad / NW) + 15) & ~15);
+    const int j0 = w * ch, j1 = min(Epad, j0 + ch);
+    int rank[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        rank[i] = 64 * i < E ? count_greater(L.key[w], j0, j1, key[i]) : 0;
+    if constexpr (!ONE) {
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            L.prank[w][lane + 64 * i] = rank[i];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            int r = 0;
+#pragma unroll
+            for (int v = 0; v < NW; v++)
+                r += L.prank[v][lane + 64 * i];
+            rank[i] = r;
+        }
+    }
+    if (w == 0) {
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            if (key[i] != 0ull && rank[i] <= K) {
+                L.id[rank[i]] = lane + 64 * i;
+                L.val[rank[i]] = val[i];
+            }
+        // rounds that found nothing above -inf pick expert 0 (its unbiased score)
+        const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(val[0]), 0));
+        if (lane >= valid_n && lane < K) {
+            L.id[lane] = 0;
+            L.val[lane] = v0;
+        }
+        if (lane == 0)
+            L.n_valid = valid_n;
+    }
+    if constexpr (ONE) {
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    } else {
+        __syncthreads();
+    }
+}
+
+// Exact routing by one wave, in the reference's arithmetic: scores
+// (sigmoid / softmax with the sequential sum / raw logits), selection values
+// scores + bias, ranks.  Fills the slot table with the unbiased scores.
+template <int NW, bool COHERENT>
+__device__ __forceinline__ void route_exact_wave(const float *lg, const float *sel_bias, int E, int K,
+                                        int gating, RouteLds<NW> &L) {
+    constexpr int NI = MAX_E / 64;
+    const int lane = threadIdx.x & 63;
     float sv[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
@@ -258,7 +342,7 @@ __device__ inline void route_select(const float *lg, const float *sel_bias, int 
 #pragma unroll
         for (int i = 0; i < NI; i++)
             sv[i] = 1.0f / (1.0f + expf(-sv[i]));
-    } else if (gating != 3) { // softmax (tensor.zig:18-28): max, exp, sequential sum, * (1/sum)
+    } else if (gating != 3) { // softmax (tensor.zig:18-28)
         float m = -INFINITY;
 #pragma unroll
         for (int i = 0; i < NI; i++)
@@ -267,11 +351,11 @@ __device__ inline void route_select(const float *lg, const float *sel_bias, int 
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             sv[i] = expf(sv[i] - m);
-            L.sc[w][lane + 64 * i] = sv[i];
+            L.sc[lane + 64 * i] = sv[i];
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        const float inv = 1.0f / lds_seq_sum(L.sc[w], E); // same value in every lane
+        const float inv = 1.0f / lds_seq_sum(L.sc, E);
 #pragma unroll
         for (int i = 0; i < NI; i++)
             sv[i] = sv[i] * inv;
@@ -283,57 +367,103 @@ __device__ inline void route_select(const float *lg, const float *sel_bias, int 
         const int e = lane + 64 * i;
         const float c = e < E ? (sel_bias ? sv[i] + sel_bias[e] : sv[i]) : -INFINITY;
         const bool valid = c > -INFINITY; // NaN and -inf never win a strict '>'
-        key[i] = valid ? ((unsigned long long)ordered_u32(c) << 32) | (0xFFFFFFFFu - (uint32_t)e)
-                       : 0ull;
+        key[i] = route_key(c, e, valid);
         valid_n += __popcll(__ballot(valid));
-        L.key[w][e] = key[i];
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    // wave w ranks experts lane + 64*i for i = w, w + NW, ...
-#pragma unroll
-    for (int i = 0; i < NI; i++) {
-        if (i % NW != w || 64 * i >= E)
-            continue;
-        int rank = 0;
-        const unsigned long long ki = key[i];
-        for (int j0 = 0; j0 < E; j0 += 16) {
-            ulonglong2 kk[8];
-#pragma unroll
-            for (int q = 0; q < 8; q++)
-                kk[q] = *(const ulonglong2 *)(&L.key[w][j0 + 2 * q]);
-#pragma unroll
-            for (int q = 0; q < 8; q++)
-                rank += (kk[q].x > ki) + (kk[q].y > ki);
-        }
-        const int e = lane + 64 * i;
-        if (ki != 0ull && rank < K) {
-            L.id[rank] = e;
-            L.gate[rank] = sv[i];
-        }
-    }
-    // rounds that found nothing above -inf pick expert 0 (its unbiased score)
-    const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[0]), 0));
-    if (w == 0 && lane >= valid_n && lane < K) {
-        L.id[lane] = 0;
-        L.gate[lane] = s0;
-    }
-    if constexpr (NW == 1) {
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    } else {
-        __syncthreads();
-    }
+    route_slots<NW, true>(key, sv, valid_n, E, K, L);
 }
 
-// Gate post-processing in slot order (moe.zig:143-157): softmax over the k
-// for softmax_topk, renorm with the f16-min clamp, scale.  Called by one
-// wave after route_select; lane s < K returns slot s's final gate.
-template <int NW>
-__device__ inline float route_gates(const RouteLds<NW> &L, int K, int gating, int weights_norm,
-                                    float weights_scale) {
+// Selection of one token by NW cooperating waves (threads [0, 64*NW)); the
+// waves hold identical copies of every expert's values.  Returns with the
+// slot table filled.  For softmax without a selection bias the table holds
+// exp values and ranks on them (route_finish settles exactness); otherwise
+// it is exact already.
+__device__ __forceinline__ bool route_is_exact(int gating, const float *sel_bias) {
+    return gating == 2 || gating == 3 || sel_bias != nullptr;
+}
+
+template <int NW, bool COHERENT>
+__device__ __forceinline__ void route_rank(const float *lg, const float *sel_bias, int E, int K, int gating,
+                                  RouteLds<NW> &L) {
+    constexpr int NI = MAX_E / 64;
     const int lane = threadIdx.x & 63;
-    float g = lane < K ? L.gate[lane] : 0.0f;
+    if (gating != 2 && gating != 3 && sel_bias) { // softmax + selection bias: exact only
+        if (NW == 1 || (int)threadIdx.x < 64)
+            route_exact_wave<NW, COHERENT>(lg, sel_bias, E, K, gating, L);
+        if constexpr (NW > 1)
+            __syncthreads();
+        return;
+    }
+    float lv[NI], val[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int e = lane + 64 * i;
+        lv[i] = e < E ? (COHERENT ? ld_dev(lg + e) : lg[e]) : -INFINITY;
+    }
+    unsigned long long key[NI];
+    int valid_n = 0;
+    if (gating == 2 || gating == 3) { // sigmoid / softmax_topk: exact selection values
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int e = lane + 64 * i;
+            val[i] = gating == 2 ? 1.0f / (1.0f + expf(-lv[i])) : lv[i];
+            const float c = e < E ? (sel_bias ? val[i] + sel_bias[e] : val[i]) : -INFINITY;
+            const bool valid = c > -INFINITY;
+            key[i] = route_key(c, e, valid);
+            valid_n += __popcll(__ballot(valid));
+        }
+    } else { // softmax: rank on e = exp(l - max)
+        float m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            m = fmaxf(m, lv[i]);
+        m = wave_max(m);
+        bool any_nan = false;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            val[i] = expf(lv[i] - m);
+            if (lane + 64 * i < E)
+                any_nan |= __builtin_isnan(val[i]);
+            if (NW == 1 || (int)threadIdx.x < 64) // the copy route_finish sums
+                L.sc[lane + 64 * i] = val[i];
+        }
+        // a NaN among the exp values makes the sum, and so every score, NaN:
+        // nothing is selectable
+        const bool none = __ballot(any_nan) != 0;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int e = lane + 64 * i;
+            const bool valid = !none && e < E;
+            key[i] = route_key(val[i], e, valid);
+            valid_n += __popcll(__ballot(valid));
+        }
+    }
+    route_slots<NW, false>(key, val, valid_n, E, K, L);
+}
+
+// Gates of the slots (moe.zig:143-157) by one wave after route_rank: softmax
+// scores p = e / sum (redo = true, uniformly, when two adjacent ranks 0..k
+// have equal p from different e: the caller then reroutes with
+// route_exact_wave and calls this again with exact = true), softmax over the
+// k for softmax_topk, renorm with the f16-min clamp, scale.  Lane s < K
+// returns slot s's gate.  exact: the slot table holds final scores.
+template <int NW>
+__device__ __forceinline__ float route_finish(RouteLds<NW> &L, int E, int K, int gating, bool exact,
+                                     int weights_norm, float weights_scale, bool &redo) {
+    const int lane = threadIdx.x & 63;
+    float g = lane < K ? L.val[lane] : 0.0f;
+    redo = false;
+    if (!exact && gating != 2 && gating != 3) {
+        const float inv = 1.0f / lds_seq_sum(L.sc, E);
+        const float pl = lane <= K ? L.val[lane] * inv : 0.0f;
+        // adjacent ranks s, s+1 (both selectable) with equal p from different e
+        const float pn = __shfl_down(pl, 1, 64);
+        const float en = __shfl_down(lane <= K ? L.val[lane] : 0.0f, 1, 64);
+        const float el = lane <= K ? L.val[lane] : 0.0f;
+        const bool tie = lane < K && lane + 1 < L.n_valid && pl == pn && el != en;
+        redo = __ballot(tie) != 0;
+        g = lane < K ? pl : 0.0f;
+    }
     if (gating == 3) {
         float m = -INFINITY;
         for (int s = 0; s < K; s++)

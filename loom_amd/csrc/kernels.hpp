@@ -99,6 +99,8 @@ struct GateParams {
 };
 bool gate_supported(int n, int n_expert, int k);
 void launch_gate(GateParams p, hipStream_t st);
+// Decode path: router GEMV (router != null) + quantization of x, no routing.
+void launch_router_small(GateParams p, hipStream_t st);
 
 // Decode path (few tokens): gate/up with an in-kernel routing prologue per
 // (token, slot) pair, then down + gated combine per token.  No bucketing and

@@ -19,7 +19,7 @@ namespace lh {
 constexpr int GT_THREADS = 256;
 constexpr int GT_ROWS = GT_THREADS / 32; // router rows per workgroup (a half-wave each)
 constexpr int GT_TOK = 4;                // tokens per chunk = tokens per half-wave pass
-constexpr int GT_UNROLL = 64; // router elements in flight per lane
+constexpr int GT_UNROLL = 32; // router elements in flight per lane
 constexpr int GT_COLS = 32 * GT_UNROLL; // columns per staged chunk
 
 // Router GEMV for up to GT_TOK tokens in dotF32 order (src/gguf/ggml.zig:
@@ -128,11 +128,22 @@ __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int 
 __device__ void route_token_wave(const GateParams &p, int t, RouteLds<1> &L) {
     const int lane = threadIdx.x & 63;
     const int E = p.n_expert, K = p.k;
-    if (p.logits_in)
-        route_select<1, false>(p.logits_in + (size_t)t * E, p.sel_bias, E, K, p.gating, L);
+    const bool coh = p.logits_in == nullptr; // logits from this launch's other work groups
+    const float *lg = coh ? p.logits + (size_t)t * E : p.logits_in + (size_t)t * E;
+    if (coh)
+        route_rank<1, true>(lg, p.sel_bias, E, K, p.gating, L);
     else
-        route_select<1, true>(p.logits + (size_t)t * E, p.sel_bias, E, K, p.gating, L);
-    const float g = route_gates<1>(L, K, p.gating, p.weights_norm, p.weights_scale);
+        route_rank<1, false>(lg, p.sel_bias, E, K, p.gating, L);
+    bool redo;
+    float g = route_finish<1>(L, E, K, p.gating, route_is_exact(p.gating, p.sel_bias),
+                              p.weights_norm, p.weights_scale, redo);
+    if (redo) {
+        if (coh)
+            route_exact_wave<1, true>(lg, p.sel_bias, E, K, p.gating, L);
+        else
+            route_exact_wave<1, false>(lg, p.sel_bias, E, K, p.gating, L);
+        g = route_finish<1>(L, E, K, p.gating, true, p.weights_norm, p.weights_scale, redo);
+    }
     if (lane < K) {
         st_dev(p.ids + (size_t)t * K + lane, (uint32_t)L.id[lane]); // read by the bucketing work group
         p.gates[(size_t)t * K + lane] = g;
@@ -299,6 +310,111 @@ void launch_combine(const float *y, const float *gates, const uint32_t *ids, con
                     int n, int k, int dim, int mode, float *out, hipStream_t st) {
     hipLaunchKernelGGL(combine_kernel, dim3((dim + 255) / 256, n), dim3(256), 0, st, y, gates, ids,
                        pair_of, k, dim, mode, out);
+    note_launch();
+}
+
+// ---- decode-path router: GEMV + input quantization, one wave per work group --------
+//
+// Work groups [0, ceil(E/2)) hold two router rows each (a half-wave per
+// row); the rest quantize one item of the input each.  A half-wave loads its
+// row and the token's x in 16-byte pieces (lane P holds columns 128c + 4P ..
+// +3), multiplies in that layout, and passes the products through LDS so
+// that lane L then adds columns 32i + L in order -- the dotF32 accumulation
+// order (src/gguf/ggml.zig:198-217) -- with a quarter of the load
+// instructions of a per-column layout.
+constexpr int RS_COLS = 2048; // columns per pass (16 float4 per lane)
+
+__global__ __launch_bounds__(64) void router_small_kernel(GateParams p) {
+    __shared__ __align__(16) float prod[2][RS_COLS];
+    __shared__ float part[2][32];
+    const int lane = threadIdx.x, hw = lane >> 5, P = lane & 31;
+    const int gemv_wgs = p.gemv_wgs; // 0 when the caller supplies the logits
+    if ((int)blockIdx.x >= gemv_wgs) {
+        const int per_vec = quant_items(p.qt, p.dim);
+        const int item = blockIdx.x - gemv_wgs;
+        if (item < per_vec * p.n) {
+            const int v = item / per_vec, it = item % per_vec;
+            quant_item_wave(p.qt, p.x + (size_t)v * p.dim, p.dim, v, it, p.qx);
+        }
+        return;
+    }
+    const int dim = p.dim;
+    const int e = blockIdx.x * 2 + hw;
+    const bool valid = e < p.n_expert;
+    const float *row = p.router + (size_t)(valid ? e : 0) * dim;
+    const int main_end = dim / 32 * 32;
+    for (int t = 0; t < p.n; t++) {
+        const float *xt = p.x + (size_t)t * dim;
+        float acc = 0.0f;
+        for (int c0 = 0; c0 < main_end; c0 += RS_COLS) {
+            const int ccols = min(RS_COLS, main_end - c0);
+            float4 wv[RS_COLS / 128], xv[RS_COLS / 128];
+#pragma unroll
+            for (int c = 0; c < RS_COLS / 128; c++) {
+                const bool in = 128 * c + 4 * P < ccols;
+                wv[c] = in ? *(const float4 *)(row + c0 + 128 * c + 4 * P) : make_float4(0.f, 0.f, 0.f, 0.f);
+                xv[c] = in ? *(const float4 *)(xt + c0 + 128 * c + 4 * P) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); // previous pass's reads are done
+#pragma unroll
+            for (int c = 0; c < RS_COLS / 128; c++) {
+                float4 pr;
+                pr.x = wv[c].x * xv[c].x;
+                pr.y = wv[c].y * xv[c].y;
+                pr.z = wv[c].z * xv[c].z;
+                pr.w = wv[c].w * xv[c].w;
+                if (128 * c + 4 * P < ccols)
+                    *(float4 *)(&prod[hw][128 * c + 4 * P]) = pr;
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            const int n32 = ccols / 32;
+            for (int i0 = 0; i0 < n32; i0 += 16) {
+                float pv[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    pv[u] = i0 + u < n32 ? prod[hw][32 * (i0 + u) + P] : 0.0f;
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    if (i0 + u < n32)
+                        acc = acc + pv[u];
+            }
+        }
+        // leftover whole 8-chunks go to accumulator 0 (lanes 0..7)
+        for (int i = main_end; i + 8 <= dim; i += 8)
+            if (P < 8) {
+                const float pr = row[i + P] * xt[i + P];
+                acc = acc + pr;
+            }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        part[hw][P] = acc;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        if (P == 0 && valid) {
+            float s = -0.0f;
+            for (int l = 0; l < 8; l++) {
+                const float v = ((part[hw][l] + part[hw][8 + l]) + part[hw][16 + l]) + part[hw][24 + l];
+                s = s + v;
+            }
+            for (int j = dim / 8 * 8; j < dim; j++) {
+                const float pr = row[j] * xt[j];
+                s = s + pr;
+            }
+            if (p.router_bias)
+                s = s + p.router_bias[e];
+            p.logits[(size_t)t * p.n_expert + e] = s;
+        }
+    }
+}
+
+void launch_router_small(GateParams p, hipStream_t st) {
+    p.gemv_wgs = p.router ? (p.n_expert + 1) / 2 : 0; // no router: logits come from the caller
+    p.quant_wgs = p.qt ? quant_items(p.qt, p.dim) * p.n : 0;
+    if (p.gemv_wgs + p.quant_wgs == 0)
+        return;
+    hipLaunchKernelGGL(router_small_kernel, dim3(p.gemv_wgs + p.quant_wgs), dim3(64), 0, st, p);
     note_launch();
 }
 

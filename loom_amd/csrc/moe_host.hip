@@ -163,7 +163,7 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
             return fail(LOOMHIP_DECLINED, "moe: ffn %zu x top-%zu exceeds the decode LDS budget",
                         m.ffn, m.k);
         gp.chain = 0;
-        launch_gate(gp, st);
+        launch_router_small(gp, st);
         if (!launch_moe_decode(m.gate_t, m.down_t, dp, (int)n, st, LOOMHIP_KT_GATE_UP, LOOMHIP_KT_DOWN))
             return fail(LOOMHIP_ERR_ARG, "moe: decode kernels declined the shape");
         return LOOMHIP_OK;
