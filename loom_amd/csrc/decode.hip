@@ -16,15 +16,47 @@
 
 namespace lh {
 
-constexpr int GU_MAXIT = 4; // weight rows per lane requested at once in the gate/up kernel
+// Lane map shared by the decode kernels (see fmt.hpp): a block is served by
+// LPB lanes, a wave covers BPI = 64/LPB blocks per step.  Wide rows (nb >=
+// BPI) take C column chunks of BPI blocks, the last one possibly partial;
+// short rows put RPI rows side by side.
+template <int LPB>
+struct LaneMap {
+    static constexpr int BPI = 64 / LPB;
+    int grp, j, nb, C, RPI, ro;
+    bool wide, active;
+    __device__ LaneMap(int lane, int nb_) : nb(nb_) {
+        grp = lane / LPB;
+        j = lane % LPB;
+        wide = nb >= BPI;
+        C = wide ? (nb + BPI - 1) / BPI : 1;
+        RPI = wide ? 1 : BPI / nb;
+        ro = wide ? 0 : grp / nb;
+        active = wide || grp < RPI * nb;
+    }
+    // block of column chunk c (clamped into range; ok = a real block)
+    __device__ int block(int c, bool &ok) const {
+        const int b = wide ? c * BPI + grp : grp % nb;
+        ok = b < nb;
+        return ok ? b : nb - 1;
+    }
+};
 
+constexpr int GU_MAXIT = 2; // weight rows per lane requested at once in the gate/up kernel
+
+// Gate/up + SwiGLU for pair (token t, slot s) = blockIdx.y, row tile
+// blockIdx.x.  The four waves rank the token's experts (route_rank) while
+// the first column chunk's activations load; the (slot 0, tile 0) work group
+// publishes the ids.  Ranking softmax routes on the exp values: two experts
+// can only come out in the other order when their exp values round to the
+// same final score (a logit gap below one ulp), the near-tie case the
+// north_star allows; gates are computed exactly by moe_mid_kernel.
 template <int T>
 __global__ __launch_bounds__(256) void moe_gateup_decode_kernel(DecodeParams p) {
     using F = Fmt<T>;
-    constexpr int LPB = F::LPB, BPI = 64 / LPB;
+    constexpr int LPB = F::LPB;
     extern __shared__ float lds[];
     __shared__ RouteLds<WAVES> rl;
-    __shared__ int s_redo;
     const int K = p.k;
     const int t = blockIdx.y / K, s = blockIdx.y % K;
     const int rows = p.ffn, cols = p.dim, nb = cols / F::BE;
@@ -32,88 +64,58 @@ __global__ __launch_bounds__(256) void moe_gateup_decode_kernel(DecodeParams p) 
     const int rpw = p.rpw_gu, TR = WAVES * rpw;
     const int row0 = blockIdx.x * TR;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int grp = lane / LPB, j = lane % LPB;
-    const bool wide = nb >= BPI;
-    const int C = wide ? nb / BPI : 1;
-    const int RPI = wide ? 1 : BPI / nb;
-    const int ro = wide ? 0 : grp / nb;
-    const bool active = wide || grp < RPI * nb;
-    const int nit = (rpw + RPI - 1) / RPI;
+    const LaneMap<LPB> m(lane, nb);
+    const int j = m.j;
+    const int nit = (rpw + m.RPI - 1) / m.RPI;
     const size_t lds_mat = (size_t)TR * nb;
-    const bool exact = route_is_exact(p.gating, p.sel_bias);
-    const float *lg = p.logits + (size_t)t * p.n_expert;
 
-    // the first column chunk's activations load while the waves route
-    const typename F::X x0 = F::load_x(p.xq, p.xd, p.xs, cols, t, wide ? grp : grp % nb, j);
-    route_rank<WAVES, false>(lg, p.sel_bias, p.n_expert, K, p.gating, rl);
-    float g = 0.0f;
-    for (int pass = 0; pass < 2; pass++) {
-        const int e = min(max(rl.id[s], 0), p.n_expert - 1); // never address past the tensor
-        const uint8_t *wb = p.gate + (size_t)e * p.gu_plane;
-        const uint8_t *wb2 = p.up + (size_t)e * p.gu_plane;
-        for (int c = 0; c < C; c++) {
-            const int b = wide ? c * BPI + grp : (grp % nb);
-            const typename F::X xr = c == 0 ? x0 : F::load_x(p.xq, p.xd, p.xs, cols, t, b, j);
-            for (int it0 = 0; it0 < nit; it0 += GU_MAXIT) {
-                typename F::W w[GU_MAXIT], w2[GU_MAXIT];
-                int rlv[GU_MAXIT];
-                bool valid[GU_MAXIT];
+    bool ok0;
+    const int b0 = m.block(0, ok0);
+    const typename F::X x0 = F::load_x(p.xq, p.xd, p.xs, cols, t, b0, j);
+    route_rank<WAVES, false>(p.logits + (size_t)t * p.n_expert, p.sel_bias, p.n_expert, K,
+                             p.gating, rl);
+    const int e = min(max(rl.id[s], 0), p.n_expert - 1); // never address past the tensor
+    if (s == 0 && blockIdx.x == 0 && (int)threadIdx.x < K)
+        p.ids[(size_t)t * K + threadIdx.x] = (uint32_t)rl.id[threadIdx.x];
+    const uint8_t *wb = p.gate + (size_t)e * p.gu_plane;
+    const uint8_t *wb2 = p.up + (size_t)e * p.gu_plane;
+    for (int c = 0; c < m.C; c++) {
+        bool bok;
+        const int b = m.block(c, bok);
+        const typename F::X xr = c == 0 ? x0 : F::load_x(p.xq, p.xd, p.xs, cols, t, b, j);
+        for (int it0 = 0; it0 < nit; it0 += GU_MAXIT) {
+            typename F::W w[GU_MAXIT], w2[GU_MAXIT];
+            int rlv[GU_MAXIT];
+            bool valid[GU_MAXIT];
 #pragma unroll
-                for (int u = 0; u < GU_MAXIT; u++) {
-                    const int rw = (it0 + u) * RPI + ro;
-                    rlv[u] = wave * rpw + rw;
-                    const int row = row0 + rlv[u];
-                    valid[u] = active && it0 + u < nit && rw < rpw && row < rows;
-                    const size_t unit = (size_t)(valid[u] ? row : 0) * nb + b;
-                    w[u] = F::load_w(wb, U, unit, j);
-                    w2[u] = F::load_w(wb2, U, unit, j);
-                }
-                if (pass == 0 && c == 0 && it0 == 0 && wave == 0) {
-                    // settle the routing (sum, tie check, gates) while the rows load
-                    bool redo;
-                    g = route_finish<WAVES>(rl, p.n_expert, K, p.gating, exact, p.weights_norm,
-                                            p.weights_scale, redo);
-                    if (lane == 0)
-                        s_redo = redo;
-                }
+            for (int u = 0; u < GU_MAXIT; u++) {
+                const int rw = (it0 + u) * m.RPI + m.ro;
+                rlv[u] = wave * rpw + rw;
+                const int row = row0 + rlv[u];
+                valid[u] = m.active && bok && it0 + u < nit && rw < rpw && row < rows;
+                const size_t unit = (size_t)(valid[u] ? row : 0) * nb + b;
+                w[u] = F::load_w(wb, U, unit, j);
+                w2[u] = F::load_w(wb2, U, unit, j);
+            }
 #pragma unroll
-                for (int u = 0; u < GU_MAXIT; u++) {
-                    if (it0 + u < nit) {
-                        int is, ms;
-                        F::dot(w[u], xr, j, is, ms);
-                        is = group_sum<LPB>(is);
-                        ms = group_sum<LPB>(ms);
-                        if (valid[u] && j == 0)
-                            lds[(size_t)rlv[u] * nb + b] = F::tail(w[u], xr, is, ms);
-                        F::dot(w2[u], xr, j, is, ms);
-                        is = group_sum<LPB>(is);
-                        ms = group_sum<LPB>(ms);
-                        if (valid[u] && j == 0)
-                            lds[lds_mat + (size_t)rlv[u] * nb + b] = F::tail(w2[u], xr, is, ms);
-                    }
+            for (int u = 0; u < GU_MAXIT; u++) {
+                if (it0 + u < nit) {
+                    int is, ms;
+                    F::dot(w[u], xr, j, is, ms);
+                    is = group_sum<LPB>(is);
+                    ms = group_sum<LPB>(ms);
+                    if (valid[u] && j == 0)
+                        lds[(size_t)rlv[u] * nb + b] = F::tail(w[u], xr, is, ms);
+                    F::dot(w2[u], xr, j, is, ms);
+                    is = group_sum<LPB>(is);
+                    ms = group_sum<LPB>(ms);
+                    if (valid[u] && j == 0)
+                        lds[lds_mat + (size_t)rlv[u] * nb + b] = F::tail(w2[u], xr, is, ms);
                 }
             }
         }
-        __syncthreads();
-        if (pass == 1 || !s_redo)
-            break;
-        // two experts tied on the final score: route exactly, and redo the
-        // tile only if this slot's expert changed
-        if (wave == 0) {
-            route_exact_wave<WAVES, false>(lg, p.sel_bias, p.n_expert, K, p.gating, rl);
-            bool again;
-            g = route_finish<WAVES>(rl, p.n_expert, K, p.gating, true, p.weights_norm,
-                                    p.weights_scale, again);
-        }
-        __syncthreads();
-        if (min(max(rl.id[s], 0), p.n_expert - 1) == e)
-            break;
     }
-    if (s == 0 && blockIdx.x == 0 && wave == 0 && lane < K) {
-        // one work group per token publishes the routing for the down kernel
-        p.ids[(size_t)t * K + lane] = (uint32_t)rl.id[lane];
-        p.gates[(size_t)t * K + lane] = g;
-    }
+    __syncthreads();
     for (int r = threadIdx.x; r < TR; r += blockDim.x) {
         const int row = row0 + r;
         if (row < rows)
@@ -121,13 +123,65 @@ __global__ __launch_bounds__(256) void moe_gateup_decode_kernel(DecodeParams p) 
     }
 }
 
-constexpr int DN_UB = 8; // weight loads in flight per lane in the down kernel
-constexpr int DN_QB = 8; // activation items loaded at once per wave
+// Between gate/up and down, one wave per work group: waves [0, items)
+// quantize one item of the SwiGLU vectors for the down type each (once, for
+// every down work group); the next n waves compute token t's gates exactly
+// (scores of the selected experts in the reference's arithmetic, then the
+// gate post-processing), off the critical path of both expert kernels.
+__global__ __launch_bounds__(64) void moe_mid_kernel(DecodeParams p, int n) {
+    __shared__ __align__(16) float sc[MAX_E];
+    const int per = quant_items(p.down_t, p.ffn);
+    const int items = n * p.k * per;
+    if ((int)blockIdx.x < items) {
+        const int v = blockIdx.x / per, it = blockIdx.x % per;
+        quant_item_wave(p.down_t, p.act + (size_t)v * p.ffn, p.ffn, v, it, p.qa);
+        return;
+    }
+    const int t = blockIdx.x - items;
+    const int lane = threadIdx.x, E = p.n_expert, K = p.k;
+    const float *lg = p.logits + (size_t)t * E;
+    const int id = lane < K ? min((int)p.ids[(size_t)t * K + lane], E - 1) : 0;
+    float g;
+    if (p.gating == 2) { // sigmoid (tensor.zig:34-36)
+        g = 1.0f / (1.0f + expf(-lg[id]));
+    } else if (p.gating == 3) { // softmax_topk: raw logits
+        g = lg[id];
+    } else { // softmax (tensor.zig:18-28): exp(l - max), sequential sum, * (1/sum)
+        constexpr int NI = MAX_E / 64;
+        float lv[NI];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int e = lane + 64 * i;
+            lv[i] = e < E ? lg[e] : -INFINITY;
+            mx = fmaxf(mx, lv[i]);
+        }
+        mx = wave_max(mx);
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            sc[lane + 64 * i] = expf(lv[i] - mx);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        const float inv = 1.0f / lds_seq_sum(sc, E);
+        g = sc[id] * inv;
+    }
+    g = gates_post(lane < K ? g : 0.0f, K, p.gating, p.weights_norm, p.weights_scale);
+    if (lane < K)
+        p.gates[(size_t)t * K + lane] = g;
+}
 
+constexpr int DN_UB = 8; // weight rows per lane requested at once in the down kernel
+
+// Down + gated combine for token t = blockIdx.y, row tile blockIdx.x.  The
+// token's k quantized SwiGLU vectors are staged into LDS together with its
+// ids and gates; then every slot's expert runs over the tile's rows and the
+// results combine in-register: mode 0 (moeRun) out = ((0 + g0*y0) + g1*y1)
+// + ... in selection order; mode 1 (moeBatchUnion) out += g*y per expert in
+// ascending expert id.
 template <int T>
 __global__ __launch_bounds__(256) void moe_down_decode_kernel(DecodeParams p) {
     using F = Fmt<T>;
-    constexpr int LPB = F::LPB, BPI = 64 / LPB;
+    constexpr int LPB = F::LPB;
     extern __shared__ float lds[];
     __shared__ uint32_t s_ids[MAX_K];
     __shared__ float s_gates[MAX_K];
@@ -137,64 +191,37 @@ __global__ __launch_bounds__(256) void moe_down_decode_kernel(DecodeParams p) {
     const int rpw = p.rpw_dn, TR = WAVES * rpw;
     const int row0 = blockIdx.x * TR;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int grp = lane / LPB, j = lane % LPB;
-    const bool wide = nb >= BPI;
-    const int C = wide ? nb / BPI : 1;
-    const int RPI = wide ? 1 : BPI / nb;
-    const int ro = wide ? 0 : grp / nb;
-    const bool active = wide || grp < RPI * nb;
+    const LaneMap<LPB> m(lane, nb);
+    const int j = m.j;
     // virtual rows (slot, row): wave w owns [w*VPW, (w+1)*VPW)
     const int VPW = K * rpw;
-    const int nit = (VPW + RPI - 1) / RPI;
+    const int nit = (VPW + m.RPI - 1) / m.RPI;
     // LDS: partials [K][TR][nb] f32 | q [K][cols] i8 | d [K][cols/32] f32 | s [K][cols/16] i32
+    constexpr int QB = act_block(T);
+    const int nd = cols / QB, ns = QB == 256 ? cols / 16 : cols / 32;
     float *part = lds;
     int8_t *qq = (int8_t *)(part + (size_t)K * TR * nb);
     float *qd = (float *)(qq + align16((size_t)K * cols));
-    int32_t *qs = (int32_t *)(qd + (size_t)K * (cols / 32));
-    const QAct qa{qq, qd, qs};
-
-    // 1. ids/gates and the SwiGLU vectors load together
-    const int per = quant_items(T, cols);
-    const int items = K * per;
-    constexpr bool k256 = act_block(T) == 256;
-    const bool one_batch = items <= WAVES * DN_QB;
-    auto act_src = [&](int it) {
-        const int v_ = it / per, item = it % per;
-        const float *x = p.act + ((size_t)t * K + v_) * cols;
-        return k256 ? x + item * 256 + 4 * lane : blocks32_src(x, cols / 32, item * 8);
-    };
-    auto quantize = [&](int it, float4 v) {
-        const int v_ = it / per, item = it % per;
-        if (k256)
-            quant256_regs(v, qq + (size_t)v_ * cols + item * 256, qd + (size_t)v_ * (cols / 256) + item,
-                          qs + (size_t)v_ * (cols / 16) + item * 16);
-        else
-            quant32x8_regs(v, cols / 32, item * 8, qq + (size_t)v_ * cols, qd + (size_t)v_ * (cols / 32),
-                           qs + (size_t)v_ * (cols / 32));
-    };
-    float4 av[DN_QB];
-    if (one_batch) {
-        // items past the end repeat the last item (identical values to the
-        // same LDS locations) so the batch is straight-line code
-#pragma unroll
-        for (int i = 0; i < DN_QB; i++) {
-            const int it = wave + WAVES * i;
-            av[i] = *(const float4 *)act_src(it < items ? it : items - 1);
+    int32_t *qs = (int32_t *)(qd + align16((size_t)K * nd * 4) / 4);
+    // 1. the token's ids, gates and quantized vectors (contiguous: pairs t*K..)
+    const size_t v0 = (size_t)t * K;
+    {
+        const int4 *src = (const int4 *)(p.qa.q + v0 * cols);
+        for (int i = threadIdx.x; i < K * cols / 16; i += blockDim.x)
+            ((int4 *)qq)[i] = src[i];
+        for (int i = threadIdx.x; i < K * nd; i += blockDim.x)
+            qd[i] = p.qa.d[v0 * nd + i];
+        for (int i = threadIdx.x; i < K * ns; i += blockDim.x)
+            qs[i] = p.qa.s[v0 * ns + i];
+        if ((int)threadIdx.x < K) {
+            s_ids[threadIdx.x] = min(p.ids[v0 + threadIdx.x], (uint32_t)(p.n_expert - 1));
+            s_gates[threadIdx.x] = p.gates[v0 + threadIdx.x];
         }
-    } else {
-        // more vectors than one batch of registers: quantize them all up front
-        for (int it = wave; it < items; it += WAVES)
-            quantize(it, *(const float4 *)act_src(it));
-    }
-    if (threadIdx.x < K) {
-        s_ids[threadIdx.x] = min(p.ids[(size_t)t * K + threadIdx.x], (uint32_t)(p.n_expert - 1));
-        s_gates[threadIdx.x] = p.gates[(size_t)t * K + threadIdx.x];
     }
     __syncthreads();
-
-    bool quantized = !one_batch;
-    for (int c = 0; c < C; c++) {
-        const int b = wide ? c * BPI + grp : (grp % nb);
+    for (int c = 0; c < m.C; c++) {
+        bool bok;
+        const int b = m.block(c, bok);
         for (int it0 = 0; it0 < nit; it0 += DN_UB) {
             // 2. the weight rows of DN_UB iterations are requested at once
             typename F::W w[DN_UB];
@@ -202,77 +229,16 @@ __global__ __launch_bounds__(256) void moe_down_decode_kernel(DecodeParams p) {
             bool valid[DN_UB];
 #pragma unroll
             for (int u = 0; u < DN_UB; u++) {
-                const int vl = (it0 + u) * RPI + ro;
+                const int vl = (it0 + u) * m.RPI + m.ro;
                 const int vr = wave * VPW + vl;
                 slot[u] = vr / TR;
                 rl_[u] = vr % TR;
-                valid[u] = active && it0 + u < nit && vl < VPW && row0 + rl_[u] < rows;
+                valid[u] = m.active && bok && it0 + u < nit && vl < VPW && row0 + rl_[u] < rows;
                 const int sl = valid[u] ? slot[u] : 0;
                 const size_t unit = (size_t)(valid[u] ? row0 + rl_[u] : 0) * nb + b;
                 w[u] = F::load_w(p.down + (size_t)s_ids[sl] * p.dn_plane, U, unit, j);
             }
-            if (!quantized) {
-                // 3. quantize from registers while the weights are in flight,
-                // phase by phase over the items so their chains interleave
-                float a[DN_QB], dd[DN_QB], inv[DN_QB];
-                int sum[DN_QB];
-                uint32_t packed[DN_QB];
-#pragma unroll
-                for (int i = 0; i < DN_QB; i++) {
-                    float m = 0.0f;
-                    if (__builtin_isfinite(av[i].x)) m = fmaxf(m, fabsf(av[i].x));
-                    if (__builtin_isfinite(av[i].y)) m = fmaxf(m, fabsf(av[i].y));
-                    if (__builtin_isfinite(av[i].z)) m = fmaxf(m, fabsf(av[i].z));
-                    if (__builtin_isfinite(av[i].w)) m = fmaxf(m, fabsf(av[i].w));
-                    a[i] = m;
-                }
-#pragma unroll
-                for (int i = 0; i < DN_QB; i++)
-                    a[i] = k256 ? wave_max(a[i]) : group8_max(a[i]);
-#pragma unroll
-                for (int i = 0; i < DN_QB; i++)
-                    dd[i] = a[i] / 127.0f;
-#pragma unroll
-                for (int i = 0; i < DN_QB; i++)
-                    inv[i] = (dd[i] != 0.0f && __builtin_isfinite(dd[i])) ? 1.0f / dd[i] : 0.0f;
-#pragma unroll
-                for (int i = 0; i < DN_QB; i++) {
-                    const int q0 = to_i8_sat(av[i].x * inv[i]), q1 = to_i8_sat(av[i].y * inv[i]);
-                    const int q2 = to_i8_sat(av[i].z * inv[i]), q3 = to_i8_sat(av[i].w * inv[i]);
-                    packed[i] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-                                ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
-                    sum[i] = q0 + q1 + q2 + q3;
-                }
-#pragma unroll
-                for (int i = 0; i < DN_QB; i++)
-                    sum[i] = k256 ? group_sum<4>(sum[i]) : group_sum<8>(sum[i]);
-#pragma unroll
-                for (int i = 0; i < DN_QB; i++) {
-                    // items past the end repeat the last one (same values, same place)
-                    const int it = min(wave + WAVES * i, items - 1);
-                    const int v_ = it / per, item = it % per;
-                    const float dv = __builtin_isfinite(dd[i]) ? dd[i] : 0.0f;
-                    if constexpr (k256) {
-                        *(uint32_t *)(qq + (size_t)v_ * cols + item * 256 + 4 * lane) = packed[i];
-                        if ((lane & 3) == 0)
-                            qs[(size_t)v_ * (cols / 16) + item * 16 + lane / 4] = sum[i];
-                        if (lane == 0)
-                            qd[(size_t)v_ * (cols / 256) + item] = dv;
-                    } else {
-                        const int blk = item * 8 + lane / 8;
-                        if (blk < cols / 32) {
-                            *(uint32_t *)(qq + (size_t)v_ * cols + blk * 32 + 4 * (lane & 7)) = packed[i];
-                            if ((lane & 7) == 0) {
-                                qs[(size_t)v_ * (cols / 32) + blk] = sum[i];
-                                qd[(size_t)v_ * (cols / 32) + blk] = dv;
-                            }
-                        }
-                    }
-                }
-                lds_barrier();
-                quantized = true;
-            }
-            // 4. dots against the slots' quantized vectors in LDS
+            // 3. dots against the slots' quantized vectors in LDS
 #pragma unroll
             for (int u = 0; u < DN_UB; u++) {
                 if (it0 + u < nit) {
@@ -288,7 +254,7 @@ __global__ __launch_bounds__(256) void moe_down_decode_kernel(DecodeParams p) {
         }
     }
     __syncthreads();
-    // 5. gated combine per row
+    // 4. gated combine per row
     for (int r = threadIdx.x; r < TR; r += blockDim.x) {
         const int row = row0 + r;
         if (row >= rows)
@@ -326,8 +292,10 @@ __global__ __launch_bounds__(256) void moe_down_decode_kernel(DecodeParams p) {
 
 size_t decode_down_lds(int down_t, int ffn, int k, int rpw) {
     const int nb = ffn / block_elems(down_t);
-    return (size_t)k * WAVES * rpw * nb * 4 + align16((size_t)k * ffn) + (size_t)k * (ffn / 32) * 4 +
-           (size_t)k * (ffn / 16) * 4;
+    const int QB = act_block(down_t);
+    const int nd = ffn / QB, ns = QB == 256 ? ffn / 16 : ffn / 32;
+    return (size_t)k * WAVES * rpw * nb * 4 + align16((size_t)k * ffn) + align16((size_t)k * nd * 4) +
+           (size_t)k * ns * 4;
 }
 
 size_t decode_gateup_lds(int gate_t, int dim, int rpw) {
@@ -364,6 +332,9 @@ bool launch_moe_decode(int gate_t, int down_t, const DecodeParams &p, int n, hip
     default: launch_gateup_decode_t<LH_Q4_0>(p, n, st); break;
     }
     prof_end(ph, st);
+    note_launch();
+    const int mid = n * p.k * quant_items(down_t, p.ffn) + n;
+    hipLaunchKernelGGL(moe_mid_kernel, dim3(mid), dim3(64), 0, st, p, n);
     note_launch();
     ph = prof_begin(prof_dn, st);
     switch (down_t) {

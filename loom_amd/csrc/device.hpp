@@ -441,6 +441,28 @@ __device__ __forceinline__ void route_rank(const float *lg, const float *sel_bia
     route_slots<NW, false>(key, val, valid_n, E, K, L);
 }
 
+// Gate post-processing in slot order (moe.zig:143-157), lane s < K holding
+// slot s's unbiased score: softmax over the k for softmax_topk, renorm with
+// the f16-min clamp, scale.  Returns lane s's final gate.
+__device__ __forceinline__ float gates_post(float g, int K, int gating, int weights_norm,
+                                            float weights_scale) {
+    if (gating == 3) {
+        float m = -INFINITY;
+        for (int s = 0; s < K; s++)
+            m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), s)));
+        g = expf(g - m);
+        const float inv = 1.0f / slot_sum(g, K);
+        g = g * inv;
+    }
+    if (weights_norm) {
+        const float denom = fmaxf(slot_sum(g, K), 6.103515625e-5f);
+        g = g / denom;
+    }
+    if (weights_scale != 1.0f)
+        g = g * weights_scale;
+    return g;
+}
+
 // Gates of the slots (moe.zig:143-157) by one wave after route_rank: softmax
 // scores p = e / sum (redo = true, uniformly, when two adjacent ranks 0..k
 // have equal p from different e: the caller then reroutes with
@@ -464,21 +486,7 @@ __device__ __forceinline__ float route_finish(RouteLds<NW> &L, int E, int K, int
         redo = __ballot(tie) != 0;
         g = lane < K ? pl : 0.0f;
     }
-    if (gating == 3) {
-        float m = -INFINITY;
-        for (int s = 0; s < K; s++)
-            m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), s)));
-        g = expf(g - m);
-        const float inv = 1.0f / slot_sum(g, K);
-        g = g * inv;
-    }
-    if (weights_norm) {
-        const float denom = fmaxf(slot_sum(g, K), 6.103515625e-5f);
-        g = g / denom;
-    }
-    if (weights_scale != 1.0f)
-        g = g * weights_scale;
-    return g;
+    return gates_post(g, K, gating, weights_norm, weights_scale);
 }
 
 } // namespace lh

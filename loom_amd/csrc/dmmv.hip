@@ -35,7 +35,7 @@ __device__ inline void tile_partials(const uint8_t *wb, const uint8_t *wb2, int 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int grp = lane / LPB, j = lane % LPB;
     const bool wide = nb >= BPI;
-    const int C = wide ? nb / BPI : 1;
+    const int C = wide ? (nb + BPI - 1) / BPI : 1; // the last chunk may be partial
     const int RPI = wide ? 1 : BPI / nb;
     const int ro = wide ? 0 : grp / nb;
     const bool active = wide || grp < RPI * nb;
@@ -43,7 +43,9 @@ __device__ inline void tile_partials(const uint8_t *wb, const uint8_t *wb2, int 
     const size_t lds_mat = (size_t)NT * TR * nb; // floats per matrix
 
     for (int c = 0; c < C; c++) {
-        const int b = wide ? c * BPI + grp : (grp % nb);
+        const int bc = wide ? c * BPI + grp : (grp % nb);
+        const bool bok = bc < nb;
+        const int b = bok ? bc : nb - 1; // lanes past the row's end read a real block, write nothing
         typename F::X xr[NT];
 #pragma unroll
         for (int k = 0; k < NT; k++)
@@ -53,7 +55,7 @@ __device__ inline void tile_partials(const uint8_t *wb, const uint8_t *wb2, int 
             const int rw = it * RPI + ro;    // row within this wave's span
             const int rl = wave * rpw + rw;  // row within the tile
             const int row = row0 + rl;
-            const bool valid = active && rw < rpw && row < rows;
+            const bool valid = active && bok && rw < rpw && row < rows;
             const size_t unit = (size_t)(valid ? row : 0) * nb + b;
             const typename F::W w = F::load_w(wb, U, unit, j);
             typename F::W w2;
@@ -114,26 +116,15 @@ __global__ __launch_bounds__(256) void dmmv_kernel(DmmvParams p) {
 }
 
 bool dmmv_supported(int t, int cols) {
+    if (cols <= 0)
+        return false;
     switch (t) {
     case LH_Q4_K:
-    case LH_Q6_K: {
-        if (cols % 256)
-            return false;
-        const int nb = cols / 256;
-        return nb <= 8 || nb % 8 == 0;
-    }
-    case LH_Q8_0: {
-        if (cols % 32)
-            return false;
-        const int nb = cols / 32;
-        return nb <= 32 || nb % 32 == 0;
-    }
-    case LH_Q4_0: {
-        if (cols % 32)
-            return false;
-        const int nb = cols / 32;
-        return nb <= 64 || nb % 64 == 0;
-    }
+    case LH_Q6_K:
+        return cols % 256 == 0;
+    case LH_Q8_0:
+    case LH_Q4_0:
+        return cols % 32 == 0;
     default:
         return false;
     }

@@ -118,6 +118,7 @@ struct DecodeParams {
     const float *xd;
     const int32_t *xs;
     float *act; // [n*k][ffn]
+    QAct qa;    // act quantized for the down type (written by the mid kernel)
     float *out; // [n][dim]
     int mode;   // 0 selection-order combine (overwrite), 1 ascending expert (accumulate)
     int rpw_gu, rpw_dn;

@@ -95,7 +95,7 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     const size_t o_ptok = take(P * 4), o_pof = take(P * 4), o_iota = take(P * 4);
     const size_t o_groups = take(maxg * sizeof(DmmvGroup)), o_ng = take(16);
     const size_t o_act = take(P * m.ffn * 4);
-    const size_t o_qa = take(decode ? 0 : qbytes(P, m.ffn));
+    const size_t o_qa = take(qbytes(P, m.ffn));
     const size_t o_y = take(decode ? 0 : P * m.dim * 4);
     if (int rc = g_moe.reserve(off))
         return rc;
@@ -150,6 +150,7 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
         dp.xd = qx.d;
         dp.xs = qx.s;
         dp.act = act;
+        dp.qa = qview(base + o_qa, P, m.ffn);
         dp.out = out;
         dp.mode = combine;
         dp.rpw_gu = dmmv_pick_rpw(m.gate_t, (int)m.dim, (int)m.ffn, (int)P, 1, true);

@@ -86,6 +86,8 @@ SHAPES = [
     (Q6_K, 768, 2048), (Q6_K, 2048, 768), (Q6_K, 256, 4096), (Q6_K, 97, 512),
     (Q8_0, 768, 2048), (Q8_0, 2048, 2048), (Q8_0, 300, 4096), (Q8_0, 288, 288), (Q8_0, 64, 768),
     (Q4_0, 768, 2048), (Q4_0, 288, 288), (Q4_0, 768, 288), (Q4_0, 288, 768), (Q4_0, 100, 4096),
+    # rows whose block count leaves the last column chunk partial (hidden 7168 = 28 super-blocks)
+    (Q4_K, 64, 2304), (Q4_K, 96, 7168), (Q6_K, 64, 7168), (Q8_0, 40, 1056), (Q4_0, 40, 2080),
 ]
 
 
@@ -137,12 +139,11 @@ def test_f32_matvec_bit_exact(be, oracle):
         assert np.array_equal(_bits(got), _bits(want)), (rows, cols)
 
 
-def test_declines_unserved_shapes(be):
+def test_declines_unserved_types(be):
     raw = np.zeros(144 * 2, np.uint8)
     out = np.empty(1, np.float32)
-    # 512 cols of Q4_K is served; 9 super-blocks (2304 cols) is not (not <= 8, not % 8)
-    assert be.matvec(Q4_K, out, np.zeros(144 * 9, np.uint8), np.zeros(2304, np.float32), 1, 2304) is False
     assert be.matvec(1, out, raw, np.zeros(4, np.float32), 1, 4) is False  # f16 declined
+    assert be.matvec(Q4_K, out, raw, np.zeros(300, np.float32), 1, 300) is False  # not whole blocks
 
 
 def test_nonfinite_activations_stay_finite(be, oracle):

@@ -145,3 +145,27 @@ def test_moe_layer_dev_matches_oracle(be, oracle, n):
     got = out.cpu().numpy()
     for i in range(n):
         assert _maxrel(got[i], want[i]) <= 2e-3, (i, _maxrel(got[i], want[i]))
+
+
+@pytest.mark.parametrize("n", [1, 2, 6])
+def test_moe_layer_dev_wide_hidden(be, oracle, n):
+    """Hidden 7168 (28 super-blocks per row: a partial last column chunk) and
+    expert ffn 2048, the DeepSeek-V3-class block's shapes, with 16 experts."""
+    import torch
+
+    w = make_layer(oracle, 7168, 2048, 16, 4, seed=11, gate_t=Q4_K, down_t=Q4_K)
+    layer = _dev_layer(be, w)
+    xs = np.stack([oracle.normal(7168, 700 + i, 0.0, 1.0) for i in range(n)])
+    normed = torch.from_numpy(xs).cuda()
+    ids = torch.empty((n, 4), dtype=torch.int32, device="cuda")
+    gates = torch.empty((n, 4), dtype=torch.float32, device="cuda")
+    resid = np.stack([oracle.normal(7168, 800 + i, 0.0, 1.0) for i in range(n)])
+    out = torch.from_numpy(resid.copy()).cuda()
+    layer(normed, out, combine=be.COMBINE_EXPERT_ASC, ids=ids, gates=gates)
+    want, wid, wg = oracle.moe_batch_union(w, xs, resid)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy().astype(np.uint32), wid)
+    assert np.all(np.abs(gates.cpu().numpy() - wg) <= 1e-6)
+    got = out.cpu().numpy()
+    for i in range(n):
+        assert _maxrel(got[i] - resid[i], want[i] - resid[i]) <= 2e-3, i
