@@ -254,7 +254,14 @@ __global__ __launch_bounds__(256) void moe_down_decode_kernel(DecodeParams p) {
         }
     }
     __syncthreads();
-    // 4. gated combine per row
+    // 4. every (slot, row) value in parallel (its blocks in order), then the
+    // gated combine per row: mode 0 (moeRun) out = ((0 + g0*y0) + g1*y1) + ...
+    // in selection order; mode 1 (moeBatchUnion) out += g*y per expert in
+    // ascending expert id
+    float *yv = part + (size_t)K * TR * nb; // reuses the activation staging
+    for (int i = threadIdx.x; i < K * TR; i += blockDim.x)
+        yv[i] = row_value<false>(part, 0, i, nb); // i = slot * TR + row
+    __syncthreads();
     for (int r = threadIdx.x; r < TR; r += blockDim.x) {
         const int row = row0 + r;
         if (row >= rows)
@@ -263,7 +270,7 @@ __global__ __launch_bounds__(256) void moe_down_decode_kernel(DecodeParams p) {
         if (p.mode == 0) {
             float acc = 0.0f;
             for (int sl = 0; sl < K; sl++) {
-                const float pr = s_gates[sl] * row_value<false>(part, 0, (size_t)sl * TR + r, nb);
+                const float pr = s_gates[sl] * yv[sl * TR + r];
                 acc = acc + pr;
             }
             *o = acc;
@@ -281,7 +288,7 @@ __global__ __launch_bounds__(256) void moe_down_decode_kernel(DecodeParams p) {
                 }
                 if (bs < 0)
                     break;
-                const float pr = s_gates[bs] * row_value<false>(part, 0, (size_t)bs * TR + r, nb);
+                const float pr = s_gates[bs] * yv[bs * TR + r];
                 acc = acc + pr;
                 prev = be;
             }
@@ -294,8 +301,9 @@ size_t decode_down_lds(int down_t, int ffn, int k, int rpw) {
     const int nb = ffn / block_elems(down_t);
     const int QB = act_block(down_t);
     const int nd = ffn / QB, ns = QB == 256 ? ffn / 16 : ffn / 32;
-    return (size_t)k * WAVES * rpw * nb * 4 + align16((size_t)k * ffn) + align16((size_t)k * nd * 4) +
-           (size_t)k * ns * 4;
+    const size_t staging = align16((size_t)k * ffn) + align16((size_t)k * nd * 4) + (size_t)k * ns * 4;
+    const size_t yv = (size_t)k * WAVES * rpw * 4; // the slot values reuse the staging
+    return (size_t)k * WAVES * rpw * nb * 4 + (staging > yv ? staging : yv);
 }
 
 size_t decode_gateup_lds(int gate_t, int dim, int rpw) {

@@ -247,20 +247,36 @@ __device__ __forceinline__ float lds_seq_sum(const float *v, int E) {
     return sum;
 }
 
-// #{keys in [j0, j1) of kl greater than ki}
-__device__ __forceinline__ int count_greater(const unsigned long long *kl, int j0, int j1,
-                                    unsigned long long ki) {
-    int rank = 0;
+// rank[i] += #{keys in [j0, j1) of kl greater than key[i]} for i < ni: each
+// key read once for all of the lane's experts, two partial counts per expert
+// to halve the add chains.
+__device__ __forceinline__ void count_greater(const unsigned long long *kl, int j0, int j1,
+                                              const unsigned long long (&key)[MAX_E / 64], int ni,
+                                              int (&rank)[MAX_E / 64]) {
+    constexpr int NI = MAX_E / 64;
+    int ra[NI], rb[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        ra[i] = rb[i] = 0;
     for (int j = j0; j < j1; j += 16) {
         ulonglong2 kk[8];
 #pragma unroll
         for (int q = 0; q < 8; q++)
             kk[q] = *(const ulonglong2 *)(kl + j + 2 * q);
 #pragma unroll
-        for (int q = 0; q < 8; q++)
-            rank += (kk[q].x > ki) + (kk[q].y > ki);
+        for (int i = 0; i < NI; i++) {
+            if (i < ni) {
+#pragma unroll
+                for (int q = 0; q < 8; q += 2) {
+                    ra[i] += (kk[q].x > key[i]) + (kk[q].y > key[i]);
+                    rb[i] += (kk[q + 1].x > key[i]) + (kk[q + 1].y > key[i]);
+                }
+            }
+        }
     }
-    return rank;
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        rank[i] = ra[i] + rb[i];
 }
 
 // Rank the experts' keys (key[i] for expert lane + 64i) and write the slot
@@ -283,9 +299,7 @@ __device__ __forceinline__ void route_slots(const unsigned long long (&key)[MAX_
     const int ch = ONE ? Epad : (((Epad / NW) + 15) & ~15);
     const int j0 = w * ch, j1 = min(Epad, j0 + ch);
     int rank[NI];
-#pragma unroll
-    for (int i = 0; i < NI; i++)
-        rank[i] = 64 * i < E ? count_greater(L.key[w], j0, j1, key[i]) : 0;
+    count_greater(L.key[w], j0, j1, key, (E + 63) / 64, rank);
     if constexpr (!ONE) {
 #pragma unroll
         for (int i = 0; i < NI; i++)
