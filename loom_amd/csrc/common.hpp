@@ -79,15 +79,10 @@ __device__ inline float half_bits_to_float(uint32_t bits16) {
 
 // Round half away from zero, saturate at +-127, non-finite -> 0
 // (src/gguf/ggml.zig:1067-1073 toI8Saturating).
+// Branch-free: round, clamp with med3, then select.
 __device__ inline int to_i8_sat(float v) {
-    if (!__builtin_isfinite(v))
-        return 0;
-    float r = __builtin_roundf(v);
-    if (r >= 127.0f)
-        return 127;
-    if (r <= -127.0f)
-        return -127;
-    return (int)r;
+    const float r = __builtin_amdgcn_fmed3f(__builtin_roundf(v), -127.0f, 127.0f);
+    return __builtin_isfinite(v) ? (int)r : 0;
 }
 
 __device__ inline int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }

@@ -104,6 +104,54 @@ __device__ inline void quant_blocks32_wave(const float *__restrict__ x, int nb, 
     quant32x8_regs(load4<COHERENT>(blocks32_src(x, nb, b0)), nb, b0, q, d, s);
 }
 
+// quantizeX (QB = 32, src/gguf/ggml.zig:1077-1098) or quantizeX256 (QB =
+// 256, ggml.zig:776-800) with each lane owning one 32-value chunk c of a
+// buffer of such chunks (v[0..8) its 32 values in order); for QB = 256 the
+// eight lanes 8g..8g+7 hold one block's chunks and share its amax.  Writes q
+// [32c, 32c+32), the per-16 sums (QB = 256: s[2c], s[2c+1]) or the block sum
+// (QB = 32: s[c]) and the block scale d, for live lanes.  All lanes of the
+// wave take part (QB = 256 reduces across lanes).
+template <int QB>
+__device__ inline void quant_chunk32(const float4 (&v)[8], bool live, int c, int8_t *__restrict__ q,
+                                     float *__restrict__ d, int32_t *__restrict__ s) {
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        if (__builtin_isfinite(v[i].x)) a = fmaxf(a, fabsf(v[i].x));
+        if (__builtin_isfinite(v[i].y)) a = fmaxf(a, fabsf(v[i].y));
+        if (__builtin_isfinite(v[i].z)) a = fmaxf(a, fabsf(v[i].z));
+        if (__builtin_isfinite(v[i].w)) a = fmaxf(a, fabsf(v[i].w));
+    }
+    if constexpr (QB == 256)
+        a = group8_max(a);
+    const float dd = a / 127.0f;
+    const float inv = (dd != 0.0f && __builtin_isfinite(dd)) ? 1.0f / dd : 0.0f;
+    uint32_t packed[8];
+    int sum[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int q0 = to_i8_sat(v[i].x * inv), q1 = to_i8_sat(v[i].y * inv);
+        const int q2 = to_i8_sat(v[i].z * inv), q3 = to_i8_sat(v[i].w * inv);
+        packed[i] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                    ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+        sum[i >> 2] += q0 + q1 + q2 + q3;
+    }
+    if (!live)
+        return;
+    *(uint4 *)(q + 32 * c) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    *(uint4 *)(q + 32 * c + 16) = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    const float dv = __builtin_isfinite(dd) ? dd : 0.0f;
+    if constexpr (QB == 256) {
+        s[2 * c] = sum[0];
+        s[2 * c + 1] = sum[1];
+        if ((c & 7) == 0)
+            d[c >> 3] = dv;
+    } else {
+        s[c] = sum[0] + sum[1];
+        d[c] = dv;
+    }
+}
+
 // Work items of quantizing one vector of `cols` values for weight type wt:
 // one 256-block (K-quants) or eight 32-blocks per item.
 __host__ __device__ inline int quant_items(int wt, int cols) {
@@ -187,8 +235,10 @@ __device__ inline bool last_arrival(int *counter, int target) {
 // index wins ties, and a round that finds nothing above -inf picks expert 0.
 // That is the order (value descending, index ascending) over values above
 // -inf, so an expert's slot is its rank in that order.  With
-// key = (ordered value << 32) | ~index every key is distinct and
-// rank = #{keys greater}.
+// key = (ordered value << 31) | (0x7FFFFFFF - index) every key is distinct
+// and rank = #{keys greater}.  Keys stay below 2^63, so "k_j > k_i" is the
+// sign bit of k_i - k_j: the comparisons are 64-bit adds of negated keys
+// and shifts, with no compare results to serialise on.
 //
 // For softmax gating without a selection bias the ranks are taken on the
 // exp values e = exp(l - max) before the sequential sum: scores p = e * inv
@@ -199,8 +249,8 @@ __device__ inline bool last_arrival(int *counter, int target) {
 
 template <int NW>
 struct __align__(16) RouteLds {
-    unsigned long long key[NW][MAX_E]; // per-wave copy of the selection keys
-    int prank[NW][MAX_E];              // partial ranks (NW > 1)
+    unsigned long long nkey[NW][MAX_E]; // per-wave copy of the negated selection keys
+    int prank[NW][MAX_E];               // partial ranks (NW > 1)
     float sc[MAX_E];                   // softmax exp values, for the sequential sum
     int id[MAX_K + 1];                 // slot -> expert (slot k: the next one)
     float val[MAX_K + 1];              // slot -> unbiased score (softmax: exp value)
@@ -222,13 +272,19 @@ __device__ __forceinline__ uint32_t ordered_u32(float f) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// 63-bit key: the value's order in bits 62..31 (-0 folded into +0: the
+// reference's '>' sees them equal), 0x7FFFFFFF - index below.  Valid keys
+// are >= 2^54; invalid ones are 0.
 __device__ __forceinline__ unsigned long long route_key(float c, int e, bool valid) {
-    return valid ? ((unsigned long long)ordered_u32(c) << 32) | (0xFFFFFFFFu - (uint32_t)e) : 0ull;
+    return valid ? ((unsigned long long)ordered_u32(c + 0.0f) << 31) | (0x7FFFFFFFu - (uint32_t)e) : 0ull;
 }
 
 // Sequential sum of v[0..E) in LDS (the reference's softmax sum order); the
 // reads of each 32-value batch are issued before its adds.
 __device__ __forceinline__ float lds_seq_sum(const float *v, int E) {
+    // unconditional over whole batches of 32: the entries past E are +0
+    // (exp(-inf - max)) and the running sum of exp values is never -0, so
+    // adding them changes nothing
     float sum = 0.0f;
     for (int e0 = 0; e0 < E; e0 += 32) {
         float4 r[8];
@@ -237,46 +293,44 @@ __device__ __forceinline__ float lds_seq_sum(const float *v, int E) {
             r[q] = *(const float4 *)(v + e0 + 4 * q);
 #pragma unroll
         for (int q = 0; q < 8; q++) {
-            const int e = e0 + 4 * q;
-            if (e + 0 < E) sum = sum + r[q].x;
-            if (e + 1 < E) sum = sum + r[q].y;
-            if (e + 2 < E) sum = sum + r[q].z;
-            if (e + 3 < E) sum = sum + r[q].w;
+            sum = sum + r[q].x;
+            sum = sum + r[q].y;
+            sum = sum + r[q].z;
+            sum = sum + r[q].w;
         }
     }
     return sum;
 }
 
-// rank[i] += #{keys in [j0, j1) of kl greater than key[i]} for i < ni: each
-// key read once for all of the lane's experts, two partial counts per expert
-// to halve the add chains.
-__device__ __forceinline__ void count_greater(const unsigned long long *kl, int j0, int j1,
+// rank[i] = #{keys of [j0, j1) greater than key[i]} for i < ni, from the
+// negated keys nk: each read once for all of the lane's experts; a key k_j
+// counts when the sign bit of key[i] + nk_j = key[i] - k_j is set.
+__device__ __forceinline__ void count_greater(const unsigned long long *nk, int j0, int j1,
                                               const unsigned long long (&key)[MAX_E / 64], int ni,
                                               int (&rank)[MAX_E / 64]) {
     constexpr int NI = MAX_E / 64;
-    int ra[NI], rb[NI];
+    int r[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++)
-        ra[i] = rb[i] = 0;
+        r[i] = 0;
     for (int j = j0; j < j1; j += 16) {
         ulonglong2 kk[8];
 #pragma unroll
         for (int q = 0; q < 8; q++)
-            kk[q] = *(const ulonglong2 *)(kl + j + 2 * q);
+            kk[q] = *(const ulonglong2 *)(nk + j + 2 * q);
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             if (i < ni) {
 #pragma unroll
-                for (int q = 0; q < 8; q += 2) {
-                    ra[i] += (kk[q].x > key[i]) + (kk[q].y > key[i]);
-                    rb[i] += (kk[q + 1].x > key[i]) + (kk[q + 1].y > key[i]);
-                }
+                for (int q = 0; q < 8; q++)
+                    r[i] += (int)((uint32_t)((key[i] + kk[q].x) >> 32) >> 31) +
+                            (int)((uint32_t)((key[i] + kk[q].y) >> 32) >> 31);
             }
         }
     }
 #pragma unroll
     for (int i = 0; i < NI; i++)
-        rank[i] = ra[i] + rb[i];
+        rank[i] = r[i];
 }
 
 // Rank the experts' keys (key[i] for expert lane + 64i) and write the slot
@@ -292,14 +346,14 @@ __device__ __forceinline__ void route_slots(const unsigned long long (&key)[MAX_
     const int lane = threadIdx.x & 63, w = ONE ? 0 : threadIdx.x >> 6;
 #pragma unroll
     for (int i = 0; i < NI; i++)
-        L.key[w][lane + 64 * i] = key[i];
+        L.nkey[w][lane + 64 * i] = 0ull - key[i];
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     const int Epad = (E + 15) & ~15; // keys past E are 0 and never count
     const int ch = ONE ? Epad : (((Epad / NW) + 15) & ~15);
     const int j0 = w * ch, j1 = min(Epad, j0 + ch);
     int rank[NI];
-    count_greater(L.key[w], j0, j1, key, (E + 63) / 64, rank);
+    count_greater(L.nkey[w], j0, j1, key, (E + 63) / 64, rank);
     if constexpr (!ONE) {
 #pragma unroll
         for (int i = 0; i < NI; i++)
@@ -408,11 +462,20 @@ __device__ __forceinline__ void route_rank(const float *lg, const float *sel_bia
             __syncthreads();
         return;
     }
-    float lv[NI], val[NI];
+    // logits and selection biases: unconditional loads (indices clamped) all
+    // issued before the first use, then the entries past E masked
+    float lv[NI], bv[NI], val[NI];
+    const float *bsrc = sel_bias ? sel_bias : lg; // read either way, used with a bias only
 #pragma unroll
     for (int i = 0; i < NI; i++) {
-        const int e = lane + 64 * i;
-        lv[i] = e < E ? (COHERENT ? ld_dev(lg + e) : lg[e]) : -INFINITY;
+        const int e = min(lane + 64 * i, E - 1);
+        lv[i] = COHERENT ? ld_dev(lg + e) : lg[e];
+        bv[i] = bsrc[e];
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        lv[i] = lane + 64 * i < E ? lv[i] : -INFINITY;
+        asm volatile("" ::"v"(bv[i])); // keeps the bias loads here, beside the logits
     }
     unsigned long long key[NI];
     int valid_n = 0;
@@ -421,7 +484,7 @@ __device__ __forceinline__ void route_rank(const float *lg, const float *sel_bia
         for (int i = 0; i < NI; i++) {
             const int e = lane + 64 * i;
             val[i] = gating == 2 ? 1.0f / (1.0f + expf(-lv[i])) : lv[i];
-            const float c = e < E ? (sel_bias ? val[i] + sel_bias[e] : val[i]) : -INFINITY;
+            const float c = e < E ? (sel_bias ? val[i] + bv[i] : val[i]) : -INFINITY;
             const bool valid = c > -INFINITY;
             key[i] = route_key(c, e, valid);
             valid_n += __popcll(__ballot(valid));

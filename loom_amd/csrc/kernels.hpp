@@ -118,11 +118,11 @@ struct DecodeParams {
     const float *xd;
     const int32_t *xs;
     float *act; // [n*k][ffn]
-    QAct qa;    // act quantized for the down type (written by the mid kernel)
     float *out; // [n][dim]
     int mode;   // 0 selection-order combine (overwrite), 1 ascending expert (accumulate)
     int rpw_gu, rpw_dn;
 };
+bool decode_supported(int gate_t, int down_t, int ffn); // ffn a multiple of 256
 size_t decode_down_lds(int down_t, int ffn, int k, int rpw);
 size_t decode_gateup_lds(int gate_t, int dim, int rpw);
 bool launch_moe_decode(int gate_t, int down_t, const DecodeParams &p, int n, hipStream_t st,

@@ -316,17 +316,16 @@ void launch_combine(const float *y, const float *gates, const uint32_t *ids, con
 // ---- decode-path router: GEMV + input quantization, one wave per work group --------
 //
 // Work groups [0, ceil(E/2)) hold two router rows each (a half-wave per
-// row); the rest quantize one item of the input each.  A half-wave loads its
-// row and the token's x in 16-byte pieces (lane P holds columns 128c + 4P ..
-// +3), multiplies in that layout, and passes the products through LDS so
-// that lane L then adds columns 32i + L in order -- the dotF32 accumulation
-// order (src/gguf/ggml.zig:198-217) -- with a quarter of the load
-// instructions of a per-column layout.
-constexpr int RS_COLS = 2048; // columns per pass (16 float4 per lane)
+// row); the rest quantize one item of the input each.  Lane P of a
+// half-wave owns dotF32's accumulator chain P (src/gguf/ggml.zig:198-217):
+// columns 32i + P, added in order of i.  For each i the 32 lanes of a row
+// read 128 contiguous bytes, so the per-column loads coalesce; the loads of
+// up to RS_STEPS steps are issued before the chain starts.  Then
+// v_l = ((c_l + c_{8+l}) + c_{16+l}) + c_{24+l} (lanes exchanged with
+// ds_bpermute), the sequential reduce over l from -0, and the tail.
+constexpr int RS_STEPS = 64; // dotF32 steps (32 columns each) per pass: dim 2048 in one
 
 __global__ __launch_bounds__(64) void router_small_kernel(GateParams p) {
-    __shared__ __align__(16) float prod[2][RS_COLS];
-    __shared__ float part[2][32];
     const int lane = threadIdx.x, hw = lane >> 5, P = lane & 31;
     const int gemv_wgs = p.gemv_wgs; // 0 when the caller supplies the logits
     if ((int)blockIdx.x >= gemv_wgs) {
@@ -342,62 +341,46 @@ __global__ __launch_bounds__(64) void router_small_kernel(GateParams p) {
     const int e = blockIdx.x * 2 + hw;
     const bool valid = e < p.n_expert;
     const float *row = p.router + (size_t)(valid ? e : 0) * dim;
-    const int main_end = dim / 32 * 32;
+    const int n32 = dim / 32; // whole dotF32 steps
     for (int t = 0; t < p.n; t++) {
         const float *xt = p.x + (size_t)t * dim;
         float acc = 0.0f;
-        for (int c0 = 0; c0 < main_end; c0 += RS_COLS) {
-            const int ccols = min(RS_COLS, main_end - c0);
-            float4 wv[RS_COLS / 128], xv[RS_COLS / 128];
+        for (int i0 = 0; i0 < n32; i0 += RS_STEPS) {
+            const int cnt = min(RS_STEPS, n32 - i0);
+            float wv[RS_STEPS], xv[RS_STEPS];
 #pragma unroll
-            for (int c = 0; c < RS_COLS / 128; c++) {
-                const bool in = 128 * c + 4 * P < ccols;
-                wv[c] = in ? *(const float4 *)(row + c0 + 128 * c + 4 * P) : make_float4(0.f, 0.f, 0.f, 0.f);
-                xv[c] = in ? *(const float4 *)(xt + c0 + 128 * c + 4 * P) : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int u = 0; u < RS_STEPS; u++) { // unconditional: steps past cnt re-read the last
+                const int c = 32 * (i0 + min(u, cnt - 1)) + P;
+                wv[u] = row[c];
+                xv[u] = xt[c];
             }
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); // previous pass's reads are done
+            // steps past cnt add +0: acc starts at +0 and a sum of products
+            // is never -0, so they change nothing
 #pragma unroll
-            for (int c = 0; c < RS_COLS / 128; c++) {
-                float4 pr;
-                pr.x = wv[c].x * xv[c].x;
-                pr.y = wv[c].y * xv[c].y;
-                pr.z = wv[c].z * xv[c].z;
-                pr.w = wv[c].w * xv[c].w;
-                if (128 * c + 4 * P < ccols)
-                    *(float4 *)(&prod[hw][128 * c + 4 * P]) = pr;
-            }
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-            const int n32 = ccols / 32;
-            for (int i0 = 0; i0 < n32; i0 += 16) {
-                float pv[16];
-#pragma unroll
-                for (int u = 0; u < 16; u++)
-                    pv[u] = i0 + u < n32 ? prod[hw][32 * (i0 + u) + P] : 0.0f;
-#pragma unroll
-                for (int u = 0; u < 16; u++)
-                    if (i0 + u < n32)
-                        acc = acc + pv[u];
+            for (int u = 0; u < RS_STEPS; u++) {
+                const float pr = u < cnt ? wv[u] * xv[u] : 0.0f;
+                acc = acc + pr;
             }
         }
         // leftover whole 8-chunks go to accumulator 0 (lanes 0..7)
-        for (int i = main_end; i + 8 <= dim; i += 8)
+        for (int i = n32 * 32; i + 8 <= dim; i += 8)
             if (P < 8) {
                 const float pr = row[i + P] * xt[i + P];
                 acc = acc + pr;
             }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        part[hw][P] = acc;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        const int src = 32 * hw + (P & 7);
+        const float c1 = __int_as_float(__builtin_amdgcn_ds_bpermute((src + 8) << 2, __float_as_int(acc)));
+        const float c2 = __int_as_float(__builtin_amdgcn_ds_bpermute((src + 16) << 2, __float_as_int(acc)));
+        const float c3 = __int_as_float(__builtin_amdgcn_ds_bpermute((src + 24) << 2, __float_as_int(acc)));
+        const float v = ((acc + c1) + c2) + c3; // v_l in lanes 32hw + l, l < 8
+        float s0 = -0.0f, s1 = -0.0f;
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            s0 = s0 + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+            s1 = s1 + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32 + l));
+        }
         if (P == 0 && valid) {
-            float s = -0.0f;
-            for (int l = 0; l < 8; l++) {
-                const float v = ((part[hw][l] + part[hw][8 + l]) + part[hw][16 + l]) + part[hw][24 + l];
-                s = s + v;
-            }
+            float s = hw ? s1 : s0;
             for (int j = dim / 8 * 8; j < dim; j++) {
                 const float pr = row[j] * xt[j];
                 s = s + pr;

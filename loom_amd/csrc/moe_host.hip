@@ -79,7 +79,7 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     if (int rc = moe_check(m, n))
         return rc;
     const size_t P = n * m.k;
-    const bool decode = n <= DECODE_MAX_TOK;
+    const bool decode = n <= DECODE_MAX_TOK && decode_supported(m.gate_t, m.down_t, (int)m.ffn);
     const int nt = moe_nt(n, m.k, m.E);
     const int maxg = moe_max_groups((int)n, (int)m.k, (int)m.E, nt);
     // workspace layout
@@ -150,7 +150,6 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
         dp.xd = qx.d;
         dp.xs = qx.s;
         dp.act = act;
-        dp.qa = qview(base + o_qa, P, m.ffn);
         dp.out = out;
         dp.mode = combine;
         dp.rpw_gu = dmmv_pick_rpw(m.gate_t, (int)m.dim, (int)m.ffn, (int)P, 1, true);

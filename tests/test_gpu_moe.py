@@ -169,3 +169,49 @@ def test_moe_layer_dev_wide_hidden(be, oracle, n):
     got = out.cpu().numpy()
     for i in range(n):
         assert _maxrel(got[i] - resid[i], want[i] - resid[i]) <= 2e-3, i
+
+
+Q8_0, Q4_0 = 8, 2
+
+# (gating, weights_norm, weights_scale, selection bias): the routing variants
+# of moe.zig:106-158 (softmax, sigmoid with DeepSeek-V3's selection bias,
+# softmax over the selected logits) through the whole layer
+_GATINGS = [(1, True, 1.0, False), (2, True, 2.5, True), (3, False, 1.0, False),
+            (1, False, 1.5, True)]
+
+
+@pytest.mark.parametrize("down_t,ffn", [(Q8_0, 512), (Q4_0, 256), (Q8_0, 288), (Q6_K, 256)])
+@pytest.mark.parametrize("gi", range(len(_GATINGS)))
+@pytest.mark.parametrize("n", [1, 3, 8])
+def test_moe_layer_dev_gatings_and_down_types(be, oracle, down_t, ffn, gi, n):
+    """Every gating mode with the 32-block down types and the K-quant one,
+    on the decode path (n <= 4, ffn a multiple of 256) and the batched path
+    (n = 8, or an ffn that is not a multiple of 256)."""
+    import torch
+
+    gating, norm, scale, has_bias = _GATINGS[gi]
+    dim, E, k = 512, 32, 4
+    w = make_layer(oracle, dim, ffn, E, k, seed=40 + gi, gate_t=Q8_0 if down_t == Q6_K else Q4_K,
+                   down_t=down_t)
+    rng = np.random.default_rng(77 + gi)
+    w.gating, w.weights_norm, w.weights_scale = gating, norm, scale
+    if has_bias:
+        w.sel_bias = ((rng.random(E) - 0.5) * 0.5).astype(np.float32)
+    layer = _dev_layer(be, w)
+    layer = be.MoeLayer(w.dim, w.ffn, E, k, *layer.keep[:4], w.gate_t, w.up_t, w.down_t,
+                        sel_bias=None if w.sel_bias is None else torch.from_numpy(w.sel_bias).cuda(),
+                        gating=gating, weights_norm=norm, weights_scale=scale)
+    xs = np.stack([oracle.normal(dim, 300 + i, 0.0, 1.0) for i in range(n)])
+    normed = torch.from_numpy(xs).cuda()
+    ids = torch.empty((n, k), dtype=torch.int32, device="cuda")
+    gates = torch.empty((n, k), dtype=torch.float32, device="cuda")
+    resid = np.stack([oracle.normal(dim, 600 + i, 0.0, 1.0) for i in range(n)])
+    out = torch.from_numpy(resid.copy()).cuda()
+    layer(normed, out, combine=be.COMBINE_EXPERT_ASC, ids=ids, gates=gates)
+    want, wid, wg = oracle.moe_batch_union(w, xs, resid)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy().astype(np.uint32), wid)
+    assert np.all(np.abs(gates.cpu().numpy() - wg) <= 1e-5 * max(1.0, scale))
+    got = out.cpu().numpy()
+    for i in range(n):
+        assert _maxrel(got[i] - resid[i], want[i] - resid[i]) <= 2e-3, i
