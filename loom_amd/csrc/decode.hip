@@ -45,13 +45,11 @@ struct LaneMap {
 constexpr int GU_MAXIT = 2; // weight rows per lane requested at once in the gate/up kernel
 
 // Gate/up + SwiGLU for pair (token t, slot s) = blockIdx.y, row tile
-// blockIdx.x.  The four waves rank the token's experts (route_rank) while
-// the first column chunk's activations load; the (slot 0, tile 0) work group
-// publishes the ids.  Ranking softmax routes on the exp values: two experts
-// can only come out in the other order when their exp values round to the
-// same final score (a logit gap below one ulp), the near-tie case the
-// north_star allows; gates are computed exactly by the down kernel.
-template <int T>
+// blockIdx.x.  The four waves find slot s's expert (route_decode_slot, NI =
+// ceil(E/64)) while the first column chunk's activations load; the (slot 0,
+// tile 0) work group publishes the ids.  Gates are computed exactly by the
+// down kernel.
+template <int T, int NI>
 __global__ __launch_bounds__(256) void moe_gateup_decode_kernel(DecodeParams p) {
     using F = Fmt<T>;
     constexpr int LPB = F::LPB;
@@ -72,11 +70,10 @@ __global__ __launch_bounds__(256) void moe_gateup_decode_kernel(DecodeParams p) 
     bool ok0;
     const int b0 = m.block(0, ok0);
     const typename F::X x0 = F::load_x(p.xq, p.xd, p.xs, cols, t, b0, j);
-    route_rank<WAVES, false>(p.logits + (size_t)t * p.n_expert, p.sel_bias, p.n_expert, K,
-                             p.gating, rl);
-    const int e = min(max(rl.id[s], 0), p.n_expert - 1); // never address past the tensor
-    if (s == 0 && blockIdx.x == 0 && (int)threadIdx.x < K)
-        p.ids[(size_t)t * K + threadIdx.x] = (uint32_t)rl.id[threadIdx.x];
+    const int e0 = route_decode_slot<NI>(p.logits + (size_t)t * p.n_expert, p.sel_bias, p.n_expert, K,
+                                         p.gating, s, rl,
+                                         s == 0 && blockIdx.x == 0 ? p.ids + (size_t)t * K : nullptr);
+    const int e = min(max(e0, 0), p.n_expert - 1); // never address past the tensor
     const uint8_t *wb = p.gate + (size_t)e * p.gu_plane;
     const uint8_t *wb2 = p.up + (size_t)e * p.gu_plane;
     for (int c = 0; c < m.C; c++) {
@@ -364,8 +361,14 @@ size_t decode_gateup_lds(int gate_t, int dim, int rpw) {
 template <int T>
 static void launch_gateup_decode_t(const DecodeParams &p, int n, hipStream_t st) {
     const int TR = WAVES * p.rpw_gu;
-    hipLaunchKernelGGL(moe_gateup_decode_kernel<T>, dim3((p.ffn + TR - 1) / TR, n * p.k), dim3(256),
-                       decode_gateup_lds(T, p.dim, p.rpw_gu), st, p);
+    const dim3 grid((p.ffn + TR - 1) / TR, n * p.k);
+    const size_t lds = decode_gateup_lds(T, p.dim, p.rpw_gu);
+    if (p.n_expert <= 64)
+        hipLaunchKernelGGL((moe_gateup_decode_kernel<T, 1>), grid, dim3(256), lds, st, p);
+    else if (p.n_expert <= 128)
+        hipLaunchKernelGGL((moe_gateup_decode_kernel<T, 2>), grid, dim3(256), lds, st, p);
+    else
+        hipLaunchKernelGGL((moe_gateup_decode_kernel<T, 4>), grid, dim3(256), lds, st, p);
 }
 
 template <int T>

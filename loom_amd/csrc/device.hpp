@@ -305,10 +305,10 @@ __device__ __forceinline__ float lds_seq_sum(const float *v, int E) {
 // rank[i] = #{keys of [j0, j1) greater than key[i]} for i < ni, from the
 // negated keys nk: each read once for all of the lane's experts; a key k_j
 // counts when the sign bit of key[i] + nk_j = key[i] - k_j is set.
+template <int NI>
 __device__ __forceinline__ void count_greater(const unsigned long long *nk, int j0, int j1,
-                                              const unsigned long long (&key)[MAX_E / 64], int ni,
-                                              int (&rank)[MAX_E / 64]) {
-    constexpr int NI = MAX_E / 64;
+                                              const unsigned long long (&key)[NI], int ni,
+                                              int (&rank)[NI]) {
     int r[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++)
@@ -353,7 +353,7 @@ __device__ __forceinline__ void route_slots(const unsigned long long (&key)[MAX_
     const int ch = ONE ? Epad : (((Epad / NW) + 15) & ~15);
     const int j0 = w * ch, j1 = min(Epad, j0 + ch);
     int rank[NI];
-    count_greater(L.nkey[w], j0, j1, key, (E + 63) / 64, rank);
+    count_greater<NI>(L.nkey[w], j0, j1, key, (E + 63) / 64, rank);
     if constexpr (!ONE) {
 #pragma unroll
         for (int i = 0; i < NI; i++)
@@ -521,6 +521,114 @@ __device__ __forceinline__ void route_rank(const float *lg, const float *sel_bia
 // Gate post-processing in slot order (moe.zig:143-157), lane s < K holding
 // slot s's unbiased score: softmax over the k for softmax_topk, renorm with
 // the f16-min clamp, scale.  Returns lane s's final gate.
+// Routing for one (token, slot s) work group of the decode path (4 waves,
+// NI = ceil(E/64)): every wave builds the token's keys, the waves split the
+// rank counting, and slot s's expert is the one whose rank is s (a ballot;
+// no slot table).  Softmax ranks on exp(l - max): two experts can come out
+// in the other order only when their exp values round to the same final
+// score, the near-tie case the reference's tests allow; the gates are
+// computed exactly elsewhere.  Softmax with a selection bias goes through
+// route_rank (exact scores).  ids, when given, receives the token's k ids
+// (wave 0).  Rounds that find nothing above -inf pick expert 0.
+template <int NI>
+__device__ __forceinline__ int route_decode_slot(const float *lg, const float *sel_bias, int E, int K,
+                                                 int gating, int s, RouteLds<4> &L, uint32_t *ids) {
+    constexpr int NW = 4;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (gating != 2 && gating != 3 && sel_bias) {
+        route_rank<NW, false>(lg, sel_bias, E, K, gating, L);
+        if (ids && (int)threadIdx.x < K)
+            ids[threadIdx.x] = (uint32_t)L.id[threadIdx.x];
+        return L.id[s];
+    }
+    // logits and selection biases: unconditional loads (indices clamped)
+    // all issued before the first use, then the entries past E masked
+    float lv[NI], bv[NI];
+    const float *bsrc = sel_bias ? sel_bias : lg; // read either way, used with a bias only
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int e = min(lane + 64 * i, E - 1);
+        lv[i] = lg[e];
+        bv[i] = bsrc[e];
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        lv[i] = lane + 64 * i < E ? lv[i] : -INFINITY;
+        asm volatile("" ::"v"(bv[i])); // keeps the bias loads here, beside the logits
+    }
+    unsigned long long key[NI];
+    int valid_n = 0;
+    if (gating == 2 || gating == 3) { // sigmoid / softmax_topk: exact selection values
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int e = lane + 64 * i;
+            const float val = gating == 2 ? 1.0f / (1.0f + expf(-lv[i])) : lv[i];
+            const float c = e < E ? (sel_bias ? val + bv[i] : val) : -INFINITY;
+            const bool valid = c > -INFINITY;
+            key[i] = route_key(c, e, valid);
+            valid_n += __popcll(__ballot(valid));
+        }
+    } else { // softmax: rank on exp(l - max)
+        float m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            m = fmaxf(m, lv[i]);
+        m = wave_max(m);
+        float val[NI];
+        bool any_nan = false;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            val[i] = expf(lv[i] - m);
+            any_nan |= lane + 64 * i < E && __builtin_isnan(val[i]);
+        }
+        // a NaN among the exp values makes the sum, and so every score, NaN:
+        // nothing is selectable
+        const bool none = __ballot(any_nan) != 0;
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            key[i] = route_key(val[i], lane + 64 * i, !none && lane + 64 * i < E);
+        valid_n = none ? 0 : E;
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        L.nkey[w][lane + 64 * i] = 0ull - key[i];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const int Epad = (E + 15) & ~15; // keys past E are 0 and never count
+    const int ch = ((Epad / NW) + 15) & ~15;
+    const int j0 = w * ch, j1 = min(Epad, j0 + ch);
+    int rank[NI];
+    count_greater<NI>(L.nkey[w], j0, j1, key, NI, rank);
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        L.prank[w][lane + 64 * i] = rank[i];
+    __syncthreads();
+    int e = 0;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        int r = 0;
+#pragma unroll
+        for (int v = 0; v < NW; v++)
+            r += L.prank[v][lane + 64 * i];
+        rank[i] = r;
+        const unsigned long long hit = __ballot(key[i] != 0ull && r == s);
+        if (hit)
+            e = 64 * i + (int)__builtin_ctzll(hit);
+    }
+    if (s >= valid_n)
+        e = 0;
+    if (ids && w == 0) {
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            if (key[i] != 0ull && rank[i] < K)
+                ids[rank[i]] = (uint32_t)(lane + 64 * i);
+        if (lane >= valid_n && lane < K)
+            ids[lane] = 0;
+    }
+    return e;
+}
+
 __device__ __forceinline__ float gates_post(float g, int K, int gating, int weights_norm,
                                             float weights_scale) {
     if (gating == 3) {
