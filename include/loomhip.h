@@ -60,6 +60,9 @@ extern "C" {
                                        (llama.zig moeRun 1363-1398) */
 #define LOOMHIP_COMBINE_EXPERT_ASC 1 /* out += per expert in ascending id order
                                         (llama.zig moeBatchUnion 1844-1903) */
+#define LOOMHIP_COMBINE_SELECTION_ADD 2 /* out = out + (the selection-order sum):
+                                           moeLayer then the residual add
+                                           (llama.zig:1222) */
 
 /* ---- lifecycle ------------------------------------------------------------ */
 
@@ -174,6 +177,67 @@ typedef struct {
 int loomhip_moe_layer_dev(const loomhip_moe_layer *L, const float *normed, size_t n_tok,
                           int combine, float *out, uint32_t *ids_out, float *gates_out,
                           void *stream);
+
+/* ---- whole-token decode frame --------------------------------------------- */
+
+/* Numerics of the frame's f32 reductions.  PARITY: every rmsnorm sums its
+ * squares in the reference's sequential order (tensor.zig:9-15), so with
+ * the matvecs, the attention within 64 positions and the per-head norms
+ * already in the reference's order the step is bit-identical to the CPU
+ * path wherever exp agrees (a sliver of inputs) -- at ~dim dependent adds per
+ * norm.  FAST: rmsnorm sums as a fixed tree (the embedding row's excepted);
+ * last-bit differences may then move one int8 step of a quantized matvec
+ * input (the 2e-3 logit tolerance). */
+#define LOOMHIP_NUMERICS_PARITY 0
+#define LOOMHIP_NUMERICS_FAST 1
+
+/* One GQA layer, the LayerSpec of src/compute/cpu.zig:116-138 with device
+ * pointers: norms f32, weights in the device layout ([out][in] rows), and
+ * either the routed MoE layer (is_moe) or a dense SwiGLU FFN. */
+typedef struct {
+    const float *attn_norm, *ffn_norm; /* [dim] */
+    const float *q_norm, *k_norm;      /* [head_dim] per-head RMSNorm weights, NULL when absent */
+    int wq_t, wk_t, wv_t, wo_t;
+    const void *wq, *wk, *wv, *wo; /* [n_heads*hd][dim], [kvd][dim] x2, [dim][n_heads*hd] */
+    int is_moe;
+    loomhip_moe_layer moe;
+    int ffn_gate_t, ffn_up_t, ffn_down_t; /* dense FFN (is_moe == 0) */
+    const void *ffn_gate, *ffn_up, *ffn_down;
+    size_t ffn;
+} loomhip_layer;
+
+typedef struct {
+    size_t dim, head_dim, n_layers, n_heads, n_kv_heads, vocab, ctx_len, rope_dim;
+    float rope_base, eps;
+    int rope_neox; /* 1: NEOX (split-half) pairs, 0: NORM (adjacent) pairs */
+    int embed_t;
+    const void *embed; /* [vocab][dim] device layout */
+    const float *out_norm;
+    int output_t;
+    const void *output;           /* [vocab][dim] device layout */
+    const loomhip_layer *layers;  /* host array of n_layers */
+    /* RoPE (cos, sin) per (position, pair) [ctx_len][rope_dim/2][2] on the
+     * device, as the caller's ropeTheta computes them (llama.zig:821-826), or
+     * NULL: the library computes them once on the host with the C library's
+     * powf/cosf/sinf in ropeTheta's expressions and keeps them. */
+    const float *rope_cs;
+    int numerics; /* LOOMHIP_NUMERICS_* */
+} loomhip_model;
+
+/* One decode step of n lanes on the device, the whole token as one
+ * stream-ordered submission: embedding of tokens[n] (device), every layer
+ * (attention against the fp16 K/V caches [n][n_layers][ctx_len][kvd], the
+ * new row appended at pos[n] (device)), the output head into logits
+ * [n][vocab] (device), then the greedy token into next[n] (device, may be
+ * NULL or alias tokens) and pos += 1.  n == 1 follows llama.step (MoE in
+ * selection order, then the residual add); n > 1 decodeBatch
+ * (moeBatchUnion).  Replaces the frame calls of src/compute/backend.zig:
+ * 141-191 (beginFrame, layerBlock x n_layers, endFrame; attnInit/kvAppend/
+ * attnHeads for the cache) for a model held on the device.  Capturable in a
+ * HIP graph once one eager call has sized the workspace for this n. */
+int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int32_t *pos, size_t n,
+                            uint16_t *k_cache, uint16_t *v_cache, float *logits, uint32_t *next,
+                            void *stream);
 
 #ifdef __cplusplus
 }

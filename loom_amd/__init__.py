@@ -20,8 +20,9 @@ HEADER = os.path.join(ROOT, "include", "loomhip.h")
 OK, DECLINED, ERR_ARG, ERR_HIP, ERR_INIT = 0, 1, -1, -2, -3
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
 GATING_SOFTMAX, GATING_SIGMOID, GATING_SOFTMAX_TOPK = 1, 2, 3
-COMBINE_SELECTION, COMBINE_EXPERT_ASC = 0, 1
+COMBINE_SELECTION, COMBINE_EXPERT_ASC, COMBINE_SELECTION_ADD = 0, 1, 2
 KT_GATE_UP, KT_DOWN, KT_DENSE = 0, 1, 2
+NUMERICS_PARITY, NUMERICS_FAST = 0, 1
 KT_NAMES = {KT_GATE_UP: "gate_up", KT_DOWN: "down", KT_DENSE: "dense"}
 
 
@@ -49,6 +50,60 @@ class MoeLayerDesc(C.Structure):
         ("gate", C.c_void_p),
         ("up", C.c_void_p),
         ("down", C.c_void_p),
+    ]
+
+
+class LayerDesc(C.Structure):
+    """Mirror of ``loomhip_layer`` in include/loomhip.h."""
+
+    _fields_ = [
+        ("attn_norm", C.c_void_p),
+        ("ffn_norm", C.c_void_p),
+        ("q_norm", C.c_void_p),
+        ("k_norm", C.c_void_p),
+        ("wq_t", C.c_int),
+        ("wk_t", C.c_int),
+        ("wv_t", C.c_int),
+        ("wo_t", C.c_int),
+        ("wq", C.c_void_p),
+        ("wk", C.c_void_p),
+        ("wv", C.c_void_p),
+        ("wo", C.c_void_p),
+        ("is_moe", C.c_int),
+        ("moe", MoeLayerDesc),
+        ("ffn_gate_t", C.c_int),
+        ("ffn_up_t", C.c_int),
+        ("ffn_down_t", C.c_int),
+        ("ffn_gate", C.c_void_p),
+        ("ffn_up", C.c_void_p),
+        ("ffn_down", C.c_void_p),
+        ("ffn", C.c_size_t),
+    ]
+
+
+class ModelDesc(C.Structure):
+    """Mirror of ``loomhip_model`` in include/loomhip.h."""
+
+    _fields_ = [
+        ("dim", C.c_size_t),
+        ("head_dim", C.c_size_t),
+        ("n_layers", C.c_size_t),
+        ("n_heads", C.c_size_t),
+        ("n_kv_heads", C.c_size_t),
+        ("vocab", C.c_size_t),
+        ("ctx_len", C.c_size_t),
+        ("rope_dim", C.c_size_t),
+        ("rope_base", C.c_float),
+        ("eps", C.c_float),
+        ("rope_neox", C.c_int),
+        ("embed_t", C.c_int),
+        ("embed", C.c_void_p),
+        ("out_norm", C.c_void_p),
+        ("output_t", C.c_int),
+        ("output", C.c_void_p),
+        ("layers", C.POINTER(LayerDesc)),
+        ("rope_cs", C.c_void_p),
+        ("numerics", C.c_int),
     ]
 
 
@@ -105,6 +160,7 @@ def lib() -> C.CDLL:
         "loomhip_matvec_dev": (i, [i, vp, vp, vp, sz, sz, sz, vp]),
         "loomhip_dequant_dev": (i, [i, vp, vp, sz, sz, vp]),
         "loomhip_moe_layer_dev": (i, [C.POINTER(MoeLayerDesc), vp, sz, i, vp, vp, vp, vp]),
+        "loomhip_token_frame_dev": (i, [C.POINTER(ModelDesc), vp, vp, sz, vp, vp, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

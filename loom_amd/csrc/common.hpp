@@ -77,6 +77,13 @@ __device__ inline float half_bits_to_float(uint32_t bits16) {
     return __half2float(__half(r));
 }
 
+// exp(x) rounded once to f32: the double-precision exponential (far below
+// half an f32 ulp of error) then one rounding, so the result is the
+// correctly rounded f32 exp except when exp(x) lies within a double ulp of
+// an f32 rounding midpoint.  The CPU path's expf is itself within 0.502 ulp,
+// so the two agree on all but a sliver of inputs.
+__device__ inline float exp_f32(float x) { return (float)exp((double)x); }
+
 // Round half away from zero, saturate at +-127, non-finite -> 0
 // (src/gguf/ggml.zig:1067-1073 toI8Saturating).
 // Branch-free: round, clamp with med3, then select.

@@ -141,7 +141,7 @@ __device__ __forceinline__ float decode_gates(const DecodeParams &p, int my_id,
             if ((my_id >> 6) == i)
                 l = v;
         }
-        g = p.gating == 2 ? 1.0f / (1.0f + expf(-l)) : l;
+        g = p.gating == 2 ? 1.0f / (1.0f + exp_f32(-l)) : l;
     } else {
         float mx = -INFINITY;
 #pragma unroll
@@ -150,7 +150,7 @@ __device__ __forceinline__ float decode_gates(const DecodeParams &p, int my_id,
         mx = wave_max(mx);
 #pragma unroll
         for (int i = 0; i < NI; i++)
-            sc[lane + 64 * i] = expf(lv[i] - mx);
+            sc[lane + 64 * i] = exp_f32(lv[i] - mx);
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         const float inv = 1.0f / lds_seq_sum(sc, p.n_expert);
@@ -174,7 +174,7 @@ constexpr int DN_UB = 8; // weight rows per lane requested at once in the down k
 //   5. every (slot, row) value summed over its blocks in block order, then
 //      the combine: mode 0 (moeRun) out = ((0 + g0*y0) + g1*y1) + ... in
 //      selection order; mode 1 (moeBatchUnion) out += g*y per expert in
-//      ascending expert id
+//      ascending expert id; mode 2 out = out + (the mode-0 sum)
 template <int T>
 __global__ __launch_bounds__(256) void moe_down_decode_kernel(DecodeParams p) {
     using F = Fmt<T>;
@@ -315,13 +315,13 @@ __global__ __launch_bounds__(256) void moe_down_decode_kernel(DecodeParams p) {
         if (row >= rows)
             continue;
         float *o = p.out + (size_t)t * rows + row;
-        if (p.mode == 0) {
+        if (p.mode != 1) {
             float acc = 0.0f;
             for (int sl = 0; sl < K; sl++) {
                 const float pr = s_gates[sl] * yv[sl * TR + r];
                 acc = acc + pr;
             }
-            *o = acc;
+            *o = p.mode == 2 ? *o + acc : acc;
         } else {
             float acc = *o;
             int prev = -1;

@@ -9,6 +9,65 @@ namespace lh {
 
 constexpr int MAX_E = 256, MAX_K = 16, MAX_TOK = 256; // routing limits
 
+// ---- exact dequant of one value from the device layout ------------------------
+// f32 arithmetic in the reference's two-rounding form (src/gguf/ggml.zig:
+// 1342-1374 Q4_K, 1420-1471 Q6_K, 1834-1849 Q4_0/Q8_0); value (r, c) of a
+// rows x cols matrix.
+__device__ inline float dequant_value(int t, const uint8_t *__restrict__ w, size_t rows, size_t cols,
+                                      size_t r, size_t c) {
+    const int be = block_elems(t);
+    const size_t nb = cols / be;
+    const size_t unit = r * nb + c / be;
+    const size_t U = rows * nb;
+    const int e = (int)(c % be);
+    if (t == LH_Q4_K) {
+        const uint8_t *blk = w + unit * 144;
+        const float d = half_bits_to_float(blk[0] | (blk[1] << 8));
+        const float dmin = half_bits_to_float(blk[2] | (blk[3] << 8));
+        const uint8_t *s = blk + 4;
+        const int g = e / 32, l = e % 32;
+        int sc, m;
+        if (g < 4) {
+            sc = s[g] & 63;
+            m = s[g + 4] & 63;
+        } else {
+            sc = (s[g + 4] & 0xF) | ((s[g - 4] >> 6) << 4);
+            m = (s[g + 4] >> 4) | ((s[g] >> 6) << 4);
+        }
+        const uint8_t byte = blk[16 + 32 * (g / 2) + l];
+        const int qv = (g & 1) ? (byte >> 4) : (byte & 0xF);
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        return d1 * (float)qv - m1;
+    }
+    if (t == LH_Q6_K) {
+        const uint8_t *ql = w + unit * 128, *qh = w + U * 128 + unit * 64;
+        const int8_t *sc = (const int8_t *)(w + U * 192 + unit * 16);
+        const uint16_t *dp = (const uint16_t *)(w + U * 208);
+        const float d = half_bits_to_float(dp[unit]);
+        const int h = e / 128, r128 = e % 128, quarter = r128 / 32, l = r128 % 32;
+        const uint8_t qlb = ql[64 * h + l + ((quarter & 1) ? 32 : 0)];
+        const uint8_t qhb = qh[32 * h + l];
+        const int nib = (quarter < 2) ? (qlb & 0xF) : (qlb >> 4);
+        const int qv = nib | (((qhb >> (2 * quarter)) & 3) << 4);
+        const float s = d * (float)sc[8 * h + l / 16 + 2 * quarter];
+        return s * ((float)qv - 32.0f);
+    }
+    if (t == LH_Q8_0) {
+        const int8_t *qs = (const int8_t *)(w + unit * 32);
+        const uint16_t *dp = (const uint16_t *)(w + U * 32);
+        return (float)qs[e] * half_bits_to_float(dp[unit]);
+    }
+    if (t == LH_Q4_0) {
+        const uint8_t *qs = w + unit * 16;
+        const uint16_t *dp = (const uint16_t *)(w + U * 16);
+        const int nib = e < 16 ? (qs[e] & 0xF) : (qs[e - 16] >> 4);
+        return (float)(nib - 8) * half_bits_to_float(dp[unit]);
+    }
+    if (t == LH_F16)
+        return half_bits_to_float(((const uint16_t *)w)[r * cols + c]);
+    return ((const float *)w)[r * cols + c];
+}
+
 // ---- wave-level int8 activation quantizers ------------------------------------
 
 // Four consecutive floats; COHERENT reads them through relaxed agent-scope
@@ -409,7 +468,7 @@ __device__ __forceinline__ void route_exact_wave(const float *lg, const float *s
     if (gating == 2) { // sigmoid (tensor.zig:34-36)
 #pragma unroll
         for (int i = 0; i < NI; i++)
-            sv[i] = 1.0f / (1.0f + expf(-sv[i]));
+            sv[i] = 1.0f / (1.0f + exp_f32(-sv[i]));
     } else if (gating != 3) { // softmax (tensor.zig:18-28)
         float m = -INFINITY;
 #pragma unroll
@@ -418,7 +477,7 @@ __device__ __forceinline__ void route_exact_wave(const float *lg, const float *s
         m = wave_max(m);
 #pragma unroll
         for (int i = 0; i < NI; i++) {
-            sv[i] = expf(sv[i] - m);
+            sv[i] = exp_f32(sv[i] - m);
             L.sc[lane + 64 * i] = sv[i];
         }
         __builtin_amdgcn_wave_barrier();
@@ -483,7 +542,7 @@ __device__ __forceinline__ void route_rank(const float *lg, const float *sel_bia
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int e = lane + 64 * i;
-            val[i] = gating == 2 ? 1.0f / (1.0f + expf(-lv[i])) : lv[i];
+            val[i] = gating == 2 ? 1.0f / (1.0f + exp_f32(-lv[i])) : lv[i];
             const float c = e < E ? (sel_bias ? val[i] + bv[i] : val[i]) : -INFINITY;
             const bool valid = c > -INFINITY;
             key[i] = route_key(c, e, valid);
@@ -498,7 +557,7 @@ __device__ __forceinline__ void route_rank(const float *lg, const float *sel_bia
         bool any_nan = false;
 #pragma unroll
         for (int i = 0; i < NI; i++) {
-            val[i] = expf(lv[i] - m);
+            val[i] = exp_f32(lv[i] - m);
             if (lane + 64 * i < E)
                 any_nan |= __builtin_isnan(val[i]);
             if (NW == 1 || (int)threadIdx.x < 64) // the copy route_finish sums
@@ -563,7 +622,7 @@ __device__ __forceinline__ int route_decode_slot(const float *lg, const float *s
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int e = lane + 64 * i;
-            const float val = gating == 2 ? 1.0f / (1.0f + expf(-lv[i])) : lv[i];
+            const float val = gating == 2 ? 1.0f / (1.0f + exp_f32(-lv[i])) : lv[i];
             const float c = e < E ? (sel_bias ? val + bv[i] : val) : -INFINITY;
             const bool valid = c > -INFINITY;
             key[i] = route_key(c, e, valid);
@@ -579,7 +638,7 @@ __device__ __forceinline__ int route_decode_slot(const float *lg, const float *s
         bool any_nan = false;
 #pragma unroll
         for (int i = 0; i < NI; i++) {
-            val[i] = expf(lv[i] - m);
+            val[i] = exp_f32(lv[i] - m);
             any_nan |= lane + 64 * i < E && __builtin_isnan(val[i]);
         }
         // a NaN among the exp values makes the sum, and so every score, NaN:
@@ -635,7 +694,7 @@ __device__ __forceinline__ float gates_post(float g, int K, int gating, int weig
         float m = -INFINITY;
         for (int s = 0; s < K; s++)
             m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), s)));
-        g = expf(g - m);
+        g = exp_f32(g - m);
         const float inv = 1.0f / slot_sum(g, K);
         g = g * inv;
     }

@@ -110,8 +110,9 @@ __global__ __launch_bounds__(256) void dmmv_kernel(DmmvParams p) {
         const int k = idx / TR, rl = idx % TR, row = row0 + rl;
         if (row >= p.rows)
             continue;
-        p.out[(size_t)p.pair_dst[g.first + k] * p.out_stride + row] =
-            row_value<FUSED>(lds, lds_mat, (size_t)k * TR + rl, nb);
+        float *o = p.out + (size_t)p.pair_dst[g.first + k] * p.out_stride + row;
+        const float v = row_value<FUSED>(lds, lds_mat, (size_t)k * TR + rl, nb);
+        *o = p.accumulate ? *o + v : v;
     }
 }
 

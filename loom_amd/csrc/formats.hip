@@ -19,66 +19,14 @@ void launch_quant_act(int wtype, const float *x, int cols, int x_stride, int nve
 }
 
 // ---- exact dequant from the device layout ---------------------------------
-// One thread per value; f32 arithmetic in the reference's two-rounding form
-// (src/gguf/ggml.zig:1342-1374, 1420-1471, 1834-1849).
+// One thread per value (dequant_value, device.hpp).
 
 __global__ void dequant_kernel(int t, const uint8_t *__restrict__ w, size_t rows, size_t cols,
                                float *__restrict__ out) {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= rows * cols)
         return;
-    const size_t r = idx / cols, c = idx % cols;
-    const int be = block_elems(t);
-    const size_t nb = cols / be;
-    const size_t unit = r * nb + c / be;
-    const size_t U = rows * nb;
-    const int e = (int)(c % be);
-    float val = 0.0f;
-    if (t == LH_Q4_K) {
-        const uint8_t *blk = w + unit * 144;
-        const float d = half_bits_to_float(blk[0] | (blk[1] << 8));
-        const float dmin = half_bits_to_float(blk[2] | (blk[3] << 8));
-        const uint8_t *s = blk + 4;
-        const int g = e / 32, l = e % 32;
-        int sc, m;
-        if (g < 4) {
-            sc = s[g] & 63;
-            m = s[g + 4] & 63;
-        } else {
-            sc = (s[g + 4] & 0xF) | ((s[g - 4] >> 6) << 4);
-            m = (s[g + 4] >> 4) | ((s[g] >> 6) << 4);
-        }
-        const uint8_t byte = blk[16 + 32 * (g / 2) + l];
-        const int qv = (g & 1) ? (byte >> 4) : (byte & 0xF);
-        const float d1 = d * (float)sc, m1 = dmin * (float)m;
-        val = d1 * (float)qv - m1;
-    } else if (t == LH_Q6_K) {
-        const uint8_t *ql = w + unit * 128, *qh = w + U * 128 + unit * 64;
-        const int8_t *sc = (const int8_t *)(w + U * 192 + unit * 16);
-        const uint16_t *dp = (const uint16_t *)(w + U * 208);
-        const float d = half_bits_to_float(dp[unit]);
-        const int h = e / 128, r128 = e % 128, quarter = r128 / 32, l = r128 % 32;
-        const uint8_t qlb = ql[64 * h + l + ((quarter & 1) ? 32 : 0)];
-        const uint8_t qhb = qh[32 * h + l];
-        const int nib = (quarter < 2) ? (qlb & 0xF) : (qlb >> 4);
-        const int qv = nib | (((qhb >> (2 * quarter)) & 3) << 4);
-        const float s = d * (float)sc[8 * h + l / 16 + 2 * quarter];
-        val = s * ((float)qv - 32.0f);
-    } else if (t == LH_Q8_0) {
-        const int8_t *qs = (const int8_t *)(w + unit * 32);
-        const uint16_t *dp = (const uint16_t *)(w + U * 32);
-        val = (float)qs[e] * half_bits_to_float(dp[unit]);
-    } else if (t == LH_Q4_0) {
-        const uint8_t *qs = w + unit * 16;
-        const uint16_t *dp = (const uint16_t *)(w + U * 16);
-        const int nib = e < 16 ? (qs[e] & 0xF) : (qs[e - 16] >> 4);
-        val = (float)(nib - 8) * half_bits_to_float(dp[unit]);
-    } else if (t == LH_F16) {
-        val = half_bits_to_float(((const uint16_t *)w)[idx]);
-    } else {
-        val = ((const float *)w)[idx];
-    }
-    out[idx] = val;
+    out[idx] = dequant_value(t, w, rows, cols, idx / cols, idx % cols);
 }
 
 void launch_dequant(int t, const void *w, size_t rows, size_t cols, float *out, hipStream_t st) {

@@ -1,0 +1,744 @@
+// frame.hip -- the whole-token decode frame: embedding, every GQA layer
+// (attention + dense FFN or routed MoE), the output head and the greedy pick,
+// stream-ordered on the device with no host round trip
+// (src/gguf/llama.zig step 1111-1227 at one lane, decodeBatch 1939-2043 at
+// n lanes; the one-submission shape of the reference's frames,
+// src/compute/backend.zig:141-191).
+//
+// Per layer:
+//   norm_quant     rmsnorm(x) * attn_norm, int8-quantized for wq/wk/wv
+//   dmmv x3        q, k, v (grouped matvec, bit-identical to the CPU kernels)
+//   qk_rope        per-head Q/K RMSNorm, RoPE (NEOX or NORM), K/V append (fp16)
+//   attn_partial   scores, softmax pieces and P.V for 64 positions x one KV
+//                  head group (split over the context, flash-decoding style;
+//                  within 64 positions the reference's own order)
+//   attn_combine   partials merged per head, int8-quantized for wo
+//   dmmv (+=)      x += wo . attn
+//   norm_quant     rmsnorm(x) * ffn_norm (f32 for the router, or int8)
+//   MoE layer      (moe_host.hip) with the residual add, or the dense SwiGLU
+//                  FFN with x += down . act
+// then norm_quant + the output dmmv + argmax (sampler.zig:7-15), pos += 1.
+//
+// Numerics: every matvec is bit-identical to the reference's int8 kernels
+// on identical inputs, and so are the attention scores (dotF32 order), the
+// per-head Q/K RMSNorm and, up to 64 positions, the softmax and P.V in the
+// reference's order.  RoPE's cos/sin come from a host table in ropeTheta's
+// own expressions, and exp is the once-rounded double exponential.
+// rmsnorm's sum of squares is the reference's sequential sum in PARITY mode
+// (and always for the embedding row) and a fixed tree in FAST mode; past 64
+// positions softmax's sum and P.V are a split-context merge.  Last-bit
+// differences from these can move one int8 step of a quantized matvec
+// input (the 2e-3 layer/logit tolerance).
+#include "device.hpp"
+#include "runtime.hpp"
+
+#include <cmath>
+#include <string>
+#include <vector>
+
+namespace lh {
+
+constexpr int ATT_TC = 64;  // positions per attention work group (one per lane of a wave)
+constexpr int MAX_HD = 256; // head_dim limit
+constexpr int MAX_G = 16;   // query heads per KV head limit
+
+struct FrameDims {
+    int dim, hd, n_heads, n_kv, qd, kvd, ctx, rope_dim, rope_neox, n_layers, vocab;
+    float rope_base, eps, scale;
+};
+
+// ---- reductions ----------------------------------------------------------------
+
+__device__ inline float wave_sum_f(float v) {
+    v = v + dpp_f<0xB1>(v, v);
+    v = v + dpp_f<0x4E>(v, v);
+    v = v + dpp_f<0x141>(v, v);
+    v = v + dpp_f<0x140>(v, v);
+    v = v + dpp_f<0x142, 0xA>(v, v);
+    v = v + dpp_f<0x143, 0xC>(v, v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Sum over the work group's waves (each value is already wave-uniform),
+// added in wave order.
+__device__ inline float block_sum_waves(float wave_total, float *lds) {
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0)
+        lds[wave] = wave_total;
+    __syncthreads();
+    float s = 0.0f;
+    for (int w = 0; w < nw; w++)
+        s = s + lds[w];
+    return s;
+}
+
+// ---- embedding: x[lane] = dequantRow(embed, token) (llama.zig:1122) -------------
+
+__global__ void embed_kernel(int t, const uint8_t *__restrict__ w, int vocab, int dim,
+                             const uint32_t *__restrict__ tokens, float *__restrict__ x) {
+    const int lane = blockIdx.y, c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= dim)
+        return;
+    const uint32_t tok = tokens[lane];
+    const size_t r = tok < (uint32_t)vocab ? tok : (uint32_t)(vocab - 1); // never past the table
+    x[(size_t)lane * dim + c] = dequant_value(t, w, vocab, dim, r, c);
+}
+
+// ---- rmsnorm (tensor.zig:9-15) + int8 quantization for weight type QB --------------
+// One work group per lane; thread c owns the 32-value chunk c (dim <= 8192).
+// out_i = (x_i * scale) * w_i with scale = 1 / sqrt(ss/n + eps).  EXACT: ss
+// is the reference's sequential sum (one thread over the squares in index
+// order, ~dim dependent adds); otherwise per chunk in order, then across
+// chunks as a fixed tree.  The exact form is used where the input is an
+// embedding row: its values sit on a few quantization levels, so int8
+// rounding of the normed vector meets exact .5 ties that a one-ulp
+// difference in the scale would flip.  qa (QB = 32 or 256) and normed are
+// each optional.
+template <int QB, bool EXACT>
+__global__ __launch_bounds__(256) void norm_quant_kernel(const float *__restrict__ x, int dim,
+                                                         const float *__restrict__ w, float eps,
+                                                         QAct qa, float *__restrict__ normed) {
+    __shared__ float red[4];
+    __shared__ __align__(16) float sq[EXACT ? 8192 : 1];
+    const int lane_v = blockIdx.x, c = threadIdx.x, chunks = dim / 32;
+    const bool live = c < chunks;
+    const int cc = live ? c : chunks - 1;
+    const float *xv = x + (size_t)lane_v * dim + (size_t)cc * 32;
+    float4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        v[i] = *(const float4 *)(xv + 4 * i);
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        ss = ss + v[i].x * v[i].x;
+        ss = ss + v[i].y * v[i].y;
+        ss = ss + v[i].z * v[i].z;
+        ss = ss + v[i].w * v[i].w;
+    }
+    ss = live ? ss : 0.0f;
+    float total;
+    if constexpr (EXACT) {
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float4 p;
+                p.x = v[i].x * v[i].x;
+                p.y = v[i].y * v[i].y;
+                p.z = v[i].z * v[i].z;
+                p.w = v[i].w * v[i].w;
+                *(float4 *)(sq + c * 32 + 4 * i) = p;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float acc = 0.0f;
+            for (int i = 0; i < dim; i += 4) {
+                const float4 p = *(const float4 *)(sq + i);
+                acc = acc + p.x;
+                acc = acc + p.y;
+                acc = acc + p.z;
+                acc = acc + p.w;
+            }
+            red[0] = acc;
+        }
+        __syncthreads();
+        total = red[0];
+    } else {
+        total = block_sum_waves(wave_sum_f(ss), red);
+    }
+    const float scale = 1.0f / sqrtf(total / (float)dim + eps);
+    const float *wv = w + (size_t)cc * 32;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 g = *(const float4 *)(wv + 4 * i);
+        v[i].x = (v[i].x * scale) * g.x;
+        v[i].y = (v[i].y * scale) * g.y;
+        v[i].z = (v[i].z * scale) * g.z;
+        v[i].w = (v[i].w * scale) * g.w;
+    }
+    if (normed && live) {
+        float *o = normed + (size_t)lane_v * dim + (size_t)c * 32;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            *(float4 *)(o + 4 * i) = v[i];
+    }
+    if constexpr (QB == 32 || QB == 256) {
+        if (qa.q) {
+            const int ns = QB == 256 ? dim / 16 : dim / 32;
+            quant_chunk32<QB>(v, live, c, qa.q + (size_t)lane_v * dim, qa.d + (size_t)lane_v * (dim / QB),
+                              qa.s + (size_t)lane_v * ns);
+        }
+    }
+}
+
+// ---- per-head Q/K RMSNorm (llama.zig:938-949), RoPE (821-855), K/V append ----------
+// Work group (head, lane): heads [0, n_heads) are query heads, the next
+// n_kv are KV heads (their k rotated and appended, v appended as is).
+__global__ __launch_bounds__(64) void qk_rope_kernel(FrameDims D, const float *__restrict__ q,
+                                                     const float *__restrict__ k,
+                                                     const float *__restrict__ v,
+                                                     const float *__restrict__ q_norm,
+                                                     const float *__restrict__ k_norm,
+                                                     const int32_t *__restrict__ pos, int li,
+                                                     const float *__restrict__ rope_cs,
+                                                     float *__restrict__ q_out,
+                                                     uint16_t *__restrict__ kc,
+                                                     uint16_t *__restrict__ vc) {
+    __shared__ float hv[MAX_HD];
+    const int h = blockIdx.x, t = blockIdx.y, hd = D.hd, tid = threadIdx.x;
+    const bool isq = h < D.n_heads;
+    const int kvh = h - D.n_heads;
+    const float *src = isq ? q + (size_t)t * D.qd + (size_t)h * hd : k + (size_t)t * D.kvd + (size_t)kvh * hd;
+    const float *nw = isq ? q_norm : k_norm;
+    __shared__ float s_inv;
+    for (int i = tid; i < hd; i += 64)
+        hv[i] = src[i];
+    if (nw) {
+        // headNorm's sum of squares in the reference's order (hd dependent
+        // adds on one thread: the normalised heads feed the attention scores
+        // and, through them, an int8-quantized matvec input)
+        __syncthreads();
+        if (tid == 0) {
+            float ss = 0.0f;
+            for (int i = 0; i < hd; i++) {
+                const float pr = hv[i] * hv[i];
+                ss = ss + pr;
+            }
+            s_inv = 1.0f / sqrtf(ss / (float)hd + D.eps);
+        }
+        __syncthreads();
+        const float inv = s_inv;
+        for (int i = tid; i < hd; i += 64)
+            hv[i] = (hv[i] * inv) * nw[i];
+    }
+    __syncthreads();
+    const int p = pos[t];
+    const int half = D.rope_dim / 2;
+    const float *csp = rope_cs + (size_t)min(max(p, 0), D.ctx - 1) * half * 2;
+    for (int i = tid; i < half; i += 64) {
+        const float cs = csp[2 * i], sn = csp[2 * i + 1];
+        const int ia = D.rope_neox ? i : 2 * i, ib = D.rope_neox ? i + half : 2 * i + 1;
+        const float a = hv[ia], b = hv[ib];
+        hv[ia] = a * cs - b * sn;
+        hv[ib] = a * sn + b * cs;
+    }
+    __syncthreads();
+    if (isq) {
+        float *o = q_out + (size_t)t * D.qd + (size_t)h * hd;
+        for (int i = tid; i < hd; i += 64)
+            o[i] = hv[i];
+        return;
+    }
+    if (p < 0 || p >= D.ctx) // a full cache takes no more rows
+        return;
+    const size_t base = (((size_t)t * D.n_layers + li) * D.ctx + p) * D.kvd + (size_t)kvh * hd;
+    const float *vs = v + (size_t)t * D.kvd + (size_t)kvh * hd;
+    for (int i = tid; i < hd; i += 64) {
+        kc[base + i] = __half_raw(__float2half(hv[i])).x;
+        vc[base + i] = __half_raw(__float2half(vs[i])).x;
+    }
+}
+
+// ---- attention over 64 positions for one KV head group (llama.zig:1162-1192) -------
+
+// dotF32 (src/gguf/ggml.zig:198-217) of a query head (f32) and a cached key
+// row (fp16, widened): 32 accumulators over whole 32-steps, leftover 8-chunks
+// into the first 8, ((a0 + a1) + a2) + a3 per lane, the lanes summed in order
+// from -0, then the scalar tail.
+__device__ inline float dot_f32_key(const float *a, const uint16_t *b, int n) {
+    float acc[32];
+#pragma unroll
+    for (int u = 0; u < 32; u++)
+        acc[u] = 0.0f;
+    int i = 0;
+    for (; i + 32 <= n; i += 32) {
+#pragma unroll
+        for (int u = 0; u < 32; u++) {
+            const float pr = a[i + u] * half_bits_to_float(b[i + u]);
+            acc[u] = acc[u] + pr;
+        }
+    }
+    for (; i + 8 <= n; i += 8) {
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const float pr = a[i + l] * half_bits_to_float(b[i + l]);
+            acc[l] = acc[l] + pr;
+        }
+    }
+    float s = -0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; l++)
+        s = s + (((acc[l] + acc[8 + l]) + acc[16 + l]) + acc[24 + l]);
+    for (; i < n; i++) {
+        const float pr = a[i] * half_bits_to_float(b[i]);
+        s = s + pr;
+    }
+    return s;
+}
+
+// Work group (chunk, kv head, lane).  Scores in dotF32 order times the scale;
+// per query head m = the chunk's max, e = exp(s - m), l = sum of e in
+// position order.  When the whole context is this one chunk (position < 64)
+// the record is the reference's own arithmetic (softmax, tensor.zig:18-28,
+// then out += p * v in position order): o = sum_t (e_t * (1/l)) * v_t with
+// l = 1; otherwise o = sum_t e_t * v_t, unnormalised, for the merge.  Record
+// per (lane, kv head, chunk): m[G], l[G], o[G][hd].
+__global__ __launch_bounds__(256) void attn_partial_kernel(FrameDims D, const float *__restrict__ q_rot,
+                                                           const uint16_t *__restrict__ kc,
+                                                           const uint16_t *__restrict__ vc,
+                                                           const int32_t *__restrict__ pos, int li,
+                                                           int n_chunks, float *__restrict__ part) {
+    extern __shared__ __align__(16) float smem[];
+    const int ch = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+    const int hd = D.hd, G = D.n_heads / D.n_kv;
+    const int p = min(pos[t], D.ctx - 1);
+    const int t0 = ch * ATT_TC, nt = min(ATT_TC, p + 1 - t0);
+    if (nt <= 0)
+        return; // past the current position: the merge reads no record from here
+    const bool single = p + 1 <= ATT_TC;
+    float *qs = smem;                                  // [G][hd]
+    float *sc = qs + G * hd;                           // [G][TC]
+    uint16_t *ks = (uint16_t *)(sc + G * ATT_TC);      // [TC][hd]
+    uint16_t *vs = ks + ATT_TC * hd;                   // [TC][hd]
+    const float *qsrc = q_rot + (size_t)t * D.qd + (size_t)kvh * G * hd;
+    for (int i = tid; i < G * hd; i += 256)
+        qs[i] = qsrc[i];
+    const size_t row0 = (((size_t)t * D.n_layers + li) * D.ctx + t0) * D.kvd + (size_t)kvh * hd;
+    const int per_row = hd / 8; // 16-byte pieces per row
+    for (int i = tid; i < nt * per_row; i += 256) {
+        const int r = i / per_row, c8 = i % per_row;
+        const size_t g = row0 + (size_t)r * D.kvd + 8 * c8;
+        *(uint4 *)(ks + r * hd + 8 * c8) = *(const uint4 *)(kc + g);
+        *(uint4 *)(vs + r * hd + 8 * c8) = *(const uint4 *)(vc + g);
+    }
+    __syncthreads();
+    for (int i = tid; i < G * ATT_TC; i += 256) {
+        const int g = i / ATT_TC, j = i % ATT_TC;
+        sc[i] = j < nt ? dot_f32_key(qs + g * hd, ks + j * hd, hd) * D.scale : -INFINITY;
+    }
+    __syncthreads();
+    const int wave = tid >> 6, ln = tid & 63;
+    float *rec = part + (((size_t)t * D.n_kv + kvh) * n_chunks + ch) * (size_t)G * (hd + 2);
+    for (int g = wave; g < G; g += 4) {
+        const float s = sc[g * ATT_TC + ln];
+        const float m = wave_max(s);
+        const float e = ln < nt ? exp_f32(s - m) : 0.0f;
+        sc[g * ATT_TC + ln] = e;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        float l = 0.0f;
+        for (int j = 0; j < nt; j++) // the reference's sum order
+            l = l + sc[g * ATT_TC + j];
+        if (single) {
+            const float inv = 1.0f / l;
+            sc[g * ATT_TC + ln] = e * inv;
+        }
+        if (ln == 0) {
+            rec[g] = m;
+            rec[G + g] = single ? 1.0f : l;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < G * hd; i += 256) {
+        const int g = i / hd, d = i % hd;
+        float acc = 0.0f;
+        for (int j = 0; j < nt; j++) {
+            const float pr = sc[g * ATT_TC + j] * half_bits_to_float(vs[j * hd + d]);
+            acc = acc + pr;
+        }
+        rec[2 * G + i] = acc;
+    }
+}
+
+// ---- merge the partials per head, quantize the attention output for wo -------------
+// Work group (256-value slice, lane); thread j -> value slice*256 + j.  Blocks
+// of QB values are QB consecutive threads (QB = 32: half a wave; 256: the
+// work group).
+template <int QB>
+__global__ __launch_bounds__(256) void attn_combine_kernel(FrameDims D, const float *__restrict__ part,
+                                                           const int32_t *__restrict__ pos,
+                                                           int n_chunks, QAct qa) {
+    __shared__ float red[4];
+    const int t = blockIdx.y, tid = threadIdx.x;
+    const int idx = blockIdx.x * 256 + tid;
+    const bool live = idx < D.qd;
+    const int hd = D.hd, G = D.n_heads / D.n_kv;
+    const int h = (live ? idx : D.qd - 1) / hd, d = (live ? idx : D.qd - 1) % hd;
+    const int kvh = h / G, g = h % G;
+    const int p = min(pos[t], D.ctx - 1);
+    const int nc = (p + 1 + ATT_TC - 1) / ATT_TC;
+    const size_t rs = (size_t)G * (hd + 2);
+    const float *rec0 = part + ((size_t)t * D.n_kv + kvh) * n_chunks * rs;
+    float val;
+    if (nc == 1) { // one chunk: its record is already the softmax-weighted sum
+        val = rec0[2 * G + (size_t)g * hd + d];
+    } else {
+        float M = -INFINITY;
+        for (int c = 0; c < nc; c++)
+            M = fmaxf(M, rec0[c * rs + g]);
+        float L = 0.0f, O = 0.0f;
+        for (int c = 0; c < nc; c++) {
+            const float wgt = exp_f32(rec0[c * rs + g] - M);
+            L = L + rec0[c * rs + G + g] * wgt;
+            O = O + rec0[c * rs + 2 * G + (size_t)g * hd + d] * wgt;
+        }
+        val = O / L;
+    }
+    // int8 quantization (quantizeX / quantizeX256) of QB-thread blocks
+    float a = live && __builtin_isfinite(val) ? fabsf(val) : 0.0f;
+    if constexpr (QB == 32) {
+        for (int m = 1; m < 32; m <<= 1)
+            a = fmaxf(a, __shfl_xor(a, m, 32));
+    } else {
+        const float wm = wave_max(a);
+        __syncthreads();
+        if ((tid & 63) == 0)
+            red[tid >> 6] = wm;
+        __syncthreads();
+        a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    }
+    const float dd = a / 127.0f;
+    const float inv = (dd != 0.0f && __builtin_isfinite(dd)) ? 1.0f / dd : 0.0f;
+    const int qv = live ? to_i8_sat(val * inv) : 0;
+    int sum = qv;
+    constexpr int SG = QB == 256 ? 16 : 32; // sum groups: per 16 (K-quants) or per block
+    for (int m = 1; m < SG; m <<= 1)
+        sum += __shfl_xor(sum, m, SG);
+    if (!live)
+        return;
+    const size_t vb = (size_t)t * D.qd;
+    qa.q[vb + idx] = (int8_t)qv;
+    if (idx % SG == 0)
+        qa.s[(size_t)t * (D.qd / SG) + idx / SG] = sum;
+    if (idx % QB == 0)
+        qa.d[(size_t)t * (D.qd / QB) + idx / QB] = __builtin_isfinite(dd) ? dd : 0.0f;
+}
+
+// ---- greedy pick (engine/sampler.zig:7-15: the first maximum wins), pos += 1 ------
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ logits, int vocab,
+                                                      uint32_t *__restrict__ next,
+                                                      int32_t *__restrict__ pos) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float *lg = logits + (size_t)t * vocab;
+    float best = -INFINITY;
+    int besti = 0x7fffffff; // no candidate yet
+    for (int i = tid; i < vocab; i += 1024) {
+        const float v = lg[i];
+        if (v > best) {
+            best = v;
+            besti = i;
+        }
+    }
+    // (value desc, index asc) over the work group
+    for (int m = 1; m < 64; m <<= 1) {
+        const float ov = __shfl_xor(best, m);
+        const int oi = __shfl_xor(besti, m);
+        if (ov > best || (ov == best && oi < besti)) {
+            best = ov;
+            besti = oi;
+        }
+    }
+    if ((tid & 63) == 0) {
+        bv[tid >> 6] = best;
+        bi[tid >> 6] = besti;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; w++)
+            if (bv[w] > best || (bv[w] == best && bi[w] < besti)) {
+                best = bv[w];
+                besti = bi[w];
+            }
+        if (next)
+            next[t] = besti == 0x7fffffff ? 0u : (uint32_t)besti; // nothing above -inf: index 0
+        pos[t] = pos[t] + 1;
+    }
+}
+
+// ---- host -------------------------------------------------------------------------
+
+static Scratch g_frame; // per-call workspace
+
+// RoPE tables computed on the host in ropeTheta's expressions
+// (llama.zig:821-826): exponent = i / rope_dim for the even index i,
+// freq = powf(base, -exponent), angle = pos * freq; kept per (ctx, rope_dim,
+// base) for the process.
+static const float *rope_table(int ctx, int rope_dim, float base) {
+    static std::unordered_map<std::string, float *> tables;
+    char key[96];
+    snprintf(key, sizeof key, "%d/%d/%a", ctx, rope_dim, base);
+    auto it = tables.find(key);
+    if (it != tables.end())
+        return it->second;
+    const int half = rope_dim / 2;
+    std::vector<float> h((size_t)ctx * half * 2);
+    for (int p = 0; p < ctx; p++)
+        for (int i = 0; i < half; i++) {
+            const float exponent = (float)(2 * i) / (float)rope_dim;
+            const float freq = powf(base, -exponent);
+            const float angle = (float)p * freq;
+            h[((size_t)p * half + i) * 2] = cosf(angle);
+            h[((size_t)p * half + i) * 2 + 1] = sinf(angle);
+        }
+    float *d = nullptr;
+    if (hipMalloc(&d, h.size() * 4) != hipSuccess)
+        return nullptr;
+    if (hipMemcpy(d, h.data(), h.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(d);
+        return nullptr;
+    }
+    tables[key] = d;
+    return d;
+}
+
+struct FrameWs {
+    float *x, *normed, *q, *k, *v, *qrot, *part, *act;
+    QAct qa_dim, qa_att, qa_ffn;
+    const DmmvGroup *groups; // lanes in groups of nt against plane 0
+    int n_groups, nt;
+    size_t bytes;
+};
+
+static FrameWs frame_layout(char *base, size_t n, const loomhip_model *m, size_t ffn_max,
+                            int n_chunks) {
+    FrameWs w{};
+    size_t off = 0;
+    auto take = [&](size_t b) {
+        size_t o = off;
+        off += align16(b);
+        return base ? base + o : nullptr;
+    };
+    const size_t dim = m->dim, qd = m->n_heads * m->head_dim, kvd = m->n_kv_heads * m->head_dim;
+    const size_t G = m->n_heads / m->n_kv_heads;
+    auto qtake = [&](size_t cols) {
+        QAct q;
+        q.q = (int8_t *)take(n * cols);
+        q.d = (float *)take(n * (cols / 32) * 4);
+        q.s = (int32_t *)take(n * (cols / 16) * 4);
+        return q;
+    };
+    w.x = (float *)take(n * dim * 4);
+    w.normed = (float *)take(n * dim * 4);
+    w.q = (float *)take(n * qd * 4);
+    w.k = (float *)take(n * kvd * 4);
+    w.v = (float *)take(n * kvd * 4);
+    w.qrot = (float *)take(n * qd * 4);
+    w.part = (float *)take(n * m->n_kv_heads * (size_t)n_chunks * G * (m->head_dim + 2) * 4);
+    w.act = (float *)take(n * (ffn_max ? ffn_max : 1) * 4);
+    w.qa_dim = qtake(dim);
+    w.qa_att = qtake(qd);
+    w.qa_ffn = qtake(ffn_max ? ffn_max : 32);
+    w.bytes = off;
+    return w;
+}
+
+static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameWs &w, size_t n,
+                         QAct x, float *out, int accumulate, hipStream_t st) {
+    DmmvParams p{};
+    p.w = (const uint8_t *)wt;
+    p.plane_bytes = 0;
+    p.rows = rows;
+    p.cols = cols;
+    p.xq = x.q;
+    p.xd = x.d;
+    p.xs = x.s;
+    p.pair_src = g_ctx.iota;
+    p.pair_dst = g_ctx.iota;
+    p.groups = w.groups;
+    p.n_groups = w.n_groups;
+    p.out = out;
+    p.out_stride = rows;
+    p.accumulate = accumulate;
+    p.rpw = dmmv_pick_rpw(t, cols, rows, w.n_groups, w.nt, false);
+    return launch_dmmv(t, w.nt, false, p, st);
+}
+
+template <bool EXACT>
+static void launch_norm_t(int qb, const float *x, int dim, const float *w, float eps, QAct qa,
+                          float *normed, size_t n, hipStream_t st) {
+    if (qb == 256)
+        hipLaunchKernelGGL((norm_quant_kernel<256, EXACT>), dim3(n), dim3(256), 0, st, x, dim, w, eps, qa,
+                           normed);
+    else if (qb == 32)
+        hipLaunchKernelGGL((norm_quant_kernel<32, EXACT>), dim3(n), dim3(256), 0, st, x, dim, w, eps, qa,
+                           normed);
+    else
+        hipLaunchKernelGGL((norm_quant_kernel<0, EXACT>), dim3(n), dim3(256), 0, st, x, dim, w, eps,
+                           QAct{}, normed);
+    note_launch();
+}
+
+static void launch_norm(int qb, const float *x, int dim, const float *w, float eps, QAct qa,
+                        float *normed, size_t n, hipStream_t st, bool exact = false) {
+    if (exact)
+        launch_norm_t<true>(qb, x, dim, w, eps, qa, normed, n, st);
+    else
+        launch_norm_t<false>(qb, x, dim, w, eps, qa, normed, n, st);
+}
+
+static int frame_check(const loomhip_model *m, size_t n, size_t *ffn_max) {
+    if (!m || !m->layers || n == 0 || n > 256)
+        return fail(LOOMHIP_ERR_ARG, "token_frame: bad model or lane count %zu (1..256)", n);
+    const size_t dim = m->dim, hd = m->head_dim, qd = m->n_heads * hd;
+    if (dim == 0 || dim % 32 || dim > 8192 || qd % 32 || hd == 0 || hd % 8 || hd > MAX_HD ||
+        m->n_kv_heads == 0 || m->n_heads % m->n_kv_heads || m->n_heads / m->n_kv_heads > MAX_G ||
+        m->rope_dim > hd || m->rope_dim % 2 || m->ctx_len == 0 || m->vocab == 0)
+        return fail(LOOMHIP_DECLINED, "token_frame: dims not served (dim %zu, head_dim %zu, heads %zu/%zu)",
+                    dim, hd, m->n_heads, m->n_kv_heads);
+    const int qb_out = act_block(m->output_t);
+    if (!dmmv_supported(m->output_t, (int)dim) || (qb_out == 256 && dim % 256))
+        return fail(LOOMHIP_DECLINED, "token_frame: output type %d not served", m->output_t);
+    *ffn_max = 0;
+    for (size_t li = 0; li < m->n_layers; li++) {
+        const loomhip_layer &l = m->layers[li];
+        const int qb = act_block(l.wq_t);
+        if (act_block(l.wk_t) != qb || act_block(l.wv_t) != qb || !dmmv_supported(l.wq_t, (int)dim) ||
+            !dmmv_supported(l.wk_t, (int)dim) || !dmmv_supported(l.wv_t, (int)dim) ||
+            !dmmv_supported(l.wo_t, (int)qd) || (qb == 256 && dim % 256) ||
+            (act_block(l.wo_t) == 256 && qd % 256))
+            return fail(LOOMHIP_DECLINED, "token_frame: layer %zu attention types not served", li);
+        if (l.is_moe) {
+            if (l.moe.dim != dim)
+                return fail(LOOMHIP_ERR_ARG, "token_frame: layer %zu MoE dim %zu != %zu", li, l.moe.dim, dim);
+        } else {
+            const int gq = act_block(l.ffn_gate_t);
+            if (l.ffn_gate_t != l.ffn_up_t || !dmmv_supported(l.ffn_gate_t, (int)dim) ||
+                !dmmv_supported(l.ffn_down_t, (int)l.ffn) || (gq == 256 && dim % 256) ||
+                (act_block(l.ffn_down_t) == 256 && l.ffn % 256) || l.ffn % 32)
+                return fail(LOOMHIP_DECLINED, "token_frame: layer %zu dense FFN types not served", li);
+            *ffn_max = l.ffn > *ffn_max ? l.ffn : *ffn_max;
+        }
+    }
+    return LOOMHIP_OK;
+}
+
+} // namespace lh
+
+using namespace lh;
+
+extern "C" {
+
+int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int32_t *pos, size_t n,
+                            uint16_t *k_cache, uint16_t *v_cache, float *logits, uint32_t *next,
+                            void *stream) {
+    if (int rc = require_ready())
+        return rc;
+    if (!tokens || !pos || !k_cache || !v_cache || !logits)
+        return fail(LOOMHIP_ERR_ARG, "token_frame: null argument");
+    size_t ffn_max = 0;
+    if (int rc = frame_check(m, n, &ffn_max))
+        return rc;
+    hipStream_t st = stream_of(stream);
+    const int n_chunks = (int)((m->ctx_len + ATT_TC - 1) / ATT_TC);
+    const FrameWs probe = frame_layout(nullptr, n, m, ffn_max, n_chunks);
+    if (int rc = g_frame.reserve(probe.bytes))
+        return rc;
+    FrameWs w = frame_layout((char *)g_frame.ptr, n, m, ffn_max, n_chunks);
+    w.nt = pick_nt((int)n);
+    w.groups = dense_groups((int)n, w.nt, &w.n_groups); // built once per lane count, before any capture
+    if (!w.groups)
+        return fail(LOOMHIP_ERR_HIP, "token_frame: group table");
+    FrameDims D;
+    D.dim = (int)m->dim;
+    D.hd = (int)m->head_dim;
+    D.n_heads = (int)m->n_heads;
+    D.n_kv = (int)m->n_kv_heads;
+    D.qd = D.n_heads * D.hd;
+    D.kvd = D.n_kv * D.hd;
+    D.ctx = (int)m->ctx_len;
+    D.rope_dim = (int)m->rope_dim;
+    D.rope_neox = m->rope_neox;
+    D.n_layers = (int)m->n_layers;
+    D.vocab = (int)m->vocab;
+    D.rope_base = m->rope_base;
+    D.eps = m->eps;
+    D.scale = 1.0f / sqrtf((float)m->head_dim); // llama.zig attn scale
+    const int G = D.n_heads / D.n_kv;
+    const size_t att_lds = (size_t)G * D.hd * 4 + (size_t)G * ATT_TC * 4 + 2 * (size_t)ATT_TC * D.hd * 2;
+    if (att_lds > 64 * 1024)
+        return fail(LOOMHIP_DECLINED, "token_frame: attention tile exceeds LDS (%zu B)", att_lds);
+
+    if (m->numerics != LOOMHIP_NUMERICS_PARITY && m->numerics != LOOMHIP_NUMERICS_FAST)
+        return fail(LOOMHIP_ERR_ARG, "token_frame: unknown numerics mode %d", m->numerics);
+    const bool parity = m->numerics == LOOMHIP_NUMERICS_PARITY;
+    const float *rope_cs = m->rope_cs ? m->rope_cs : rope_table(D.ctx, D.rope_dim, D.rope_base);
+    if (!rope_cs)
+        return fail(LOOMHIP_ERR_HIP, "token_frame: rope table");
+    hipLaunchKernelGGL(embed_kernel, dim3((D.dim + 255) / 256, n), dim3(256), 0, st, m->embed_t,
+                       (const uint8_t *)m->embed, D.vocab, D.dim, tokens, w.x);
+    note_launch();
+    for (size_t li = 0; li < m->n_layers; li++) {
+        const loomhip_layer &l = m->layers[li];
+        // attention block (llama.zig:1127-1201)
+        // layer 0 normalises the embedding row: exact sum in either mode
+        launch_norm(act_block(l.wq_t), w.x, D.dim, l.attn_norm, D.eps, w.qa_dim, nullptr, n, st,
+                    parity || li == 0);
+        if (!frame_matvec(l.wq_t, l.wq, D.qd, D.dim, w, n, w.qa_dim, w.q, 0, st) ||
+            !frame_matvec(l.wk_t, l.wk, D.kvd, D.dim, w, n, w.qa_dim, w.k, 0, st) ||
+            !frame_matvec(l.wv_t, l.wv, D.kvd, D.dim, w, n, w.qa_dim, w.v, 0, st))
+            return fail(LOOMHIP_ERR_ARG, "token_frame: q/k/v matvec declined");
+        hipLaunchKernelGGL(qk_rope_kernel, dim3(D.n_heads + D.n_kv, n), dim3(64), 0, st, D, w.q, w.k,
+                           w.v, l.q_norm, l.k_norm, pos, (int)li, rope_cs, w.qrot, k_cache, v_cache);
+        note_launch();
+        hipLaunchKernelGGL(attn_partial_kernel, dim3(n_chunks, D.n_kv, n), dim3(256), att_lds, st, D,
+                           w.qrot, k_cache, v_cache, pos, (int)li, n_chunks, w.part);
+        note_launch();
+        const int qb_o = act_block(l.wo_t);
+        if (qb_o == 256)
+            hipLaunchKernelGGL(attn_combine_kernel<256>, dim3((D.qd + 255) / 256, n), dim3(256), 0, st, D,
+                               w.part, pos, n_chunks, w.qa_att);
+        else
+            hipLaunchKernelGGL(attn_combine_kernel<32>, dim3((D.qd + 255) / 256, n), dim3(256), 0, st, D,
+                               w.part, pos, n_chunks, w.qa_att);
+        note_launch();
+        if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st))
+            return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
+        // FFN block (llama.zig:1203-1224)
+        if (l.is_moe) {
+            launch_norm(0, w.x, D.dim, l.ffn_norm, D.eps, QAct{}, w.normed, n, st, parity);
+            const int combine = n == 1 ? LOOMHIP_COMBINE_SELECTION_ADD : LOOMHIP_COMBINE_EXPERT_ASC;
+            if (int rc = loomhip_moe_layer_dev(&l.moe, w.normed, n, combine, w.x, nullptr, nullptr, st))
+                return rc;
+        } else {
+            launch_norm(act_block(l.ffn_gate_t), w.x, D.dim, l.ffn_norm, D.eps, w.qa_dim, nullptr, n, st,
+                        parity);
+            DmmvParams p{};
+            p.w = (const uint8_t *)l.ffn_gate;
+            p.w2 = (const uint8_t *)l.ffn_up;
+            p.rows = (int)l.ffn;
+            p.cols = D.dim;
+            p.xq = w.qa_dim.q;
+            p.xd = w.qa_dim.d;
+            p.xs = w.qa_dim.s;
+            p.pair_src = g_ctx.iota;
+            p.pair_dst = g_ctx.iota;
+            p.groups = w.groups;
+            p.n_groups = w.n_groups;
+            p.out = w.act;
+            p.out_stride = (int)l.ffn;
+            p.rpw = dmmv_pick_rpw(l.ffn_gate_t, D.dim, (int)l.ffn, w.n_groups, w.nt, true);
+            if (!launch_dmmv(l.ffn_gate_t, w.nt, true, p, st))
+                return fail(LOOMHIP_ERR_ARG, "token_frame: gate/up matvec declined");
+            launch_quant_act(l.ffn_down_t, w.act, (int)l.ffn, (int)l.ffn, (int)n, w.qa_ffn, st);
+            if (!frame_matvec(l.ffn_down_t, l.ffn_down, D.dim, (int)l.ffn, w, n, w.qa_ffn, w.x, 1, st))
+                return fail(LOOMHIP_ERR_ARG, "token_frame: down matvec declined");
+        }
+    }
+    // head (llama.zig:1225-1227) and the greedy pick
+    launch_norm(act_block(m->output_t), w.x, D.dim, m->out_norm, D.eps, w.qa_dim, nullptr, n, st, parity);
+    if (!frame_matvec(m->output_t, m->output, D.vocab, D.dim, w, n, w.qa_dim, logits, 0, st))
+        return fail(LOOMHIP_ERR_ARG, "token_frame: output matvec declined");
+    hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(1024), 0, st, logits, D.vocab, next, pos);
+    note_launch();
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return hip_fail(e, "token_frame launch");
+    return LOOMHIP_OK;
+}
+
+} // extern "C"

@@ -36,7 +36,8 @@ struct DmmvParams {
     int n_groups;            // host-side group count (upper bound when n_groups_dev set)
     float *out;              // out[dst * out_stride + row]
     int out_stride;
-    int rpw; // rows per wave
+    int rpw;        // rows per wave
+    int accumulate; // 1: out = out + value (a residual add, tensor.zig:50-52)
 };
 
 void note_launch();
@@ -119,7 +120,8 @@ struct DecodeParams {
     const int32_t *xs;
     float *act; // [n*k][ffn]
     float *out; // [n][dim]
-    int mode;   // 0 selection-order combine (overwrite), 1 ascending expert (accumulate)
+    int mode;   // LOOMHIP_COMBINE_*: 0 selection order, 1 ascending expert (accumulate),
+                // 2 selection order added to out
     int rpw_gu, rpw_dn;
 };
 bool decode_supported(int gate_t, int down_t, int ffn); // ffn a multiple of 256

@@ -268,6 +268,7 @@ __global__ __launch_bounds__(GT_THREADS) void moe_gate_kernel(GateParams p) {
 // ---- gated combine (batched path) --------------------------------------------------
 // mode 0 (moeRun): out = ((0 + g0*y0) + g1*y1) + ... in selection order.
 // mode 1 (moeBatchUnion): out += g*y per expert in ascending expert id.
+// mode 2 (moeRun then the residual add, llama.zig:1222): out = out + acc.
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ y,
                                                       const float *__restrict__ gates,
                                                       const uint32_t *__restrict__ ids,
@@ -277,13 +278,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     if (i >= dim)
         return;
     const size_t base = (size_t)t * k;
-    if (mode == 0) {
+    if (mode != 1) {
         float acc = 0.0f;
         for (int s = 0; s < k; s++) {
             const float pr = gates[base + s] * y[(size_t)pair_of[base + s] * dim + i];
             acc = acc + pr;
         }
-        out[(size_t)t * dim + i] = acc;
+        float *o = out + (size_t)t * dim + i;
+        *o = mode == 2 ? *o + acc : acc;
     } else {
         float acc = out[(size_t)t * dim + i];
         int prev = -1;

@@ -78,6 +78,8 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
                    int combine, float *out, uint32_t *ids_out, float *gates_out, hipStream_t st) {
     if (int rc = moe_check(m, n))
         return rc;
+    if (combine < LOOMHIP_COMBINE_SELECTION || combine > LOOMHIP_COMBINE_SELECTION_ADD)
+        return fail(LOOMHIP_ERR_ARG, "moe: unknown combine mode %d", combine);
     const size_t P = n * m.k;
     const bool decode = n <= DECODE_MAX_TOK && decode_supported(m.gate_t, m.down_t, (int)m.ffn);
     const int nt = moe_nt(n, m.k, m.E);
@@ -336,7 +338,7 @@ int loomhip_moe_ffn_routed(const float *normed, size_t n_tok, size_t dim, const 
         e = hipMemcpyAsync(dl, logits, n_tok * n_expert * 4, hipMemcpyHostToDevice, st);
     if (e == hipSuccess && sel_bias)
         e = hipMemcpyAsync(dsb, sel_bias, n_expert * 4, hipMemcpyHostToDevice, st);
-    if (e == hipSuccess && combine == LOOMHIP_COMBINE_EXPERT_ASC)
+    if (e == hipSuccess && combine != LOOMHIP_COMBINE_SELECTION)
         e = hipMemcpyAsync(dout, out, n_tok * dim * 4, hipMemcpyHostToDevice, st);
     if (e != hipSuccess)
         return hip_fail(e, "moe_ffn_routed staging");

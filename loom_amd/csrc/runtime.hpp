@@ -47,6 +47,8 @@ void clear_weight_cache();
 int matvec_dev_impl(int t, float *out, const void *w, const float *x, size_t n, size_t rows,
                     size_t cols, hipStream_t st);
 int pick_nt(int n);
+// Device group table for n vectors in groups of nt against plane 0 (cached per (n, nt)).
+const DmmvGroup *dense_groups(int n, int nt, int *count);
 void moe_release_scratch();
 
 } // namespace lh

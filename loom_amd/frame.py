@@ -1,0 +1,251 @@
+"""Whole-token decode on the device: the model held in HBM and the frame
+call (``loomhip_token_frame_dev``) that runs one decode step for n lanes.
+
+This is the host mirror of the reference's model/frame seam
+(src/gguf/llama.zig step 1111-1227 and decodeBatch 1939-2043 behind
+src/compute/backend.zig:141-191): ``ModelSpec`` names the shapes and GGML
+types of a llama- or qwen3moe-architecture model, ``DeviceModel`` holds its
+tensors in the device layout, and ``Decoder`` owns the per-lane state (fp16
+K/V caches, positions, tokens, logits) and steps it.  Synthetic weights are
+generated on the device (seeded, GGML block layout, then repacked), which is
+how the benchmark builds the 17 GB Qwen3-30B-A3B-shaped model without a
+checkpoint.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import (GATING_SOFTMAX, NUMERICS_PARITY, Q4_0, Q4_K, Q6_K, LayerDesc, ModelDesc,
+               MoeLayerDesc, check, lib)
+from .backend import _ptr, _stream, repack_dev, synth_ggml_dev
+
+
+@dataclass
+class ModelSpec:
+    dim: int
+    head_dim: int
+    n_layers: int
+    n_heads: int
+    n_kv_heads: int
+    vocab: int
+    ctx_len: int
+    rope_dim: int
+    rope_base: float
+    eps: float
+    rope_neox: bool
+    qk_norm: bool
+    embed_t: int
+    output_t: int
+    wq_t: int
+    wk_t: int
+    wv_t: int
+    wo_t: int
+    # dense SwiGLU FFN (n_expert == 0)
+    ffn: int = 0
+    ffn_gate_t: int = Q4_0
+    ffn_down_t: int = Q4_0
+    # routed MoE (n_expert > 0)
+    n_expert: int = 0
+    n_used: int = 0
+    moe_ffn: int = 0
+    moe_gate_t: int = Q4_K
+    moe_down_t: int = Q6_K
+    router_bias: bool = False
+    gating: int = GATING_SOFTMAX
+    weights_norm: bool = True
+    weights_scale: float = 1.0
+    std: float = 0.02
+
+    @property
+    def qd(self) -> int:
+        return self.n_heads * self.head_dim
+
+    @property
+    def kvd(self) -> int:
+        return self.n_kv_heads * self.head_dim
+
+
+def stories15m(ctx_len: int = 256) -> ModelSpec:
+    """Config 1: the stories15M shape, llama architecture, Q4_0 throughout."""
+    return ModelSpec(dim=288, head_dim=48, n_layers=6, n_heads=6, n_kv_heads=6, vocab=32000,
+                     ctx_len=ctx_len, rope_dim=48, rope_base=10000.0, eps=1e-5, rope_neox=False,
+                     qk_norm=False, embed_t=Q4_0, output_t=Q4_0, wq_t=Q4_0, wk_t=Q4_0, wv_t=Q4_0,
+                     wo_t=Q4_0, ffn=768, ffn_gate_t=Q4_0, ffn_down_t=Q4_0)
+
+
+def qwen3_30b_a3b(ctx_len: int = 4160, n_layers: int = 48, vocab: int = 151936,
+                  n_expert: int = 128) -> ModelSpec:
+    """Config 4: the Qwen3-30B-A3B shape (GQA 32/4, head_dim 128, QK-norm,
+    NEOX rope, 128 experts top-8 of ffn 768), Q4_K_M mix: Q4_K with Q6_K for
+    attn_v, ffn_down and output."""
+    return ModelSpec(dim=2048, head_dim=128, n_layers=n_layers, n_heads=32, n_kv_heads=4,
+                     vocab=vocab, ctx_len=ctx_len, rope_dim=128, rope_base=1000000.0, eps=1e-6,
+                     rope_neox=True, qk_norm=True, embed_t=Q4_K, output_t=Q6_K, wq_t=Q4_K,
+                     wk_t=Q4_K, wv_t=Q6_K, wo_t=Q4_K, n_expert=n_expert, n_used=8, moe_ffn=768,
+                     moe_gate_t=Q4_K, moe_down_t=Q6_K, router_bias=True)
+
+
+@dataclass
+class _Tensor:
+    t: int
+    rows: int
+    cols: int
+    planes: int
+    dev: object               # device layout (torch uint8)
+    ggml: object = None       # GGML bytes on the device, when kept
+
+
+class DeviceModel:
+    """A model's tensors in HBM plus its ``loomhip_model`` descriptor."""
+
+    def __init__(self, spec: ModelSpec):
+        self.spec = spec
+        self.tensors: dict[str, _Tensor] = {}
+        self.f32: dict[str, object] = {}
+        self.numerics = NUMERICS_PARITY
+
+    def set_numerics(self, mode: int) -> None:
+        """NUMERICS_PARITY (sequential rmsnorm sums, bit-identical steps) or
+        NUMERICS_FAST (tree sums)."""
+        self.numerics = mode
+        self.desc.numerics = mode
+
+    # ---- construction ----------------------------------------------------
+    @classmethod
+    def synth(cls, spec: ModelSpec, seed: int = 1, keep_ggml: bool = False) -> "DeviceModel":
+        """Seeded synthetic weights: GGML blocks from the device generator,
+        norms = 1, router N(0, 1/sqrt(dim)) plus a Zipf(1.1) logit bias."""
+        import torch
+
+        m = cls(spec)
+        s = spec
+        counter = [seed * 1000]
+
+        def q(name, t, rows, cols, planes=1):
+            counter[0] += 1
+            g = synth_ggml_dev(t, rows, cols, planes, counter[0], s.std)
+            dev = repack_dev(t, g, rows, cols, planes)
+            m.tensors[name] = _Tensor(t, rows, cols, planes, dev, g if keep_ggml else None)
+            if not keep_ggml:
+                del g
+
+        ones = torch.ones(s.dim, dtype=torch.float32, device="cuda")
+        m.f32["ones_dim"] = ones
+        m.f32["ones_hd"] = torch.ones(s.head_dim, dtype=torch.float32, device="cuda")
+        q("embed", s.embed_t, s.vocab, s.dim)
+        q("output", s.output_t, s.vocab, s.dim)
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(seed)
+        for li in range(s.n_layers):
+            p = f"l{li}."
+            q(p + "wq", s.wq_t, s.qd, s.dim)
+            q(p + "wk", s.wk_t, s.kvd, s.dim)
+            q(p + "wv", s.wv_t, s.kvd, s.dim)
+            q(p + "wo", s.wo_t, s.dim, s.qd)
+            if s.n_expert:
+                q(p + "gate", s.moe_gate_t, s.moe_ffn, s.dim, s.n_expert)
+                q(p + "up", s.moe_gate_t, s.moe_ffn, s.dim, s.n_expert)
+                q(p + "down", s.moe_down_t, s.dim, s.moe_ffn, s.n_expert)
+                m.f32[p + "router"] = (torch.randn(s.n_expert, s.dim, generator=gen, device="cuda")
+                                       / np.sqrt(s.dim)).contiguous()
+                if s.router_bias:
+                    ranks = torch.randperm(s.n_expert, generator=gen, device="cuda").float() + 1
+                    z = -1.1 * torch.log(ranks)
+                    m.f32[p + "router_bias"] = (z - z.mean()).contiguous()
+            else:
+                q(p + "ffn_gate", s.ffn_gate_t, s.ffn, s.dim)
+                q(p + "ffn_up", s.ffn_gate_t, s.ffn, s.dim)
+                q(p + "ffn_down", s.ffn_down_t, s.dim, s.ffn)
+        m._build_desc()
+        return m
+
+    def _ptr(self, name):
+        t = self.tensors.get(name)
+        return None if t is None else t.dev.data_ptr()
+
+    def _f(self, name):
+        t = self.f32.get(name)
+        return None if t is None else t.data_ptr()
+
+    def _build_desc(self):
+        s = self.spec
+        layers = (LayerDesc * s.n_layers)()
+        for li in range(s.n_layers):
+            p = f"l{li}."
+            L = layers[li]
+            L.attn_norm = L.ffn_norm = self._f("ones_dim")
+            L.q_norm = L.k_norm = self._f("ones_hd") if s.qk_norm else None
+            L.wq_t, L.wk_t, L.wv_t, L.wo_t = s.wq_t, s.wk_t, s.wv_t, s.wo_t
+            L.wq, L.wk, L.wv, L.wo = (self._ptr(p + n) for n in ("wq", "wk", "wv", "wo"))
+            if s.n_expert:
+                L.is_moe = 1
+                L.moe = MoeLayerDesc(s.dim, s.moe_ffn, s.n_expert, s.n_used, s.gating,
+                                     int(s.weights_norm), s.weights_scale, self._f(p + "router"),
+                                     self._f(p + "router_bias"), None, s.moe_gate_t, s.moe_gate_t,
+                                     s.moe_down_t, self._ptr(p + "gate"), self._ptr(p + "up"),
+                                     self._ptr(p + "down"))
+            else:
+                L.is_moe = 0
+                L.ffn_gate_t = L.ffn_up_t = s.ffn_gate_t
+                L.ffn_down_t = s.ffn_down_t
+                L.ffn_gate, L.ffn_up, L.ffn_down = (self._ptr(p + n)
+                                                    for n in ("ffn_gate", "ffn_up", "ffn_down"))
+                L.ffn = s.ffn
+        self.layers = layers
+        self.desc = ModelDesc(s.dim, s.head_dim, s.n_layers, s.n_heads, s.n_kv_heads, s.vocab,
+                              s.ctx_len, s.rope_dim, s.rope_base, s.eps, int(s.rope_neox),
+                              s.embed_t, self._ptr("embed"), self._f("ones_dim"), s.output_t,
+                              self._ptr("output"), C.cast(layers, C.POINTER(LayerDesc)), None,
+                              self.numerics)
+
+    def weight_bytes(self) -> int:
+        """Bytes of every quantized tensor plus the f32 ones (routers, norms)."""
+        n = sum(t.dev.numel() for t in self.tensors.values())
+        return n + sum(v.numel() * 4 for v in self.f32.values())
+
+
+class Decoder:
+    """Per-lane decode state on the device: fp16 K/V caches
+    [n][n_layers][ctx_len][kvd], positions, tokens and logits."""
+
+    def __init__(self, model: DeviceModel, n: int):
+        import torch
+
+        s = model.spec
+        self.model, self.n = model, n
+        shape = (n, s.n_layers, s.ctx_len, s.kvd)
+        self.k_cache = torch.zeros(shape, dtype=torch.int16, device="cuda")
+        self.v_cache = torch.zeros(shape, dtype=torch.int16, device="cuda")
+        self.pos = torch.zeros(n, dtype=torch.int32, device="cuda")
+        self.tokens = torch.zeros(n, dtype=torch.int32, device="cuda")
+        self.logits = torch.empty((n, s.vocab), dtype=torch.float32, device="cuda")
+
+    def prefill_random(self, n_pos: int, seed: int = 7, scale: float = 1.0):
+        """Fill cache rows [0, n_pos) of every lane and layer with seeded
+        random fp16 K/V and set pos = n_pos (the benchmark's prefilled
+        context)."""
+        import torch
+
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        for c in (self.k_cache, self.v_cache):
+            for lane in range(self.n):
+                r = torch.randn((c.shape[1], n_pos, c.shape[3]), generator=g, device="cuda") * scale
+                c[lane, :, :n_pos, :] = r.to(torch.float16).view(torch.int16)
+        self.pos.fill_(n_pos)
+
+    def step(self, tokens=None, next_out=True) -> int:
+        """One decode step of every lane: tokens (device int32 [n]) default to
+        ``self.tokens``; the greedy pick is written back into ``self.tokens``
+        when ``next_out``."""
+        tok = self.tokens if tokens is None else tokens
+        nxt = self.tokens if next_out else None
+        return check(lib().loomhip_token_frame_dev(
+            C.byref(self.model.desc), _ptr(tok), _ptr(self.pos), self.n, _ptr(self.k_cache),
+            _ptr(self.v_cache), _ptr(self.logits), _ptr(nxt), _stream()), "token_frame_dev")
+
+
+__all__ = ["DeviceModel", "Decoder", "ModelSpec", "qwen3_30b_a3b", "stories15m"]
