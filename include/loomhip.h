@@ -83,7 +83,10 @@ uint64_t loomhip_take_launch_count(void);
 #define LOOMHIP_KT_GATE_UP 0 /* grouped gate/up + SwiGLU expert kernel */
 #define LOOMHIP_KT_DOWN 1    /* grouped down expert kernel */
 #define LOOMHIP_KT_DENSE 2   /* dense dequant-fused matvec */
-#define LOOMHIP_KT_COUNT 3
+#define LOOMHIP_KT_ATTN 3    /* token frame: attention over the K/V cache (partials) */
+#define LOOMHIP_KT_HEAD 4    /* token frame: output head matvec */
+#define LOOMHIP_KT_QKV 5     /* token frame: q, k, v and wo matvecs */
+#define LOOMHIP_KT_COUNT 6
 void loomhip_profile_kernels(int enable);
 /* Waits for the recorded events; total milliseconds and launch count of tag. */
 int loomhip_kernel_time(int tag, double *total_ms, uint64_t *launches);
@@ -222,6 +225,10 @@ typedef struct {
      * powf/cosf/sinf in ropeTheta's expressions and keeps them. */
     const float *rope_cs;
     int numerics; /* LOOMHIP_NUMERICS_* */
+    /* Optional telemetry: each MoE layer li writes its routed expert ids to
+     * ids_out[li][n][n_used] (device), the per-expert access counts of
+     * Stats/hottestWithinBudget (src/core/stats.zig:135-160). */
+    uint32_t *ids_out;
 } loomhip_model;
 
 /* One decode step of n lanes on the device, the whole token as one

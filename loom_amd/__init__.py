@@ -21,9 +21,10 @@ OK, DECLINED, ERR_ARG, ERR_HIP, ERR_INIT = 0, 1, -1, -2, -3
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
 GATING_SOFTMAX, GATING_SIGMOID, GATING_SOFTMAX_TOPK = 1, 2, 3
 COMBINE_SELECTION, COMBINE_EXPERT_ASC, COMBINE_SELECTION_ADD = 0, 1, 2
-KT_GATE_UP, KT_DOWN, KT_DENSE = 0, 1, 2
+KT_GATE_UP, KT_DOWN, KT_DENSE, KT_ATTN, KT_HEAD, KT_QKV = 0, 1, 2, 3, 4, 5
 NUMERICS_PARITY, NUMERICS_FAST = 0, 1
-KT_NAMES = {KT_GATE_UP: "gate_up", KT_DOWN: "down", KT_DENSE: "dense"}
+KT_NAMES = {KT_GATE_UP: "gate_up", KT_DOWN: "down", KT_DENSE: "dense", KT_ATTN: "attn",
+            KT_HEAD: "head", KT_QKV: "qkvo"}
 
 
 class LoomHipError(RuntimeError):
@@ -104,6 +105,7 @@ class ModelDesc(C.Structure):
         ("layers", C.POINTER(LayerDesc)),
         ("rope_cs", C.c_void_p),
         ("numerics", C.c_int),
+        ("ids_out", C.c_void_p),
     ]
 
 

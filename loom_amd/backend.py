@@ -133,9 +133,12 @@ def profileKernels(enable: bool) -> None:
 
 
 _KERNEL_SYMBOLS = {
-    "gate_up": "dmmv_kernel<Q4_K|Q6_K|..., NT, FUSED=true> (grouped gate/up + SwiGLU)",
-    "down": "dmmv_kernel<..., NT, FUSED=false> (grouped down)",
-    "dense": "dmmv_kernel<..., NT, false> (dense matvec)",
+    "gate_up": "moe_gateup_decode_kernel (n <= 4) / dmmv_kernel<T, NT, FUSED=true> (grouped gate/up + SwiGLU)",
+    "down": "moe_down_decode_kernel (n <= 4) / dmmv_kernel<T, NT, FUSED=false> (grouped down)",
+    "dense": "dmmv_kernel<T, NT, false> (dense matvec)",
+    "attn": "attn_partial_kernel (attention over the fp16 K/V cache)",
+    "head": "dmmv_kernel<T, NT, false> (output head)",
+    "qkvo": "dmmv_kernel<T, NT, false> (q, k, v, wo)",
 }
 
 

@@ -538,7 +538,7 @@ static FrameWs frame_layout(char *base, size_t n, const loomhip_model *m, size_t
 }
 
 static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameWs &w, size_t n,
-                         QAct x, float *out, int accumulate, hipStream_t st) {
+                         QAct x, float *out, int accumulate, hipStream_t st, int tag = LOOMHIP_KT_QKV) {
     DmmvParams p{};
     p.w = (const uint8_t *)wt;
     p.plane_bytes = 0;
@@ -555,7 +555,10 @@ static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameW
     p.out_stride = rows;
     p.accumulate = accumulate;
     p.rpw = dmmv_pick_rpw(t, cols, rows, w.n_groups, w.nt, false);
-    return launch_dmmv(t, w.nt, false, p, st);
+    const int ph = prof_begin(tag, st);
+    const bool ok = launch_dmmv(t, w.nt, false, p, st);
+    prof_end(ph, st);
+    return ok;
 }
 
 template <bool EXACT>
@@ -685,8 +688,10 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         hipLaunchKernelGGL(qk_rope_kernel, dim3(D.n_heads + D.n_kv, n), dim3(64), 0, st, D, w.q, w.k,
                            w.v, l.q_norm, l.k_norm, pos, (int)li, rope_cs, w.qrot, k_cache, v_cache);
         note_launch();
+        int ph = prof_begin(LOOMHIP_KT_ATTN, st);
         hipLaunchKernelGGL(attn_partial_kernel, dim3(n_chunks, D.n_kv, n), dim3(256), att_lds, st, D,
                            w.qrot, k_cache, v_cache, pos, (int)li, n_chunks, w.part);
+        prof_end(ph, st);
         note_launch();
         const int qb_o = act_block(l.wo_t);
         if (qb_o == 256)
@@ -702,7 +707,8 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         if (l.is_moe) {
             launch_norm(0, w.x, D.dim, l.ffn_norm, D.eps, QAct{}, w.normed, n, st, parity);
             const int combine = n == 1 ? LOOMHIP_COMBINE_SELECTION_ADD : LOOMHIP_COMBINE_EXPERT_ASC;
-            if (int rc = loomhip_moe_layer_dev(&l.moe, w.normed, n, combine, w.x, nullptr, nullptr, st))
+            uint32_t *ids = m->ids_out ? m->ids_out + li * n * l.moe.n_used : nullptr;
+            if (int rc = loomhip_moe_layer_dev(&l.moe, w.normed, n, combine, w.x, ids, nullptr, st))
                 return rc;
         } else {
             launch_norm(act_block(l.ffn_gate_t), w.x, D.dim, l.ffn_norm, D.eps, w.qa_dim, nullptr, n, st,
@@ -731,7 +737,8 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     }
     // head (llama.zig:1225-1227) and the greedy pick
     launch_norm(act_block(m->output_t), w.x, D.dim, m->out_norm, D.eps, w.qa_dim, nullptr, n, st, parity);
-    if (!frame_matvec(m->output_t, m->output, D.vocab, D.dim, w, n, w.qa_dim, logits, 0, st))
+    if (!frame_matvec(m->output_t, m->output, D.vocab, D.dim, w, n, w.qa_dim, logits, 0, st,
+                      LOOMHIP_KT_HEAD))
         return fail(LOOMHIP_ERR_ARG, "token_frame: output matvec declined");
     hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(1024), 0, st, logits, D.vocab, next, pos);
     note_launch();

@@ -199,7 +199,7 @@ class DeviceModel:
                               s.ctx_len, s.rope_dim, s.rope_base, s.eps, int(s.rope_neox),
                               s.embed_t, self._ptr("embed"), self._f("ones_dim"), s.output_t,
                               self._ptr("output"), C.cast(layers, C.POINTER(LayerDesc)), None,
-                              self.numerics)
+                              self.numerics, None)
 
     def weight_bytes(self) -> int:
         """Bytes of every quantized tensor plus the f32 ones (routers, norms)."""

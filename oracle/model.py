@@ -1,7 +1,7 @@
-"""Test infrastructure: the oracle's restated llama.step / decodeBatch
-(oracle/model_ref.c, src/gguf/llama.zig:1111-1227, 1939-2043) built over
-host copies of a DeviceModel's GGML bytes, so device and oracle see the same
-weights."""
+"""TEST INFRASTRUCTURE: the oracle's restated llama.step / decodeBatch
+(model_ref.c: src/gguf/llama.zig:1111-1227, 1939-2043) over host copies of a
+device model's GGML bytes, so device and oracle see the same weights.  Used
+by tests/ and by bench.py's CPU-baseline leg only."""
 from __future__ import annotations
 
 import ctypes as C
@@ -10,15 +10,19 @@ import numpy as np
 
 
 class OracleModel:
+    """lo_model over `dm` (a loom_amd.frame.DeviceModel built with
+    keep_ggml=True): dm.tensors[name].ggml (device GGML bytes) and dm.f32."""
+
     def __init__(self, oracle, dm):
         o = oracle
         s = dm.spec
         self.o, self.spec = o, s
         self.keep = []
+        self.host = {}
 
         def host(name):
             a = dm.tensors[name].ggml.cpu().numpy()
-            self.keep.append(a)
+            self.host[name] = a
             return a
 
         def f32(name):

@@ -13,7 +13,7 @@ Two kinds of check:
 import numpy as np
 import pytest
 
-from frame_ref import OracleModel, maxrel
+from oracle.model import OracleModel, maxrel
 
 pytestmark = pytest.mark.gpu
 
