@@ -243,112 +243,129 @@ __global__ __launch_bounds__(64) void qk_rope_kernel(FrameDims D, const float *_
 
 // ---- attention over 64 positions for one KV head group (llama.zig:1162-1192) -------
 
-// dotF32 (src/gguf/ggml.zig:198-217) of a query head (f32) and a cached key
-// row (fp16, widened): 32 accumulators over whole 32-steps, leftover 8-chunks
-// into the first 8, ((a0 + a1) + a2) + a3 per lane, the lanes summed in order
-// from -0, then the scalar tail.
-__device__ inline float dot_f32_key(const float *a, const uint16_t *b, int n) {
+// dotF32 (src/gguf/ggml.zig:198-217) of a query head (f32, LDS, read as
+// broadcasts) and a cached key row (fp16, a padded LDS row), 8 values per
+// 16-byte read: 32 accumulators over whole 32-steps, leftover 8-chunks into
+// the first 8, ((a0 + a1) + a2) + a3 per lane, the lanes summed in order
+// from -0 (HD is a multiple of 8).
+template <int HD>
+__device__ __forceinline__ float dot_f32_key(const float *a, const uint16_t *krow) {
     float acc[32];
 #pragma unroll
     for (int u = 0; u < 32; u++)
         acc[u] = 0.0f;
-    int i = 0;
-    for (; i + 32 <= n; i += 32) {
 #pragma unroll
-        for (int u = 0; u < 32; u++) {
-            const float pr = a[i + u] * half_bits_to_float(b[i + u]);
-            acc[u] = acc[u] + pr;
-        }
-    }
-    for (; i + 8 <= n; i += 8) {
+    for (int i = 0; i < HD; i += 8) {
+        const uint4 kv = *(const uint4 *)(krow + i);
+        const float4 qa = *(const float4 *)(a + i), qb = *(const float4 *)(a + i + 4);
+        const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+        const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const int base = i < HD / 32 * 32 ? i % 32 : 0; // whole 32-steps, then chunks into acc[0..8)
 #pragma unroll
-        for (int l = 0; l < 8; l++) {
-            const float pr = a[i + l] * half_bits_to_float(b[i + l]);
-            acc[l] = acc[l] + pr;
+        for (int e = 0; e < 8; e++) {
+            const float k = half_bits_to_float((uint16_t)(kw[e >> 1] >> (16 * (e & 1))));
+            const float pr = qv[e] * k;
+            acc[base + e] = acc[base + e] + pr;
         }
     }
     float s = -0.0f;
 #pragma unroll
     for (int l = 0; l < 8; l++)
         s = s + (((acc[l] + acc[8 + l]) + acc[16 + l]) + acc[24 + l]);
-    for (; i < n; i++) {
-        const float pr = a[i] * half_bits_to_float(b[i]);
-        s = s + pr;
-    }
     return s;
 }
 
-// Work group (chunk, kv head, lane).  Scores in dotF32 order times the scale;
-// per query head m = the chunk's max, e = exp(s - m), l = sum of e in
-// position order.  When the whole context is this one chunk (position < 64)
-// the record is the reference's own arithmetic (softmax, tensor.zig:18-28,
-// then out += p * v in position order): o = sum_t (e_t * (1/l)) * v_t with
-// l = 1; otherwise o = sum_t e_t * v_t, unnormalised, for the merge.  Record
-// per (lane, kv head, chunk): m[G], l[G], o[G][hd].
+// Work group (chunk, kv head, lane).  The chunk's keys and values are
+// staged through LDS with coalesced loads (keys in rows padded by 16 bytes,
+// so that lane j reading row j with 16-byte reads meets no bank conflict).
+// Wave w takes query heads w, w+4, ...: lane j scores key j (dotF32 order,
+// times the scale), and per head m = the chunk's max, e = exp(s - m), l =
+// sum of e in position order, then P.V with each lane on two columns.
+// When the whole context is this one chunk (position < 64) the record is the
+// reference's own arithmetic (softmax, tensor.zig:18-28, then out += p * v
+// in position order): o = sum_t (e_t * (1/l)) * v_t with l = 1; otherwise
+// o = sum_t e_t * v_t, unnormalised, for the merge.  Record per (lane, kv
+// head, chunk): m[G], l[G], o[G][HD].
+template <int HD>
 __global__ __launch_bounds__(256) void attn_partial_kernel(FrameDims D, const float *__restrict__ q_rot,
                                                            const uint16_t *__restrict__ kc,
                                                            const uint16_t *__restrict__ vc,
                                                            const int32_t *__restrict__ pos, int li,
                                                            int n_chunks, float *__restrict__ part) {
     extern __shared__ __align__(16) float smem[];
+    constexpr int KS = HD + 8;  // padded key row (halves)
+    constexpr int PR = HD / 8;  // 16-byte pieces per row
     const int ch = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
-    const int hd = D.hd, G = D.n_heads / D.n_kv;
+    const int G = D.n_heads / D.n_kv;
     const int p = min(pos[t], D.ctx - 1);
     const int t0 = ch * ATT_TC, nt = min(ATT_TC, p + 1 - t0);
     if (nt <= 0)
         return; // past the current position: the merge reads no record from here
     const bool single = p + 1 <= ATT_TC;
-    float *qs = smem;                                  // [G][hd]
-    float *sc = qs + G * hd;                           // [G][TC]
-    uint16_t *ks = (uint16_t *)(sc + G * ATT_TC);      // [TC][hd]
-    uint16_t *vs = ks + ATT_TC * hd;                   // [TC][hd]
-    const float *qsrc = q_rot + (size_t)t * D.qd + (size_t)kvh * G * hd;
-    for (int i = tid; i < G * hd; i += 256)
-        qs[i] = qsrc[i];
-    const size_t row0 = (((size_t)t * D.n_layers + li) * D.ctx + t0) * D.kvd + (size_t)kvh * hd;
-    const int per_row = hd / 8; // 16-byte pieces per row
-    for (int i = tid; i < nt * per_row; i += 256) {
-        const int r = i / per_row, c8 = i % per_row;
-        const size_t g = row0 + (size_t)r * D.kvd + 8 * c8;
-        *(uint4 *)(ks + r * hd + 8 * c8) = *(const uint4 *)(kc + g);
-        *(uint4 *)(vs + r * hd + 8 * c8) = *(const uint4 *)(vc + g);
-    }
-    __syncthreads();
-    for (int i = tid; i < G * ATT_TC; i += 256) {
-        const int g = i / ATT_TC, j = i % ATT_TC;
-        sc[i] = j < nt ? dot_f32_key(qs + g * hd, ks + j * hd, hd) * D.scale : -INFINITY;
-    }
-    __syncthreads();
+    float *qs = smem;                                  // [G][HD]
+    uint16_t *ks = (uint16_t *)(qs + G * HD);          // [TC][KS]
+    uint16_t *vs = ks + ATT_TC * KS;                   // [TC][HD]
     const int wave = tid >> 6, ln = tid & 63;
-    float *rec = part + (((size_t)t * D.n_kv + kvh) * n_chunks + ch) * (size_t)G * (hd + 2);
+    const size_t row0 = (((size_t)t * D.n_layers + li) * D.ctx + t0) * D.kvd + (size_t)kvh * HD;
+    const float *qsrc = q_rot + (size_t)t * D.qd + (size_t)kvh * G * HD;
+    for (int i = tid; i < G * HD; i += 256)
+        qs[i] = qsrc[i];
+    for (int i = tid; i < ATT_TC * PR; i += 256) {
+        const int r = i / PR, c8 = i % PR;
+        if (r < nt) {
+            const size_t gi = row0 + (size_t)r * D.kvd + 8 * c8;
+            *(uint4 *)(ks + r * KS + 8 * c8) = *(const uint4 *)(kc + gi);
+            *(uint4 *)(vs + r * HD + 8 * c8) = *(const uint4 *)(vc + gi);
+        }
+    }
+    __syncthreads();
+    const uint16_t *krow = ks + min(ln, nt - 1) * KS;
+    float *rec = part + (((size_t)t * D.n_kv + kvh) * n_chunks + ch) * (size_t)G * (HD + 2);
+    // wave w: query heads w, w+4, ...; lane j: position j (scores), then
+    // columns 2j, 2j+1 (P.V, with p_j broadcast from lane j by readlane)
+    const int d0 = 2 * ln;
+    const bool dv = d0 < HD;
     for (int g = wave; g < G; g += 4) {
-        const float s = sc[g * ATT_TC + ln];
+        const float s = ln < nt ? dot_f32_key<HD>(qs + g * HD, krow) * D.scale : -INFINITY;
         const float m = wave_max(s);
-        const float e = ln < nt ? exp_f32(s - m) : 0.0f;
-        sc[g * ATT_TC + ln] = e;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        float e = ln < nt ? exp_f32(s - m) : 0.0f;
         float l = 0.0f;
         for (int j = 0; j < nt; j++) // the reference's sum order
-            l = l + sc[g * ATT_TC + j];
+            l = l + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
         if (single) {
             const float inv = 1.0f / l;
-            sc[g * ATT_TC + ln] = e * inv;
+            e = e * inv;
         }
         if (ln == 0) {
             rec[g] = m;
             rec[G + g] = single ? 1.0f : l;
         }
-    }
-    __syncthreads();
-    for (int i = tid; i < G * hd; i += 256) {
-        const int g = i / hd, d = i % hd;
-        float acc = 0.0f;
-        for (int j = 0; j < nt; j++) {
-            const float pr = sc[g * ATT_TC + j] * half_bits_to_float(vs[j * hd + d]);
-            acc = acc + pr;
+        float a0 = 0.0f, a1 = 0.0f;
+        for (int j0 = 0; j0 < nt; j0 += 8) {
+            uint32_t vw[8];
+            float pj[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int j = j0 + u;
+                const bool in = j < nt;
+                vw[u] = in && dv ? *(const uint32_t *)(vs + j * HD + d0) : 0u;
+                const float pr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j & 63));
+                pj[u] = in ? pr : 0.0f;
+            }
+            // positions past nt add +0 (p = 0, v = 0) to accumulators that
+            // are never -0: no change
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const float p0 = pj[u] * half_bits_to_float((uint16_t)(vw[u] & 0xffff));
+                const float p1 = pj[u] * half_bits_to_float((uint16_t)(vw[u] >> 16));
+                a0 = a0 + p0;
+                a1 = a1 + p1;
+            }
         }
-        rec[2 * G + i] = acc;
+        if (dv) {
+            rec[2 * G + g * HD + d0] = a0;
+            rec[2 * G + g * HD + d0 + 1] = a1;
+        }
     }
 }
 
@@ -588,7 +605,7 @@ static int frame_check(const loomhip_model *m, size_t n, size_t *ffn_max) {
     if (!m || !m->layers || n == 0 || n > 256)
         return fail(LOOMHIP_ERR_ARG, "token_frame: bad model or lane count %zu (1..256)", n);
     const size_t dim = m->dim, hd = m->head_dim, qd = m->n_heads * hd;
-    if (dim == 0 || dim % 32 || dim > 8192 || qd % 32 || hd == 0 || hd % 8 || hd > MAX_HD ||
+    if (dim == 0 || dim % 32 || dim > 8192 || qd % 32 || (hd != 48 && hd != 64 && hd != 128) ||
         m->n_kv_heads == 0 || m->n_heads % m->n_kv_heads || m->n_heads / m->n_kv_heads > MAX_G ||
         m->rope_dim > hd || m->rope_dim % 2 || m->ctx_len == 0 || m->vocab == 0)
         return fail(LOOMHIP_DECLINED, "token_frame: dims not served (dim %zu, head_dim %zu, heads %zu/%zu)",
@@ -662,7 +679,7 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     D.eps = m->eps;
     D.scale = 1.0f / sqrtf((float)m->head_dim); // llama.zig attn scale
     const int G = D.n_heads / D.n_kv;
-    const size_t att_lds = (size_t)G * D.hd * 4 + (size_t)G * ATT_TC * 4 + 2 * (size_t)ATT_TC * D.hd * 2;
+    const size_t att_lds = (size_t)G * D.hd * 4 + (size_t)ATT_TC * (D.hd + 8) * 2 + (size_t)ATT_TC * D.hd * 2;
     if (att_lds > 64 * 1024)
         return fail(LOOMHIP_DECLINED, "token_frame: attention tile exceeds LDS (%zu B)", att_lds);
 
@@ -689,8 +706,16 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
                            w.v, l.q_norm, l.k_norm, pos, (int)li, rope_cs, w.qrot, k_cache, v_cache);
         note_launch();
         int ph = prof_begin(LOOMHIP_KT_ATTN, st);
-        hipLaunchKernelGGL(attn_partial_kernel, dim3(n_chunks, D.n_kv, n), dim3(256), att_lds, st, D,
-                           w.qrot, k_cache, v_cache, pos, (int)li, n_chunks, w.part);
+        const dim3 agrid(n_chunks, D.n_kv, n);
+        if (D.hd == 128)
+            hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(256), att_lds, st, D, w.qrot, k_cache,
+                               v_cache, pos, (int)li, n_chunks, w.part);
+        else if (D.hd == 64)
+            hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(256), att_lds, st, D, w.qrot, k_cache,
+                               v_cache, pos, (int)li, n_chunks, w.part);
+        else
+            hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(256), att_lds, st, D, w.qrot, k_cache,
+                               v_cache, pos, (int)li, n_chunks, w.part);
         prof_end(ph, st);
         note_launch();
         const int qb_o = act_block(l.wo_t);
