@@ -308,14 +308,25 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(FrameDims D, const fl
     const int wave = tid >> 6, ln = tid & 63;
     const size_t row0 = (((size_t)t * D.n_layers + li) * D.ctx + t0) * D.kvd + (size_t)kvh * HD;
     const float *qsrc = q_rot + (size_t)t * D.qd + (size_t)kvh * G * HD;
+    // every K/V load is issued before the first LDS store; rows past nt
+    // repeat row nt-1 and are never read
+    constexpr int NPC = (ATT_TC * PR + 255) / 256; // 16-byte pieces per thread
+    uint4 kr[NPC], vr[NPC];
+#pragma unroll
+    for (int u = 0; u < NPC; u++) {
+        const int i = tid + 256 * u;
+        const size_t gi = row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR);
+        kr[u] = *(const uint4 *)(kc + gi);
+        vr[u] = *(const uint4 *)(vc + gi);
+    }
     for (int i = tid; i < G * HD; i += 256)
         qs[i] = qsrc[i];
-    for (int i = tid; i < ATT_TC * PR; i += 256) {
-        const int r = i / PR, c8 = i % PR;
-        if (r < nt) {
-            const size_t gi = row0 + (size_t)r * D.kvd + 8 * c8;
-            *(uint4 *)(ks + r * KS + 8 * c8) = *(const uint4 *)(kc + gi);
-            *(uint4 *)(vs + r * HD + 8 * c8) = *(const uint4 *)(vc + gi);
+#pragma unroll
+    for (int u = 0; u < NPC; u++) {
+        const int i = tid + 256 * u;
+        if (i < ATT_TC * PR) {
+            *(uint4 *)(ks + (i / PR) * KS + 8 * (i % PR)) = kr[u];
+            *(uint4 *)(vs + (i / PR) * HD + 8 * (i % PR)) = vr[u];
         }
     }
     __syncthreads();
@@ -370,19 +381,32 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(FrameDims D, const fl
 }
 
 // ---- merge the partials per head, quantize the attention output for wo -------------
-// Work group (256-value slice, lane); thread j -> value slice*256 + j.  Blocks
-// of QB values are QB consecutive threads (QB = 32: half a wave; 256: the
-// work group).
+// Work group (256-value slice, lane), 1024 threads: value v = tid % 256 of the
+// slice, chunk quarter cq = tid / 256 (chunks cq, cq+4, ...).  Blocks of QB
+// values are QB consecutive values (QB = 32: half a wave; 256: the slice).
+// The merge weights of the slice's heads (at most CMB_NH of them) are formed
+// once, one wave per head: M = max_c m_c, w_c = exp(m_c - M), L = sum_c w_c
+// l_c; each quarter then sums w_c o_c[d] over its chunks with the o loads
+// issued before the weights are known, and o = (the quarters' sums in order)
+// / L.
+constexpr int CMB_NH = 8;  // heads a 256-value slice can touch (head_dim >= 48)
+constexpr int CMB_OP = 24; // chunks per quarter held in registers (contexts up to 6144 in one pass)
+
 template <int QB>
-__global__ __launch_bounds__(256) void attn_combine_kernel(FrameDims D, const float *__restrict__ part,
-                                                           const int32_t *__restrict__ pos,
-                                                           int n_chunks, QAct qa) {
-    __shared__ float red[4];
-    const int t = blockIdx.y, tid = threadIdx.x;
-    const int idx = blockIdx.x * 256 + tid;
-    const bool live = idx < D.qd;
+__global__ __launch_bounds__(1024) void attn_combine_kernel(FrameDims D, const float *__restrict__ part,
+                                                            const int32_t *__restrict__ pos,
+                                                            int n_chunks, QAct qa) {
+    extern __shared__ float cmb[]; // [4][256] quarter sums, then [CMB_NH][n_chunks] weights
+    __shared__ float red[4], Ls[CMB_NH];
+    const int t = blockIdx.y, tid = threadIdx.x, v = tid & 255, cq = tid >> 8;
+    const int wave = tid >> 6, ln = tid & 63;
+    const int idx = blockIdx.x * 256 + v;
+    const bool live = idx < D.qd && cq == 0;
     const int hd = D.hd, G = D.n_heads / D.n_kv;
-    const int h = (live ? idx : D.qd - 1) / hd, d = (live ? idx : D.qd - 1) % hd;
+    const int ic = idx < D.qd ? idx : D.qd - 1;
+    const int h = ic / hd, d = ic % hd;
+    const int h_lo = blockIdx.x * 256 / hd;
+    const int nh = (min(blockIdx.x * 256 + 255, D.qd - 1)) / hd - h_lo + 1;
     const int kvh = h / G, g = h % G;
     const int p = min(pos[t], D.ctx - 1);
     const int nc = (p + 1 + ATT_TC - 1) / ATT_TC;
@@ -392,16 +416,43 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(FrameDims D, const fl
     if (nc == 1) { // one chunk: its record is already the softmax-weighted sum
         val = rec0[2 * G + (size_t)g * hd + d];
     } else {
-        float M = -INFINITY;
-        for (int c = 0; c < nc; c++)
-            M = fmaxf(M, rec0[c * rs + g]);
-        float L = 0.0f, O = 0.0f;
-        for (int c = 0; c < nc; c++) {
-            const float wgt = exp_f32(rec0[c * rs + g] - M);
-            L = L + rec0[c * rs + G + g] * wgt;
-            O = O + rec0[c * rs + 2 * G + (size_t)g * hd + d] * wgt;
+        float *wt = cmb + 4 * 256;
+        const float *orow = rec0 + 2 * G + (size_t)g * hd + d;
+        float ov[CMB_OP];
+#pragma unroll
+        for (int u = 0; u < CMB_OP; u++)
+            ov[u] = orow[(size_t)min(cq + 4 * u, nc - 1) * rs];
+        if (wave < nh) {
+            const int hw = h_lo + wave, kw = hw / G, gw = hw % G;
+            const float *r0 = part + ((size_t)t * D.n_kv + kw) * n_chunks * rs;
+            float M = -INFINITY;
+            for (int c = ln; c < nc; c += 64)
+                M = fmaxf(M, r0[(size_t)c * rs + gw]);
+            M = wave_max(M);
+            float lp = 0.0f;
+            for (int c = ln; c < nc; c += 64) {
+                const float wc = exp_f32(r0[(size_t)c * rs + gw] - M);
+                wt[wave * nc + c] = wc;
+                lp = lp + r0[(size_t)c * rs + G + gw] * wc;
+            }
+            const float L = wave_sum_f(lp);
+            if (ln == 0)
+                Ls[wave] = L;
         }
-        val = O / L;
+        __syncthreads();
+        const float *wh = wt + (h - h_lo) * nc;
+        float o = 0.0f;
+#pragma unroll
+        for (int u = 0; u < CMB_OP; u++) {
+            const int c = cq + 4 * u;
+            if (c < nc)
+                o = o + wh[c] * ov[u];
+        }
+        for (int c = cq + 4 * CMB_OP; c < nc; c += 4)
+            o = o + wh[c] * orow[(size_t)c * rs];
+        cmb[cq * 256 + v] = o;
+        __syncthreads();
+        val = (((cmb[v] + cmb[256 + v]) + cmb[512 + v]) + cmb[768 + v]) / Ls[h - h_lo];
     }
     // int8 quantization (quantizeX / quantizeX256) of QB-thread blocks
     float a = live && __builtin_isfinite(val) ? fabsf(val) : 0.0f;
@@ -410,9 +461,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(FrameDims D, const fl
             a = fmaxf(a, __shfl_xor(a, m, 32));
     } else {
         const float wm = wave_max(a);
-        __syncthreads();
-        if ((tid & 63) == 0)
-            red[tid >> 6] = wm;
+        if (wave < 4 && ln == 0)
+            red[wave] = wm;
         __syncthreads();
         a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     }
@@ -682,6 +732,9 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     const size_t att_lds = (size_t)G * D.hd * 4 + (size_t)ATT_TC * (D.hd + 8) * 2 + (size_t)ATT_TC * D.hd * 2;
     if (att_lds > 64 * 1024)
         return fail(LOOMHIP_DECLINED, "token_frame: attention tile exceeds LDS (%zu B)", att_lds);
+    const size_t cmb_lds = (4 * 256 + (size_t)CMB_NH * n_chunks) * 4;
+    if (cmb_lds > 64 * 1024)
+        return fail(LOOMHIP_DECLINED, "token_frame: context %zu exceeds the merge's LDS", m->ctx_len);
 
     if (m->numerics != LOOMHIP_NUMERICS_PARITY && m->numerics != LOOMHIP_NUMERICS_FAST)
         return fail(LOOMHIP_ERR_ARG, "token_frame: unknown numerics mode %d", m->numerics);
@@ -720,11 +773,11 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         note_launch();
         const int qb_o = act_block(l.wo_t);
         if (qb_o == 256)
-            hipLaunchKernelGGL(attn_combine_kernel<256>, dim3((D.qd + 255) / 256, n), dim3(256), 0, st, D,
-                               w.part, pos, n_chunks, w.qa_att);
+            hipLaunchKernelGGL(attn_combine_kernel<256>, dim3((D.qd + 255) / 256, n), dim3(1024), cmb_lds, st,
+                               D, w.part, pos, n_chunks, w.qa_att);
         else
-            hipLaunchKernelGGL(attn_combine_kernel<32>, dim3((D.qd + 255) / 256, n), dim3(256), 0, st, D,
-                               w.part, pos, n_chunks, w.qa_att);
+            hipLaunchKernelGGL(attn_combine_kernel<32>, dim3((D.qd + 255) / 256, n), dim3(1024), cmb_lds, st,
+                               D, w.part, pos, n_chunks, w.qa_att);
         note_launch();
         if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st))
             return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
