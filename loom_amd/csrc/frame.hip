@@ -275,26 +275,33 @@ __device__ __forceinline__ float dot_f32_key(const float *a, const uint16_t *kro
     return s;
 }
 
-// Work group (chunk, kv head, lane).  The chunk's keys and values are
-// staged through LDS with coalesced loads (keys in rows padded by 16 bytes,
-// so that lane j reading row j with 16-byte reads meets no bank conflict).
-// Wave w takes query heads w, w+4, ...: lane j scores key j (dotF32 order,
-// times the scale), and per head m = the chunk's max, e = exp(s - m), l =
-// sum of e in position order, then P.V with each lane on two columns.
-// When the whole context is this one chunk (position < 64) the record is the
-// reference's own arithmetic (softmax, tensor.zig:18-28, then out += p * v
-// in position order): o = sum_t (e_t * (1/l)) * v_t with l = 1; otherwise
-// o = sum_t e_t * v_t, unnormalised, for the merge.  Record per (lane, kv
-// head, chunk): m[G], l[G], o[G][HD].
+// Work group (chunk, kv head, lane), 8 waves.  The chunk's keys and values
+// are staged through LDS with coalesced loads, every load issued up front
+// (keys in rows padded by 16 bytes, so that lane j reading row j with
+// 16-byte reads meets no bank conflict); the values' stores to LDS wait only
+// after the scores.  Wave w takes query heads w, w+8, ...: lane j scores key
+// j (dotF32 order, times the scale); per head m = the chunk's max, e =
+// exp(s - m), l = sum of e; then P.V with each lane on CPL columns, the
+// positions in order.  When the whole context is this one chunk (position <
+// 64) the record is the reference's own arithmetic (softmax, tensor.zig:18-28,
+// with l summed in position order, then out += p * v in position order): o =
+// sum_t (e_t * (1/l)) * v_t with l = 1; otherwise o = sum_t e_t * v_t,
+// unnormalised, and l a tree sum, for the merge.  Record per (lane, kv head,
+// chunk): m[G], l[G], o[G][HD].
+constexpr int ATT_WAVES = 8;
+
 template <int HD>
-__global__ __launch_bounds__(256) void attn_partial_kernel(FrameDims D, const float *__restrict__ q_rot,
-                                                           const uint16_t *__restrict__ kc,
-                                                           const uint16_t *__restrict__ vc,
-                                                           const int32_t *__restrict__ pos, int li,
-                                                           int n_chunks, float *__restrict__ part) {
+__global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims D, const float *__restrict__ q_rot,
+                                                                      const uint16_t *__restrict__ kc,
+                                                                      const uint16_t *__restrict__ vc,
+                                                                      const int32_t *__restrict__ pos, int li,
+                                                                      int n_chunks, float *__restrict__ part) {
     extern __shared__ __align__(16) float smem[];
-    constexpr int KS = HD + 8;  // padded key row (halves)
-    constexpr int PR = HD / 8;  // 16-byte pieces per row
+    constexpr int NT = 64 * ATT_WAVES;
+    constexpr int KS = HD + 8;                 // padded key row (halves)
+    constexpr int PR = HD / 8;                 // 16-byte pieces per row
+    constexpr int CPL = HD > 64 ? 2 : 1;       // P.V columns per lane
+    constexpr int NPC = (ATT_TC * PR + NT - 1) / NT; // 16-byte pieces per thread
     const int ch = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
     const int G = D.n_heads / D.n_kv;
     const int p = min(pos[t], D.ctx - 1);
@@ -303,80 +310,92 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(FrameDims D, const fl
         return; // past the current position: the merge reads no record from here
     const bool single = p + 1 <= ATT_TC;
     float *qs = smem;                                  // [G][HD]
-    uint16_t *ks = (uint16_t *)(qs + G * HD);          // [TC][KS]
+    float *sc = qs + G * HD;                           // [G][TC]: p of head g, position j
+    uint16_t *ks = (uint16_t *)(sc + G * ATT_TC);      // [TC][KS]
     uint16_t *vs = ks + ATT_TC * KS;                   // [TC][HD]
     const int wave = tid >> 6, ln = tid & 63;
     const size_t row0 = (((size_t)t * D.n_layers + li) * D.ctx + t0) * D.kvd + (size_t)kvh * HD;
     const float *qsrc = q_rot + (size_t)t * D.qd + (size_t)kvh * G * HD;
-    // every K/V load is issued before the first LDS store; rows past nt
-    // repeat row nt-1 and are never read
-    constexpr int NPC = (ATT_TC * PR + 255) / 256; // 16-byte pieces per thread
+    // rows past nt repeat row nt-1 and are never read
     uint4 kr[NPC], vr[NPC];
 #pragma unroll
     for (int u = 0; u < NPC; u++) {
-        const int i = tid + 256 * u;
-        const size_t gi = row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR);
-        kr[u] = *(const uint4 *)(kc + gi);
-        vr[u] = *(const uint4 *)(vc + gi);
+        const int i = tid + NT * u;
+        kr[u] = *(const uint4 *)(kc + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR));
     }
-    for (int i = tid; i < G * HD; i += 256)
+#pragma unroll
+    for (int u = 0; u < NPC; u++) {
+        const int i = tid + NT * u;
+        vr[u] = *(const uint4 *)(vc + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR));
+    }
+    for (int i = tid; i < G * HD; i += NT)
         qs[i] = qsrc[i];
 #pragma unroll
     for (int u = 0; u < NPC; u++) {
-        const int i = tid + 256 * u;
-        if (i < ATT_TC * PR) {
+        const int i = tid + NT * u;
+        if (i < ATT_TC * PR)
             *(uint4 *)(ks + (i / PR) * KS + 8 * (i % PR)) = kr[u];
-            *(uint4 *)(vs + (i / PR) * HD + 8 * (i % PR)) = vr[u];
-        }
     }
     __syncthreads();
     const uint16_t *krow = ks + min(ln, nt - 1) * KS;
     float *rec = part + (((size_t)t * D.n_kv + kvh) * n_chunks + ch) * (size_t)G * (HD + 2);
-    // wave w: query heads w, w+4, ...; lane j: position j (scores), then
-    // columns 2j, 2j+1 (P.V, with p_j broadcast from lane j by readlane)
-    const int d0 = 2 * ln;
-    const bool dv = d0 < HD;
-    for (int g = wave; g < G; g += 4) {
+    for (int g = wave; g < G; g += ATT_WAVES) {
         const float s = ln < nt ? dot_f32_key<HD>(qs + g * HD, krow) * D.scale : -INFINITY;
         const float m = wave_max(s);
         float e = ln < nt ? exp_f32(s - m) : 0.0f;
-        float l = 0.0f;
-        for (int j = 0; j < nt; j++) // the reference's sum order
-            l = l + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+        float l;
         if (single) {
+            l = 0.0f;
+            for (int j = 0; j < nt; j++) // the reference's sum order
+                l = l + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
             const float inv = 1.0f / l;
             e = e * inv;
+        } else {
+            l = wave_sum_f(e);
         }
+        sc[g * ATT_TC + ln] = e;
         if (ln == 0) {
             rec[g] = m;
             rec[G + g] = single ? 1.0f : l;
         }
+    }
+#pragma unroll
+    for (int u = 0; u < NPC; u++) {
+        const int i = tid + NT * u;
+        if (i < ATT_TC * PR)
+            *(uint4 *)(vs + (i / PR) * HD + 8 * (i % PR)) = vr[u];
+    }
+    __syncthreads();
+    const int d0 = CPL * ln;
+    if (d0 >= HD)
+        return;
+    for (int g = wave; g < G; g += ATT_WAVES) {
+        const float *pg = sc + g * ATT_TC;
         float a0 = 0.0f, a1 = 0.0f;
         for (int j0 = 0; j0 < nt; j0 += 8) {
+            const float4 pa = *(const float4 *)(pg + j0), pb = *(const float4 *)(pg + j0 + 4);
+            const float pj[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
             uint32_t vw[8];
-            float pj[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                const int j = j0 + u;
-                const bool in = j < nt;
-                vw[u] = in && dv ? *(const uint32_t *)(vs + j * HD + d0) : 0u;
-                const float pr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j & 63));
-                pj[u] = in ? pr : 0.0f;
+                const int j = min(j0 + u, ATT_TC - 1);
+                if constexpr (CPL == 2)
+                    vw[u] = *(const uint32_t *)(vs + j * HD + d0);
+                else
+                    vw[u] = vs[j * HD + d0];
             }
-            // positions past nt add +0 (p = 0, v = 0) to accumulators that
-            // are never -0: no change
+            // positions past nt have p = 0 and a finite v (a repeated row):
+            // they add +0 to accumulators that are never -0, no change
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                const float p0 = pj[u] * half_bits_to_float((uint16_t)(vw[u] & 0xffff));
-                const float p1 = pj[u] * half_bits_to_float((uint16_t)(vw[u] >> 16));
-                a0 = a0 + p0;
-                a1 = a1 + p1;
+                a0 = a0 + pj[u] * half_bits_to_float((uint16_t)(vw[u] & 0xffff));
+                if constexpr (CPL == 2)
+                    a1 = a1 + pj[u] * half_bits_to_float((uint16_t)(vw[u] >> 16));
             }
         }
-        if (dv) {
-            rec[2 * G + g * HD + d0] = a0;
+        rec[2 * G + g * HD + d0] = a0;
+        if constexpr (CPL == 2)
             rec[2 * G + g * HD + d0 + 1] = a1;
-        }
     }
 }
 
@@ -729,7 +748,8 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     D.eps = m->eps;
     D.scale = 1.0f / sqrtf((float)m->head_dim); // llama.zig attn scale
     const int G = D.n_heads / D.n_kv;
-    const size_t att_lds = (size_t)G * D.hd * 4 + (size_t)ATT_TC * (D.hd + 8) * 2 + (size_t)ATT_TC * D.hd * 2;
+    const size_t att_lds = (size_t)G * D.hd * 4 + (size_t)G * ATT_TC * 4 + (size_t)ATT_TC * (D.hd + 8) * 2 +
+                           (size_t)ATT_TC * D.hd * 2;
     if (att_lds > 64 * 1024)
         return fail(LOOMHIP_DECLINED, "token_frame: attention tile exceeds LDS (%zu B)", att_lds);
     const size_t cmb_lds = (4 * 256 + (size_t)CMB_NH * n_chunks) * 4;
@@ -761,13 +781,13 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         int ph = prof_begin(LOOMHIP_KT_ATTN, st);
         const dim3 agrid(n_chunks, D.n_kv, n);
         if (D.hd == 128)
-            hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(256), att_lds, st, D, w.qrot, k_cache,
+            hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, w.qrot, k_cache,
                                v_cache, pos, (int)li, n_chunks, w.part);
         else if (D.hd == 64)
-            hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(256), att_lds, st, D, w.qrot, k_cache,
+            hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, w.qrot, k_cache,
                                v_cache, pos, (int)li, n_chunks, w.part);
         else
-            hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(256), att_lds, st, D, w.qrot, k_cache,
+            hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, w.qrot, k_cache,
                                v_cache, pos, (int)li, n_chunks, w.part);
         prof_end(ph, st);
         note_launch();
