@@ -16,7 +16,7 @@
  *     (src/compute/backend.zig:75-96);
  *   - device-resident calls (suffix _dev): every tensor pointer is a device
  *     pointer in the device weight layout, work is stream-ordered on the
- *     given stream (NULL = the library's compute stream) and nothing is
+ *     given stream (NULL = the null stream, as in HIP) and nothing is
  *     copied to or from the host.  These are the hot path.
  *
  * Numerics: LOOMHIP_NUM_CPU_PARITY (default) quantizes activations to int8
@@ -245,6 +245,93 @@ typedef struct {
 int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int32_t *pos, size_t n,
                             uint16_t *k_cache, uint16_t *v_cache, float *logits, uint32_t *next,
                             void *stream);
+
+/* ---- expert cache: pinned host memory -> HBM LRU ----------------------------
+ * The tiers of ExpertCache (src/engine/expert_cache.zig:150-249) with HBM as
+ * the cache and pinned host memory as the backing store that readBlock
+ * (197-215) reads: a pinned hot set held in HBM for good (pin, 217-227), an
+ * LRU of `capacity` HBM slots (Lru, 39-148: touch-to-front on a hit, fill
+ * never-used slots before evicting the tail, abort on a failed fill), and
+ * the host copy.  A miss copies the block host -> HBM on the library's copy
+ * stream; the caller's stream waits for that copy and nothing else, and a
+ * refill of an evicted slot waits for the work that last used the slot.
+ * Single-threaded, like the reference's generation thread. */
+typedef struct loomhip_ec loomhip_ec;
+
+/* Stats (expert_cache.zig:18-36): misses = disk_misses, bytes_read their
+ * bytes; warm-up reads (pin, prefetch) are counted apart. */
+typedef struct {
+    uint64_t pin_hits, lru_hits, misses, bytes_read, warmup_reads, warmup_bytes;
+} loomhip_ec_stats;
+
+/* Pinned (page-locked) host memory for the backing store: the copy source
+ * must be pinned for the copies to run asynchronously. */
+void *loomhip_host_alloc(size_t bytes);
+void loomhip_host_free(void *p);
+
+/* ExpertCache.init (expert_cache.zig:160-185): `capacity` LRU slots and
+ * `pin_slots` pinned ones of `slot_bytes` each in HBM, expert ids
+ * [0, n_ids). */
+int loomhip_ec_create(size_t capacity, size_t pin_slots, size_t slot_bytes, size_t n_ids,
+                      loomhip_ec **out);
+void loomhip_ec_destroy(loomhip_ec *ec);
+/* The backing block of expert `id` (the manifest entry readBlock reads,
+ * expert_cache.zig:197-200): len <= slot_bytes bytes of host memory, which
+ * the caller keeps alive and unchanged while the cache exists. */
+int loomhip_ec_set_source(loomhip_ec *ec, size_t id, const void *host, size_t len);
+/* ExpertCache.pin (217-227): load `ids` into the pinned HBM set; idempotent
+ * per id; warm-up reads.  Returns when the copies are done. */
+int loomhip_ec_pin(loomhip_ec *ec, const uint32_t *ids, size_t n);
+/* ExpertCache.get (230-249): the HBM address of expert `id`'s block, valid
+ * for work enqueued on `stream` until a later get or prefetch evicts it.
+ * access_count[id] += 1; pinned hit, LRU hit, or miss (reserve a slot,
+ * async copy, `stream` waits for it).  A missing source aborts the reserve
+ * (Lru.abort, 138-147) and fails. */
+int loomhip_ec_get(loomhip_ec *ec, size_t id, void *stream, void **dev_out);
+/* Record that the blocks handed out since the last release are used by work
+ * already enqueued on `stream`: a later refill of their slots waits for that
+ * work only (without it, a refill waits for all work enqueued on the stream
+ * by the time of the eviction). */
+int loomhip_ec_release(loomhip_ec *ec, void *stream);
+/* Warm the LRU with `ids` ahead of their gets: absent ids are reserved (MRU)
+ * and copied asynchronously (warm-up reads); present ones are left as they
+ * are.  Not in the reference's cache: the GPU tier's copy/compute overlap. */
+int loomhip_ec_prefetch(loomhip_ec *ec, const uint32_t *ids, size_t n);
+int loomhip_ec_get_stats(const loomhip_ec *ec, loomhip_ec_stats *out);
+/* access_count[0..n) (the STATS input of hottestWithinBudget, stats.zig:
+ * 135-160). */
+int loomhip_ec_access_counts(const loomhip_ec *ec, uint64_t *out, size_t n);
+/* Lru.clear (128-133): drop every LRU entry (pinned set and stats kept). */
+int loomhip_ec_clear(loomhip_ec *ec);
+
+/* A routed MoE layer whose experts live in the cache: expert e's block is
+ * cache id id_base + e (checkpoint.expertId, src/engine/checkpoint.zig:
+ * 162-164) holding gate [ffn][dim] and up [ffn][dim] of type gate_t and down
+ * [dim][ffn] of type down_t (device layout) at the given byte offsets. */
+typedef struct {
+    size_t dim, ffn, n_expert, n_used;
+    int gating, weights_norm;
+    float weights_scale;
+    const float *router;      /* [n_expert][dim] f32, device */
+    const float *router_bias; /* [n_expert] logit bias or NULL */
+    const float *sel_bias;    /* [n_expert] selection-only bias or NULL */
+    int gate_t, down_t;
+    size_t id_base;
+    size_t gate_off, up_off, down_off;
+} loomhip_moe_layer_ec;
+
+/* moe.moeFFN's routed part (src/engine/moe.zig:97-124) on the device with
+ * the cache: router, route (device), the ids to the host, then one get per
+ * routed expert and the experts' SwiGLU FFNs, out[t] = sum g * FFN_e(x_t)
+ * from +0.  n_tok == 1: the selection order of moeFFN (one get per slot);
+ * n_tok > 1: each distinct expert once per call in ascending order, its
+ * tokens batched (moeBatchUnion, llama.zig:1828-1924).  More distinct
+ * experts than capacity run in rounds of at most `capacity` gets.  out is
+ * [n_tok][dim] (device, overwritten); ids_out/gates_out ([n_tok][n_used],
+ * host) are optional.  Synchronises `stream` once per call (the ids). */
+int loomhip_moe_layer_cached(const loomhip_moe_layer_ec *L, loomhip_ec *ec, const float *normed,
+                             size_t n_tok, float *out, uint32_t *ids_out, float *gates_out,
+                             void *stream);
 
 #ifdef __cplusplus
 }

@@ -109,6 +109,36 @@ class ModelDesc(C.Structure):
     ]
 
 
+class EcStats(C.Structure):
+    """Mirror of ``loomhip_ec_stats`` in include/loomhip.h."""
+
+    _fields_ = [(n, C.c_uint64) for n in ("pin_hits", "lru_hits", "misses", "bytes_read",
+                                          "warmup_reads", "warmup_bytes")]
+
+
+class MoeLayerEcDesc(C.Structure):
+    """Mirror of ``loomhip_moe_layer_ec`` in include/loomhip.h."""
+
+    _fields_ = [
+        ("dim", C.c_size_t),
+        ("ffn", C.c_size_t),
+        ("n_expert", C.c_size_t),
+        ("n_used", C.c_size_t),
+        ("gating", C.c_int),
+        ("weights_norm", C.c_int),
+        ("weights_scale", C.c_float),
+        ("router", C.c_void_p),
+        ("router_bias", C.c_void_p),
+        ("sel_bias", C.c_void_p),
+        ("gate_t", C.c_int),
+        ("down_t", C.c_int),
+        ("id_base", C.c_size_t),
+        ("gate_off", C.c_size_t),
+        ("up_off", C.c_size_t),
+        ("down_off", C.c_size_t),
+    ]
+
+
 def header_symbols() -> list[str]:
     """Every function name declared in include/loomhip.h."""
     text = open(HEADER).read()
@@ -163,6 +193,19 @@ def lib() -> C.CDLL:
         "loomhip_dequant_dev": (i, [i, vp, vp, sz, sz, vp]),
         "loomhip_moe_layer_dev": (i, [C.POINTER(MoeLayerDesc), vp, sz, i, vp, vp, vp, vp]),
         "loomhip_token_frame_dev": (i, [C.POINTER(ModelDesc), vp, vp, sz, vp, vp, vp, vp, vp]),
+        "loomhip_host_alloc": (vp, [sz]),
+        "loomhip_host_free": (None, [vp]),
+        "loomhip_ec_create": (i, [sz, sz, sz, sz, C.POINTER(vp)]),
+        "loomhip_ec_destroy": (None, [vp]),
+        "loomhip_ec_set_source": (i, [vp, sz, vp, sz]),
+        "loomhip_ec_pin": (i, [vp, vp, sz]),
+        "loomhip_ec_get": (i, [vp, sz, vp, C.POINTER(vp)]),
+        "loomhip_ec_release": (i, [vp, vp]),
+        "loomhip_ec_prefetch": (i, [vp, vp, sz]),
+        "loomhip_ec_get_stats": (i, [vp, C.POINTER(EcStats)]),
+        "loomhip_ec_access_counts": (i, [vp, vp, sz]),
+        "loomhip_ec_clear": (i, [vp]),
+        "loomhip_moe_layer_cached": (i, [C.POINTER(MoeLayerEcDesc), vp, vp, sz, vp, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

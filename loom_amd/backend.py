@@ -171,6 +171,8 @@ def clearWeightCache() -> None:
 
 
 def _stream():
+    """torch's current stream as a handle for the C ABI (NULL = the null
+    stream for both)."""
     import torch
 
     return C.c_void_p(torch.cuda.current_stream().cuda_stream)

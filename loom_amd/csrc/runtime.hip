@@ -87,7 +87,7 @@ int hip_fail(hipError_t e, const char *what) {
     return fail(LOOMHIP_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-hipStream_t stream_of(void *s) { return s ? (hipStream_t)s : g_ctx.compute; }
+hipStream_t stream_of(void *s) { return (hipStream_t)s; } // NULL: the null stream
 
 int Scratch::reserve(size_t bytes) {
     if (bytes <= cap)
@@ -322,6 +322,7 @@ void loomhip_shutdown(void) {
     g_ctx.xstage.release();
     g_ctx.ostage.release();
     moe_release_scratch();
+    ec_release_scratch();
     prof_drain();
     for (hipEvent_t e : g_prof_pool)
         (void)hipEventDestroy(e);

@@ -50,5 +50,6 @@ int pick_nt(int n);
 // Device group table for n vectors in groups of nt against plane 0 (cached per (n, nt)).
 const DmmvGroup *dense_groups(int n, int nt, int *count);
 void moe_release_scratch();
+void ec_release_scratch();
 
 } // namespace lh

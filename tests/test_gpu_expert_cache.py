@@ -1,0 +1,218 @@
+"""GPU tests of the HBM expert cache (src/engine/expert_cache.zig on the
+device tier) and the routed MoE layer that reads its experts through it.
+
+  * the hit/miss bookkeeping equals the oracle's replay of ExpertCache.get
+    (oracle/cache_ref.c, itself pinned to the reference's LRU KAT and an
+    OrderedDict replay) on the same access trace, exactly;
+  * every block handed out holds its backing bytes (read back from HBM);
+  * the cached MoE layer's output is bit-identical to the resident layer's
+    (loomhip_moe_layer_dev) on the same weights, at one token (moeFFN's
+    selection order) and at batches forced through several rounds;
+  * pin, prefetch, clear and a missing backing block behave as the
+    reference's pin / (warm-up reads) / Lru.clear / Lru.abort.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+Q4_K, Q6_K = 12, 14
+
+
+@pytest.fixture(scope="module")
+def ec_mod(oracle):
+    import loom_amd
+
+    loom_amd.init(0)
+    from loom_amd import expert_cache
+
+    return expert_cache
+
+
+def _hip():
+    """The HIP runtime torch loaded (for reading raw device addresses back)."""
+    for line in open("/proc/self/maps"):
+        if "libamdhip64" in line:
+            L = C.CDLL(line.split()[-1])
+            L.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+            return L
+    raise RuntimeError("libamdhip64 not loaded")
+
+
+def _read_dev(addr, n):
+    import torch
+
+    torch.cuda.synchronize()
+    out = np.empty(n, np.uint8)
+    assert _hip().hipMemcpy(out.ctypes.data, addr, n, 2) == 0  # device -> host
+    return out
+
+
+def _zipf_trace(rng, n_ids, n, s=1.1):
+    p = 1.0 / np.arange(1, n_ids + 1) ** s
+    perm = rng.permutation(n_ids)
+    return perm[rng.choice(n_ids, size=n, p=p / p.sum())].astype(np.uint32)
+
+
+def test_get_matches_oracle_replay_and_contents(ec_mod, oracle):
+    n_ids, slot, cap = 40, 4096, 6
+    rng = np.random.default_rng(3)
+    host = ec_mod.HostBuffer(n_ids * slot)
+    host.array[:] = rng.integers(0, 256, host.nbytes, dtype=np.uint8)
+    ec = ec_mod.ExpertCache(cap, slot, n_ids, pin_slots=2)
+    for i in range(n_ids):
+        ec.set_source(i, host, i * slot, slot)
+    ec.pin([0, 3])
+    assert ec.pinnedCount() == 2
+    trace = _zipf_trace(rng, n_ids, 400)
+    for j, i in enumerate(trace):
+        addr = ec.get(int(i))
+        if j % 37 == 0:
+            assert np.array_equal(_read_dev(addr, slot), host.array[i * slot:(i + 1) * slot]), j
+    pinned = np.zeros(n_ids, np.uint8)
+    pinned[[0, 3]] = 1
+    counts, _ = oracle.cache_replay(cap, trace, pinned=pinned, n_ids=n_ids)
+    st = ec.stats
+    assert (st.pin_hits, st.lru_hits, st.disk_misses) == tuple(int(c) for c in counts)
+    assert st.bytes_read == st.disk_misses * slot
+    assert (st.warmup_reads, st.warmup_bytes) == (2, 2 * slot)
+    assert abs(st.hitRate() - (counts[0] + counts[1]) / len(trace)) < 1e-12
+    acc = ec.access_counts()
+    assert np.array_equal(acc, np.bincount(trace, minlength=n_ids).astype(np.uint64))
+    # the pinner's input: stats.hottestWithinBudget over these counts
+    assert oracle.hottest_within_budget(acc, slot, 3 * slot)[0] == int(np.argmax(acc))
+    ec.close()
+
+
+def test_refill_waits_for_the_slot_users(ec_mod):
+    """Capacity 1: every get of another id evicts the only slot; each block's
+    bytes are read by a device copy enqueued right after its get, before
+    the next eviction, and must be that block's bytes."""
+    import torch
+
+    n_ids, slot = 8, 1 << 20
+    rng = np.random.default_rng(5)
+    host = ec_mod.HostBuffer(n_ids * slot)
+    host.array[:] = rng.integers(0, 256, host.nbytes, dtype=np.uint8)
+    ec = ec_mod.ExpertCache(1, slot, n_ids)
+    for i in range(n_ids):
+        ec.set_source(i, host, i * slot, slot)
+    seq = [1, 2, 1, 5, 7, 7, 0, 3]
+    outs = []
+    hip = _hip()
+    hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    st = torch.cuda.current_stream()
+    for i in seq:
+        addr = ec.get(i)
+        o = torch.empty(slot, dtype=torch.uint8, device="cuda")
+        assert hip.hipMemcpyAsync(o.data_ptr(), addr, slot, 3, C.c_void_p(st.cuda_stream)) == 0
+        ec.release()
+        outs.append(o)
+    torch.cuda.synchronize()
+    for i, o in zip(seq, outs):
+        assert np.array_equal(o.cpu().numpy(), host.array[i * slot:(i + 1) * slot]), i
+    assert ec.stats.disk_misses == 7 and ec.stats.lru_hits == 1
+    ec.close()
+
+
+def test_missing_source_aborts_and_prefetch_warms(ec_mod):
+    from loom_amd import LoomHipError
+
+    n_ids, slot = 10, 256
+    host = ec_mod.HostBuffer(n_ids * slot)
+    host.array[:] = np.arange(host.nbytes, dtype=np.uint64).astype(np.uint8)
+    ec = ec_mod.ExpertCache(3, slot, n_ids)
+    for i in range(n_ids - 1):  # id 9 has no backing block
+        ec.set_source(i, host, i * slot, slot)
+    ec.get(0)
+    with pytest.raises(LoomHipError):
+        ec.get(9)
+    # the failed reserve returned its slot: ids 1 and 2 still fit without evicting 0
+    ec.get(1)
+    ec.get(2)
+    ec.get(0)
+    st = ec.stats
+    assert (st.lru_hits, st.disk_misses) == (1, 3)
+    ec.prefetch([4, 0])  # 4 absent: warm-up read (evicts the LRU tail, 1); 0 present: untouched
+    ec.get(4)
+    st = ec.stats
+    assert (st.lru_hits, st.disk_misses, st.warmup_reads) == (2, 3, 1)
+    ec.clear()
+    ec.get(0)
+    assert ec.stats.disk_misses == 4
+    ec.close()
+
+
+def _layer(E, dim, ffn, k, seed, gating):
+    import torch
+
+    from loom_amd import backend as be
+
+    gate = be.repack_dev(Q4_K, be.synth_ggml_dev(Q4_K, ffn, dim, E, seed * 10 + 1, 0.02), ffn, dim, E)
+    up = be.repack_dev(Q4_K, be.synth_ggml_dev(Q4_K, ffn, dim, E, seed * 10 + 2, 0.02), ffn, dim, E)
+    down = be.repack_dev(Q6_K, be.synth_ggml_dev(Q6_K, dim, ffn, E, seed * 10 + 3, 0.02), dim, ffn, E)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    router = (torch.randn(E, dim, generator=g, device="cuda") / np.sqrt(dim)).contiguous()
+    ranks = torch.randperm(E, generator=g, device="cuda").float() + 1
+    z = -1.1 * torch.log(ranks)
+    bias = (z - z.mean()).contiguous()
+    res = be.MoeLayer(dim, ffn, E, k, router, gate, up, down, Q4_K, Q4_K, Q6_K, router_bias=bias,
+                      gating=gating)
+    return res, (gate, up, down, router, bias)
+
+
+def _cached_setup(ec_mod, E, dim, ffn, k, cap, tensors, gating, pin=()):
+    import torch
+
+    from loom_amd import MoeLayerEcDesc, plane_bytes
+
+    gate, up, down, router, bias = tensors
+    gb, db = plane_bytes(Q4_K, ffn, dim), plane_bytes(Q6_K, dim, ffn)
+    slot = 2 * gb + db
+    host = ec_mod.HostBuffer(E * slot)
+    hv = torch.from_numpy(host.array)
+    for e in range(E):
+        o = e * slot
+        hv[o:o + gb].copy_(gate[e * gb:(e + 1) * gb].cpu())
+        hv[o + gb:o + 2 * gb].copy_(up[e * gb:(e + 1) * gb].cpu())
+        hv[o + 2 * gb:o + slot].copy_(down[e * db:(e + 1) * db].cpu())
+    ec = ec_mod.ExpertCache(cap, slot, E, pin_slots=len(pin))
+    for e in range(E):
+        ec.set_source(e, host, e * slot, slot)
+    if pin:
+        ec.pin(list(pin))
+    desc = MoeLayerEcDesc(dim, ffn, E, k, gating, 1, 1.0, router.data_ptr(), bias.data_ptr(), None, Q4_K,
+                          Q6_K, 0, 0, gb, 2 * gb)
+    return ec, desc, host
+
+
+@pytest.mark.parametrize("n_tok,cap,pin", [(1, 5, ()), (1, 3, (2,)), (6, 4, ()), (24, 7, (0, 5))])
+def test_cached_layer_matches_resident(ec_mod, oracle, n_tok, cap, pin):
+    import torch
+
+    from loom_amd import COMBINE_EXPERT_ASC, COMBINE_SELECTION, GATING_SOFTMAX
+
+    E, dim, ffn, k = 32, 512, 256, 4
+    res, tensors = _layer(E, dim, ffn, k, 11, GATING_SOFTMAX)
+    ec, desc, host = _cached_setup(ec_mod, E, dim, ffn, k, cap, tensors, GATING_SOFTMAX, pin)
+    g = torch.Generator(device="cuda").manual_seed(n_tok)
+    trace = []
+    for step in range(5):
+        x = torch.randn(n_tok, dim, generator=g, device="cuda")
+        want = torch.zeros(n_tok, dim, device="cuda")
+        ids_res = torch.zeros(n_tok, k, dtype=torch.int32, device="cuda")
+        res(x, want, COMBINE_SELECTION if n_tok == 1 else COMBINE_EXPERT_ASC, ids=ids_res)
+        got = torch.full((n_tok, dim), float("nan"), device="cuda")
+        ids, gates = ec.moe_layer(desc, x, got, n_tok, want_ids=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(ids.astype(np.int32), ids_res.cpu().numpy())
+        assert torch.equal(got, want), (step, float((got - want).abs().max()))
+        trace += list(ids[0]) if n_tok == 1 else sorted(set(ids.ravel().tolist()))
+    pinned = np.zeros(E, np.uint8)
+    pinned[list(pin)] = 1
+    counts, _ = oracle.cache_replay(cap, np.array(trace, np.uint32), pinned=pinned, n_ids=E)
+    st = ec.stats
+    assert (st.pin_hits, st.lru_hits, st.disk_misses) == tuple(int(c) for c in counts)
+    ec.close()
