@@ -63,6 +63,8 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="0 = the reference's default, host cores - 2 (capped at the box's share)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    ap.add_argument("--no-cache", action="store_true", help="skip the config-5 expert-cache streaming run")
+    ap.add_argument("--cache-steps", type=int, default=1024, help="config-5 decode steps at batch 1")
     return ap.parse_args()
 
 
@@ -106,13 +108,17 @@ def bench_batch(dm, b, args):
     ms = ev0.elapsed_time(ev1) / args.steps
 
     # kernel pass: eager steps with HIP events around the tagged launches and
-    # the routed ids recorded for the distinct-expert count
+    # the routed ids recorded for the distinct-expert count.  A spin kernel
+    # ahead of each step holds the stream while the host enqueues the step,
+    # so the events time the kernels back to back, as the graph runs them,
+    # not the host's launch rate.
     ids = torch.zeros((dm.spec.n_layers, b, TOP_K), dtype=torch.int32, device="cuda")
     dm.desc.ids_out = ids.data_ptr()
     dec.pos.fill_(args.ctx)
     be.profileKernels(True)
     distinct = []
     for _ in range(min(args.steps, 6)):
+        torch.cuda._sleep(50_000_000)
         dec.step()
         torch.cuda.synchronize()
         h = ids.cpu().numpy()
@@ -211,6 +217,128 @@ def cpu_baseline(seconds, threads, ctx):
                       f"head {th * 1e3:.1f} ms over {n_head} runs), scaled to {N_LAYERS} layers"}
 
 
+C5_DIM, C5_FFN, C5_E, C5_K, C5_SLOTS = 7168, 2048, 256, 8, 64
+
+
+def _c5_layer():
+    """Config 5's routed block: 256 experts of Q4_K gate/up [2048][7168] and
+    down [7168][2048] (24,772,608 B each) in pinned host memory, the f32
+    router with a Zipf(1.1) logit bias, sigmoid top-8 with renorm."""
+    import torch
+
+    from loom_amd import GATING_SIGMOID, Q4_K, MoeLayerEcDesc, plane_bytes
+    from loom_amd import backend as be
+    from loom_amd.expert_cache import HostBuffer
+
+    gb, db = plane_bytes(Q4_K, C5_FFN, C5_DIM), plane_bytes(Q4_K, C5_DIM, C5_FFN)
+    slot = 2 * gb + db
+    host = HostBuffer(C5_E * slot)
+    hv = torch.from_numpy(host.array)
+    chunk = 16
+    for e0 in range(0, C5_E, chunk):
+        for k, (rows, cols, off) in enumerate(((C5_FFN, C5_DIM, 0), (C5_FFN, C5_DIM, gb), (C5_DIM, C5_FFN, 2 * gb))):
+            pb = plane_bytes(Q4_K, rows, cols)
+            dev = be.repack_dev(Q4_K, be.synth_ggml_dev(Q4_K, rows, cols, chunk, 5000 + 10 * e0 + k, 0.02),
+                                rows, cols, chunk)
+            d = dev.view(chunk, pb).cpu()
+            for i in range(chunk):
+                hv[(e0 + i) * slot + off:(e0 + i) * slot + off + pb].copy_(d[i])
+            del dev
+    g = torch.Generator(device="cuda").manual_seed(55)
+    router = (torch.randn(C5_E, C5_DIM, generator=g, device="cuda") / np.sqrt(C5_DIM)).contiguous()
+    ranks = torch.randperm(C5_E, generator=g, device="cuda").float() + 1
+    z = -1.1 * torch.log(ranks)
+    bias = (z - z.mean()).contiguous()
+    desc = MoeLayerEcDesc(C5_DIM, C5_FFN, C5_E, C5_K, GATING_SIGMOID, 1, 1.0, router.data_ptr(),
+                          bias.data_ptr(), None, Q4_K, Q4_K, 0, 0, gb, 2 * gb)
+    return host, slot, gb, desc, (router, bias)
+
+
+def bench_cache(args):
+    """Config 5: the routed block decoding with its experts streamed from
+    pinned host memory through a 64-slot HBM LRU (loomhip_moe_layer_cached);
+    tok/s, hit rate and bytes over each link at batch 1 and 64."""
+    import torch
+
+    from loom_amd.expert_cache import ExpertCache
+
+    t0 = time.perf_counter()
+    host, slot, gb, desc, keep = _c5_layer()
+    log(f"config 5: {C5_E} experts x {slot} B in pinned host memory in {time.perf_counter() - t0:.1f} s")
+    ec = ExpertCache(C5_SLOTS, slot, C5_E)
+    for e in range(C5_E):
+        ec.set_source(e, host, e * slot, slot)
+    # the fill rate alone: 64 distinct misses
+    out1 = torch.empty(1, C5_DIM, device="cuda")
+    torch.cuda.synchronize()
+    s0 = ec.stats
+    t0 = time.perf_counter()
+    for e in range(C5_SLOTS):
+        ec.get(e)
+    ec.release()
+    torch.cuda.synchronize()
+    fill_s = time.perf_counter() - t0
+    fill_gbs = (ec.stats.bytes_read - s0.bytes_read) / fill_s / 1e9
+    ec.clear()
+    res = {"fill_GBs": round(fill_gbs, 2)}
+    g = torch.Generator(device="cuda").manual_seed(77)
+    for b, steps in ((1, args.cache_steps), (64, max(4, args.cache_steps // 32))):
+        warm = 16 if b == 1 else 2
+        x = torch.randn(warm + steps, b, C5_DIM, generator=g, device="cuda")
+        out = torch.empty(b, C5_DIM, device="cuda")
+        for i in range(warm):
+            ec.moe_layer(desc, x[i], out, b)
+        torch.cuda.synchronize()
+        s0 = ec.stats
+        t0 = time.perf_counter()
+        for i in range(warm, warm + steps):
+            ec.moe_layer(desc, x[i], out, b)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        s1 = ec.stats
+        hits = (s1.pin_hits - s0.pin_hits) + (s1.lru_hits - s0.lru_hits)
+        miss = s1.disk_misses - s0.disk_misses
+        res[f"b{b}"] = {
+            "steps": steps, "tok_s": round(b * steps / dt, 2), "ms_per_step": round(dt / steps * 1e3, 3),
+            "hit_rate": round(hits / max(1, hits + miss), 4), "gets_per_step": round((hits + miss) / steps, 2),
+            "misses_per_step": round(miss / steps, 2),
+            "host_link_GBs": round((s1.bytes_read - s0.bytes_read) / dt / 1e9, 2),
+            "hbm_hit_bytes_per_step": int(hits * slot / steps),
+        }
+        log(f"config 5 batch {b}: {res[f'b{b}']}")
+    ec.close()
+    return res, host, gb, keep
+
+
+def cpu_baseline_c5(host, gb, keep, threads, seconds):
+    """Loom's CPU MoE block (the oracle's moeRun restatement, row-parallel
+    pool) on the same 256 experts, read from the pinned host copy."""
+    import oracle as o
+
+    o.build()
+    router, bias = (t.cpu().numpy() for t in keep)
+    slot = host.nbytes // C5_E
+    db = slot - 2 * gb
+    a = host.array.reshape(C5_E, slot)
+    gate = np.ascontiguousarray(a[:, :gb])
+    up = np.ascontiguousarray(a[:, gb:2 * gb])
+    down = np.ascontiguousarray(a[:, 2 * gb:2 * gb + db])
+    w = o.MoeWeights(C5_DIM, C5_FFN, C5_E, C5_K, router, gate, up, down, 12, 12, 12, router_bias=bias,
+                     gating=o.GATING_SIGMOID, weights_norm=True)
+    rng = np.random.default_rng(9)
+    with o.Pool(threads):
+        o.moe_layer_token(w, rng.standard_normal(C5_DIM).astype(np.float32))
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < seconds:
+            o.moe_layer_token(w, rng.standard_normal(C5_DIM).astype(np.float32))
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+    return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} tokens through the config-5 routed block (moeRun order) with all 256 experts "
+                      f"in host memory ({dt * 1e3:.1f} ms/token)"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -269,12 +397,23 @@ def main():
                              "distinct_experts_per_layer": round(rb["distinct"], 2),
                              "roofline": rb["roofline"], "step_roofline": step_roof(rb),
                              "kernels": rb["per_kernel"]}
+    cores = args.cpu_threads or max(1, min(16, os.cpu_count() or 1) - 2)
+    del dm
+    torch.cuda.empty_cache()
     if not args.no_cpu:
-        cores = args.cpu_threads or max(1, min(16, os.cpu_count() or 1) - 2)
-        del dm
-        torch.cuda.empty_cache()
         log(f"cpu baseline: {cores} threads, {args.cpu_seconds} s sample")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, cores, args.ctx)
+    if not args.no_cache:
+        c5, host, gb, keep = bench_cache(args)
+        line["expert_cache"] = {
+            "workload": f"config 5: DeepSeek-V3-class routed block, hidden {C5_DIM}, {C5_E} experts top-{C5_K} "
+                        "(sigmoid, renorm, Zipf(1.1) logit bias), expert ffn 2048, Q4_K gate/up/down "
+                        "(24,772,608 B per expert), 6.34 GB pinned host backing store, "
+                        f"{C5_SLOTS}-slot HBM LRU (1.59 GB); synthetic hidden states",
+            **c5}
+        if not args.no_cpu:
+            line["expert_cache"]["cpu_baseline"] = cpu_baseline_c5(host, gb, keep, cores, args.cpu_seconds / 3)
+        host.free()
     print(json.dumps(line), flush=True)
 
 
