@@ -143,7 +143,7 @@ def per_launch_bytes(name, b, ctx, distinct, layers):
     if name == "head":
         return HEAD_BYTES
     if name == "qkvo":
-        return ATTN_W_BYTES / 4  # four launches per layer
+        return ATTN_W_BYTES / 2  # two launches per layer: q/k/v, then wo
     return 0
 
 

@@ -85,7 +85,7 @@ uint64_t loomhip_take_launch_count(void);
 #define LOOMHIP_KT_DENSE 2   /* dense dequant-fused matvec */
 #define LOOMHIP_KT_ATTN 3    /* token frame: attention over the K/V cache (partials) */
 #define LOOMHIP_KT_HEAD 4    /* token frame: output head matvec */
-#define LOOMHIP_KT_QKV 5     /* token frame: q, k, v and wo matvecs */
+#define LOOMHIP_KT_QKV 5     /* token frame: the q/k/v matvec launch and the wo matvec */
 #define LOOMHIP_KT_COUNT 6
 void loomhip_profile_kernels(int enable);
 /* Waits for the recorded events; total milliseconds and launch count of tag. */

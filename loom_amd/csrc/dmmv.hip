@@ -86,18 +86,13 @@ __device__ inline void tile_partials(const uint8_t *wb, const uint8_t *wb2, int 
 // ---- grouped matvec: one work group per (row tile, group of <= NT vectors
 // sharing one weight plane) -------------------------------------------------------
 template <int T, int NT, bool FUSED>
-__global__ __launch_bounds__(256) void dmmv_kernel(DmmvParams p) {
+__device__ __forceinline__ void dmmv_tile(const DmmvParams &p, int tile, int group, float *lds, int *vec) {
     using F = Fmt<T>;
-    extern __shared__ float lds[];
-    __shared__ int vec[NT];
-    const int ng = p.n_groups_dev ? *p.n_groups_dev : p.n_groups;
-    if ((int)blockIdx.y >= ng)
-        return;
-    const DmmvGroup g = p.groups[blockIdx.y];
+    const DmmvGroup g = p.groups[group];
     const int n = g.n;
     const int nb = p.cols / F::BE;
     const int TR = WAVES * p.rpw;
-    const int row0 = blockIdx.x * TR;
+    const int row0 = tile * TR;
     if (threadIdx.x < NT)
         vec[threadIdx.x] = p.pair_src[g.first + ((int)threadIdx.x < n ? threadIdx.x : 0)];
     __syncthreads();
@@ -114,6 +109,83 @@ __global__ __launch_bounds__(256) void dmmv_kernel(DmmvParams p) {
         const float v = row_value<FUSED>(lds, lds_mat, (size_t)k * TR + rl, nb);
         *o = p.accumulate ? *o + v : v;
     }
+}
+
+template <int T, int NT, bool FUSED>
+__global__ __launch_bounds__(256) void dmmv_kernel(DmmvParams p) {
+    extern __shared__ float lds[];
+    __shared__ int vec[NT];
+    const int ng = p.n_groups_dev ? *p.n_groups_dev : p.n_groups;
+    if ((int)blockIdx.y >= ng)
+        return;
+    dmmv_tile<T, NT, FUSED>(p, blockIdx.x, blockIdx.y, lds, vec);
+}
+
+// ---- several matrices against one activation set in one launch ------------------
+// Work groups [0, tiles_0) serve segment 0, the next tiles_1 segment 1, ...;
+// each segment has its own type, rows, rows per wave and output.  Same
+// arithmetic per row as dmmv_kernel.
+template <int NT>
+__global__ __launch_bounds__(256) void dmmv_seg_kernel(DmmvSegParams sp) {
+    extern __shared__ float lds[];
+    __shared__ int vec[NT];
+    int s = 0, bx = blockIdx.x;
+    while (s + 1 < sp.n_seg && bx >= sp.seg[s].tiles) {
+        bx -= sp.seg[s].tiles;
+        s++;
+    }
+    DmmvParams p = sp.base;
+    p.w = sp.seg[s].w;
+    p.rows = sp.seg[s].rows;
+    p.rpw = sp.seg[s].rpw;
+    p.out = sp.seg[s].out;
+    p.out_stride = sp.seg[s].rows;
+    switch (sp.seg[s].t) {
+    case LH_Q4_K:
+        dmmv_tile<LH_Q4_K, NT, false>(p, bx, blockIdx.y, lds, vec);
+        break;
+    case LH_Q6_K:
+        dmmv_tile<LH_Q6_K, NT, false>(p, bx, blockIdx.y, lds, vec);
+        break;
+    case LH_Q8_0:
+        dmmv_tile<LH_Q8_0, NT, false>(p, bx, blockIdx.y, lds, vec);
+        break;
+    default:
+        dmmv_tile<LH_Q4_0, NT, false>(p, bx, blockIdx.y, lds, vec);
+        break;
+    }
+}
+
+bool launch_dmmv_seg(int nt, DmmvSegParams sp, hipStream_t st) {
+    size_t lds = 0;
+    int tiles = 0;
+    for (int i = 0; i < sp.n_seg; i++) {
+        DmmvSeg &g = sp.seg[i];
+        g.rpw = dmmv_pick_rpw(g.t, sp.base.cols, g.rows, sp.base.n_groups, nt, false);
+        g.tiles = (g.rows + WAVES * g.rpw - 1) / (WAVES * g.rpw);
+        tiles += g.tiles;
+        const size_t l = dmmv_lds_bytes(g.t, sp.base.cols, nt, false, g.rpw);
+        lds = l > lds ? l : lds;
+    }
+    if (lds > 64 * 1024)
+        return false;
+    const dim3 grid(tiles, sp.base.n_groups);
+    switch (nt) {
+    case 1:
+        hipLaunchKernelGGL(dmmv_seg_kernel<1>, grid, dim3(256), lds, st, sp);
+        break;
+    case 2:
+        hipLaunchKernelGGL(dmmv_seg_kernel<2>, grid, dim3(256), lds, st, sp);
+        break;
+    case 4:
+        hipLaunchKernelGGL(dmmv_seg_kernel<4>, grid, dim3(256), lds, st, sp);
+        break;
+    default:
+        hipLaunchKernelGGL(dmmv_seg_kernel<8>, grid, dim3(256), lds, st, sp);
+        break;
+    }
+    note_launch();
+    return true;
 }
 
 bool dmmv_supported(int t, int cols) {

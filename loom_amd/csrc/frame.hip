@@ -647,6 +647,28 @@ static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameW
     return ok;
 }
 
+// q, k and v of one layer against the normalised input, one launch.
+static bool frame_qkv(const loomhip_layer &l, const FrameDims &D, const FrameWs &w, hipStream_t st) {
+    DmmvSegParams sp{};
+    DmmvParams &p = sp.base;
+    p.cols = D.dim;
+    p.xq = w.qa_dim.q;
+    p.xd = w.qa_dim.d;
+    p.xs = w.qa_dim.s;
+    p.pair_src = g_ctx.iota;
+    p.pair_dst = g_ctx.iota;
+    p.groups = w.groups;
+    p.n_groups = w.n_groups;
+    sp.seg[0] = DmmvSeg{(const uint8_t *)l.wq, l.wq_t, D.qd, w.q, 0, 0};
+    sp.seg[1] = DmmvSeg{(const uint8_t *)l.wk, l.wk_t, D.kvd, w.k, 0, 0};
+    sp.seg[2] = DmmvSeg{(const uint8_t *)l.wv, l.wv_t, D.kvd, w.v, 0, 0};
+    sp.n_seg = 3;
+    const int ph = prof_begin(LOOMHIP_KT_QKV, st);
+    const bool ok = launch_dmmv_seg(w.nt, sp, st);
+    prof_end(ph, st);
+    return ok;
+}
+
 template <bool EXACT>
 static void launch_norm_t(int qb, const float *x, int dim, const float *w, float eps, QAct qa,
                           float *normed, size_t n, hipStream_t st) {
@@ -771,9 +793,7 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         // layer 0 normalises the embedding row: exact sum in either mode
         launch_norm(act_block(l.wq_t), w.x, D.dim, l.attn_norm, D.eps, w.qa_dim, nullptr, n, st,
                     parity || li == 0);
-        if (!frame_matvec(l.wq_t, l.wq, D.qd, D.dim, w, n, w.qa_dim, w.q, 0, st) ||
-            !frame_matvec(l.wk_t, l.wk, D.kvd, D.dim, w, n, w.qa_dim, w.k, 0, st) ||
-            !frame_matvec(l.wv_t, l.wv, D.kvd, D.dim, w, n, w.qa_dim, w.v, 0, st))
+        if (!frame_qkv(l, D, w, st))
             return fail(LOOMHIP_ERR_ARG, "token_frame: q/k/v matvec declined");
         hipLaunchKernelGGL(qk_rope_kernel, dim3(D.n_heads + D.n_kv, n), dim3(64), 0, st, D, w.q, w.k,
                            w.v, l.q_norm, l.k_norm, pos, (int)li, rope_cs, w.qrot, k_cache, v_cache);

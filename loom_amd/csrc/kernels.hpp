@@ -40,6 +40,23 @@ struct DmmvParams {
     int accumulate; // 1: out = out + value (a residual add, tensor.zig:50-52)
 };
 
+// Up to DMMV_MAX_SEG matrices of any supported types against one activation
+// set (same cols, groups and pairs) in one launch.  base holds the shared
+// fields; rpw and tiles are filled by launch_dmmv_seg.
+constexpr int DMMV_MAX_SEG = 3;
+struct DmmvSeg {
+    const uint8_t *w;
+    int t, rows;
+    float *out; // out[dst * rows + row]
+    int rpw, tiles;
+};
+struct DmmvSegParams {
+    DmmvParams base;
+    DmmvSeg seg[DMMV_MAX_SEG];
+    int n_seg;
+};
+bool launch_dmmv_seg(int nt, DmmvSegParams sp, hipStream_t st);
+
 void note_launch();
 // Event timing around tagged launches (LOOMHIP_KT_*); -1 when disabled.
 int prof_begin(int tag, hipStream_t st);
