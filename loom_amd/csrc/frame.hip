@@ -275,33 +275,61 @@ __device__ __forceinline__ float dot_f32_key(const float *a, const uint16_t *kro
     return s;
 }
 
-// Work group (chunk, kv head, lane), 8 waves.  The chunk's keys and values
-// are staged through LDS with coalesced loads, every load issued up front
-// (keys in rows padded by 16 bytes, so that lane j reading row j with
-// 16-byte reads meets no bank conflict); the values' stores to LDS wait only
-// after the scores.  Wave w takes query heads w, w+8, ...: lane j scores key
-// j (dotF32 order, times the scale); per head m = the chunk's max, e =
-// exp(s - m), l = sum of e; then P.V with each lane on CPL columns, the
-// positions in order.  When the whole context is this one chunk (position <
-// 64) the record is the reference's own arithmetic (softmax, tensor.zig:18-28,
-// with l summed in position order, then out += p * v in position order): o =
-// sum_t (e_t * (1/l)) * v_t with l = 1; otherwise o = sum_t e_t * v_t,
-// unnormalised, and l a tree sum, for the merge.  Record per (lane, kv head,
-// chunk): m[G], l[G], o[G][HD].
+// Work group (chunk, kv head, lane), 8 waves.  Waves 0-3 load the chunk's
+// keys and the group's query heads, waves 4-7 its values, all loads issued
+// up front (rows past nt repeat row nt-1: finite, never weighted).
+//
+// One chunk (position < 64): the reference's own arithmetic (softmax,
+// tensor.zig:18-28, then out += p * v in position order), on the VALU.
+// Wave w takes query heads w, w+8, ...: lane j scores key j in dotF32 order
+// (keys in LDS rows padded by 16 bytes), m = max, e = exp(s - m), l = sum of e
+// in position order, p = e * (1/l); P.V with each lane on CPL columns,
+// positions in order.  Record: m, l = 1, o = sum_t p_t v_t.
+//
+// Split context in FAST numerics (HD a multiple of 32): matrix cores.  (In
+// PARITY numerics a split context takes the VALU path above, its scores in
+// dotF32 order and l a tree sum, for the merge.)  The group's query
+// heads are the 16 rows of the MFMA tiles (G <= 16; rows past G are zero).
+// Scores S = Q K^T with v_mfma_f32_16x16x32_f16: the f32 query split into
+// two f16 parts (hi = f16(q), lo = f16(q - hi), 22 significant bits) against
+// the exact fp16 keys, f32 accumulation; wave w < 4 scores positions 16w..
+// 16w+15.  Per head m = max, e = exp(s - m), l = a tree sum of e.  Then
+// O = P V with p split the same way against the fp16 values (staged by
+// waves 4-7 while the scores run, rows padded by 4 bytes, each lane
+// gathering its 8 positions of one column); wave w computes columns
+// 16w..16w+15.  Record: m, l, o = sum_t e_t v_t,
+// unnormalised, for the merge.  Record per (lane, kv head, chunk): m[G],
+// l[G], o[G][HD].
 constexpr int ATT_WAVES = 8;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// 8 floats -> (f16 hi, f16 lo) with hi + lo = v to 22 significant bits.
+__device__ __forceinline__ void split_f16(const float4 &a, const float4 &b, half8_t &hi, half8_t &lo) {
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const _Float16 h = (_Float16)v[i];
+        hi[i] = h;
+        lo[i] = (_Float16)(v[i] - (float)h);
+    }
+}
 
 template <int HD>
 __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims D, const float *__restrict__ q_rot,
                                                                       const uint16_t *__restrict__ kc,
                                                                       const uint16_t *__restrict__ vc,
                                                                       const int32_t *__restrict__ pos, int li,
-                                                                      int n_chunks, float *__restrict__ part) {
+                                                                      int n_chunks, int use_mfma,
+                                                                      float *__restrict__ part) {
     extern __shared__ __align__(16) float smem[];
-    constexpr int NT = 64 * ATT_WAVES;
     constexpr int KS = HD + 8;                 // padded key row (halves)
+    constexpr int VS = HD + 2;                 // padded value row (halves)
     constexpr int PR = HD / 8;                 // 16-byte pieces per row
-    constexpr int CPL = HD > 64 ? 2 : 1;       // P.V columns per lane
-    constexpr int NPC = (ATT_TC * PR + NT - 1) / NT; // 16-byte pieces per thread
+    constexpr int CPL = HD > 64 ? 2 : 1;       // VALU P.V columns per lane
+    constexpr int NPW = (ATT_TC * PR + 255) / 256; // 16-byte pieces per thread of a half work group
+    constexpr bool MF = HD % 32 == 0;
     const int ch = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
     const int G = D.n_heads / D.n_kv;
     const int p = min(pos[t], D.ctx - 1);
@@ -309,93 +337,194 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
     if (nt <= 0)
         return; // past the current position: the merge reads no record from here
     const bool single = p + 1 <= ATT_TC;
-    float *qs = smem;                                  // [G][HD]
-    float *sc = qs + G * HD;                           // [G][TC]: p of head g, position j
-    uint16_t *ks = (uint16_t *)(sc + G * ATT_TC);      // [TC][KS]
-    uint16_t *vs = ks + ATT_TC * KS;                   // [TC][HD]
-    const int wave = tid >> 6, ln = tid & 63;
+    float *qs = smem;                                  // [G][HD] f32
+    float *sc = qs + G * HD;                           // [16][TC] f32: p of head g, position j
+    uint16_t *ks = (uint16_t *)(sc + 16 * ATT_TC);     // [TC][KS]
+    uint16_t *vs = ks + ATT_TC * KS;                   // [TC][VS]
+    __shared__ float red[2][4][16];
+    const int wave = tid >> 6, ln = tid & 63, half = tid >> 8, ht = tid & 255;
     const size_t row0 = (((size_t)t * D.n_layers + li) * D.ctx + t0) * D.kvd + (size_t)kvh * HD;
     const float *qsrc = q_rot + (size_t)t * D.qd + (size_t)kvh * G * HD;
-    // rows past nt repeat row nt-1 and are never read
-    uint4 kr[NPC], vr[NPC];
+    // half 0: keys (and the queries below), half 1: values
+    const uint16_t *src = half ? vc : kc;
+    uint4 pc[NPW];
 #pragma unroll
-    for (int u = 0; u < NPC; u++) {
-        const int i = tid + NT * u;
-        kr[u] = *(const uint4 *)(kc + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR));
+    for (int u = 0; u < NPW; u++) {
+        const int i = ht + 256 * u;
+        pc[u] = *(const uint4 *)(src + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR));
     }
+    if (half == 0) {
+        for (int i = ht; i < G * HD; i += 256)
+            qs[i] = qsrc[i];
 #pragma unroll
-    for (int u = 0; u < NPC; u++) {
-        const int i = tid + NT * u;
-        vr[u] = *(const uint4 *)(vc + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR));
-    }
-    for (int i = tid; i < G * HD; i += NT)
-        qs[i] = qsrc[i];
-#pragma unroll
-    for (int u = 0; u < NPC; u++) {
-        const int i = tid + NT * u;
-        if (i < ATT_TC * PR)
-            *(uint4 *)(ks + (i / PR) * KS + 8 * (i % PR)) = kr[u];
+        for (int u = 0; u < NPW; u++) {
+            const int i = ht + 256 * u;
+            if (i < ATT_TC * PR)
+                *(uint4 *)(ks + (i / PR) * KS + 8 * (i % PR)) = pc[u];
+        }
     }
     __syncthreads();
-    const uint16_t *krow = ks + min(ln, nt - 1) * KS;
     float *rec = part + (((size_t)t * D.n_kv + kvh) * n_chunks + ch) * (size_t)G * (HD + 2);
-    for (int g = wave; g < G; g += ATT_WAVES) {
-        const float s = ln < nt ? dot_f32_key<HD>(qs + g * HD, krow) * D.scale : -INFINITY;
-        const float m = wave_max(s);
-        float e = ln < nt ? exp_f32(s - m) : 0.0f;
-        float l;
-        if (single) {
-            l = 0.0f;
-            for (int j = 0; j < nt; j++) // the reference's sum order
-                l = l + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-            const float inv = 1.0f / l;
-            e = e * inv;
-        } else {
-            l = wave_sum_f(e);
-        }
-        sc[g * ATT_TC + ln] = e;
-        if (ln == 0) {
-            rec[g] = m;
-            rec[G + g] = single ? 1.0f : l;
-        }
-    }
+
+    if (half) { // values: 4-byte stores into the padded rows
 #pragma unroll
-    for (int u = 0; u < NPC; u++) {
-        const int i = tid + NT * u;
-        if (i < ATT_TC * PR)
-            *(uint4 *)(vs + (i / PR) * HD + 8 * (i % PR)) = vr[u];
+        for (int u = 0; u < NPW; u++) {
+            const int i = ht + 256 * u;
+            if (i < ATT_TC * PR) {
+                uint32_t *vrow = (uint32_t *)(vs + (i / PR) * VS + 8 * (i % PR));
+                vrow[0] = pc[u].x;
+                vrow[1] = pc[u].y;
+                vrow[2] = pc[u].z;
+                vrow[3] = pc[u].w;
+            }
+        }
     }
-    __syncthreads();
-    const int d0 = CPL * ln;
-    if (d0 >= HD)
+    if (!MF || single || !use_mfma) {
+        const uint16_t *krow = ks + min(ln, nt - 1) * KS;
+        for (int g = wave; g < G; g += ATT_WAVES) {
+            const float s = ln < nt ? dot_f32_key<HD>(qs + g * HD, krow) * D.scale : -INFINITY;
+            const float m = wave_max(s);
+            float e = ln < nt ? exp_f32(s - m) : 0.0f;
+            float l;
+            if (single) {
+                l = 0.0f;
+                for (int j = 0; j < nt; j++) // the reference's sum order
+                    l = l + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+                const float inv = 1.0f / l;
+                e = e * inv;
+            } else {
+                l = wave_sum_f(e);
+            }
+            sc[g * ATT_TC + ln] = e;
+            if (ln == 0) {
+                rec[g] = m;
+                rec[G + g] = single ? 1.0f : l;
+            }
+        }
+        __syncthreads();
+        const int d0 = CPL * ln;
+        if (d0 >= HD)
+            return;
+        for (int g = wave; g < G; g += ATT_WAVES) {
+            const float *pg = sc + g * ATT_TC;
+            float a0 = 0.0f, a1 = 0.0f;
+            for (int j0 = 0; j0 < nt; j0 += 8) {
+                const float4 pa = *(const float4 *)(pg + j0), pb = *(const float4 *)(pg + j0 + 4);
+                const float pj[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+                uint32_t vw[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int j = min(j0 + u, ATT_TC - 1);
+                    if constexpr (CPL == 2)
+                        vw[u] = *(const uint32_t *)(vs + j * VS + d0);
+                    else
+                        vw[u] = vs[j * VS + d0];
+                }
+                // positions past nt have p = 0 and a finite v (a repeated row):
+                // they add +0 to accumulators that are never -0, no change
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    a0 = a0 + pj[u] * half_bits_to_float((uint16_t)(vw[u] & 0xffff));
+                    if constexpr (CPL == 2)
+                        a1 = a1 + pj[u] * half_bits_to_float((uint16_t)(vw[u] >> 16));
+                }
+            }
+            rec[2 * G + g * HD + d0] = a0;
+            if constexpr (CPL == 2)
+                rec[2 * G + g * HD + d0 + 1] = a1;
+        }
         return;
-    for (int g = wave; g < G; g += ATT_WAVES) {
-        const float *pg = sc + g * ATT_TC;
-        float a0 = 0.0f, a1 = 0.0f;
-        for (int j0 = 0; j0 < nt; j0 += 8) {
-            const float4 pa = *(const float4 *)(pg + j0), pb = *(const float4 *)(pg + j0 + 4);
-            const float pj[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-            uint32_t vw[8];
+    }
+
+    if constexpr (MF) {
+        const int r16 = ln & 15, q4 = ln >> 4; // tile row/column, k-quarter
+        float sv[4];
+        if (half == 0) {
+            // scores of positions 16w..16w+15
+            const int j = 16 * wave + r16;
+            const uint16_t *krow = ks + min(j, nt - 1) * KS;
+            const bool hrow = r16 < G;
+            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int j = min(j0 + u, ATT_TC - 1);
-                if constexpr (CPL == 2)
-                    vw[u] = *(const uint32_t *)(vs + j * HD + d0);
-                else
-                    vw[u] = vs[j * HD + d0];
+            for (int kk = 0; kk < HD / 32; kk++) {
+                const int d = 32 * kk + 8 * q4;
+                const half8_t b = *(const half8_t *)(krow + d);
+                float4 qa = {0.0f, 0.0f, 0.0f, 0.0f}, qb = qa;
+                if (hrow) {
+                    qa = *(const float4 *)(qs + r16 * HD + d);
+                    qb = *(const float4 *)(qs + r16 * HD + d + 4);
+                }
+                half8_t ahi, alo;
+                split_f16(qa, qb, ahi, alo);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, acc, 0, 0, 0);
             }
-            // positions past nt have p = 0 and a finite v (a repeated row):
-            // they add +0 to accumulators that are never -0, no change
+            // lane: position j, heads 4*q4 .. 4*q4+3
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                a0 = a0 + pj[u] * half_bits_to_float((uint16_t)(vw[u] & 0xffff));
-                if constexpr (CPL == 2)
-                    a1 = a1 + pj[u] * half_bits_to_float((uint16_t)(vw[u] >> 16));
+            for (int r = 0; r < 4; r++) {
+                sv[r] = j < nt ? acc[r] * D.scale : -INFINITY;
+                float v = sv[r];
+                v = fmaxf(v, __shfl_xor(v, 1, 16));
+                v = fmaxf(v, __shfl_xor(v, 2, 16));
+                v = fmaxf(v, __shfl_xor(v, 4, 16));
+                v = fmaxf(v, __shfl_xor(v, 8, 16));
+                if (r16 == 0)
+                    red[0][wave][4 * q4 + r] = v;
             }
         }
-        rec[2 * G + g * HD + d0] = a0;
-        if constexpr (CPL == 2)
-            rec[2 * G + g * HD + d0 + 1] = a1;
+        __syncthreads();
+        if (half == 0) {
+            const int j = 16 * wave + r16;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int hh = 4 * q4 + r;
+                const float m = fmaxf(fmaxf(red[0][0][hh], red[0][1][hh]), fmaxf(red[0][2][hh], red[0][3][hh]));
+                const float e = j < nt ? exp_f32(sv[r] - m) : 0.0f;
+                sc[hh * ATT_TC + j] = e;
+                float v = e;
+                v = v + __shfl_xor(v, 1, 16);
+                v = v + __shfl_xor(v, 2, 16);
+                v = v + __shfl_xor(v, 4, 16);
+                v = v + __shfl_xor(v, 8, 16);
+                if (r16 == 0)
+                    red[1][wave][hh] = v;
+                if (wave == 0 && r16 == 0 && hh < G)
+                    rec[hh] = m;
+            }
+        }
+        __syncthreads();
+        if (tid < G)
+            rec[G + tid] = ((red[1][0][tid] + red[1][1][tid]) + red[1][2][tid]) + red[1][3][tid];
+        if (wave < HD / 16) {
+            // O columns 16w..16w+15: rows = heads, k = positions
+            const int dcol = 16 * wave + r16;
+            const bool hrow = r16 < G;
+            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks2 = 0; ks2 < ATT_TC / 32; ks2++) {
+                const int j = 32 * ks2 + 8 * q4;
+                half8_t b;
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    b[e] = __builtin_bit_cast(_Float16, vs[(j + e) * VS + dcol]);
+                float4 pa = {0.0f, 0.0f, 0.0f, 0.0f}, pb = pa;
+                if (hrow) {
+                    pa = *(const float4 *)(sc + r16 * ATT_TC + j);
+                    pb = *(const float4 *)(sc + r16 * ATT_TC + j + 4);
+                }
+                half8_t ahi, alo;
+                split_f16(pa, pb, ahi, alo);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, acc, 0, 0, 0);
+            }
+            // lane: column dcol, heads 4*q4 .. 4*q4+3
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int hh = 4 * q4 + r;
+                if (hh < G)
+                    rec[2 * G + hh * HD + dcol] = acc[r];
+            }
+        }
     }
 }
 
@@ -770,8 +899,8 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     D.eps = m->eps;
     D.scale = 1.0f / sqrtf((float)m->head_dim); // llama.zig attn scale
     const int G = D.n_heads / D.n_kv;
-    const size_t att_lds = (size_t)G * D.hd * 4 + (size_t)G * ATT_TC * 4 + (size_t)ATT_TC * (D.hd + 8) * 2 +
-                           (size_t)ATT_TC * D.hd * 2;
+    const size_t att_lds = (size_t)G * D.hd * 4 + (size_t)16 * ATT_TC * 4 + (size_t)ATT_TC * (D.hd + 8) * 2 +
+                           (size_t)ATT_TC * (D.hd + 2) * 2;
     if (att_lds > 64 * 1024)
         return fail(LOOMHIP_DECLINED, "token_frame: attention tile exceeds LDS (%zu B)", att_lds);
     const size_t cmb_lds = (4 * 256 + (size_t)CMB_NH * n_chunks) * 4;
@@ -802,13 +931,13 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         const dim3 agrid(n_chunks, D.n_kv, n);
         if (D.hd == 128)
             hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, w.qrot, k_cache,
-                               v_cache, pos, (int)li, n_chunks, w.part);
+                               v_cache, pos, (int)li, n_chunks, parity ? 0 : 1, w.part);
         else if (D.hd == 64)
             hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, w.qrot, k_cache,
-                               v_cache, pos, (int)li, n_chunks, w.part);
+                               v_cache, pos, (int)li, n_chunks, parity ? 0 : 1, w.part);
         else
             hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, w.qrot, k_cache,
-                               v_cache, pos, (int)li, n_chunks, w.part);
+                               v_cache, pos, (int)li, n_chunks, parity ? 0 : 1, w.part);
         prof_end(ph, st);
         note_launch();
         const int qb_o = act_block(l.wo_t);
