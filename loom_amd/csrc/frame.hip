@@ -716,6 +716,8 @@ struct FrameWs {
     QAct qa_dim, qa_att, qa_ffn;
     const DmmvGroup *groups; // lanes in groups of nt against plane 0
     int n_groups, nt;
+    const DmmvGroup *groups32; // lanes in groups of 32 (matrix-core matmuls)
+    int n_groups32;
     size_t bytes;
 };
 
@@ -752,8 +754,12 @@ static FrameWs frame_layout(char *base, size_t n, const loomhip_model *m, size_t
     return w;
 }
 
+// mmq_ok: the matrix cores from MMQ_MIN_TOK lanes on (the head: many rows
+// per lane group); the attention matrices stay on the grouped matvec, which
+// is faster for them at these lane counts.
 static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameWs &w, size_t n,
-                         QAct x, float *out, int accumulate, hipStream_t st, int tag = LOOMHIP_KT_QKV) {
+                         QAct x, float *out, int accumulate, hipStream_t st, int tag = LOOMHIP_KT_QKV,
+                         bool mmq_ok = false) {
     DmmvParams p{};
     p.w = (const uint8_t *)wt;
     p.plane_bytes = 0;
@@ -769,15 +775,20 @@ static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameW
     p.out = out;
     p.out_stride = rows;
     p.accumulate = accumulate;
-    p.rpw = dmmv_pick_rpw(t, cols, rows, w.n_groups, w.nt, false);
+    const bool mq = mmq_ok && use_mmq(t, cols, (int)n, 32, false);
+    if (mq) {
+        p.groups = w.groups32;
+        p.n_groups = w.n_groups32;
+    }
+    p.rpw = mq ? 0 : dmmv_pick_rpw(t, cols, rows, w.n_groups, w.nt, false);
     const int ph = prof_begin(tag, st);
-    const bool ok = launch_dmmv(t, w.nt, false, p, st);
+    const bool ok = mq ? launch_mmq(t, 32, false, p, st) : launch_dmmv(t, w.nt, false, p, st);
     prof_end(ph, st);
     return ok;
 }
 
 // q, k and v of one layer against the normalised input, one launch.
-static bool frame_qkv(const loomhip_layer &l, const FrameDims &D, const FrameWs &w, hipStream_t st) {
+static bool frame_qkv(const loomhip_layer &l, const FrameDims &D, const FrameWs &w, size_t n, hipStream_t st) {
     DmmvSegParams sp{};
     DmmvParams &p = sp.base;
     p.cols = D.dim;
@@ -881,7 +892,8 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     FrameWs w = frame_layout((char *)g_frame.ptr, n, m, ffn_max, n_chunks);
     w.nt = pick_nt((int)n);
     w.groups = dense_groups((int)n, w.nt, &w.n_groups); // built once per lane count, before any capture
-    if (!w.groups)
+    w.groups32 = dense_groups((int)n, 32, &w.n_groups32);
+    if (!w.groups || !w.groups32)
         return fail(LOOMHIP_ERR_HIP, "token_frame: group table");
     FrameDims D;
     D.dim = (int)m->dim;
@@ -922,7 +934,7 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         // layer 0 normalises the embedding row: exact sum in either mode
         launch_norm(act_block(l.wq_t), w.x, D.dim, l.attn_norm, D.eps, w.qa_dim, nullptr, n, st,
                     parity || li == 0);
-        if (!frame_qkv(l, D, w, st))
+        if (!frame_qkv(l, D, w, n, st))
             return fail(LOOMHIP_ERR_ARG, "token_frame: q/k/v matvec declined");
         hipLaunchKernelGGL(qk_rope_kernel, dim3(D.n_heads + D.n_kv, n), dim3(64), 0, st, D, w.q, w.k,
                            w.v, l.q_norm, l.k_norm, pos, (int)li, rope_cs, w.qrot, k_cache, v_cache);
@@ -985,7 +997,7 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     // head (llama.zig:1225-1227) and the greedy pick
     launch_norm(act_block(m->output_t), w.x, D.dim, m->out_norm, D.eps, w.qa_dim, nullptr, n, st, parity);
     if (!frame_matvec(m->output_t, m->output, D.vocab, D.dim, w, n, w.qa_dim, logits, 0, st,
-                      LOOMHIP_KT_HEAD))
+                      LOOMHIP_KT_HEAD, true))
         return fail(LOOMHIP_ERR_ARG, "token_frame: output matvec declined");
     hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(1024), 0, st, logits, D.vocab, next, pos);
     note_launch();

@@ -75,6 +75,11 @@ void launch_synth(int t, void *dst, size_t rows, size_t cols, size_t planes, uin
 bool dmmv_supported(int t, int cols);
 // Returns false (launching nothing) when the partials would not fit in LDS.
 bool launch_dmmv(int t, int nt, bool fused, const DmmvParams &p, hipStream_t st);
+// Matrix-core variant for Q4_K / Q6_K with groups of up to max_tok (<= 32)
+// tokens: the same results bit for bit.  False (nothing launched) when the
+// type or the LDS need is not served.
+bool mmq_supported(int t, int cols, int max_tok, bool fused);
+bool launch_mmq(int t, int max_tok, bool fused, const DmmvParams &p, hipStream_t st);
 // Rows per wave chosen for a launch of `rows` rows x `groups` groups.
 int dmmv_pick_rpw(int t, int cols, int rows, int groups, int nt, bool fused);
 size_t dmmv_lds_bytes(int t, int cols, int nt, bool fused, int rpw);

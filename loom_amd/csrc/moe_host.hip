@@ -82,7 +82,11 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
         return fail(LOOMHIP_ERR_ARG, "moe: unknown combine mode %d", combine);
     const size_t P = n * m.k;
     const bool decode = n <= DECODE_MAX_TOK && decode_supported(m.gate_t, m.down_t, (int)m.ffn);
-    const int nt = moe_nt(n, m.k, m.E);
+    // matrix cores for the expert matmuls from MMQ_MIN_TOK tokens on, groups
+    // of up to 16 tokens per expert
+    const bool mq = !decode && use_mmq(m.gate_t, (int)m.dim, (int)n, 16, true) &&
+                    use_mmq(m.down_t, (int)m.ffn, (int)n, 16, false);
+    const int nt = mq ? 16 : moe_nt(n, m.k, m.E);
     const int maxg = moe_max_groups((int)n, (int)m.k, (int)m.E, nt);
     // workspace layout
     size_t off = 0;
@@ -201,9 +205,9 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     gu.n_groups = maxg;
     gu.out = act;
     gu.out_stride = (int)m.ffn;
-    gu.rpw = dmmv_pick_rpw(m.gate_t, (int)m.dim, (int)m.ffn, exp_groups, nt, true);
+    gu.rpw = mq ? 0 : dmmv_pick_rpw(m.gate_t, (int)m.dim, (int)m.ffn, exp_groups, nt, true);
     int ph = prof_begin(LOOMHIP_KT_GATE_UP, st);
-    bool launched = launch_dmmv(m.gate_t, nt, true, gu, st);
+    bool launched = mq ? launch_mmq(m.gate_t, nt, true, gu, st) : launch_dmmv(m.gate_t, nt, true, gu, st);
     prof_end(ph, st);
     if (!launched)
         return fail(LOOMHIP_ERR_ARG, "moe: gate/up partials exceed LDS");
@@ -226,9 +230,9 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     dn.n_groups = maxg;
     dn.out = y;
     dn.out_stride = (int)m.dim;
-    dn.rpw = dmmv_pick_rpw(m.down_t, (int)m.ffn, (int)m.dim, exp_groups, nt, false);
+    dn.rpw = mq ? 0 : dmmv_pick_rpw(m.down_t, (int)m.ffn, (int)m.dim, exp_groups, nt, false);
     ph = prof_begin(LOOMHIP_KT_DOWN, st);
-    launched = launch_dmmv(m.down_t, nt, false, dn, st);
+    launched = mq ? launch_mmq(m.down_t, nt, false, dn, st) : launch_dmmv(m.down_t, nt, false, dn, st);
     prof_end(ph, st);
     if (!launched)
         return fail(LOOMHIP_ERR_ARG, "moe: down partials exceed LDS");

@@ -225,7 +225,8 @@ int matvec_dev_impl(int t, float *out, const void *w, const float *x, size_t n, 
     qa.d = (float *)((char *)g_ctx.act.ptr + align16(n * cols));
     qa.s = (int32_t *)((char *)qa.d + align16(n * cols / 32 * 4));
     launch_quant_act(t, x, (int)cols, (int)cols, (int)n, qa, st);
-    const int nt = pick_nt((int)n);
+    const bool mq = use_mmq(t, (int)cols, (int)n, 32, false);
+    const int nt = mq ? 32 : pick_nt((int)n);
     int ng = 0;
     const DmmvGroup *groups = dense_groups((int)n, nt, &ng);
     if (!groups)
@@ -246,9 +247,9 @@ int matvec_dev_impl(int t, float *out, const void *w, const float *x, size_t n, 
     p.n_groups = ng;
     p.out = out;
     p.out_stride = (int)rows;
-    p.rpw = dmmv_pick_rpw(t, (int)cols, (int)rows, ng, nt, false);
+    p.rpw = mq ? 0 : dmmv_pick_rpw(t, (int)cols, (int)rows, ng, nt, false);
     const int ph = prof_begin(LOOMHIP_KT_DENSE, st);
-    const bool launched = launch_dmmv(t, nt, false, p, st);
+    const bool launched = mq ? launch_mmq(t, nt, false, p, st) : launch_dmmv(t, nt, false, p, st);
     prof_end(ph, st);
     if (!launched)
         return fail(LOOMHIP_DECLINED, "dmmv: partials exceed LDS for %zu columns", cols);

@@ -47,6 +47,12 @@ void clear_weight_cache();
 int matvec_dev_impl(int t, float *out, const void *w, const float *x, size_t n, size_t rows,
                     size_t cols, hipStream_t st);
 int pick_nt(int n);
+// From this many vectors per weight plane on, Q4_K / Q6_K matmuls run on the
+// matrix cores (mmq.hip) in groups of up to 32 (dense) or 16 (experts).
+constexpr int MMQ_MIN_TOK = 16;
+inline bool use_mmq(int t, int cols, int n, int group_tok, bool fused) {
+    return n >= MMQ_MIN_TOK && mmq_supported(t, cols, group_tok, fused);
+}
 // Device group table for n vectors in groups of nt against plane 0 (cached per (n, nt)).
 const DmmvGroup *dense_groups(int n, int nt, int *count);
 void moe_release_scratch();

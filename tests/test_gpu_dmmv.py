@@ -129,6 +129,22 @@ def test_matmul_bit_exact_to_per_vector_oracle(be, oracle, t):
         assert np.array_equal(_bits(got), _bits(want)), n
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("rows,cols", [(37, 768), (300, 4096), (64, 256), (130, 2048)])
+def test_matmul_matrix_cores_bit_exact(be, oracle, t, rows, cols):
+    """From 16 vectors on, Q4_K / Q6_K matmuls run on the int8 matrix cores
+    (mmq.hip, groups of 32): bit-identical to per-vector oracle matvecs,
+    including ragged row tiles and groups."""
+    rng = np.random.default_rng(77 + t + rows)
+    raw = npref.pinned_scale_blocks(t, rows, cols, rng)
+    for n in (16, 17, 32, 45):
+        xs = np.stack([oracle.normal(cols, 3000 * n + k, 0.0, float(k % 5 + 1)) for k in range(n)])
+        got = np.empty((n, rows), np.float32)
+        assert be.matmul(t, got, raw, xs, n, rows, cols)
+        want = np.stack([oracle.matvec(t, raw, xs[k], rows, cols) for k in range(n)])
+        assert np.array_equal(_bits(got), _bits(want)), n
+
+
 def test_f32_matvec_bit_exact(be, oracle):
     for rows, cols in ((128, 2048), (64, 288), (30, 100), (8, 7)):
         w = oracle.normal(rows * cols, rows, 0.0, 1.0 / np.sqrt(cols)).reshape(rows, cols)

@@ -150,10 +150,11 @@ def test_qwen3moe_frame_prefilled_context(lh, oracle, numerics):
     assert (rels <= 2e-3).mean() >= 0.75, rels
 
 
-@pytest.mark.parametrize("n", [3, 6])
+@pytest.mark.parametrize("n", [3, 6, 16])
 def test_qwen3moe_frame_batch(lh, oracle, n):
     """decodeBatch semantics at n lanes (moeBatchUnion; n = 3 takes the
-    few-token MoE path, n = 6 the grouped one): per-lane logits against
+    few-token MoE path, n = 6 the grouped one, n = 16 the matrix-core
+    matmuls for the experts and the head): per-lane logits against
     lo_decode_batch over 6 steps on identical state."""
     import torch
 
