@@ -19,7 +19,7 @@
  *     given stream (NULL = the null stream, as in HIP) and nothing is
  *     copied to or from the host.  These are the hot path.
  *
- * Numerics: LOOMHIP_NUM_CPU_PARITY (default) quantizes activations to int8
+ * Numerics: every matvec/matmul quantizes activations to int8
  * exactly as the reference CPU path does (src/gguf/ggml.zig:776-800,
  * 1077-1098), runs exact integer block dots and reproduces the f32 tail and
  * the block summation order, so matvec/matmul are bit-identical to the
