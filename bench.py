@@ -65,6 +65,9 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cache", action="store_true", help="skip the config-5 expert-cache streaming run")
     ap.add_argument("--cache-steps", type=int, default=1024, help="config-5 decode steps at batch 1")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
+                    help="first copy MB megabytes device to device three times: the known-size kernel that "
+                         "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
     return ap.parse_args()
 
 
@@ -351,6 +354,14 @@ def main():
     from loom_amd.frame import DeviceModel, qwen3_30b_a3b
 
     loom_amd.init(0)
+    if args.copy_probe:
+        src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 x {args.copy_probe} MB device to device")
+        del src, dst
     batches = [int(v) for v in args.batch.split(",") if v]
     spec = qwen3_30b_a3b(ctx_len=args.ctx + 2 * args.warmup + args.steps + 64, n_layers=args.layers)
     t0 = time.perf_counter()
