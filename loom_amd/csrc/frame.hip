@@ -7,17 +7,20 @@
 //
 // Per layer:
 //   norm_quant     rmsnorm(x) * attn_norm, int8-quantized for wq/wk/wv
-//   dmmv x3        q, k, v (grouped matvec, bit-identical to the CPU kernels)
-//   qk_rope        per-head Q/K RMSNorm, RoPE (NEOX or NORM), K/V append (fp16)
-//   attn_partial   scores, softmax pieces and P.V for 64 positions x one KV
-//                  head group (split over the context, flash-decoding style;
+//   dmmv_seg       q, k and v in one launch (bit-identical to the CPU kernels)
+//   qk_rope        (more than 4 lanes) per-head Q/K RMSNorm, RoPE, K/V append
+//   attn_partial   per 64 positions x one KV head group: (up to 4 lanes) the
+//                  group's query heads' RMSNorm and RoPE, the new K/V row's
+//                  (appended, fp16, by the chunk that holds it), then scores, softmax pieces
+//                  and P.V (split over the context, flash-decoding style;
 //                  within 64 positions the reference's own order)
 //   attn_combine   partials merged per head, int8-quantized for wo
 //   dmmv (+=)      x += wo . attn
-//   norm_quant     rmsnorm(x) * ffn_norm (f32 for the router, or int8)
+//   norm_quant     rmsnorm(x) * ffn_norm (f32 for the router, or int8; FAST
+//                  numerics at few lanes: folded into the router launch)
 //   MoE layer      (moe_host.hip) with the residual add, or the dense SwiGLU
 //                  FFN with x += down . act
-// then norm_quant + the output dmmv + argmax (sampler.zig:7-15), pos += 1.
+// then norm_quant + the output matvec + argmax (sampler.zig:7-15), pos += 1.
 //
 // Numerics: every matvec is bit-identical to the reference's int8 kernels
 // on identical inputs, and so are the attention scores (dotF32 order), the
@@ -301,6 +304,7 @@ __device__ __forceinline__ float dot_f32_key(const float *a, const uint16_t *kro
 // unnormalised, for the merge.  Record per (lane, kv head, chunk): m[G],
 // l[G], o[G][HD].
 constexpr int ATT_WAVES = 8;
+constexpr size_t ATT_FUSE_MAX_LANES = 4; // lanes up to which rope/append run inside the attention
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -317,11 +321,16 @@ __device__ __forceinline__ void split_f16(const float4 &a, const float4 &b, half
 }
 
 template <int HD>
-__global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims D, const float *__restrict__ q_rot,
-                                                                      const uint16_t *__restrict__ kc,
-                                                                      const uint16_t *__restrict__ vc,
+__global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims D, const float *__restrict__ qraw,
+                                                                      const float *__restrict__ kraw,
+                                                                      const float *__restrict__ vraw,
+                                                                      const float *__restrict__ q_norm,
+                                                                      const float *__restrict__ k_norm,
+                                                                      const float *__restrict__ rope_cs,
+                                                                      uint16_t *__restrict__ kc,
+                                                                      uint16_t *__restrict__ vc,
                                                                       const int32_t *__restrict__ pos, int li,
-                                                                      int n_chunks, int use_mfma,
+                                                                      int n_chunks, int use_mfma, int fuse,
                                                                       float *__restrict__ part) {
     extern __shared__ __align__(16) float smem[];
     constexpr int KS = HD + 8;                 // padded key row (halves)
@@ -332,20 +341,29 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
     constexpr bool MF = HD % 32 == 0;
     const int ch = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
     const int G = D.n_heads / D.n_kv;
-    const int p = min(pos[t], D.ctx - 1);
+    const int p_raw = pos[t];
+    const int p = min(p_raw, D.ctx - 1);
     const int t0 = ch * ATT_TC, nt = min(ATT_TC, p + 1 - t0);
     if (nt <= 0)
         return; // past the current position: the merge reads no record from here
     const bool single = p + 1 <= ATT_TC;
+    // fuse (few lanes): the query heads arrive raw and get their RMSNorm and
+    // RoPE here; the chunk that holds the new position appends the step's
+    // K/V row (a full cache takes no more rows) and uses it from LDS.
+    // Otherwise qk_rope_kernel did both and qraw holds the rotated queries.
+    const bool own = fuse && p_raw >= 0 && p_raw < D.ctx && p_raw >= t0 && p_raw < t0 + ATT_TC;
+    const int rp = min(max(p_raw, 0), D.ctx - 1); // rope position
     float *qs = smem;                                  // [G][HD] f32
     float *sc = qs + G * HD;                           // [16][TC] f32: p of head g, position j
     uint16_t *ks = (uint16_t *)(sc + 16 * ATT_TC);     // [TC][KS]
     uint16_t *vs = ks + ATT_TC * KS;                   // [TC][VS]
     __shared__ float red[2][4][16];
+    __shared__ float kn[HD], sinv[MAX_G + 1];
     const int wave = tid >> 6, ln = tid & 63, half = tid >> 8, ht = tid & 255;
     const size_t row0 = (((size_t)t * D.n_layers + li) * D.ctx + t0) * D.kvd + (size_t)kvh * HD;
-    const float *qsrc = q_rot + (size_t)t * D.qd + (size_t)kvh * G * HD;
-    // half 0: keys (and the queries below), half 1: values
+    const float *qsrc = qraw + (size_t)t * D.qd + (size_t)kvh * G * HD;
+    const size_t kvo = (size_t)t * D.kvd + (size_t)kvh * HD;
+    // half 0: keys and the group's query heads, half 1: values (and the new row)
     const uint16_t *src = half ? vc : kc;
     uint4 pc[NPW];
 #pragma unroll
@@ -353,6 +371,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
         const int i = ht + 256 * u;
         pc[u] = *(const uint4 *)(src + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR));
     }
+    float vnew = 0.0f;
     if (half == 0) {
         for (int i = ht; i < G * HD; i += 256)
             qs[i] = qsrc[i];
@@ -362,13 +381,13 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
             if (i < ATT_TC * PR)
                 *(uint4 *)(ks + (i / PR) * KS + 8 * (i % PR)) = pc[u];
         }
-    }
-    __syncthreads();
-    float *rec = part + (((size_t)t * D.n_kv + kvh) * n_chunks + ch) * (size_t)G * (HD + 2);
-
-    if (half) { // values: 4-byte stores into the padded rows
+    } else {
+        if (own && ht < HD) {
+            kn[ht] = kraw[kvo + ht];
+            vnew = vraw[kvo + ht];
+        }
 #pragma unroll
-        for (int u = 0; u < NPW; u++) {
+        for (int u = 0; u < NPW; u++) { // values: 4-byte stores into the padded rows
             const int i = ht + 256 * u;
             if (i < ATT_TC * PR) {
                 uint32_t *vrow = (uint32_t *)(vs + (i / PR) * VS + 8 * (i % PR));
@@ -379,6 +398,69 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
             }
         }
     }
+    __syncthreads();
+    if (fuse) {
+    // per-head RMSNorm (llama.zig:938-949): the sum of squares in the
+    // reference's order, one thread per head
+    if (q_norm && tid < G) {
+        float ss = 0.0f;
+        for (int i = 0; i < HD; i++) {
+            const float pr = qs[tid * HD + i] * qs[tid * HD + i];
+            ss = ss + pr;
+        }
+        sinv[tid] = 1.0f / sqrtf(ss / (float)HD + D.eps);
+    }
+    if (own && k_norm && tid == 256) {
+        float ss = 0.0f;
+        for (int i = 0; i < HD; i++) {
+            const float pr = kn[i] * kn[i];
+            ss = ss + pr;
+        }
+        sinv[MAX_G] = 1.0f / sqrtf(ss / (float)HD + D.eps);
+    }
+    __syncthreads();
+    if (half == 0) {
+        if (q_norm)
+            for (int i = ht; i < G * HD; i += 256)
+                qs[i] = (qs[i] * sinv[i / HD]) * q_norm[i % HD];
+    } else if (own && k_norm && ht < HD) {
+        kn[ht] = (kn[ht] * sinv[MAX_G]) * k_norm[ht];
+    }
+    __syncthreads();
+    // RoPE (llama.zig:821-855) from the (cos, sin) table at the position
+    {
+        const int hr = D.rope_dim / 2;
+        const float *csp = rope_cs + (size_t)rp * hr * 2;
+        if (half == 0) {
+            for (int i = ht; i < G * hr; i += 256) {
+                const int g = i / hr, r = i % hr;
+                const float cs = csp[2 * r], sn = csp[2 * r + 1];
+                const int ia = D.rope_neox ? r : 2 * r, ib = D.rope_neox ? r + hr : 2 * r + 1;
+                const float a = qs[g * HD + ia], b = qs[g * HD + ib];
+                qs[g * HD + ia] = a * cs - b * sn;
+                qs[g * HD + ib] = a * sn + b * cs;
+            }
+        } else if (own && ht < hr) {
+            const float cs = csp[2 * ht], sn = csp[2 * ht + 1];
+            const int ia = D.rope_neox ? ht : 2 * ht, ib = D.rope_neox ? ht + hr : 2 * ht + 1;
+            const float a = kn[ia], b = kn[ib];
+            kn[ia] = a * cs - b * sn;
+            kn[ib] = a * sn + b * cs;
+        }
+    }
+    __syncthreads();
+    if (own && half && ht < HD) { // the new row: to the cache and over its stale LDS copy
+        const uint16_t kh = __half_raw(__float2half(kn[ht])).x, vh = __half_raw(__float2half(vnew)).x;
+        const size_t crow = (((size_t)t * D.n_layers + li) * D.ctx + p_raw) * D.kvd + (size_t)kvh * HD;
+        kc[crow + ht] = kh;
+        vc[crow + ht] = vh;
+        ks[(p_raw - t0) * KS + ht] = kh;
+        vs[(p_raw - t0) * VS + ht] = vh;
+    }
+    __syncthreads();
+    }
+    float *rec = part + (((size_t)t * D.n_kv + kvh) * n_chunks + ch) * (size_t)G * (HD + 2);
+
     if (!MF || single || !use_mfma) {
         const uint16_t *krow = ks + min(ln, nt - 1) * KS;
         for (int g = wave; g < G; g += ATT_WAVES) {
@@ -633,44 +715,62 @@ __global__ __launch_bounds__(1024) void attn_combine_kernel(FrameDims D, const f
 
 // ---- greedy pick (engine/sampler.zig:7-15: the first maximum wins), pos += 1 ------
 
-__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ logits, int vocab,
-                                                      uint32_t *__restrict__ next,
-                                                      int32_t *__restrict__ pos) {
-    __shared__ float bv[16];
-    __shared__ int bi[16];
-    const int t = blockIdx.x, tid = threadIdx.x;
+// Two launches: ARGMAX_SLICES work groups per lane each take a contiguous
+// slice (threads walk it in index order, strict >, so each keeps its first
+// maximum), then one wave per lane merges the slices by (value desc, index
+// asc) -- the first maximum overall.  No value above -inf (all -inf or NaN):
+// index 0, as the reference's loop leaves it.
+constexpr int ARGMAX_SLICES = 64;
+
+__device__ __forceinline__ void argmax_pair(float &best, int &besti, float ov, int oi) {
+    if (ov > best || (ov == best && oi < besti)) {
+        best = ov;
+        besti = oi;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_part_kernel(const float *__restrict__ logits, int vocab,
+                                                          float *__restrict__ pv, int *__restrict__ pi) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const int s = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int slice = (vocab + ARGMAX_SLICES - 1) / ARGMAX_SLICES;
+    const int lo = s * slice, hi = min(vocab, lo + slice);
     const float *lg = logits + (size_t)t * vocab;
     float best = -INFINITY;
     int besti = 0x7fffffff; // no candidate yet
-    for (int i = tid; i < vocab; i += 1024) {
+    for (int i = lo + tid; i < hi; i += 256) {
         const float v = lg[i];
         if (v > best) {
             best = v;
             besti = i;
         }
     }
-    // (value desc, index asc) over the work group
-    for (int m = 1; m < 64; m <<= 1) {
-        const float ov = __shfl_xor(best, m);
-        const int oi = __shfl_xor(besti, m);
-        if (ov > best || (ov == best && oi < besti)) {
-            best = ov;
-            besti = oi;
-        }
-    }
+    for (int m = 1; m < 64; m <<= 1)
+        argmax_pair(best, besti, __shfl_xor(best, m), __shfl_xor(besti, m));
     if ((tid & 63) == 0) {
         bv[tid >> 6] = best;
         bi[tid >> 6] = besti;
     }
     __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < 16; w++)
-            if (bv[w] > best || (bv[w] == best && bi[w] < besti)) {
-                best = bv[w];
-                besti = bi[w];
-            }
+        for (int w = 1; w < 4; w++)
+            argmax_pair(best, besti, bv[w], bi[w]);
+        pv[t * ARGMAX_SLICES + s] = best;
+        pi[t * ARGMAX_SLICES + s] = besti;
+    }
+}
+
+__global__ __launch_bounds__(64) void argmax_merge_kernel(const float *__restrict__ pv, const int *__restrict__ pi,
+                                                          uint32_t *__restrict__ next, int32_t *__restrict__ pos) {
+    const int t = blockIdx.x, ln = threadIdx.x;
+    float best = ln < ARGMAX_SLICES ? pv[t * ARGMAX_SLICES + ln] : -INFINITY;
+    int besti = ln < ARGMAX_SLICES ? pi[t * ARGMAX_SLICES + ln] : 0x7fffffff;
+    for (int m = 1; m < 64; m <<= 1)
+        argmax_pair(best, besti, __shfl_xor(best, m), __shfl_xor(besti, m));
+    if (ln == 0) {
         if (next)
-            next[t] = besti == 0x7fffffff ? 0u : (uint32_t)besti; // nothing above -inf: index 0
+            next[t] = besti == 0x7fffffff ? 0u : (uint32_t)besti;
         pos[t] = pos[t] + 1;
     }
 }
@@ -712,7 +812,8 @@ static const float *rope_table(int ctx, int rope_dim, float base) {
 }
 
 struct FrameWs {
-    float *x, *normed, *q, *k, *v, *qrot, *part, *act;
+    float *x, *normed, *q, *k, *v, *qrot, *part, *act, *amax_v;
+    int *amax_i;
     QAct qa_dim, qa_att, qa_ffn;
     const DmmvGroup *groups; // lanes in groups of nt against plane 0
     int n_groups, nt;
@@ -747,6 +848,8 @@ static FrameWs frame_layout(char *base, size_t n, const loomhip_model *m, size_t
     w.qrot = (float *)take(n * qd * 4);
     w.part = (float *)take(n * m->n_kv_heads * (size_t)n_chunks * G * (m->head_dim + 2) * 4);
     w.act = (float *)take(n * (ffn_max ? ffn_max : 1) * 4);
+    w.amax_v = (float *)take(n * ARGMAX_SLICES * 4);
+    w.amax_i = (int *)take(n * ARGMAX_SLICES * 4);
     w.qa_dim = qtake(dim);
     w.qa_att = qtake(qd);
     w.qa_ffn = qtake(ffn_max ? ffn_max : 32);
@@ -936,20 +1039,30 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
                     parity || li == 0);
         if (!frame_qkv(l, D, w, n, st))
             return fail(LOOMHIP_ERR_ARG, "token_frame: q/k/v matvec declined");
-        hipLaunchKernelGGL(qk_rope_kernel, dim3(D.n_heads + D.n_kv, n), dim3(64), 0, st, D, w.q, w.k,
-                           w.v, l.q_norm, l.k_norm, pos, (int)li, rope_cs, w.qrot, k_cache, v_cache);
-        note_launch();
+        // few lanes: norm/rope/append inside the attention launch; more lanes:
+        // once per head in their own launch (the attention is then
+        // throughput-bound and the fused prologue would repeat per chunk)
+        const bool fuse_rope = n <= ATT_FUSE_MAX_LANES;
+        if (!fuse_rope) {
+            hipLaunchKernelGGL(qk_rope_kernel, dim3(D.n_heads + D.n_kv, n), dim3(64), 0, st, D, w.q, w.k, w.v,
+                               l.q_norm, l.k_norm, pos, (int)li, rope_cs, w.qrot, k_cache, v_cache);
+            note_launch();
+        }
+        const float *qin = fuse_rope ? w.q : w.qrot;
         int ph = prof_begin(LOOMHIP_KT_ATTN, st);
         const dim3 agrid(n_chunks, D.n_kv, n);
         if (D.hd == 128)
-            hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, w.qrot, k_cache,
-                               v_cache, pos, (int)li, n_chunks, parity ? 0 : 1, w.part);
+            hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
+                               l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
+                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
         else if (D.hd == 64)
-            hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, w.qrot, k_cache,
-                               v_cache, pos, (int)li, n_chunks, parity ? 0 : 1, w.part);
+            hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
+                               l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
+                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
         else
-            hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, w.qrot, k_cache,
-                               v_cache, pos, (int)li, n_chunks, parity ? 0 : 1, w.part);
+            hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
+                               l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
+                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
         prof_end(ph, st);
         note_launch();
         const int qb_o = act_block(l.wo_t);
@@ -964,9 +1077,15 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
             return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
         // FFN block (llama.zig:1203-1224)
         if (l.is_moe) {
-            launch_norm(0, w.x, D.dim, l.ffn_norm, D.eps, QAct{}, w.normed, n, st, parity);
             const int combine = n == 1 ? LOOMHIP_COMBINE_SELECTION_ADD : LOOMHIP_COMBINE_EXPERT_ASC;
             uint32_t *ids = m->ids_out ? m->ids_out + li * n * l.moe.n_used : nullptr;
+            if (!parity && moe_decode_fusable(&l.moe, n)) {
+                // FAST: the router launch applies the rmsnorm itself
+                if (int rc = moe_layer_fused_norm(&l.moe, w.x, l.ffn_norm, D.eps, n, combine, w.x, ids, st))
+                    return rc;
+                continue;
+            }
+            launch_norm(0, w.x, D.dim, l.ffn_norm, D.eps, QAct{}, w.normed, n, st, parity);
             if (int rc = loomhip_moe_layer_dev(&l.moe, w.normed, n, combine, w.x, ids, nullptr, st))
                 return rc;
         } else {
@@ -999,7 +1118,10 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     if (!frame_matvec(m->output_t, m->output, D.vocab, D.dim, w, n, w.qa_dim, logits, 0, st,
                       LOOMHIP_KT_HEAD, true))
         return fail(LOOMHIP_ERR_ARG, "token_frame: output matvec declined");
-    hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(1024), 0, st, logits, D.vocab, next, pos);
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(ARGMAX_SLICES, n), dim3(256), 0, st, logits, D.vocab, w.amax_v,
+                       w.amax_i);
+    hipLaunchKernelGGL(argmax_merge_kernel, dim3(n), dim3(64), 0, st, w.amax_v, w.amax_i, next, pos);
+    note_launch();
     note_launch();
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess)

@@ -117,6 +117,10 @@ struct GateParams {
     int nt;
     int *sync;
     int chain; // 1: route + bucket after the GEMV (last-arrival chain); 0: GEMV + quantize only
+    // decode router only: x is the residual stream and the kernel applies
+    // rmsnorm (weights norm_w, tree-summed squares) itself; null: x is normed
+    const float *norm_w;
+    float norm_eps;
     // set by launch_gate
     int n_chunks, wgs_per_chunk, gemv_wgs, quant_wgs;
 };

@@ -327,7 +327,43 @@ void launch_combine(const float *y, const float *gates, const uint32_t *ids, con
 // ds_bpermute), the sequential reduce over l from -0, and the tail.
 constexpr int RS_STEPS = 64; // dotF32 steps (32 columns each) per pass: dim 2048 in one
 
+// rmsnorm of x[dim] into out[dim] by one wave (dim a multiple of 32): lane l
+// sums the squares of chunks l, l+64, ... (32 values each, in order), the
+// lanes are summed as a fixed tree; out = (x * inv) * w (tensor.zig:9-15's
+// expression, FAST-numerics sum order).
+__device__ inline void wave_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, int dim, float eps,
+                                    float *__restrict__ out) {
+    const int lane = threadIdx.x & 63, chunks = dim / 32;
+    float ss = 0.0f;
+    for (int c = lane; c < chunks; c += 64) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 v = *(const float4 *)(x + 32 * c + 4 * i);
+            ss = ss + v.x * v.x;
+            ss = ss + v.y * v.y;
+            ss = ss + v.z * v.z;
+            ss = ss + v.w * v.w;
+        }
+    }
+    float total = ss;
+    for (int m = 1; m < 64; m <<= 1)
+        total = total + __shfl_xor(total, m);
+    const float inv = 1.0f / sqrtf(total / (float)dim + eps);
+    for (int i = 4 * lane; i < dim; i += 256) {
+        const float4 v = *(const float4 *)(x + i), g = *(const float4 *)(w + i);
+        float4 o;
+        o.x = (v.x * inv) * g.x;
+        o.y = (v.y * inv) * g.y;
+        o.z = (v.z * inv) * g.z;
+        o.w = (v.w * inv) * g.w;
+        *(float4 *)(out + i) = o;
+    }
+}
+
+constexpr int RS_MAX_DIM = 8192; // fused-norm router: LDS row
+
 __global__ __launch_bounds__(64) void router_small_kernel(GateParams p) {
+    __shared__ __align__(16) float xn[RS_MAX_DIM];
     const int lane = threadIdx.x, hw = lane >> 5, P = lane & 31;
     const int gemv_wgs = p.gemv_wgs; // 0 when the caller supplies the logits
     if ((int)blockIdx.x >= gemv_wgs) {
@@ -335,7 +371,13 @@ __global__ __launch_bounds__(64) void router_small_kernel(GateParams p) {
         const int item = blockIdx.x - gemv_wgs;
         if (item < per_vec * p.n) {
             const int v = item / per_vec, it = item % per_vec;
-            quant_item_wave(p.qt, p.x + (size_t)v * p.dim, p.dim, v, it, p.qx);
+            const float *xv = p.x + (size_t)v * p.dim;
+            if (p.norm_w) {
+                wave_rmsnorm(xv, p.norm_w, p.dim, p.norm_eps, xn);
+                __syncthreads();
+                xv = xn;
+            }
+            quant_item_wave(p.qt, xv, p.dim, v, it, p.qx);
         }
         return;
     }
@@ -344,8 +386,23 @@ __global__ __launch_bounds__(64) void router_small_kernel(GateParams p) {
     const bool valid = e < p.n_expert;
     const float *row = p.router + (size_t)(valid ? e : 0) * dim;
     const int n32 = dim / 32; // whole dotF32 steps
+    // one pass of RS_STEPS covers the row: its loads go out before the
+    // tokens' inputs (and their norms) are ready
+    const bool one_pass = n32 <= RS_STEPS;
+    float wpre[RS_STEPS];
+    if (one_pass) {
+#pragma unroll
+        for (int u = 0; u < RS_STEPS; u++)
+            wpre[u] = row[32 * min(u, n32 - 1) + P];
+    }
     for (int t = 0; t < p.n; t++) {
         const float *xt = p.x + (size_t)t * dim;
+        if (p.norm_w) {
+            __syncthreads(); // the previous token's reads of xn are done
+            wave_rmsnorm(xt, p.norm_w, dim, p.norm_eps, xn);
+            __syncthreads();
+            xt = xn;
+        }
         float acc = 0.0f;
         for (int i0 = 0; i0 < n32; i0 += RS_STEPS) {
             const int cnt = min(RS_STEPS, n32 - i0);
@@ -353,7 +410,7 @@ __global__ __launch_bounds__(64) void router_small_kernel(GateParams p) {
 #pragma unroll
             for (int u = 0; u < RS_STEPS; u++) { // unconditional: steps past cnt re-read the last
                 const int c = 32 * (i0 + min(u, cnt - 1)) + P;
-                wv[u] = row[c];
+                wv[u] = one_pass ? wpre[u] : row[c];
                 xv[u] = xt[c];
             }
             // steps past cnt add +0: acc starts at +0 and a sum of products

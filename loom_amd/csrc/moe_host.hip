@@ -22,6 +22,8 @@ struct MoeRun {
     const float *router, *router_bias, *sel_bias; // router null: logits given
     int gate_t, up_t, down_t;
     const void *gate, *up, *down;
+    const float *norm_w = nullptr; // decode path: rmsnorm the input first (normed = residual x)
+    float norm_eps = 0.0f;
 };
 
 static int moe_check(const MoeRun &m, size_t n) {
@@ -170,12 +172,16 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
             return fail(LOOMHIP_DECLINED, "moe: ffn %zu x top-%zu exceeds the decode LDS budget",
                         m.ffn, m.k);
         gp.chain = 0;
+        gp.norm_w = m.norm_w;
+        gp.norm_eps = m.norm_eps;
         launch_router_small(gp, st);
         if (!launch_moe_decode(m.gate_t, m.down_t, dp, (int)n, st, LOOMHIP_KT_GATE_UP, LOOMHIP_KT_DOWN))
             return fail(LOOMHIP_ERR_ARG, "moe: decode kernels declined the shape");
         return LOOMHIP_OK;
     }
 
+    if (m.norm_w)
+        return fail(LOOMHIP_ERR_ARG, "moe: a fused input norm is served on the decode path only");
     const QAct qa = qview(base + o_qa, P, m.ffn);
     MoeBuckets b;
     b.pair_tok = (int *)(base + o_ptok);
@@ -239,6 +245,21 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
 
     launch_combine(y, gates, ids, b.pair_of, (int)n, (int)m.k, (int)m.dim, combine, out, st);
     return LOOMHIP_OK;
+}
+
+int moe_layer_fused_norm(const loomhip_moe_layer *L, const float *x, const float *norm_w, float eps, size_t n_tok,
+                         int combine, float *out, uint32_t *ids_out, hipStream_t st) {
+    MoeRun m{L->dim, L->ffn, L->n_expert, L->n_used, L->gating, L->weights_norm, L->weights_scale,
+             L->router, L->router_bias, L->sel_bias, L->gate_t, L->up_t, L->down_t, L->gate,
+             L->up, L->down};
+    m.norm_w = norm_w;
+    m.norm_eps = eps;
+    return moe_run(m, x, nullptr, n_tok, combine, out, ids_out, nullptr, st);
+}
+
+bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok) {
+    return n_tok <= DECODE_MAX_TOK && decode_supported(L->gate_t, L->down_t, (int)L->ffn) && L->router &&
+           L->dim <= 8192 && L->dim % 32 == 0;
 }
 
 } // namespace lh

@@ -56,6 +56,11 @@ inline bool use_mmq(int t, int cols, int n, int group_tok, bool fused) {
 // Device group table for n vectors in groups of nt against plane 0 (cached per (n, nt)).
 const DmmvGroup *dense_groups(int n, int nt, int *count);
 void moe_release_scratch();
+// The decode MoE path with its rmsnorm fused into the router launch (x = the
+// residual stream); moe_decode_fusable says whether the layer takes it.
+int moe_layer_fused_norm(const loomhip_moe_layer *L, const float *x, const float *norm_w, float eps, size_t n_tok,
+                         int combine, float *out, uint32_t *ids_out, hipStream_t st);
+bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok);
 void ec_release_scratch();
 
 } // namespace lh
