@@ -150,6 +150,18 @@ def per_launch_bytes(name, b, ctx, distinct, layers):
     return 0
 
 
+def measured_traffic(b, tag):
+    """HBM bytes per launch of a tagged kernel from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic_per_launch.json")
+    try:
+        with open(path) as f:
+            doc = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return doc.get(f"batch{b}", {}).get(tag)
+
+
 def roofline(r, b, ctx, layers):
     stats = r["stats"]
     dom = max(stats, key=lambda k: stats[k]["ms"])
@@ -162,7 +174,7 @@ def roofline(r, b, ctx, layers):
                                    / (v["ms"] / v["count"] / 1e3) / 1e9, 1)}
                   for k, v in stats.items()}
     return {"bound": "hbm", "kernel": s["name"], "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(b, dom),
             "avg_launch_us": round(avg_s * 1e6, 2), "bytes_per_launch": int(byts)}, per_kernel
 
 

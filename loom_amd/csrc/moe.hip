@@ -334,6 +334,39 @@ constexpr int RS_STEPS = 64; // dotF32 steps (32 columns each) per pass: dim 204
 __device__ inline void wave_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, int dim, float eps,
                                     float *__restrict__ out) {
     const int lane = threadIdx.x & 63, chunks = dim / 32;
+    if (chunks <= 64) { // one chunk per lane: x and w loaded once, together
+        const int c = min(lane, chunks - 1);
+        float4 xv[8], wv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            xv[i] = *(const float4 *)(x + 32 * c + 4 * i);
+            wv[i] = *(const float4 *)(w + 32 * c + 4 * i);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            ss = ss + xv[i].x * xv[i].x;
+            ss = ss + xv[i].y * xv[i].y;
+            ss = ss + xv[i].z * xv[i].z;
+            ss = ss + xv[i].w * xv[i].w;
+        }
+        float total = lane < chunks ? ss : 0.0f;
+        for (int m = 1; m < 64; m <<= 1)
+            total = total + __shfl_xor(total, m);
+        const float inv = 1.0f / sqrtf(total / (float)dim + eps);
+        if (lane < chunks) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float4 o;
+                o.x = (xv[i].x * inv) * wv[i].x;
+                o.y = (xv[i].y * inv) * wv[i].y;
+                o.z = (xv[i].z * inv) * wv[i].z;
+                o.w = (xv[i].w * inv) * wv[i].w;
+                *(float4 *)(out + 32 * c + 4 * i) = o;
+            }
+        }
+        return;
+    }
     float ss = 0.0f;
     for (int c = lane; c < chunks; c += 64) {
 #pragma unroll
