@@ -42,6 +42,46 @@ __device__ inline void tile_partials(const uint8_t *wb, const uint8_t *wb2, int 
     const int nit = (rpw + RPI - 1) / RPI;
     const size_t lds_mat = (size_t)NT * TR * nb; // floats per matrix
 
+    if constexpr (NT == 1 && !FUSED) {
+        // one vector, up to 4 chunks per row: every chunk's activations, then
+        // all of a row's chunks' weights, are in flight together
+        if (wide && C <= 4) {
+            typename F::X xc[4];
+            int bcs[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int bc = c * BPI + grp;
+                bcs[c] = bc;
+                if (c < C)
+                    xc[c] = F::load_x(xq, xd, xs, cols, vec[0], bc < nb ? bc : nb - 1, j);
+            }
+#pragma unroll 2
+            for (int it = 0; it < rpw; it++) {
+                const int rl = wave * rpw + it;
+                const int row = row0 + rl;
+                const bool rok = row < rows;
+                typename F::W w[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    if (c < C) {
+                        const int b = bcs[c] < nb ? bcs[c] : nb - 1;
+                        w[c] = F::load_w(wb, U, (size_t)(rok ? row : 0) * nb + b, j);
+                    }
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    if (c < C) {
+                        int is, ms;
+                        F::dot(w[c], xc[c], j, is, ms);
+                        is = group_sum<LPB>(is);
+                        ms = group_sum<LPB>(ms);
+                        if (rok && bcs[c] < nb && j == 0)
+                            lds[(size_t)rl * nb + bcs[c]] = F::tail(w[c], xc[c], is, ms);
+                    }
+            }
+            return;
+        }
+    }
+
     for (int c = 0; c < C; c++) {
         const int bc = wide ? c * BPI + grp : (grp % nb);
         const bool bok = bc < nb;
