@@ -400,23 +400,47 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
     }
     __syncthreads();
     if (fuse) {
-    // per-head RMSNorm (llama.zig:938-949): the sum of squares in the
-    // reference's order, one thread per head
-    if (q_norm && tid < G) {
-        float ss = 0.0f;
-        for (int i = 0; i < HD; i++) {
-            const float pr = qs[tid * HD + i] * qs[tid * HD + i];
-            ss = ss + pr;
+    // per-head RMSNorm (llama.zig:938-949): PARITY sums the squares in the
+    // reference's order, one thread per head; FAST (use_mfma) one wave per
+    // head, a fixed tree
+    if (q_norm) {
+        if (use_mfma) {
+            if (half == 0)
+                for (int g = wave; g < G; g += 4) {
+                    float ss = 0.0f;
+                    for (int i = ln; i < HD; i += 64)
+                        ss = ss + qs[g * HD + i] * qs[g * HD + i];
+                    ss = wave_sum_f(ss);
+                    if (ln == 0)
+                        sinv[g] = 1.0f / sqrtf(ss / (float)HD + D.eps);
+                }
+        } else if (tid < G) {
+            float ss = 0.0f;
+            for (int i = 0; i < HD; i++) {
+                const float pr = qs[tid * HD + i] * qs[tid * HD + i];
+                ss = ss + pr;
+            }
+            sinv[tid] = 1.0f / sqrtf(ss / (float)HD + D.eps);
         }
-        sinv[tid] = 1.0f / sqrtf(ss / (float)HD + D.eps);
     }
-    if (own && k_norm && tid == 256) {
-        float ss = 0.0f;
-        for (int i = 0; i < HD; i++) {
-            const float pr = kn[i] * kn[i];
-            ss = ss + pr;
+    if (own && k_norm) {
+        if (use_mfma) {
+            if (wave == 4) {
+                float ss = 0.0f;
+                for (int i = ln; i < HD; i += 64)
+                    ss = ss + kn[i] * kn[i];
+                ss = wave_sum_f(ss);
+                if (ln == 0)
+                    sinv[MAX_G] = 1.0f / sqrtf(ss / (float)HD + D.eps);
+            }
+        } else if (tid == 256) {
+            float ss = 0.0f;
+            for (int i = 0; i < HD; i++) {
+                const float pr = kn[i] * kn[i];
+                ss = ss + pr;
+            }
+            sinv[MAX_G] = 1.0f / sqrtf(ss / (float)HD + D.eps);
         }
-        sinv[MAX_G] = 1.0f / sqrtf(ss / (float)HD + D.eps);
     }
     __syncthreads();
     if (half == 0) {
