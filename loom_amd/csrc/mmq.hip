@@ -26,9 +26,11 @@ constexpr uint64_t NIB = 0x0F0F0F0F0F0F0F0Full;
 // mins, per 16 for Q6_K's -32 offsets.
 template <int T> constexpr int sum_span() { return T == LH_Q4_K ? 32 : 16; }
 
+// Token rows of sums are padded by 4 ints: the four tokens a lane reads sit
+// in different banks.
 static size_t mmq_lds_bytes(int t, int cols, int mt, int rg, bool fused) {
     const int nb = cols / 256, tok = 16 * mt, ks = 4 / rg;
-    const size_t sums = (size_t)tok * (cols / (t == LH_Q4_K ? 32 : 16));
+    const size_t sums = (size_t)tok * (cols / (t == LH_Q4_K ? 32 : 16) + 4);
     const size_t part = ks > 1 ? (size_t)(fused ? 2 : 1) * rg * 16 * tok * nb : 0;
     return 4 * (sums + (size_t)tok * nb + part);
 }
@@ -155,20 +157,21 @@ __global__ __launch_bounds__(256) void mmq_kernel(DmmvParams p) {
     if ((int)blockIdx.y >= ng)
         return;
     const DmmvGroup grp = p.groups[blockIdx.y];
-    const int n = grp.n, cols = p.cols, nb = cols / 256, nsum = cols / SPAN, n16 = cols / 16;
+    const int n = grp.n, cols = p.cols, nb = cols / 256, nsr = cols / SPAN, nsum = nsr + 4, n16 = cols / 16;
     const int tid = threadIdx.x, wave = tid >> 6, ln = tid & 63, r16 = ln & 15, q4 = ln >> 4;
     const int rg = wave % RG, ks = wave / RG;
     const int row0 = blockIdx.x * 16 * RG;
-    int32_t *xs = mlds;                          // [TOK][nsum]
+    int32_t *xs = mlds;                          // [TOK][nsum] (nsr used)
     float *xdl = (float *)(xs + TOK * nsum);     // [TOK][nb]
     float *part = xdl + TOK * nb;                // [FUSED + 1][RG * 16][TOK][nb] (KS > 1)
     if (tid < TOK)
         vec[tid] = p.pair_src[grp.first + (tid < n ? tid : n - 1)];
     __syncthreads();
     // per-SPAN sums from the per-16 sums (exact integers)
-    for (int i = tid; i < TOK * nsum; i += 256) {
-        const int32_t *sv = p.xs + (size_t)vec[i / nsum] * n16 + (i % nsum) * (SPAN / 16);
-        xs[i] = SPAN == 32 ? sv[0] + sv[1] : sv[0];
+    for (int i = tid; i < TOK * nsr; i += 256) {
+        const int tk = i / nsr, k = i % nsr;
+        const int32_t *sv = p.xs + (size_t)vec[tk] * n16 + k * (SPAN / 16);
+        xs[tk * nsum + k] = SPAN == 32 ? sv[0] + sv[1] : sv[0];
     }
     for (int i = tid; i < TOK * nb; i += 256)
         xdl[i] = p.xd[(size_t)vec[i / nb] * nb + i % nb];
