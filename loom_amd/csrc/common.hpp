@@ -138,6 +138,25 @@ __device__ inline float group8_max(float v) {
     return v;
 }
 
+// Max and sum over aligned groups of 16 lanes (a DPP row), in every lane of
+// the row: quad xor 1 and 2, then the half-row and row mirrors.  Each step
+// adds a lane's value to its partner's, so every lane holds the same result.
+__device__ inline float group16_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v, v));
+    v = fmaxf(v, dpp_f<0x4E>(v, v));
+    v = fmaxf(v, dpp_f<0x141>(v, v));
+    v = fmaxf(v, dpp_f<0x140>(v, v));
+    return v;
+}
+
+__device__ inline float group16_sum(float v) {
+    v = v + dpp_f<0xB1>(v, v);
+    v = v + dpp_f<0x4E>(v, v);
+    v = v + dpp_f<0x141>(v, v);
+    v = v + dpp_f<0x140>(v, v);
+    return v;
+}
+
 // sdot4 over the four dwords of two 16-byte vectors.
 __device__ inline int dot16(const int4 &w, const int4 &x, int acc) {
     acc = sdot4(w.x, x.x, acc);

@@ -569,11 +569,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 sv[r] = j < nt ? acc[r] * D.scale : -INFINITY;
-                float v = sv[r];
-                v = fmaxf(v, __shfl_xor(v, 1, 16));
-                v = fmaxf(v, __shfl_xor(v, 2, 16));
-                v = fmaxf(v, __shfl_xor(v, 4, 16));
-                v = fmaxf(v, __shfl_xor(v, 8, 16));
+                const float v = group16_max(sv[r]);
                 if (r16 == 0)
                     red[0][wave][4 * q4 + r] = v;
             }
@@ -585,13 +581,11 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
             for (int r = 0; r < 4; r++) {
                 const int hh = 4 * q4 + r;
                 const float m = fmaxf(fmaxf(red[0][0][hh], red[0][1][hh]), fmaxf(red[0][2][hh], red[0][3][hh]));
-                const float e = j < nt ? exp_f32(sv[r] - m) : 0.0f;
+                // FAST numerics only: the hardware exp (a few ulp) in place of
+                // the once-rounded double exp
+                const float e = j < nt ? __expf(sv[r] - m) : 0.0f;
                 sc[hh * ATT_TC + j] = e;
-                float v = e;
-                v = v + __shfl_xor(v, 1, 16);
-                v = v + __shfl_xor(v, 2, 16);
-                v = v + __shfl_xor(v, 4, 16);
-                v = v + __shfl_xor(v, 8, 16);
+                const float v = group16_sum(e);
                 if (r16 == 0)
                     red[1][wave][hh] = v;
                 if (wave == 0 && r16 == 0 && hh < G)
