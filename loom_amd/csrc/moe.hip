@@ -19,7 +19,7 @@ namespace lh {
 constexpr int GT_THREADS = 256;
 constexpr int GT_ROWS = GT_THREADS / 32; // router rows per workgroup (a half-wave each)
 constexpr int GT_TOK = 4;                // tokens per chunk = tokens per half-wave pass
-constexpr int GT_UNROLL = 32; // router elements in flight per lane
+constexpr int GT_UNROLL = 64; // router elements in flight per lane (dim 2048: one chunk)
 constexpr int GT_COLS = 32 * GT_UNROLL; // columns per staged chunk
 
 // Router GEMV for up to GT_TOK tokens in dotF32 order (src/gguf/ggml.zig:
@@ -53,10 +53,12 @@ __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int 
             xv[q] = k < nt ? *(const float4 *)(p.x + (size_t)(t0 + k) * dim + c0 + col)
                            : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+        // unconditional loads (steps past cnt re-read the chunk's last step,
+        // their products are never added), so they all go out together
         float wv[GT_UNROLL];
 #pragma unroll
         for (int u = 0; u < GT_UNROLL; u++)
-            wv[u] = (valid && u < cnt) ? row[c0 + 32 * u + L] : 0.0f;
+            wv[u] = row[c0 + 32 * min(u, cnt - 1) + L];
         if (c0 > 0)
             lds_barrier(); // the previous chunk's readers are done with xs
 #pragma unroll
@@ -67,15 +69,30 @@ __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int 
                 *(float4 *)(xs + k * GT_COLS + col) = xv[q];
         }
         lds_barrier();
+        // tokens past nt compute on stale LDS and are not stored.  A full
+        // chunk has no per-step guard, so its LDS reads issue back to back
+        // (a guard per step compiles to a branch around each read).
+        if (cnt == GT_UNROLL) {
+            // tokens innermost: GT_TOK independent sums, each still in
+            // column order
 #pragma unroll
-        for (int k = 0; k < GT_TOK; k++) {
-            if (k < nt) {
+            for (int u = 0; u < GT_UNROLL; u++) {
+#pragma unroll
+                for (int k = 0; k < GT_TOK; k++) {
+                    const float pr = wv[u] * xs[k * GT_COLS + 32 * u + L];
+                    acc[k] = acc[k] + pr;
+                }
+            }
+        } else {
+            // steps past cnt add +0 (acc starts at +0 and a sum of products
+            // is never -0)
+#pragma unroll
+            for (int k = 0; k < GT_TOK; k++) {
 #pragma unroll
                 for (int u = 0; u < GT_UNROLL; u++) {
-                    if (u < cnt) {
-                        const float pr = wv[u] * xs[k * GT_COLS + 32 * u + L];
-                        acc[k] = acc[k] + pr;
-                    }
+                    const float xv = xs[k * GT_COLS + 32 * min(u, cnt - 1) + L];
+                    const float pr = u < cnt ? wv[u] * xv : 0.0f;
+                    acc[k] = acc[k] + pr;
                 }
             }
         }
