@@ -835,8 +835,6 @@ struct FrameWs {
     QAct qa_dim, qa_att, qa_ffn;
     const DmmvGroup *groups; // lanes in groups of nt against plane 0
     int n_groups, nt;
-    const DmmvGroup *groups32; // lanes in groups of 32 (matrix-core matmuls)
-    int n_groups32;
     size_t bytes;
 };
 
@@ -875,9 +873,7 @@ static FrameWs frame_layout(char *base, size_t n, const loomhip_model *m, size_t
     return w;
 }
 
-// mmq_ok: the matrix cores from MMQ_MIN_TOK lanes on (the head: many rows
-// per lane group); the attention matrices stay on the grouped matvec, which
-// is faster for them at these lane counts.
+// mmq_ok: the matrix cores from MMQ_MIN_TOK lanes on, in groups of 32 lanes.
 static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameWs &w, size_t n,
                          QAct x, float *out, int accumulate, hipStream_t st, int tag = LOOMHIP_KT_QKV,
                          bool mmq_ok = false) {
@@ -897,10 +893,8 @@ static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameW
     p.out_stride = rows;
     p.accumulate = accumulate;
     const bool mq = mmq_ok && use_mmq(t, cols, (int)n, 32, false);
-    if (mq) {
-        p.groups = w.groups32;
-        p.n_groups = w.n_groups32;
-    }
+    if (mq)
+        p.ident_n = (int)n;
     p.rpw = mq ? 0 : dmmv_pick_rpw(t, cols, rows, w.n_groups, w.nt, false);
     const int ph = prof_begin(tag, st);
     const bool ok = mq ? launch_mmq(t, 32, false, p, st) : launch_dmmv(t, w.nt, false, p, st);
@@ -924,6 +918,12 @@ static bool frame_qkv(const loomhip_layer &l, const FrameDims &D, const FrameWs 
     sp.seg[1] = DmmvSeg{(const uint8_t *)l.wk, l.wk_t, D.kvd, w.k, 0, 0};
     sp.seg[2] = DmmvSeg{(const uint8_t *)l.wv, l.wv_t, D.kvd, w.v, 0, 0};
     sp.n_seg = 3;
+    // from MMQ_MIN_TOK lanes: the matrix cores, one launch per matrix
+    if (use_mmq(l.wq_t, D.dim, (int)n, 32, false) && use_mmq(l.wk_t, D.dim, (int)n, 32, false) &&
+        use_mmq(l.wv_t, D.dim, (int)n, 32, false))
+        return frame_matvec(l.wq_t, l.wq, D.qd, D.dim, w, n, w.qa_dim, w.q, 0, st, LOOMHIP_KT_QKV, true) &&
+               frame_matvec(l.wk_t, l.wk, D.kvd, D.dim, w, n, w.qa_dim, w.k, 0, st, LOOMHIP_KT_QKV, true) &&
+               frame_matvec(l.wv_t, l.wv, D.kvd, D.dim, w, n, w.qa_dim, w.v, 0, st, LOOMHIP_KT_QKV, true);
     const int ph = prof_begin(LOOMHIP_KT_QKV, st);
     const bool ok = launch_dmmv_seg(w.nt, sp, st);
     prof_end(ph, st);
@@ -1013,8 +1013,7 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     FrameWs w = frame_layout((char *)g_frame.ptr, n, m, ffn_max, n_chunks);
     w.nt = pick_nt((int)n);
     w.groups = dense_groups((int)n, w.nt, &w.n_groups); // built once per lane count, before any capture
-    w.groups32 = dense_groups((int)n, 32, &w.n_groups32);
-    if (!w.groups || !w.groups32)
+    if (!w.groups)
         return fail(LOOMHIP_ERR_HIP, "token_frame: group table");
     FrameDims D;
     D.dim = (int)m->dim;
@@ -1091,7 +1090,7 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
             hipLaunchKernelGGL(attn_combine_kernel<32>, dim3((D.qd + 255) / 256, n), dim3(1024), cmb_lds, st,
                                D, w.part, pos, n_chunks, w.qa_att);
         note_launch();
-        if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st))
+        if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_QKV, true))
             return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
         // FFN block (llama.zig:1203-1224)
         if (l.is_moe) {

@@ -38,6 +38,8 @@ struct DmmvParams {
     int out_stride;
     int rpw;        // rows per wave
     int accumulate; // 1: out = out + value (a residual add, tensor.zig:50-52)
+    int ident_n;    // launch_mmq only: > 0 means ident_n vectors in groups of consecutive
+                    // vectors, identity pair maps, plane 0 -- no group or pair table is read
 };
 
 // Up to DMMV_MAX_SEG matrices of any supported types against one activation

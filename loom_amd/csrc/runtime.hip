@@ -248,6 +248,7 @@ int matvec_dev_impl(int t, float *out, const void *w, const float *x, size_t n, 
     p.out = out;
     p.out_stride = (int)rows;
     p.rpw = mq ? 0 : dmmv_pick_rpw(t, (int)cols, (int)rows, ng, nt, false);
+    p.ident_n = mq ? (int)n : 0;
     const int ph = prof_begin(LOOMHIP_KT_DENSE, st);
     const bool launched = mq ? launch_mmq(t, nt, false, p, st) : launch_dmmv(t, nt, false, p, st);
     prof_end(ph, st);
