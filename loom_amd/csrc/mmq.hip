@@ -278,8 +278,14 @@ __global__ __launch_bounds__(64 * MMQ_WAVES) void mmq_kernel(DmmvParams p, int R
             for (int i = 0; i < 4; i++)
                 op[j].xd[mt][i] = p.xd[(size_t)vout[mt][i] * nb + bj[j]];
         }
+    // 3. the first output of this thread (the common case is one per thread):
+    // its destination and, for a residual add, the value it adds to
+    const int idx0 = threadIdx.x, tk0 = idx0 / R, rr0 = idx0 % R;
+    const bool out0 = idx0 < n * R && row0 + rr0 < p.rows;
+    const int dst0 = ident ? grp.first + tk0 : p.pair_dst[grp.first + min(tk0, n - 1)];
+    const float old0 = out0 && p.accumulate ? p.out[(size_t)dst0 * p.out_stride + row0 + rr0] : 0.0f;
     __builtin_amdgcn_sched_barrier(0); // every load above is in flight before the first MFMA
-    // 3. the tiles
+    // 4. the tiles
 #pragma unroll
     for (int j = 0; j < SBW; j++) {
         float r[MT][4], r2[MT][4];
@@ -318,9 +324,140 @@ __global__ __launch_bounds__(64 * MMQ_WAVES) void mmq_kernel(DmmvParams p, int R
                 acc2 = acc2 + pv[mat + (size_t)b * TOK * RS];
             v = swiglu1(acc, acc2);
         }
-        const int dst = ident ? grp.first + tk : p.pair_dst[grp.first + tk];
+        const bool first = idx == idx0;
+        const int dst = first ? dst0 : ident ? grp.first + tk : p.pair_dst[grp.first + tk];
         float *o = p.out + (size_t)dst * p.out_stride + row0 + rr;
-        *o = p.accumulate ? *o + v : v;
+        if (p.accumulate)
+            v = (first ? old0 : *o) + v;
+        *o = v;
+    }
+}
+
+// Streaming variant for one super-block per wave (nb <= MMQ_WAVES): a work
+// group walks NTILE consecutive row tiles of its group (each RG x 16 rows).  The activations are loaded once; each
+// tile's weights are requested while the previous tile computes, in two
+// register sets, and the values meet in two LDS buffers, one barrier per
+// tile.  Same arithmetic and order as mmq_kernel.
+template <int T, int MT, bool FUSED>
+__global__ __launch_bounds__(64 * MMQ_WAVES) void mmq_stream_kernel(DmmvParams p, int RG, int NTILE) {
+    extern __shared__ __align__(16) float part[];
+    constexpr int TOK = 16 * MT;
+    using Tile = typename std::conditional<T == LH_Q4_K, Q4kTile, Q6kTile>::type;
+    const bool ident = p.ident_n > 0;
+    DmmvGroup grp;
+    if (ident) {
+        grp.plane = 0;
+        grp.first = (int)blockIdx.y * TOK;
+        grp.n = min(TOK, p.ident_n - grp.first);
+    } else {
+        const int ng = p.n_groups_dev ? *p.n_groups_dev : p.n_groups;
+        if ((int)blockIdx.y >= ng)
+            return;
+        grp = p.groups[blockIdx.y];
+    }
+    const int n = grp.n, cols = p.cols, nb = cols / 256;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ln = threadIdx.x & 63;
+    const int r16 = ln & 15, q4 = ln >> 4;
+    const int rg = wave % RG, b = wave / RG; // this wave's super-block
+    const int R = 16 * RG, RS = R + 1;
+    const int rl = 16 * rg + r16;
+    const int tile0 = blockIdx.x * NTILE;
+    const int nti = min(NTILE, (p.rows + R - 1) / R - tile0);
+    const size_t U = (size_t)p.rows * nb;
+    const size_t mat = (size_t)nb * TOK * RS;
+    const size_t buf = (size_t)(FUSED ? 2 : 1) * mat;
+    const uint8_t *wb = p.w + (size_t)grp.plane * p.plane_bytes;
+    const uint8_t *wb2 = FUSED ? p.w2 + (size_t)grp.plane * p.plane_bytes : nullptr;
+    auto load_tile = [&](int tile, Tile &a, Tile &a2) {
+        const size_t unit = (size_t)min(tile * R + rl, p.rows - 1) * nb + b;
+        if constexpr (T == LH_Q4_K) {
+            a = q4k_load(wb + unit * 144, q4);
+            if constexpr (FUSED)
+                a2 = q4k_load(wb2 + unit * 144, q4);
+        } else {
+            a = q6k_load(wb, U, unit, q4);
+        }
+    };
+    Tile wa, wa2, wbt, wbt2;
+    load_tile(tile0, wa, wa2);
+    int vrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+        vrow[mt] = ident ? grp.first + min(16 * mt + r16, n - 1) : p.pair_src[grp.first + min(16 * mt + r16, n - 1)];
+    typename std::conditional<T == LH_Q4_K, mmq_i4[MT][4], long[MT][8]>::type xa;
+    float xd[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        if constexpr (T == LH_Q4_K) {
+            const int8_t *xr = p.xq + (size_t)vrow[mt] * cols + 256 * b + 16 * q4;
+#pragma unroll
+            for (int s4 = 0; s4 < 4; s4++)
+                xa[mt][s4] = *(const mmq_i4 *)(xr + 64 * s4);
+        } else {
+            const int8_t *xr = p.xq + (size_t)vrow[mt] * cols + 256 * b + 8 * q4;
+#pragma unroll
+            for (int g = 0; g < 8; g++)
+                xa[mt][g] = *(const long *)(xr + 32 * g);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            xd[mt][i] = p.xd[(size_t)__shfl(vrow[mt], 4 * q4 + i) * nb + b];
+    }
+    // one tile: its values into LDS buffer pb, the barrier, then the outputs
+    auto run_tile = [&](int it, const Tile &w, const Tile &w2) {
+        float *pb = part + (size_t)(it & 1) * buf;
+        float r[MT][4], r2[MT][4];
+        if constexpr (T == LH_Q4_K) {
+            q4k_tile<MT>(w, q4, xa, xd, r);
+            if constexpr (FUSED)
+                q4k_tile<MT>(w2, q4, xa, xd, r2);
+        } else {
+            q6k_tile<MT>(w, q4, xa, xd, r);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const size_t o = ((size_t)b * TOK + 16 * mt + 4 * q4 + i) * RS + rl;
+                pb[o] = r[mt][i];
+                if constexpr (FUSED)
+                    pb[mat + o] = r2[mt][i];
+            }
+        // a buffer is written again two tiles on, after every thread has
+        // passed the next tile's barrier
+        __syncthreads();
+        const int row0 = (tile0 + it) * R;
+        for (int idx = threadIdx.x; idx < n * R; idx += blockDim.x) {
+            const int tk = idx / R, rr = idx % R;
+            if (row0 + rr >= p.rows)
+                continue;
+            const float *pv = pb + (size_t)tk * RS + rr;
+            float acc = 0.0f;
+            for (int bb = 0; bb < nb; bb++)
+                acc = acc + pv[(size_t)bb * TOK * RS];
+            float v = acc;
+            if constexpr (FUSED) {
+                float acc2 = 0.0f;
+                for (int bb = 0; bb < nb; bb++)
+                    acc2 = acc2 + pv[mat + (size_t)bb * TOK * RS];
+                v = swiglu1(acc, acc2);
+            }
+            const int dst = ident ? grp.first + tk : p.pair_dst[grp.first + tk];
+            float *o = p.out + (size_t)dst * p.out_stride + row0 + rr;
+            *o = p.accumulate ? *o + v : v;
+        }
+    };
+    for (int it = 0; it < nti; it += 2) {
+        if (it + 1 < nti)
+            load_tile(tile0 + it + 1, wbt, wbt2);
+        __builtin_amdgcn_sched_barrier(0);
+        run_tile(it, wa, wa2);
+        if (it + 1 >= nti)
+            break;
+        if (it + 2 < nti)
+            load_tile(tile0 + it + 2, wa, wa2);
+        __builtin_amdgcn_sched_barrier(0);
+        run_tile(it + 1, wbt, wbt2);
     }
 }
 
@@ -353,11 +490,29 @@ bool mmq_supported(int t, int cols, int max_tok, bool fused) {
     return mmq_shape(16, cols, (max_tok + 15) / 16, fused, rg, ks, sbw);
 }
 
+// Row tiles per streaming work group: about MMQ_STREAM_WGS work groups, at
+// most MMQ_MAX_NTILE tiles each; 1 = the one-shot kernel.  Streaming serves
+// the lane-group (identity) launches with many row tiles (the head): for the
+// grouped expert launches the one-shot kernel measured faster (its groups
+// already give thousands of short work groups).
+constexpr int MMQ_STREAM_WGS = 512;
+constexpr int MMQ_MAX_NTILE = 8;
+
 template <int T, int MT, bool FUSED>
 static void mmq_launch_t(const DmmvParams &p, int rg, int ks, int sbw, hipStream_t st) {
     const size_t lds = mmq_lds_bytes(p.cols, MT, rg, FUSED);
     const int groups = p.ident_n > 0 ? (p.ident_n + 16 * MT - 1) / (16 * MT) : p.n_groups;
-    const dim3 grid((p.rows + 16 * rg - 1) / (16 * rg), groups), block(64 * rg * ks);
+    const int tiles = (p.rows + 16 * rg - 1) / (16 * rg);
+    if (sbw == 1 && p.ident_n > 0 && 2 * lds <= 64 * 1024) {
+        int ntile = (int)((long)tiles * groups / MMQ_STREAM_WGS);
+        ntile = ntile > MMQ_MAX_NTILE ? MMQ_MAX_NTILE : ntile;
+        if (ntile > 1) {
+            const dim3 grid((tiles + ntile - 1) / ntile, groups), block(64 * rg * ks);
+            hipLaunchKernelGGL((mmq_stream_kernel<T, MT, FUSED>), grid, block, 2 * lds, st, p, rg, ntile);
+            return;
+        }
+    }
+    const dim3 grid(tiles, groups), block(64 * rg * ks);
     if (sbw == 1)
         hipLaunchKernelGGL((mmq_kernel<T, MT, FUSED, 1>), grid, block, lds, st, p, rg, ks);
     else if (sbw == 2)
