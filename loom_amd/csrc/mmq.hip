@@ -5,8 +5,8 @@
 //
 // The integer part of every block dot runs on the int8 MFMAs: the activations
 // of 16 tokens are the A rows, 16 weight rows the B columns (Q4_K:
-// v_mfma_i32_16x16x64_i8 over a 64-value quant span; Q6_K:
-// v_mfma_i32_16x16x32_i8 over a 32-value group).  Integer dots are exact in
+// v_mfma_i32_16x16x64_i8 over a 64-value quant span; Q6_K: the same MFMA
+// over four 16-value runs, one run per MFMA).  Integer dots are exact in
 // any order, so isum = sum sc * dot and msum = sum mn * bsum are the
 // reference's integers; the f32 tail per (token, row, super-block) is the
 // reference's expression, and each output sums its blocks in block order
@@ -110,9 +110,16 @@ __device__ __forceinline__ void q4k_tile(const Q4kTile &w, int q4, const mmq_i4 
         }
 }
 
-// Q6_K (device SoA ql[U][128] | qh[U][64] | sc[U][16] | d[U]).
+// Q6_K (device SoA ql[U][128] | qh[U][64] | sc[U][16] | d[U]) on
+// v_mfma_i32_16x16x64_i8: MFMA h spans values [64h, 64h + 64) and lane
+// quarter q4 holds the 16 values [64h + 16*q4, +16) -- exactly the 16-value
+// run 4h + q4 -- so activation and weight loads are 16 contiguous bytes per
+// lane.  Each run has its own scale: one MFMA per run, the other quarters'
+// weights zeroed.  The weights enter as q - 32 (-32..31 fits int8), so isum =
+// sum_run sc[run] * dot(q - 32, x), the reference's sum sc * (dot(q, x) - 32 *
+// sum(x)) as one exact integer.
 struct Q6kTile {
-    uint64_t ql[2][2], qh[2];
+    uint4 ql[2], qh[2]; // half n's 16 bytes of low bits / high bits for this lane's quarter
     uint4 sc;
     uint16_t d;
 };
@@ -121,25 +128,28 @@ __device__ __forceinline__ Q6kTile q6k_load(const uint8_t *base, size_t U, size_
     Q6kTile w;
 #pragma unroll
     for (int n = 0; n < 2; n++) {
-#pragma unroll
-        for (int o = 0; o < 2; o++)
-            w.ql[n][o] = *(const uint64_t *)(base + unit * 128 + 64 * n + 32 * o + 8 * q4);
-        w.qh[n] = *(const uint64_t *)(base + U * 128 + unit * 64 + 32 * n + 8 * q4);
+        w.ql[n] = *(const uint4 *)(base + unit * 128 + 64 * n + 16 * q4);
+        w.qh[n] = *(const uint4 *)(base + U * 128 + unit * 64 + 32 * n + 16 * (q4 & 1));
     }
     w.sc = *(const uint4 *)(base + U * 192 + unit * 16);
     w.d = *(const uint16_t *)(base + U * 208 + unit * 2);
     return w;
 }
 
+// 4 bytes of 6-bit quants (low nibble at shift ls, two high bits at shift hs)
+// -> q - 32 as int8: flip bit 5, then sign-extend it into bits 6 and 7
+// where it is set (the values below 32)
+__device__ __forceinline__ int q6_minus32(uint32_t ql, uint32_t qh, int ls, int hs) {
+    const uint32_t v = ((ql >> ls) & 0x0F0F0F0Fu) | (((qh >> hs) & 0x03030303u) << 4);
+    const uint32_t y = v ^ 0x20202020u;
+    const uint32_t m = y & 0x20202020u;
+    return (int)(y | (m << 1) | (m << 2));
+}
+
 template <int MT>
-__device__ __forceinline__ void q6k_tile(const Q6kTile &w, int q4, const long (&xa)[MT][8],
+__device__ __forceinline__ void q6k_tile(const Q6kTile &w, int q4, const mmq_i4 (&xa)[MT][4],
                                          const float (&xd)[MT][4], float (&r)[MT][4]) {
-    int sc[16];
-#pragma unroll
-    for (int k = 0; k < 16; k++)
-        sc[k] = (int)(int8_t)byte_of(w.sc, k);
     const float dw = half_bits_to_float(w.d);
-    const bool lo_run = q4 < 2; // values 32g + 8*q4 .. +7 lie in run 2g (q4 < 2) or 2g+1
     const mmq_i4 z = {0, 0, 0, 0};
     int isum[MT][4];
 #pragma unroll
@@ -148,22 +158,21 @@ __device__ __forceinline__ void q6k_tile(const Q6kTile &w, int q4, const long (&
         for (int i = 0; i < 4; i++)
             isum[mt][i] = 0;
 #pragma unroll
-    for (int g = 0; g < 8; g++) {
-        const int n = g >> 2, qd = g & 3;
-        const uint64_t l4 = qd >= 2 ? (w.ql[n][qd & 1] >> 4) & NIB : w.ql[n][qd & 1] & NIB;
-        const uint64_t v = l4 | (((w.qh[n] >> (2 * qd)) & 0x0303030303030303ull) << 4);
-        // bytes 0..63 -> q - 32 as int8: flip bit 5, then sign-extend it
-        // into bits 6 and 7 where it is set (the values below 32)
-        const uint64_t y = v ^ 0x2020202020202020ull;
-        const uint64_t m = y & 0x2020202020202020ull;
-        const long vs = (long)(y | (m << 1) | (m << 2));
+    for (int h = 0; h < 4; h++) {
+        const int n = h >> 1, ls = 4 * (h & 1), hs = 4 * (h & 1) + 2 * (q4 >> 1);
+        const mmq_i4 vs = {q6_minus32(w.ql[n].x, w.qh[n].x, ls, hs), q6_minus32(w.ql[n].y, w.qh[n].y, ls, hs),
+                           q6_minus32(w.ql[n].z, w.qh[n].z, ls, hs), q6_minus32(w.ql[n].w, w.qh[n].w, ls, hs)};
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            const mmq_i4 d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa[mt][g], lo_run ? vs : 0l, z, 0, 0, 0);
-            const mmq_i4 d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa[mt][g], lo_run ? 0l : vs, z, 0, 0, 0);
+        for (int qq = 0; qq < 4; qq++) {
+            const int sc = (int)(int8_t)byte_of(w.sc, 4 * h + qq);
+            const mmq_i4 bq = q4 == qq ? vs : z;
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                isum[mt][i] += sc[2 * g] * d0[i] + sc[2 * g + 1] * d1[i];
+            for (int mt = 0; mt < MT; mt++) {
+                const mmq_i4 dq = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[mt][h], bq, z, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    isum[mt][i] += sc * dq[i];
+            }
         }
     }
 #pragma unroll
@@ -189,11 +198,11 @@ constexpr int MMQ_MAX_SBW = 4; // super-blocks per wave (at most): cols <= 8192 
 constexpr int MMQ_WAVES = 8;
 
 // One wave's operands for one super-block: the activations as the MFMA A
-// operands (Q4_K: 16 bytes per span; Q6_K: 8 bytes per 32-value group).
+// operands (16 bytes per 64-value span and lane quarter).
 template <int T, int MT, bool FUSED>
 struct MmqOps {
     typename std::conditional<T == LH_Q4_K, Q4kTile, Q6kTile>::type w, w2;
-    typename std::conditional<T == LH_Q4_K, mmq_i4[MT][4], long[MT][8]>::type xa;
+    mmq_i4 xa[MT][4];
     float xd[MT][4];
 };
 
@@ -263,17 +272,10 @@ __global__ __launch_bounds__(64 * MMQ_WAVES) void mmq_kernel(DmmvParams p, int R
     for (int j = 0; j < SBW; j++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
-            if constexpr (T == LH_Q4_K) {
-                const int8_t *xr = p.xq + (size_t)vrow[mt] * cols + 256 * bj[j] + 16 * q4;
+            const int8_t *xr = p.xq + (size_t)vrow[mt] * cols + 256 * bj[j] + 16 * q4;
 #pragma unroll
-                for (int s4 = 0; s4 < 4; s4++)
-                    op[j].xa[mt][s4] = *(const mmq_i4 *)(xr + 64 * s4);
-            } else {
-                const int8_t *xr = p.xq + (size_t)vrow[mt] * cols + 256 * bj[j] + 8 * q4;
-#pragma unroll
-                for (int g = 0; g < 8; g++)
-                    op[j].xa[mt][g] = *(const long *)(xr + 32 * g);
-            }
+            for (int s4 = 0; s4 < 4; s4++)
+                op[j].xa[mt][s4] = *(const mmq_i4 *)(xr + 64 * s4);
 #pragma unroll
             for (int i = 0; i < 4; i++)
                 op[j].xd[mt][i] = p.xd[(size_t)vout[mt][i] * nb + bj[j]];
@@ -384,21 +386,14 @@ __global__ __launch_bounds__(64 * MMQ_WAVES) void mmq_stream_kernel(DmmvParams p
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
         vrow[mt] = ident ? grp.first + min(16 * mt + r16, n - 1) : p.pair_src[grp.first + min(16 * mt + r16, n - 1)];
-    typename std::conditional<T == LH_Q4_K, mmq_i4[MT][4], long[MT][8]>::type xa;
+    mmq_i4 xa[MT][4];
     float xd[MT][4];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-        if constexpr (T == LH_Q4_K) {
-            const int8_t *xr = p.xq + (size_t)vrow[mt] * cols + 256 * b + 16 * q4;
+        const int8_t *xr = p.xq + (size_t)vrow[mt] * cols + 256 * b + 16 * q4;
 #pragma unroll
-            for (int s4 = 0; s4 < 4; s4++)
-                xa[mt][s4] = *(const mmq_i4 *)(xr + 64 * s4);
-        } else {
-            const int8_t *xr = p.xq + (size_t)vrow[mt] * cols + 256 * b + 8 * q4;
-#pragma unroll
-            for (int g = 0; g < 8; g++)
-                xa[mt][g] = *(const long *)(xr + 32 * g);
-        }
+        for (int s4 = 0; s4 < 4; s4++)
+            xa[mt][s4] = *(const mmq_i4 *)(xr + 64 * s4);
 #pragma unroll
         for (int i = 0; i < 4; i++)
             xd[mt][i] = p.xd[(size_t)__shfl(vrow[mt], 4 * q4 + i) * nb + b];
