@@ -187,6 +187,7 @@ __global__ __launch_bounds__(64) void qk_rope_kernel(FrameDims D, const float *_
                                                      const int32_t *__restrict__ pos, int li,
                                                      const float *__restrict__ rope_cs,
                                                      float *__restrict__ q_out,
+                                                     uint16_t *__restrict__ q_split,
                                                      uint16_t *__restrict__ kc,
                                                      uint16_t *__restrict__ vc) {
     __shared__ float hv[MAX_HD];
@@ -229,9 +230,18 @@ __global__ __launch_bounds__(64) void qk_rope_kernel(FrameDims D, const float *_
     }
     __syncthreads();
     if (isq) {
-        float *o = q_out + (size_t)t * D.qd + (size_t)h * hd;
+        const size_t qo = (size_t)t * D.qd + (size_t)h * hd;
         for (int i = tid; i < hd; i += 64)
-            o[i] = hv[i];
+            q_out[qo + i] = hv[i];
+        if (q_split) { // (f16 hi, f16 lo) with hi + lo = q to 22 bits, for the MFMA scores
+            const size_t nq = (size_t)gridDim.y * D.qd;
+            for (int i = tid; i < hd; i += 64) {
+                const _Float16 hi = (_Float16)hv[i];
+                const _Float16 lo = (_Float16)(hv[i] - (float)hi);
+                q_split[qo + i] = __builtin_bit_cast(uint16_t, hi);
+                q_split[nq + qo + i] = __builtin_bit_cast(uint16_t, lo);
+            }
+        }
         return;
     }
     if (p < 0 || p >= D.ctx) // a full cache takes no more rows
@@ -331,6 +341,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
                                                                       uint16_t *__restrict__ vc,
                                                                       const int32_t *__restrict__ pos, int li,
                                                                       int n_chunks, int use_mfma, int fuse,
+                                                                      const uint16_t *__restrict__ qsplit,
                                                                       float *__restrict__ part) {
     extern __shared__ __align__(16) float smem[];
     constexpr int KS = HD + 8;                 // padded key row (halves)
@@ -353,10 +364,15 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
     // Otherwise qk_rope_kernel did both and qraw holds the rotated queries.
     const bool own = fuse && p_raw >= 0 && p_raw < D.ctx && p_raw >= t0 && p_raw < t0 + ATT_TC;
     const int rp = min(max(p_raw, 0), D.ctx - 1); // rope position
-    float *qs = smem;                                  // [G][HD] f32
-    float *sc = qs + G * HD;                           // [16][TC] f32: p of head g, position j
-    uint16_t *ks = (uint16_t *)(sc + 16 * ATT_TC);     // [TC][KS]
-    uint16_t *vs = ks + ATT_TC * KS;                   // [TC][VS]
+    // direct (qsplit given: FAST, rope done, MFMA head size): the scores take
+    // their keys from HBM and the split queries from qsplit straight into the
+    // MFMA operands, LDS holds p and the values only, and a one-chunk context
+    // also takes this path (its record is merged like any other)
+    const bool direct = MF && qsplit != nullptr;
+    float *qs = smem;                                      // [G][HD] f32
+    float *sc = direct ? smem : qs + G * HD;               // [16][TC] f32: p of head g, position j
+    uint16_t *ks = (uint16_t *)(sc + 16 * ATT_TC);         // [TC][KS]
+    uint16_t *vs = direct ? ks : ks + ATT_TC * KS;         // [TC][VS]
     __shared__ float red[2][4][16];
     __shared__ float kn[HD], sinv[MAX_G + 1];
     const int wave = tid >> 6, ln = tid & 63, half = tid >> 8, ht = tid & 255;
@@ -366,13 +382,60 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
     // half 0: keys and the group's query heads, half 1: values (and the new row)
     const uint16_t *src = half ? vc : kc;
     uint4 pc[NPW];
+    float sv[4]; // MFMA path: this lane's scores (position 16w + r16, heads 4*q4 ..)
+    if (direct && half == 0) {
+        if constexpr (MF) {
+            // scores of positions 16w..16w+15 straight from the operands
+            const int r16 = ln & 15, q4 = ln >> 4, j = 16 * wave + r16;
+            const uint16_t *kr = kc + row0 + (size_t)min(j, nt - 1) * D.kvd + 8 * q4;
+            const size_t qo = (size_t)t * D.qd + ((size_t)kvh * G + min(r16, G - 1)) * HD + 8 * q4;
+            const size_t nq = (size_t)gridDim.z * D.qd;
+            const bool hrow = r16 < G;
+            half8_t kb[HD / 32], qh[HD / 32], ql[HD / 32];
 #pragma unroll
-    for (int u = 0; u < NPW; u++) {
-        const int i = ht + 256 * u;
-        pc[u] = *(const uint4 *)(src + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR));
+            for (int kk = 0; kk < HD / 32; kk++) {
+                kb[kk] = *(const half8_t *)(kr + 32 * kk);
+                qh[kk] = *(const half8_t *)(qsplit + qo + 32 * kk);
+                ql[kk] = *(const half8_t *)(qsplit + nq + qo + 32 * kk);
+            }
+            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            const half8_t zh = {};
+#pragma unroll
+            for (int kk = 0; kk < HD / 32; kk++) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(hrow ? qh[kk] : zh, kb[kk], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(hrow ? ql[kk] : zh, kb[kk], acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                sv[r] = j < nt ? acc[r] * D.scale : -INFINITY;
+                const float v = group16_max(sv[r]);
+                if (r16 == 0)
+                    red[0][wave][4 * q4 + r] = v;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < NPW; u++) {
+            const int i = ht + 256 * u;
+            pc[u] = *(const uint4 *)(src + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR));
+        }
     }
     float vnew = 0.0f;
-    if (half == 0) {
+    if (direct) {
+        if (half == 1) {
+#pragma unroll
+            for (int u = 0; u < NPW; u++) { // values: 4-byte stores into the padded rows
+                const int i = ht + 256 * u;
+                if (i < ATT_TC * PR) {
+                    uint32_t *vrow = (uint32_t *)(vs + (i / PR) * VS + 8 * (i % PR));
+                    vrow[0] = pc[u].x;
+                    vrow[1] = pc[u].y;
+                    vrow[2] = pc[u].z;
+                    vrow[3] = pc[u].w;
+                }
+            }
+        }
+    } else if (half == 0) {
         for (int i = ht; i < G * HD; i += 256)
             qs[i] = qsrc[i];
 #pragma unroll
@@ -398,7 +461,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
             }
         }
     }
-    __syncthreads();
+    if (!direct)
+        __syncthreads();
     if (fuse) {
     // per-head RMSNorm (llama.zig:938-949): PARITY sums the squares in the
     // reference's order, one thread per head; FAST (use_mfma) one wave per
@@ -485,7 +549,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
     }
     float *rec = part + (((size_t)t * D.n_kv + kvh) * n_chunks + ch) * (size_t)G * (HD + 2);
 
-    if (!MF || single || !use_mfma) {
+    if (!MF || (single && !direct) || !use_mfma) {
         const uint16_t *krow = ks + min(ln, nt - 1) * KS;
         for (int g = wave; g < G; g += ATT_WAVES) {
             const float s = ln < nt ? dot_f32_key<HD>(qs + g * HD, krow) * D.scale : -INFINITY;
@@ -544,8 +608,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
 
     if constexpr (MF) {
         const int r16 = ln & 15, q4 = ln >> 4; // tile row/column, k-quarter
-        float sv[4];
-        if (half == 0) {
+        if (half == 0 && !direct) { // (direct: the scores are in already)
             // scores of positions 16w..16w+15
             const int j = 16 * wave + r16;
             const uint16_t *krow = ks + min(j, nt - 1) * KS;
@@ -643,7 +706,7 @@ constexpr int CMB_OP = 24; // chunks per quarter held in registers (contexts up 
 template <int QB>
 __global__ __launch_bounds__(1024) void attn_combine_kernel(FrameDims D, const float *__restrict__ part,
                                                             const int32_t *__restrict__ pos,
-                                                            int n_chunks, QAct qa) {
+                                                            int n_chunks, int merge_one, QAct qa) {
     extern __shared__ float cmb[]; // [4][256] quarter sums, then [CMB_NH][n_chunks] weights
     __shared__ float red[4], Ls[CMB_NH];
     const int t = blockIdx.y, tid = threadIdx.x, v = tid & 255, cq = tid >> 8;
@@ -661,7 +724,7 @@ __global__ __launch_bounds__(1024) void attn_combine_kernel(FrameDims D, const f
     const size_t rs = (size_t)G * (hd + 2);
     const float *rec0 = part + ((size_t)t * D.n_kv + kvh) * n_chunks * rs;
     float val;
-    if (nc == 1) { // one chunk: its record is already the softmax-weighted sum
+    if (nc == 1 && !merge_one) { // one chunk: its record is already the softmax-weighted sum
         val = rec0[2 * G + (size_t)g * hd + d];
     } else {
         float *wt = cmb + 4 * 256;
@@ -831,6 +894,7 @@ static const float *rope_table(int ctx, int rope_dim, float base) {
 
 struct FrameWs {
     float *x, *normed, *q, *k, *v, *qrot, *part, *act, *amax_v;
+    uint16_t *qsplit; // the rotated queries as (f16 hi, f16 lo) planes, [2][n][qd]
     int *amax_i;
     QAct qa_dim, qa_att, qa_ffn;
     const DmmvGroup *groups; // lanes in groups of nt against plane 0
@@ -862,6 +926,7 @@ static FrameWs frame_layout(char *base, size_t n, const loomhip_model *m, size_t
     w.k = (float *)take(n * kvd * 4);
     w.v = (float *)take(n * kvd * 4);
     w.qrot = (float *)take(n * qd * 4);
+    w.qsplit = (uint16_t *)take(n * qd * 4);
     w.part = (float *)take(n * m->n_kv_heads * (size_t)n_chunks * G * (m->head_dim + 2) * 4);
     w.act = (float *)take(n * (ffn_max ? ffn_max : 1) * 4);
     w.amax_v = (float *)take(n * ARGMAX_SLICES * 4);
@@ -1035,6 +1100,8 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
                            (size_t)ATT_TC * (D.hd + 2) * 2;
     if (att_lds > 64 * 1024)
         return fail(LOOMHIP_DECLINED, "token_frame: attention tile exceeds LDS (%zu B)", att_lds);
+    // the direct form keeps p and the values only
+    const size_t att_lds_direct = (size_t)16 * ATT_TC * 4 + (size_t)ATT_TC * (D.hd + 2) * 2;
     const size_t cmb_lds = (4 * 256 + (size_t)CMB_NH * n_chunks) * 4;
     if (cmb_lds > 64 * 1024)
         return fail(LOOMHIP_DECLINED, "token_frame: context %zu exceeds the merge's LDS", m->ctx_len);
@@ -1060,35 +1127,40 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         // once per head in their own launch (the attention is then
         // throughput-bound and the fused prologue would repeat per chunk)
         const bool fuse_rope = n <= ATT_FUSE_MAX_LANES;
+        // FAST with rope done apart and an MFMA head size: the attention takes
+        // its query operands pre-split and its keys straight from HBM
+        const bool direct = !parity && !fuse_rope && D.hd % 32 == 0;
+        uint16_t *qsplit = direct ? w.qsplit : nullptr;
         if (!fuse_rope) {
             hipLaunchKernelGGL(qk_rope_kernel, dim3(D.n_heads + D.n_kv, n), dim3(64), 0, st, D, w.q, w.k, w.v,
-                               l.q_norm, l.k_norm, pos, (int)li, rope_cs, w.qrot, k_cache, v_cache);
+                               l.q_norm, l.k_norm, pos, (int)li, rope_cs, w.qrot, qsplit, k_cache, v_cache);
             note_launch();
         }
         const float *qin = fuse_rope ? w.q : w.qrot;
         int ph = prof_begin(LOOMHIP_KT_ATTN, st);
         const dim3 agrid(n_chunks, D.n_kv, n);
+        const size_t lds_a = direct ? att_lds_direct : att_lds;
         if (D.hd == 128)
-            hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
+            hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(64 * ATT_WAVES), lds_a, st, D, qin, w.k, w.v,
                                l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
-                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
+                               parity ? 0 : 1, fuse_rope ? 1 : 0, qsplit, w.part);
         else if (D.hd == 64)
-            hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
+            hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(64 * ATT_WAVES), lds_a, st, D, qin, w.k, w.v,
                                l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
-                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
+                               parity ? 0 : 1, fuse_rope ? 1 : 0, qsplit, w.part);
         else
-            hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
+            hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(64 * ATT_WAVES), lds_a, st, D, qin, w.k, w.v,
                                l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
-                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
+                               parity ? 0 : 1, fuse_rope ? 1 : 0, qsplit, w.part);
         prof_end(ph, st);
         note_launch();
         const int qb_o = act_block(l.wo_t);
         if (qb_o == 256)
             hipLaunchKernelGGL(attn_combine_kernel<256>, dim3((D.qd + 255) / 256, n), dim3(1024), cmb_lds, st,
-                               D, w.part, pos, n_chunks, w.qa_att);
+                               D, w.part, pos, n_chunks, direct ? 1 : 0, w.qa_att);
         else
             hipLaunchKernelGGL(attn_combine_kernel<32>, dim3((D.qd + 255) / 256, n), dim3(1024), cmb_lds, st,
-                               D, w.part, pos, n_chunks, w.qa_att);
+                               D, w.part, pos, n_chunks, direct ? 1 : 0, w.qa_att);
         note_launch();
         if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_QKV, true))
             return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
