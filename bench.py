@@ -65,6 +65,10 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cache", action="store_true", help="skip the config-5 expert-cache streaming run")
     ap.add_argument("--cache-steps", type=int, default=1024, help="config-5 decode steps at batch 1")
+    ap.add_argument("--sweep", action="store_true",
+                    help="config 2 instead: the dequant-fused matvec alone, GB/s per type x shape x vectors")
+    ap.add_argument("--moe-layer", action="store_true",
+                    help="config 3 instead: one MoE layer at token batches 1, 8, 32 and 128")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="first copy MB megabytes device to device three times: the known-size kernel that "
                          "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -120,7 +124,8 @@ def bench_batch(dm, b, args):
     dec.pos.fill_(args.ctx)
     be.profileKernels(True)
     distinct = []
-    for _ in range(min(args.steps, 6)):
+    prof_steps = min(args.steps, 6)
+    for _ in range(prof_steps):
         torch.cuda._sleep(50_000_000)
         dec.step()
         torch.cuda.synchronize()
@@ -132,11 +137,13 @@ def bench_batch(dm, b, args):
     del dec, graph
     torch.cuda.empty_cache()
     return dict(ms=ms, wall_ms=wall / args.steps * 1e3, tok_s=b * 1e3 / ms, stats=stats,
-                distinct=float(np.mean(distinct)))
+                distinct=float(np.mean(distinct)), prof_steps=prof_steps)
 
 
-def per_launch_bytes(name, b, ctx, distinct, layers):
-    """Algorithmic HBM bytes of one launch of the tagged kernel."""
+def per_launch_bytes(name, b, ctx, distinct, layers, per_layer=2.0):
+    """Algorithmic HBM bytes of one launch of the tagged kernel (per_layer:
+    launches of the tag per layer, for the attention matrices: q/k/v + wo,
+    or q, k, v and wo apart from 16 lanes)."""
     if name == "gate_up":
         return distinct * 2 * GATE_BYTES
     if name == "down":
@@ -146,7 +153,7 @@ def per_launch_bytes(name, b, ctx, distinct, layers):
     if name == "head":
         return HEAD_BYTES
     if name == "qkvo":
-        return ATTN_W_BYTES / 2  # two launches per layer: q/k/v, then wo
+        return ATTN_W_BYTES / per_layer
     return 0
 
 
@@ -167,10 +174,12 @@ def roofline(r, b, ctx, layers):
     dom = max(stats, key=lambda k: stats[k]["ms"])
     s = stats[dom]
     avg_s = s["ms"] / s["count"] / 1e3
-    byts = per_launch_bytes(dom, b, ctx, r["distinct"], layers)
+    def pl(k):  # launches of tag k per layer in the profiled steps
+        return stats[k]["count"] / (layers * r["prof_steps"])
+    byts = per_launch_bytes(dom, b, ctx, r["distinct"], layers, pl(dom))
     achieved = byts / avg_s / 1e9
     per_kernel = {k: {"avg_us": round(v["ms"] / v["count"] * 1e3, 2), "launches": v["count"],
-                      "GBs": round(per_launch_bytes(k, b, ctx, r["distinct"], layers)
+                      "GBs": round(per_launch_bytes(k, b, ctx, r["distinct"], layers, pl(k))
                                    / (v["ms"] / v["count"] / 1e3) / 1e9, 1)}
                   for k, v in stats.items()}
     return {"bound": "hbm", "kernel": s["name"], "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
@@ -230,6 +239,155 @@ def cpu_baseline(seconds, threads, ctx):
             "sample": f"{n_tok} tokens of a 2-layer model at the config-4 shapes with the full "
                       f"151936-row head against a {ctx}-token fp16 context ({t2 * 1e3:.1f} ms/token; "
                       f"head {th * 1e3:.1f} ms over {n_head} runs), scaled to {N_LAYERS} layers"}
+
+
+SWEEP_TYPES = (("Q4_0", 2), ("Q8_0", 8), ("Q4_K", 12), ("Q6_K", 14))
+SWEEP_SHAPES = ((2048, 2048), (4096, 4096), (768, 2048))  # rows (out) x cols (in)
+SWEEP_N = (1, 4, 16)
+RING_BYTES = 1 << 30  # distinct weight copies per (type, shape): 4x the 256 MB MALL
+
+
+def bench_sweep(args):
+    """Config 2: the dequant-fused matvec alone.  Per (type, shape) a ring of
+    >= 1 GB of distinct weight copies is rotated launch by launch; HIP events
+    around each matvec launch (the library's tagged timing) give its mean time
+    in each of 5 rounds, the median round is reported; GB/s = weight bytes /
+    time.  The CPU leg times the oracle's matvec on the host cores at n = 1."""
+    import torch
+
+    from loom_amd import backend as be
+    from loom_amd import plane_bytes
+
+    rows_out = []
+    for tname, t in SWEEP_TYPES:
+        for rows, cols in SWEEP_SHAPES:
+            pb = plane_bytes(t, rows, cols)
+            copies = max(4, -(-RING_BYTES // pb))
+            w = be.repack_dev(t, be.synth_ggml_dev(t, rows, cols, copies, 17 + t, 0.02), rows, cols, copies)
+            for n in SWEEP_N:
+                x = torch.randn(n, cols, device="cuda")
+                out = torch.empty(n, rows, device="cuda")
+                planes = [w[i * pb:(i + 1) * pb] for i in range(copies)]
+                for pl in planes:  # warm: every copy once
+                    be.matvec_dev(t, out, pl, x, n, rows, cols)
+                torch.cuda.synchronize()
+                rounds = []
+                for _ in range(5):
+                    be.profileKernels(True)
+                    for pl in planes:
+                        be.matvec_dev(t, out, pl, x, n, rows, cols)
+                    torch.cuda.synchronize()
+                    st = be.kernelStats()["dense"]
+                    be.profileKernels(False)
+                    rounds.append(st["ms"] / st["count"])
+                ms = float(np.median(rounds))
+                rows_out.append({"type": tname, "rows": rows, "cols": cols, "n": n, "weight_bytes": pb,
+                                 "us": round(ms * 1e3, 2), "GBs": round(pb / (ms / 1e3) / 1e9, 1),
+                                 "frac": round(pb / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4), "ring_copies": copies})
+                log(f"sweep {tname} {rows}x{cols} n={n}: {ms * 1e3:.2f} us, {rows_out[-1]['GBs']} GB/s")
+            del w, planes
+            torch.cuda.empty_cache()
+    cpu = None
+    if not args.no_cpu:
+        cpu = sweep_cpu(args)
+    return {"metric": "dequant-fused matvec GB/s of weight bytes (config 2)", "unit": "GB/s", "n_gpus": 1,
+            "peak_GBs": HBM_PEAK_GBS, "data": "synthetic", "dtype": "int8",
+            "config": {"workload": "config 2: weights N(0, 0.02) quantized with the GGUF rule, x ~ N(0, 1), "
+                                   "each (type, shape) a ring of >= 1 GB of distinct copies rotated per launch"},
+            "results": rows_out, "cpu_baseline": cpu}
+
+
+def sweep_cpu(args):
+    """The oracle's matvec (the reference's int8-activation kernels) on the
+    host cores at n = 1 for the 4096 x 4096 shape of each type."""
+    import oracle as o
+    from loom_amd import ggml_bytes
+
+    o.build()
+    threads = args.cpu_threads or max(1, min(16, (os.cpu_count() or 2) - 2))
+    rng = np.random.default_rng(5)
+    out = []
+    with o.Pool(threads):
+        for tname, t in SWEEP_TYPES:
+            rows, cols = 4096, 4096
+            nbytes = ggml_bytes(t, rows, cols)
+            w = o.quantize(t, o.normal(rows * cols, 91 + t, 0.0, 0.02).reshape(rows, cols))
+            x = rng.standard_normal(cols).astype(np.float32)
+            o.matvec(t, w, x, rows, cols)
+            t0 = time.perf_counter()
+            k = 0
+            while time.perf_counter() - t0 < max(0.5, args.cpu_seconds / 8):
+                o.matvec(t, w, x, rows, cols)
+                k += 1
+            sec = (time.perf_counter() - t0) / k
+            out.append({"type": tname, "rows": rows, "cols": cols, "n": 1, "ms": round(sec * 1e3, 3),
+                        "GBs": round(nbytes / sec / 1e9, 2)})
+    return {"unit": "GB/s", "cores": threads, "kind": "port", "results": out,
+            "sample": "the oracle's matvec, 4096 x 4096 per type at n = 1"}
+
+
+def bench_moe_layer(args):
+    """Config 3: one MoE layer (hidden 2048, 128 experts top-8, ffn 768, Q4_K
+    gate/up, Q6_K down, f32 router N(0, 1/sqrt(2048)) with a Zipf(1.1) logit
+    bias) at token batches 1, 8, 32, 128; 3 distinct layer copies (~1.2 GB)
+    rotated per call.  Bytes = distinct experts x 3,059,712 + the router."""
+    import torch
+
+    from loom_amd import COMBINE_EXPERT_ASC, COMBINE_SELECTION, Q4_K, Q6_K
+    from loom_amd import backend as be
+
+    E, D, F, K = N_EXPERT, DIM, 768, TOP_K
+    layers = []
+    for c in range(3):
+        gate = be.repack_dev(Q4_K, be.synth_ggml_dev(Q4_K, F, D, E, 300 + 10 * c, 0.02), F, D, E)
+        up = be.repack_dev(Q4_K, be.synth_ggml_dev(Q4_K, F, D, E, 301 + 10 * c, 0.02), F, D, E)
+        down = be.repack_dev(Q6_K, be.synth_ggml_dev(Q6_K, D, F, E, 302 + 10 * c, 0.02), D, F, E)
+        g = torch.Generator(device="cuda").manual_seed(400 + c)
+        router = (torch.randn(E, D, generator=g, device="cuda") / np.sqrt(D)).contiguous()
+        ranks = torch.randperm(E, generator=g, device="cuda").float() + 1
+        z = -1.1 * torch.log(ranks)
+        bias = (z - z.mean()).contiguous()
+        layers.append((be.MoeLayer(D, F, E, K, router, gate, up, down, Q4_K, Q4_K, Q6_K, router_bias=bias),
+                       (gate, up, down, router, bias)))
+    res = []
+    for b in (1, 8, 32, 128):
+        g = torch.Generator(device="cuda").manual_seed(b)
+        xs = [torch.randn(b, D, generator=g, device="cuda") for _ in range(3)]
+        out = torch.zeros(b, D, device="cuda")
+        ids = torch.zeros(b, K, dtype=torch.int32, device="cuda")
+        comb = COMBINE_SELECTION if b == 1 else COMBINE_EXPERT_ASC
+        for i in range(6):
+            layers[i % 3][0](xs[i % 3], out, comb)
+        torch.cuda.synchronize()
+        n_calls = max(30, args.steps)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for i in range(n_calls):
+            layers[i % 3][0](xs[i % 3], out, comb)
+        ev1.record()
+        torch.cuda.synchronize()
+        ms = ev0.elapsed_time(ev1) / n_calls
+        distinct = []
+        for c in range(3):
+            layers[c][0](xs[c], out, comb, ids=ids)
+            torch.cuda.synchronize()
+            distinct.append(len(np.unique(ids.cpu().numpy())))
+        dist = float(np.mean(distinct))
+        byts = dist * (2 * GATE_BYTES + DOWN_BYTES) + ROUTER_BYTES
+        gbs = byts / (ms / 1e3) / 1e9
+        flops = b * K * 9_437_184 + b * 524_288
+        res.append({"batch": b, "us_per_layer": round(ms * 1e3, 2), "tok_s": round(b / (ms / 1e3), 1),
+                    "distinct_experts": round(dist, 1), "bytes": int(byts), "GBs": round(gbs, 1),
+                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "flops": flops,
+                    "TFLOPs": round(flops / (ms / 1e3) / 1e12, 2),
+                    "path": "decode kernels" if b <= 4 else "grouped matrix-core matmul" if b >= 16 else
+                            "grouped matvec"})
+        log(f"moe layer batch {b}: {ms * 1e3:.2f} us, {dist:.1f} distinct experts, {gbs:.0f} GB/s")
+    return {"metric": "one MoE layer: us per layer and GB/s of distinct expert bytes (config 3)", "n_gpus": 1,
+            "peak_GBs": HBM_PEAK_GBS, "data": "synthetic", "dtype": "int8",
+            "config": {"workload": "config 3: hidden 2048, 128 experts top-8, ffn 768, Q4_K gate/up, Q6_K "
+                                   "down, f32 router with a Zipf(1.1) logit bias; 3 layer copies rotated"},
+            "results": res}
 
 
 C5_DIM, C5_FFN, C5_E, C5_K, C5_SLOTS = 7168, 2048, 256, 8, 64
@@ -366,6 +524,10 @@ def main():
     from loom_amd.frame import DeviceModel, qwen3_30b_a3b
 
     loom_amd.init(0)
+    if args.sweep or args.moe_layer:
+        line = bench_sweep(args) if args.sweep else bench_moe_layer(args)
+        print(json.dumps(line), flush=True)
+        return
     if args.copy_probe:
         src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device="cuda").fill_(1)
         dst = torch.empty_like(src)

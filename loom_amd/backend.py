@@ -133,12 +133,15 @@ def profileKernels(enable: bool) -> None:
 
 
 _KERNEL_SYMBOLS = {
-    "gate_up": "moe_gateup_decode_kernel (n <= 4) / dmmv_kernel<T, NT, FUSED=true> (grouped gate/up + SwiGLU)",
-    "down": "moe_down_decode_kernel (n <= 4) / dmmv_kernel<T, NT, FUSED=false> (grouped down)",
-    "dense": "dmmv_kernel<T, NT, false> (dense matvec)",
+    "gate_up": "moe_gateup_decode_kernel (n <= 4) / dmmv_kernel<T, NT, FUSED=true> / from 16 tokens "
+               "mmq_kernel<T, 1, FUSED=true, SBW> (grouped gate/up + SwiGLU)",
+    "down": "moe_down_decode_kernel (n <= 4) / dmmv_kernel<T, NT, FUSED=false> / from 16 tokens "
+            "mmq_kernel<T, 1, false, SBW> (grouped down)",
+    "dense": "dmmv_kernel<T, NT, false> / from 16 vectors mmq_kernel<T, MT, false, SBW> (dense matvec)",
     "attn": "attn_partial_kernel (attention over the fp16 K/V cache)",
-    "head": "dmmv_kernel<T, NT, false> (output head)",
-    "qkvo": "dmmv_kernel<T, NT, false> (q, k, v, wo)",
+    "head": "dmmv_kernel<T, NT, false> / from 16 lanes mmq_stream_kernel<T, MT, false> (output head)",
+    "qkvo": "dmmv_seg_kernel<NT> + dmmv_kernel<T, NT, false> / from 16 lanes mmq_kernel<T, 2, false, SBW> "
+            "(q, k, v, wo)",
 }
 
 
