@@ -983,12 +983,18 @@ static bool frame_qkv(const loomhip_layer &l, const FrameDims &D, const FrameWs 
     sp.seg[1] = DmmvSeg{(const uint8_t *)l.wk, l.wk_t, D.kvd, w.k, 0, 0};
     sp.seg[2] = DmmvSeg{(const uint8_t *)l.wv, l.wv_t, D.kvd, w.v, 0, 0};
     sp.n_seg = 3;
-    // from MMQ_MIN_TOK lanes: the matrix cores, one launch per matrix
+    // from MMQ_MIN_TOK lanes: the matrix cores, the three matrices in one
+    // launch, lanes in groups of 32
     if (use_mmq(l.wq_t, D.dim, (int)n, 32, false) && use_mmq(l.wk_t, D.dim, (int)n, 32, false) &&
-        use_mmq(l.wv_t, D.dim, (int)n, 32, false))
-        return frame_matvec(l.wq_t, l.wq, D.qd, D.dim, w, n, w.qa_dim, w.q, 0, st, LOOMHIP_KT_QKV, true) &&
-               frame_matvec(l.wk_t, l.wk, D.kvd, D.dim, w, n, w.qa_dim, w.k, 0, st, LOOMHIP_KT_QKV, true) &&
-               frame_matvec(l.wv_t, l.wv, D.kvd, D.dim, w, n, w.qa_dim, w.v, 0, st, LOOMHIP_KT_QKV, true);
+        use_mmq(l.wv_t, D.dim, (int)n, 32, false)) {
+        DmmvSegParams mp = sp;
+        mp.base.ident_n = (int)n;
+        const int ph = prof_begin(LOOMHIP_KT_QKV, st);
+        const bool ok = launch_mmq_seg(mp, st);
+        prof_end(ph, st);
+        if (ok)
+            return true;
+    }
     const int ph = prof_begin(LOOMHIP_KT_QKV, st);
     const bool ok = launch_dmmv_seg(w.nt, sp, st);
     prof_end(ph, st);

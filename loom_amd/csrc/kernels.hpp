@@ -82,6 +82,7 @@ bool launch_dmmv(int t, int nt, bool fused, const DmmvParams &p, hipStream_t st)
 // type or the LDS need is not served.
 bool mmq_supported(int t, int cols, int max_tok, bool fused);
 bool launch_mmq(int t, int max_tok, bool fused, const DmmvParams &p, hipStream_t st);
+bool launch_mmq_seg(DmmvSegParams sp, hipStream_t st);
 // Rows per wave chosen for a launch of `rows` rows x `groups` groups.
 int dmmv_pick_rpw(int t, int cols, int rows, int groups, int nt, bool fused);
 size_t dmmv_lds_bytes(int t, int cols, int nt, bool fused, int rpw);

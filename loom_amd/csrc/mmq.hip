@@ -212,28 +212,28 @@ struct MmqOps {
 // weights first, before its first MFMA.  The values meet in LDS; every output
 // sums its blocks in block order (the reference's `acc += r`), SwiGLU(gate,
 // up) when FUSED, and is stored or added.
+// The work group's part of mmq_kernel: row tile bx, group by.
 template <int T, int MT, bool FUSED, int SBW>
-__global__ __launch_bounds__(64 * MMQ_WAVES) void mmq_kernel(DmmvParams p, int RG, int KS) {
-    extern __shared__ __align__(16) float part[];
+__device__ __forceinline__ void mmq_body(const DmmvParams &p, int bx, int by, int RG, int KS, float *part) {
     constexpr int TOK = 16 * MT;
     const bool ident = p.ident_n > 0;
     DmmvGroup grp;
     if (ident) {
         grp.plane = 0;
-        grp.first = (int)blockIdx.y * TOK;
+        grp.first = by * TOK;
         grp.n = min(TOK, p.ident_n - grp.first);
     } else {
         const int ng = p.n_groups_dev ? *p.n_groups_dev : p.n_groups;
-        if ((int)blockIdx.y >= ng)
+        if (by >= ng)
             return;
-        grp = p.groups[blockIdx.y];
+        grp = p.groups[by];
     }
     const int n = grp.n, cols = p.cols, nb = cols / 256;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ln = threadIdx.x & 63;
     const int r16 = ln & 15, q4 = ln >> 4;
     const int rg = wave % RG, ks = wave / RG;
     const int R = 16 * RG, RS = R + 1;
-    const int row0 = blockIdx.x * R;
+    const int row0 = bx * R;
     const int rl = 16 * rg + r16;
     const int row = min(row0 + rl, p.rows - 1);
     const size_t U = (size_t)p.rows * nb;
@@ -333,6 +333,33 @@ __global__ __launch_bounds__(64 * MMQ_WAVES) void mmq_kernel(DmmvParams p, int R
             v = (first ? old0 : *o) + v;
         *o = v;
     }
+}
+
+template <int T, int MT, bool FUSED, int SBW>
+__global__ __launch_bounds__(64 * MMQ_WAVES) void mmq_kernel(DmmvParams p, int RG, int KS) {
+    extern __shared__ __align__(16) float part[];
+    mmq_body<T, MT, FUSED, SBW>(p, blockIdx.x, blockIdx.y, RG, KS, part);
+}
+
+// Up to DMMV_MAX_SEG matrices (Q4_K or Q6_K, same columns, same lane groups)
+// in one launch: the row tiles of the segments one after another along x.
+template <int MT, int SBW>
+__global__ __launch_bounds__(64 * MMQ_WAVES) void mmq_seg_kernel(DmmvSegParams sp, int RG, int KS) {
+    extern __shared__ __align__(16) float part[];
+    int tile = blockIdx.x, s = 0;
+    while (s + 1 < sp.n_seg && tile >= sp.seg[s].tiles) {
+        tile -= sp.seg[s].tiles;
+        s++;
+    }
+    DmmvParams p = sp.base;
+    p.w = sp.seg[s].w;
+    p.rows = sp.seg[s].rows;
+    p.out = sp.seg[s].out;
+    p.out_stride = sp.seg[s].rows;
+    if (sp.seg[s].t == LH_Q4_K)
+        mmq_body<LH_Q4_K, MT, false, SBW>(p, tile, blockIdx.y, RG, KS, part);
+    else
+        mmq_body<LH_Q6_K, MT, false, SBW>(p, tile, blockIdx.y, RG, KS, part);
 }
 
 // Streaming variant for one super-block per wave (nb <= MMQ_WAVES): a work
@@ -514,6 +541,41 @@ static void mmq_launch_t(const DmmvParams &p, int rg, int ks, int sbw, hipStream
         hipLaunchKernelGGL((mmq_kernel<T, MT, FUSED, 2>), grid, block, lds, st, p, rg, ks);
     else if constexpr (MT == 1)
         hipLaunchKernelGGL((mmq_kernel<T, MT, FUSED, 4>), grid, block, lds, st, p, rg, ks);
+}
+
+// Segments of Q4_K / Q6_K matrices over the same columns, lane groups of
+// up to 32 (identity pairs, sp.base.ident_n set); declined (false) when a
+// segment's type or the shape is not served.
+bool launch_mmq_seg(DmmvSegParams sp, hipStream_t st) {
+    const DmmvParams &p = sp.base;
+    if (p.ident_n < 1 || sp.n_seg < 1 || sp.n_seg > DMMV_MAX_SEG)
+        return false;
+    const int mt = p.ident_n > 16 ? 2 : 1;
+    int rg = MMQ_WAVES, ks = 0, sbw = 0, tiles = 0;
+    for (int i = 0; i < sp.n_seg; i++) {
+        if ((sp.seg[i].t != LH_Q4_K && sp.seg[i].t != LH_Q6_K) || !mmq_supported(sp.seg[i].t, p.cols, 16 * mt, false))
+            return false;
+        int r, k, b;
+        if (!mmq_shape(sp.seg[i].rows, p.cols, mt, false, r, k, b))
+            return false;
+        if (r < rg)
+            rg = r;
+        ks = k;
+        sbw = b;
+    }
+    if (sbw > 2)
+        return false;
+    for (int i = 0; i < sp.n_seg; i++) {
+        sp.seg[i].tiles = (sp.seg[i].rows + 16 * rg - 1) / (16 * rg);
+        tiles += sp.seg[i].tiles;
+    }
+    const size_t lds = mmq_lds_bytes(p.cols, mt, rg, false);
+    const dim3 grid(tiles, (p.ident_n + 16 * mt - 1) / (16 * mt)), block(64 * rg * ks);
+    auto kern = mt == 1 ? (sbw == 1 ? mmq_seg_kernel<1, 1> : mmq_seg_kernel<1, 2>)
+                        : (sbw == 1 ? mmq_seg_kernel<2, 1> : mmq_seg_kernel<2, 2>);
+    hipLaunchKernelGGL(kern, grid, block, lds, st, sp, rg, ks);
+    note_launch();
+    return true;
 }
 
 // Groups of at most max_tok (<= 32) tokens (with p.ident_n: max_tok sets
