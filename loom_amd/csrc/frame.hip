@@ -315,6 +315,7 @@ __device__ __forceinline__ float dot_f32_key(const float *a, const uint16_t *kro
 // l[G], o[G][HD].
 constexpr int ATT_WAVES = 8;
 constexpr size_t ATT_FUSE_MAX_LANES = 4; // lanes up to which rope/append run inside the attention
+constexpr int ATT_TC_DIRECT = 128;         // positions per work group of attn_direct_kernel
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -691,6 +692,170 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
     }
 }
 
+// ---- attention, FAST with rope done apart (more than ATT_FUSE_MAX_LANES lanes) -------
+// Work group (chunk of TC positions, KV head, lane), 8 waves.  Wave w scores
+// positions 16w + 16*8*i .. (TC/16 tiles over the 8 waves) on the matrix cores
+// from keys loaded straight from HBM into the MFMA operands and the queries
+// pre-split into (f16 hi, f16 lo) by qk_rope_kernel; every thread stages its
+// share of the values into LDS meanwhile.  Then p = exp(s - m) against the
+// chunk max of each head (hardware exp: FAST numerics), the chunk sums, and
+// O = P V with p split the same way, wave w taking columns 16w..16w+15.
+// Record per (lane, KV head, chunk): m[G], l[G], o[G][HD] unnormalised.
+template <int HD, int TC>
+__global__ __launch_bounds__(64 * ATT_WAVES) void attn_direct_kernel(FrameDims D, const uint16_t *__restrict__ kc,
+                                                                     const uint16_t *__restrict__ vc,
+                                                                     const int32_t *__restrict__ pos, int li,
+                                                                     int n_chunks,
+                                                                     const uint16_t *__restrict__ qsplit,
+                                                                     float *__restrict__ part) {
+    static_assert(HD % 32 == 0 && (TC == 64 || TC % 128 == 0), "MFMA head size; 64 or a multiple of 128 positions");
+    extern __shared__ __align__(16) float smem[];
+    constexpr int VS = HD + 2;                      // padded value row (halves)
+    constexpr int PR = HD / 8;                      // 16-byte pieces per row
+    constexpr int NPW = (TC * PR + 511) / 512;      // value pieces per thread
+    constexpr int NK = HD / 32;
+    constexpr int NT = TC / 16 / ATT_WAVES > 0 ? TC / 16 / ATT_WAVES : 1; // score tiles per wave
+    constexpr int SW = TC / 16 < ATT_WAVES ? TC / 16 : ATT_WAVES;        // waves that score
+    const int ch = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+    const int G = D.n_heads / D.n_kv;
+    const int p = min(pos[t], D.ctx - 1);
+    const int t0 = ch * TC, nt = min(TC, p + 1 - t0);
+    if (nt <= 0)
+        return; // past the current position: the merge reads no record from here
+    float *sc = smem;                              // [16][TC] f32: p of head g, position j
+    uint16_t *vs = (uint16_t *)(sc + 16 * TC);     // [TC][VS]
+    __shared__ float red[2][ATT_WAVES][16];
+    const int wave = tid >> 6, ln = tid & 63;
+    const int r16 = ln & 15, q4 = ln >> 4;
+    const size_t row0 = (((size_t)t * D.n_layers + li) * D.ctx + t0) * D.kvd + (size_t)kvh * HD;
+    const bool hrow = r16 < G;
+    const bool scorer = wave < SW;
+    // 1. the loads: keys and split queries (scoring waves), values (all)
+    half8_t kb[NT][NK], qh[NK], ql[NK];
+    if (scorer) {
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            const int j = 16 * (wave + ATT_WAVES * i) + r16;
+            const uint16_t *kr = kc + row0 + (size_t)min(j, nt - 1) * D.kvd + 8 * q4;
+#pragma unroll
+            for (int kk = 0; kk < NK; kk++)
+                kb[i][kk] = *(const half8_t *)(kr + 32 * kk);
+        }
+        const size_t qo = (size_t)t * D.qd + ((size_t)kvh * G + min(r16, G - 1)) * HD + 8 * q4;
+        const size_t nq = (size_t)gridDim.z * D.qd;
+        const half8_t zh = {};
+#pragma unroll
+        for (int kk = 0; kk < NK; kk++) {
+            qh[kk] = hrow ? *(const half8_t *)(qsplit + qo + 32 * kk) : zh;
+            ql[kk] = hrow ? *(const half8_t *)(qsplit + nq + qo + 32 * kk) : zh;
+        }
+    }
+    uint4 pv[NPW];
+#pragma unroll
+    for (int u = 0; u < NPW; u++) {
+        const int i = tid + 512 * u;
+        pv[u] = *(const uint4 *)(vc + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR));
+    }
+    // 2. scores and the chunk max per head
+    float sv[NT][4];
+    if (scorer) {
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            const int j = 16 * (wave + ATT_WAVES * i) + r16;
+            f32x4_t a = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kk = 0; kk < NK; kk++) {
+                a = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[kk], kb[i][kk], a, 0, 0, 0);
+                a = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[kk], kb[i][kk], a, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                sv[i][r] = j < nt ? a[r] * D.scale : -INFINITY;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float m = sv[0][r];
+#pragma unroll
+            for (int i = 1; i < NT; i++)
+                m = fmaxf(m, sv[i][r]);
+            const float v = group16_max(m);
+            if (r16 == 0)
+                red[0][wave][4 * q4 + r] = v;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < NPW; u++) { // values: 4-byte stores into the padded rows
+        const int i = tid + 512 * u;
+        if (i < TC * PR) {
+            uint32_t *vrow = (uint32_t *)(vs + (i / PR) * VS + 8 * (i % PR));
+            vrow[0] = pv[u].x;
+            vrow[1] = pv[u].y;
+            vrow[2] = pv[u].z;
+            vrow[3] = pv[u].w;
+        }
+    }
+    __syncthreads();
+    // 3. p = exp(s - m), the chunk sums
+    float *rec = part + (((size_t)t * D.n_kv + kvh) * n_chunks + ch) * (size_t)G * (HD + 2);
+    if (scorer) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int hh = 4 * q4 + r;
+            float m = red[0][0][hh];
+            for (int w = 1; w < SW; w++)
+                m = fmaxf(m, red[0][w][hh]);
+            float ssum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NT; i++) {
+                const int j = 16 * (wave + ATT_WAVES * i) + r16;
+                const float e = j < nt ? __expf(sv[i][r] - m) : 0.0f;
+                sc[hh * TC + j] = e;
+                ssum = ssum + e;
+            }
+            const float v = group16_sum(ssum);
+            if (r16 == 0)
+                red[1][wave][hh] = v;
+            if (wave == 0 && r16 == 0 && hh < G)
+                rec[hh] = m;
+        }
+    }
+    __syncthreads();
+    if (tid < G) {
+        float l = red[1][0][tid];
+        for (int w = 1; w < SW; w++)
+            l = l + red[1][w][tid];
+        rec[G + tid] = l;
+    }
+    // 4. O columns 16w..16w+15: rows = heads, k = positions
+    if (wave < HD / 16) {
+        const int dcol = 16 * wave + r16;
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks2 = 0; ks2 < TC / 32; ks2++) {
+            const int j = 32 * ks2 + 8 * q4;
+            half8_t b;
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                b[e] = __builtin_bit_cast(_Float16, vs[(j + e) * VS + dcol]);
+            float4 pa = {0.0f, 0.0f, 0.0f, 0.0f}, pb = pa;
+            if (hrow) {
+                pa = *(const float4 *)(sc + r16 * TC + j);
+                pb = *(const float4 *)(sc + r16 * TC + j + 4);
+            }
+            half8_t ahi, alo;
+            split_f16(pa, pb, ahi, alo);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int hh = 4 * q4 + r;
+            if (hh < G)
+                rec[2 * G + hh * HD + dcol] = acc[r];
+        }
+    }
+}
+
 // ---- merge the partials per head, quantize the attention output for wo -------------
 // Work group (256-value slice, lane), 1024 threads: value v = tid % 256 of the
 // slice, chunk quarter cq = tid / 256 (chunks cq, cq+4, ...).  Blocks of QB
@@ -706,7 +871,7 @@ constexpr int CMB_OP = 24; // chunks per quarter held in registers (contexts up 
 template <int QB>
 __global__ __launch_bounds__(1024) void attn_combine_kernel(FrameDims D, const float *__restrict__ part,
                                                             const int32_t *__restrict__ pos,
-                                                            int n_chunks, int merge_one, QAct qa) {
+                                                            int n_chunks, int span, int merge_one, QAct qa) {
     extern __shared__ float cmb[]; // [4][256] quarter sums, then [CMB_NH][n_chunks] weights
     __shared__ float red[4], Ls[CMB_NH];
     const int t = blockIdx.y, tid = threadIdx.x, v = tid & 255, cq = tid >> 8;
@@ -720,7 +885,7 @@ __global__ __launch_bounds__(1024) void attn_combine_kernel(FrameDims D, const f
     const int nh = (min(blockIdx.x * 256 + 255, D.qd - 1)) / hd - h_lo + 1;
     const int kvh = h / G, g = h % G;
     const int p = min(pos[t], D.ctx - 1);
-    const int nc = (p + 1 + ATT_TC - 1) / ATT_TC;
+    const int nc = p / span + 1; // records that hold positions
     const size_t rs = (size_t)G * (hd + 2);
     const float *rec0 = part + ((size_t)t * D.n_kv + kvh) * n_chunks * rs;
     float val;
@@ -1107,7 +1272,7 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     if (att_lds > 64 * 1024)
         return fail(LOOMHIP_DECLINED, "token_frame: attention tile exceeds LDS (%zu B)", att_lds);
     // the direct form keeps p and the values only
-    const size_t att_lds_direct = (size_t)16 * ATT_TC * 4 + (size_t)ATT_TC * (D.hd + 2) * 2;
+    const size_t att_lds_direct = (size_t)16 * ATT_TC_DIRECT * 4 + (size_t)ATT_TC_DIRECT * (D.hd + 2) * 2;
     const size_t cmb_lds = (4 * 256 + (size_t)CMB_NH * n_chunks) * 4;
     if (cmb_lds > 64 * 1024)
         return fail(LOOMHIP_DECLINED, "token_frame: context %zu exceeds the merge's LDS", m->ctx_len);
@@ -1145,8 +1310,19 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         const float *qin = fuse_rope ? w.q : w.qrot;
         int ph = prof_begin(LOOMHIP_KT_ATTN, st);
         const dim3 agrid(n_chunks, D.n_kv, n);
-        const size_t lds_a = direct ? att_lds_direct : att_lds;
-        if (D.hd == 128)
+        const size_t lds_a = att_lds;
+        // records of the merge: chunks of ATT_TC positions, ATT_TC_DIRECT direct
+        const int span = direct ? ATT_TC_DIRECT : ATT_TC;
+        const int n_rec = (int)((m->ctx_len + span - 1) / span);
+        if (direct) {
+            const dim3 dgrid(n_rec, D.n_kv, n);
+            if (D.hd == 128)
+                hipLaunchKernelGGL((attn_direct_kernel<128, ATT_TC_DIRECT>), dgrid, dim3(64 * ATT_WAVES),
+                                   att_lds_direct, st, D, k_cache, v_cache, pos, (int)li, n_rec, qsplit, w.part);
+            else
+                hipLaunchKernelGGL((attn_direct_kernel<64, ATT_TC_DIRECT>), dgrid, dim3(64 * ATT_WAVES),
+                                   att_lds_direct, st, D, k_cache, v_cache, pos, (int)li, n_rec, qsplit, w.part);
+        } else if (D.hd == 128)
             hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(64 * ATT_WAVES), lds_a, st, D, qin, w.k, w.v,
                                l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
                                parity ? 0 : 1, fuse_rope ? 1 : 0, qsplit, w.part);
@@ -1163,10 +1339,10 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         const int qb_o = act_block(l.wo_t);
         if (qb_o == 256)
             hipLaunchKernelGGL(attn_combine_kernel<256>, dim3((D.qd + 255) / 256, n), dim3(1024), cmb_lds, st,
-                               D, w.part, pos, n_chunks, direct ? 1 : 0, w.qa_att);
+                               D, w.part, pos, n_rec, span, direct ? 1 : 0, w.qa_att);
         else
             hipLaunchKernelGGL(attn_combine_kernel<32>, dim3((D.qd + 255) / 256, n), dim3(1024), cmb_lds, st,
-                               D, w.part, pos, n_chunks, direct ? 1 : 0, w.qa_att);
+                               D, w.part, pos, n_rec, span, direct ? 1 : 0, w.qa_att);
         note_launch();
         if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_QKV, true))
             return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
