@@ -342,7 +342,6 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
                                                                       uint16_t *__restrict__ vc,
                                                                       const int32_t *__restrict__ pos, int li,
                                                                       int n_chunks, int use_mfma, int fuse,
-                                                                      const uint16_t *__restrict__ qsplit,
                                                                       float *__restrict__ part) {
     extern __shared__ __align__(16) float smem[];
     constexpr int KS = HD + 8;                 // padded key row (halves)
@@ -365,15 +364,10 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
     // Otherwise qk_rope_kernel did both and qraw holds the rotated queries.
     const bool own = fuse && p_raw >= 0 && p_raw < D.ctx && p_raw >= t0 && p_raw < t0 + ATT_TC;
     const int rp = min(max(p_raw, 0), D.ctx - 1); // rope position
-    // direct (qsplit given: FAST, rope done, MFMA head size): the scores take
-    // their keys from HBM and the split queries from qsplit straight into the
-    // MFMA operands, LDS holds p and the values only, and a one-chunk context
-    // also takes this path (its record is merged like any other)
-    const bool direct = MF && qsplit != nullptr;
-    float *qs = smem;                                      // [G][HD] f32
-    float *sc = direct ? smem : qs + G * HD;               // [16][TC] f32: p of head g, position j
-    uint16_t *ks = (uint16_t *)(sc + 16 * ATT_TC);         // [TC][KS]
-    uint16_t *vs = direct ? ks : ks + ATT_TC * KS;         // [TC][VS]
+    float *qs = smem;                                  // [G][HD] f32
+    float *sc = qs + G * HD;                           // [16][TC] f32: p of head g, position j
+    uint16_t *ks = (uint16_t *)(sc + 16 * ATT_TC);     // [TC][KS]
+    uint16_t *vs = ks + ATT_TC * KS;                   // [TC][VS]
     __shared__ float red[2][4][16];
     __shared__ float kn[HD], sinv[MAX_G + 1];
     const int wave = tid >> 6, ln = tid & 63, half = tid >> 8, ht = tid & 255;
@@ -383,60 +377,13 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
     // half 0: keys and the group's query heads, half 1: values (and the new row)
     const uint16_t *src = half ? vc : kc;
     uint4 pc[NPW];
-    float sv[4]; // MFMA path: this lane's scores (position 16w + r16, heads 4*q4 ..)
-    if (direct && half == 0) {
-        if constexpr (MF) {
-            // scores of positions 16w..16w+15 straight from the operands
-            const int r16 = ln & 15, q4 = ln >> 4, j = 16 * wave + r16;
-            const uint16_t *kr = kc + row0 + (size_t)min(j, nt - 1) * D.kvd + 8 * q4;
-            const size_t qo = (size_t)t * D.qd + ((size_t)kvh * G + min(r16, G - 1)) * HD + 8 * q4;
-            const size_t nq = (size_t)gridDim.z * D.qd;
-            const bool hrow = r16 < G;
-            half8_t kb[HD / 32], qh[HD / 32], ql[HD / 32];
 #pragma unroll
-            for (int kk = 0; kk < HD / 32; kk++) {
-                kb[kk] = *(const half8_t *)(kr + 32 * kk);
-                qh[kk] = *(const half8_t *)(qsplit + qo + 32 * kk);
-                ql[kk] = *(const half8_t *)(qsplit + nq + qo + 32 * kk);
-            }
-            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-            const half8_t zh = {};
-#pragma unroll
-            for (int kk = 0; kk < HD / 32; kk++) {
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(hrow ? qh[kk] : zh, kb[kk], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(hrow ? ql[kk] : zh, kb[kk], acc, 0, 0, 0);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                sv[r] = j < nt ? acc[r] * D.scale : -INFINITY;
-                const float v = group16_max(sv[r]);
-                if (r16 == 0)
-                    red[0][wave][4 * q4 + r] = v;
-            }
-        }
-    } else {
-#pragma unroll
-        for (int u = 0; u < NPW; u++) {
-            const int i = ht + 256 * u;
-            pc[u] = *(const uint4 *)(src + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR));
-        }
+    for (int u = 0; u < NPW; u++) {
+        const int i = ht + 256 * u;
+        pc[u] = *(const uint4 *)(src + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR));
     }
     float vnew = 0.0f;
-    if (direct) {
-        if (half == 1) {
-#pragma unroll
-            for (int u = 0; u < NPW; u++) { // values: 4-byte stores into the padded rows
-                const int i = ht + 256 * u;
-                if (i < ATT_TC * PR) {
-                    uint32_t *vrow = (uint32_t *)(vs + (i / PR) * VS + 8 * (i % PR));
-                    vrow[0] = pc[u].x;
-                    vrow[1] = pc[u].y;
-                    vrow[2] = pc[u].z;
-                    vrow[3] = pc[u].w;
-                }
-            }
-        }
-    } else if (half == 0) {
+    if (half == 0) {
         for (int i = ht; i < G * HD; i += 256)
             qs[i] = qsrc[i];
 #pragma unroll
@@ -462,8 +409,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
             }
         }
     }
-    if (!direct)
-        __syncthreads();
+    __syncthreads();
     if (fuse) {
     // per-head RMSNorm (llama.zig:938-949): PARITY sums the squares in the
     // reference's order, one thread per head; FAST (use_mfma) one wave per
@@ -550,7 +496,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
     }
     float *rec = part + (((size_t)t * D.n_kv + kvh) * n_chunks + ch) * (size_t)G * (HD + 2);
 
-    if (!MF || (single && !direct) || !use_mfma) {
+    if (!MF || single || !use_mfma) {
         const uint16_t *krow = ks + min(ln, nt - 1) * KS;
         for (int g = wave; g < G; g += ATT_WAVES) {
             const float s = ln < nt ? dot_f32_key<HD>(qs + g * HD, krow) * D.scale : -INFINITY;
@@ -609,7 +555,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
 
     if constexpr (MF) {
         const int r16 = ln & 15, q4 = ln >> 4; // tile row/column, k-quarter
-        if (half == 0 && !direct) { // (direct: the scores are in already)
+        float sv[4];
+        if (half == 0) {
             // scores of positions 16w..16w+15
             const int j = 16 * wave + r16;
             const uint16_t *krow = ks + min(j, nt - 1) * KS;
@@ -1310,7 +1257,6 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         const float *qin = fuse_rope ? w.q : w.qrot;
         int ph = prof_begin(LOOMHIP_KT_ATTN, st);
         const dim3 agrid(n_chunks, D.n_kv, n);
-        const size_t lds_a = att_lds;
         // records of the merge: chunks of ATT_TC positions, ATT_TC_DIRECT direct
         const int span = direct ? ATT_TC_DIRECT : ATT_TC;
         const int n_rec = (int)((m->ctx_len + span - 1) / span);
@@ -1323,17 +1269,17 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
                 hipLaunchKernelGGL((attn_direct_kernel<64, ATT_TC_DIRECT>), dgrid, dim3(64 * ATT_WAVES),
                                    att_lds_direct, st, D, k_cache, v_cache, pos, (int)li, n_rec, qsplit, w.part);
         } else if (D.hd == 128)
-            hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(64 * ATT_WAVES), lds_a, st, D, qin, w.k, w.v,
+            hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
                                l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
-                               parity ? 0 : 1, fuse_rope ? 1 : 0, qsplit, w.part);
+                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
         else if (D.hd == 64)
-            hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(64 * ATT_WAVES), lds_a, st, D, qin, w.k, w.v,
+            hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
                                l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
-                               parity ? 0 : 1, fuse_rope ? 1 : 0, qsplit, w.part);
+                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
         else
-            hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(64 * ATT_WAVES), lds_a, st, D, qin, w.k, w.v,
+            hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
                                l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
-                               parity ? 0 : 1, fuse_rope ? 1 : 0, qsplit, w.part);
+                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
         prof_end(ph, st);
         note_launch();
         const int qb_o = act_block(l.wo_t);
