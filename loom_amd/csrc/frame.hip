@@ -1050,10 +1050,12 @@ static FrameWs frame_layout(char *base, size_t n, const loomhip_model *m, size_t
     return w;
 }
 
-// mmq_ok: the matrix cores from MMQ_MIN_TOK lanes on, in groups of 32 lanes.
+// mmq_ok: the matrix cores from MMQ_MIN_TOK lanes on, in groups of mmq_group
+// lanes (16 for wo: more work groups for its 2048 rows; 32 for the head,
+// whose 255 MB would be read once per group).
 static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameWs &w, size_t n,
                          QAct x, float *out, int accumulate, hipStream_t st, int tag = LOOMHIP_KT_QKV,
-                         bool mmq_ok = false) {
+                         bool mmq_ok = false, int mmq_group = 32) {
     DmmvParams p{};
     p.w = (const uint8_t *)wt;
     p.plane_bytes = 0;
@@ -1074,7 +1076,7 @@ static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameW
         p.ident_n = (int)n;
     p.rpw = mq ? 0 : dmmv_pick_rpw(t, cols, rows, w.n_groups, w.nt, false);
     const int ph = prof_begin(tag, st);
-    const bool ok = mq ? launch_mmq(t, 32, false, p, st) : launch_dmmv(t, w.nt, false, p, st);
+    const bool ok = mq ? launch_mmq(t, mmq_group, false, p, st) : launch_dmmv(t, w.nt, false, p, st);
     prof_end(ph, st);
     return ok;
 }
@@ -1096,7 +1098,7 @@ static bool frame_qkv(const loomhip_layer &l, const FrameDims &D, const FrameWs 
     sp.seg[2] = DmmvSeg{(const uint8_t *)l.wv, l.wv_t, D.kvd, w.v, 0, 0};
     sp.n_seg = 3;
     // from MMQ_MIN_TOK lanes: the matrix cores, the three matrices in one
-    // launch, lanes in groups of 32
+    // launch, lanes in groups of 16
     if (use_mmq(l.wq_t, D.dim, (int)n, 32, false) && use_mmq(l.wk_t, D.dim, (int)n, 32, false) &&
         use_mmq(l.wv_t, D.dim, (int)n, 32, false)) {
         DmmvSegParams mp = sp;
@@ -1290,7 +1292,7 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
             hipLaunchKernelGGL(attn_combine_kernel<32>, dim3((D.qd + 255) / 256, n), dim3(1024), cmb_lds, st,
                                D, w.part, pos, n_rec, span, direct ? 1 : 0, w.qa_att);
         note_launch();
-        if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_QKV, true))
+        if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_QKV, true, 16))
             return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
         // FFN block (llama.zig:1203-1224)
         if (l.is_moe) {

@@ -543,14 +543,15 @@ static void mmq_launch_t(const DmmvParams &p, int rg, int ks, int sbw, hipStream
         hipLaunchKernelGGL((mmq_kernel<T, MT, FUSED, 4>), grid, block, lds, st, p, rg, ks);
 }
 
-// Segments of Q4_K / Q6_K matrices over the same columns, lane groups of
-// up to 32 (identity pairs, sp.base.ident_n set); declined (false) when a
-// segment's type or the shape is not served.
+// Segments of Q4_K / Q6_K matrices over the same columns, lanes in groups of
+// 16 (identity pairs, sp.base.ident_n set: twice the work groups of 32-lane
+// groups measured faster for these small matrices at 32 lanes); declined
+// (false) when a segment's type or the shape is not served.
 bool launch_mmq_seg(DmmvSegParams sp, hipStream_t st) {
     const DmmvParams &p = sp.base;
     if (p.ident_n < 1 || sp.n_seg < 1 || sp.n_seg > DMMV_MAX_SEG)
         return false;
-    const int mt = p.ident_n > 16 ? 2 : 1;
+    constexpr int mt = 1;
     int rg = MMQ_WAVES, ks = 0, sbw = 0, tiles = 0;
     for (int i = 0; i < sp.n_seg; i++) {
         if ((sp.seg[i].t != LH_Q4_K && sp.seg[i].t != LH_Q6_K) || !mmq_supported(sp.seg[i].t, p.cols, 16 * mt, false))
@@ -571,8 +572,7 @@ bool launch_mmq_seg(DmmvSegParams sp, hipStream_t st) {
     }
     const size_t lds = mmq_lds_bytes(p.cols, mt, rg, false);
     const dim3 grid(tiles, (p.ident_n + 16 * mt - 1) / (16 * mt)), block(64 * rg * ks);
-    auto kern = mt == 1 ? (sbw == 1 ? mmq_seg_kernel<1, 1> : mmq_seg_kernel<1, 2>)
-                        : (sbw == 1 ? mmq_seg_kernel<2, 1> : mmq_seg_kernel<2, 2>);
+    auto kern = sbw == 1 ? mmq_seg_kernel<mt, 1> : mmq_seg_kernel<mt, 2>;
     hipLaunchKernelGGL(kern, grid, block, lds, st, sp, rg, ks);
     note_launch();
     return true;
