@@ -162,7 +162,7 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
         dp.mode = combine;
         dp.rpw_gu = dmmv_pick_rpw(m.gate_t, (int)m.dim, (int)m.ffn, (int)P, 1, true);
         // down: 4-row tiles unless the token count alone fills the chip
-        int rpw = 1;
+        int rpw = 2;
         while (rpw < 8 && ((int)m.dim / (4 * rpw)) * (int)n >= 1024)
             rpw *= 2;
         while (rpw > 1 && decode_down_lds(m.down_t, (int)m.ffn, (int)m.k, rpw) > 48 * 1024)
