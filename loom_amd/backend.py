@@ -138,10 +138,11 @@ _KERNEL_SYMBOLS = {
     "down": "moe_down_decode_kernel (n <= 4) / dmmv_kernel<T, NT, FUSED=false> / from 16 tokens "
             "mmq_kernel<T, 1, false, SBW> (grouped down)",
     "dense": "dmmv_kernel<T, NT, false> / from 16 vectors mmq_kernel<T, MT, false, SBW> (dense matvec)",
-    "attn": "attn_partial_kernel (attention over the fp16 K/V cache)",
+    "attn": "attn_direct_kernel (FAST numerics, more than 4 lanes) / attn_partial_kernel (attention over "
+            "the fp16 K/V cache)",
     "head": "dmmv_kernel<T, NT, false> / from 16 lanes mmq_stream_kernel<T, MT, false> (output head)",
-    "qkvo": "dmmv_seg_kernel<NT> + dmmv_kernel<T, NT, false> / from 16 lanes mmq_kernel<T, 2, false, SBW> "
-            "(q, k, v, wo)",
+    "qkvo": "dmmv_seg_kernel<NT> + dmmv_kernel<T, NT, false> / from 16 lanes mmq_seg_kernel<1, SBW> (q, k, v) "
+            "+ mmq_kernel<T, 1, false, SBW> (wo)",
 }
 
 
