@@ -843,8 +843,8 @@ __global__ __launch_bounds__(1024) void attn_combine_kernel(FrameDims D, const f
         const float *orow = rec0 + 2 * G + (size_t)g * hd + d;
         float ov[CMB_OP];
 #pragma unroll
-        for (int u = 0; u < CMB_OP; u++)
-            ov[u] = orow[(size_t)min(cq + 4 * u, nc - 1) * rs];
+        for (int u = 0; u < CMB_OP; u++) // cq is uniform per wave: chunks past nc are not requested
+            ov[u] = cq + 4 * u < nc ? orow[(size_t)(cq + 4 * u) * rs] : 0.0f;
         if (wave < nh) {
             const int hw = h_lo + wave, kw = hw / G, gw = hw % G;
             const float *r0 = part + ((size_t)t * D.n_kv + kw) * n_chunks * rs;
