@@ -108,10 +108,13 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(const float *__restrict
     const bool live = c < chunks;
     const int cc = live ? c : chunks - 1;
     const float *xv = x + (size_t)lane_v * dim + (size_t)cc * 32;
-    float4 v[8];
+    float4 v[8], gw[8]; // the norm weights are requested with x, not after the reduction
 #pragma unroll
     for (int i = 0; i < 8; i++)
         v[i] = *(const float4 *)(xv + 4 * i);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        gw[i] = *(const float4 *)(w + (size_t)cc * 32 + 4 * i);
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -152,10 +155,9 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(const float *__restrict
         total = block_sum_waves(wave_sum_f(ss), red);
     }
     const float scale = 1.0f / sqrtf(total / (float)dim + eps);
-    const float *wv = w + (size_t)cc * 32;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const float4 g = *(const float4 *)(wv + 4 * i);
+        const float4 g = gw[i];
         v[i].x = (v[i].x * scale) * g.x;
         v[i].y = (v[i].y * scale) * g.y;
         v[i].z = (v[i].z * scale) * g.z;
