@@ -199,8 +199,27 @@ __global__ __launch_bounds__(64) void qk_rope_kernel(FrameDims D, const float *_
     const float *src = isq ? q + (size_t)t * D.qd + (size_t)h * hd : k + (size_t)t * D.kvd + (size_t)kvh * hd;
     const float *nw = isq ? q_norm : k_norm;
     __shared__ float s_inv;
+    // the position, norm weights, value row and rope entries are requested
+    // up front: none of them waits behind the norm's reduction
+    constexpr int HPT = MAX_HD / 64, RPT = MAX_HD / 128;
+    const int p = pos[t];
+    const int half = D.rope_dim / 2;
+    float nwv[HPT], vv[HPT];
+#pragma unroll
+    for (int u = 0; u < HPT; u++) {
+        const int i = tid + 64 * u;
+        nwv[u] = nw && i < hd ? nw[i] : 0.0f;
+        vv[u] = !isq && i < hd ? v[(size_t)t * D.kvd + (size_t)kvh * hd + i] : 0.0f;
+    }
     for (int i = tid; i < hd; i += 64)
         hv[i] = src[i];
+    const float *csp = rope_cs + (size_t)min(max(p, 0), D.ctx - 1) * half * 2;
+    float2 csv[RPT];
+#pragma unroll
+    for (int u = 0; u < RPT; u++) {
+        const int i = tid + 64 * u;
+        csv[u] = i < half ? make_float2(csp[2 * i], csp[2 * i + 1]) : make_float2(0.0f, 0.0f);
+    }
     if (nw) {
         // headNorm's sum of squares in the reference's order (hd dependent
         // adds on one thread: the normalised heads feed the attention scores
@@ -216,19 +235,24 @@ __global__ __launch_bounds__(64) void qk_rope_kernel(FrameDims D, const float *_
         }
         __syncthreads();
         const float inv = s_inv;
-        for (int i = tid; i < hd; i += 64)
-            hv[i] = (hv[i] * inv) * nw[i];
+#pragma unroll
+        for (int u = 0; u < HPT; u++) {
+            const int i = tid + 64 * u;
+            if (i < hd)
+                hv[i] = (hv[i] * inv) * nwv[u];
+        }
     }
     __syncthreads();
-    const int p = pos[t];
-    const int half = D.rope_dim / 2;
-    const float *csp = rope_cs + (size_t)min(max(p, 0), D.ctx - 1) * half * 2;
-    for (int i = tid; i < half; i += 64) {
-        const float cs = csp[2 * i], sn = csp[2 * i + 1];
-        const int ia = D.rope_neox ? i : 2 * i, ib = D.rope_neox ? i + half : 2 * i + 1;
-        const float a = hv[ia], b = hv[ib];
-        hv[ia] = a * cs - b * sn;
-        hv[ib] = a * sn + b * cs;
+#pragma unroll
+    for (int u = 0; u < RPT; u++) {
+        const int i = tid + 64 * u;
+        if (i < half) {
+            const float cs = csv[u].x, sn = csv[u].y;
+            const int ia = D.rope_neox ? i : 2 * i, ib = D.rope_neox ? i + half : 2 * i + 1;
+            const float a = hv[ia], b = hv[ib];
+            hv[ia] = a * cs - b * sn;
+            hv[ib] = a * sn + b * cs;
+        }
     }
     __syncthreads();
     if (isq) {
@@ -249,10 +273,13 @@ __global__ __launch_bounds__(64) void qk_rope_kernel(FrameDims D, const float *_
     if (p < 0 || p >= D.ctx) // a full cache takes no more rows
         return;
     const size_t base = (((size_t)t * D.n_layers + li) * D.ctx + p) * D.kvd + (size_t)kvh * hd;
-    const float *vs = v + (size_t)t * D.kvd + (size_t)kvh * hd;
-    for (int i = tid; i < hd; i += 64) {
-        kc[base + i] = __half_raw(__float2half(hv[i])).x;
-        vc[base + i] = __half_raw(__float2half(vs[i])).x;
+#pragma unroll
+    for (int u = 0; u < HPT; u++) {
+        const int i = tid + 64 * u;
+        if (i < hd) {
+            kc[base + i] = __half_raw(__float2half(hv[i])).x;
+            vc[base + i] = __half_raw(__float2half(vv[u])).x;
+        }
     }
 }
 
