@@ -678,7 +678,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_partial_kernel(FrameDims 
 // O = P V with p split the same way, wave w taking columns 16w..16w+15.
 // Record per (lane, KV head, chunk): m[G], l[G], o[G][HD] unnormalised.
 template <int HD, int TC>
-__global__ __launch_bounds__(64 * ATT_WAVES) void attn_direct_kernel(FrameDims D, const uint16_t *__restrict__ kc,
+__global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(6))) void attn_direct_kernel(FrameDims D, const uint16_t *__restrict__ kc,
                                                                      const uint16_t *__restrict__ vc,
                                                                      const int32_t *__restrict__ pos, int li,
                                                                      int n_chunks,
