@@ -842,10 +842,10 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
 // issued before the weights are known, and o = (the quarters' sums in order)
 // / L.
 constexpr int CMB_NH = 8;  // heads a 256-value slice can touch (head_dim >= 48)
-constexpr int CMB_OP = 24; // chunks per quarter held in registers (contexts up to 6144 in one pass)
+constexpr int CMB_OP = 16; // chunks per quarter held in registers (64 chunks in one pass; more in a tail loop)
 
 template <int QB>
-__global__ __launch_bounds__(1024) void attn_combine_kernel(FrameDims D, const float *__restrict__ part,
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) void attn_combine_kernel(FrameDims D, const float *__restrict__ part,
                                                             const int32_t *__restrict__ pos,
                                                             int n_chunks, int span, int merge_one, QAct qa) {
     extern __shared__ float cmb[]; // [4][256] quarter sums, then [CMB_NH][n_chunks] weights
