@@ -512,13 +512,15 @@ bool mmq_supported(int t, int cols, int max_tok, bool fused) {
     return mmq_shape(16, cols, (max_tok + 15) / 16, fused, rg, ks, sbw);
 }
 
-// Row tiles per streaming work group: about MMQ_STREAM_WGS work groups, at
-// most MMQ_MAX_NTILE tiles each; 1 = the one-shot kernel.  Streaming serves
-// the lane-group (identity) launches with many row tiles (the head): for the
-// grouped expert launches the one-shot kernel measured faster (its groups
-// already give thousands of short work groups).
-constexpr int MMQ_STREAM_WGS = 512;
-constexpr int MMQ_MAX_NTILE = 8;
+// Streaming serves the lane-group (identity) launches with at least
+// MMQ_STREAM_MIN (row tile, group) pairs (the head): for the grouped expert
+// launches the one-shot kernel measured faster (its groups already give
+// thousands of short work groups).  Its two register sets hold one work
+// group per CU, so the pairs are split over about MMQ_STREAM_WGS work groups
+// (one per CU, no partial second round), at most MMQ_MAX_NTILE tiles each.
+constexpr int MMQ_STREAM_MIN = 1024;
+constexpr int MMQ_STREAM_WGS = 256;
+constexpr int MMQ_MAX_NTILE = 64;
 
 template <int T, int MT, bool FUSED>
 static void mmq_launch_t(const DmmvParams &p, int rg, int ks, int sbw, hipStream_t st) {
@@ -526,7 +528,8 @@ static void mmq_launch_t(const DmmvParams &p, int rg, int ks, int sbw, hipStream
     const int groups = p.ident_n > 0 ? (p.ident_n + 16 * MT - 1) / (16 * MT) : p.n_groups;
     const int tiles = (p.rows + 16 * rg - 1) / (16 * rg);
     if (sbw == 1 && p.ident_n > 0 && 2 * lds <= 64 * 1024) {
-        int ntile = (int)((long)tiles * groups / MMQ_STREAM_WGS);
+        const long pairs = (long)tiles * groups;
+        int ntile = pairs < MMQ_STREAM_MIN ? 1 : (int)((pairs + MMQ_STREAM_WGS - 1) / MMQ_STREAM_WGS);
         ntile = ntile > MMQ_MAX_NTILE ? MMQ_MAX_NTILE : ntile;
         if (ntile > 1) {
             const dim3 grid((tiles + ntile - 1) / ntile, groups), block(64 * rg * ks);
