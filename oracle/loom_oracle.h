@@ -175,6 +175,9 @@ size_t lo_seq_cache_bytes(const lo_model *m);
 int lo_step(const lo_model *m, lo_seq *seq, uint32_t token, float *logits);
 /* Continuous batching (llama.decodeBatch): n lanes, out [n][vocab]. */
 int lo_decode_batch(const lo_model *m, lo_seq *seqs, const uint32_t *tokens, size_t n, float *out);
+/* Test-only planted mistakes in lo_decode_batch (0 = none): 1 cross-lane cache
+ * read, 2 K/V row written at the batch index, 3 rope at lane 0's position. */
+void lo_set_batch_slip(int slip);
 
 /* ---- expert cache bookkeeping (engine/expert_cache.zig:18-148,
  *      core/stats.zig:135-160) ------------------------------------------- */

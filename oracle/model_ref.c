@@ -8,8 +8,12 @@
  * shared experts are absent from every config here and are not restated.
  *
  * Unpinned without running Zig: @exp, @sqrt, std.math.pow, @cos, @sin map to
- * C libm expf, sqrtf, powf, cosf, sinf (sqrtf is exact; the others agree to
- * within an ulp, absorbed by the tolerances of the tests that use them).
+ * C libm sqrtf, powf, cosf, sinf and, for @exp, the once-rounded double
+ * exponential (float)exp((double)x) -- the f32 exponential rounded once from
+ * a double result, which is the correctly rounded value except where the
+ * double lands within an ulp of a float midpoint (about 2^-29 of inputs).
+ * Any libm expf agrees with it to within an ulp; the GPU computes the same
+ * expression, so softmax, SiLU and sigmoid agree bit for bit.
  */
 #include "loom_oracle.h"
 
@@ -18,6 +22,9 @@
 #include <string.h>
 
 /* ---- core/tensor.zig ------------------------------------------------------ */
+
+/* @exp on f32 (tensor.zig:24,31,35): the once-rounded double exponential. */
+static inline float exp_f32(float x) { return (float)exp((double)x); }
 
 /* tensor.zig:9-15 */
 void lo_rmsnorm(float *out, const float *x, const float *w, size_t n, float eps) {
@@ -40,7 +47,7 @@ void lo_softmax(float *x, size_t n) {
         m = fmaxf(m, x[i]);
     float sum = 0.0f;
     for (size_t i = 0; i < n; i++) {
-        x[i] = expf(x[i] - m);
+        x[i] = exp_f32(x[i] - m);
         sum = sum + x[i];
     }
     float inv = 1.0f / sum;
@@ -49,8 +56,8 @@ void lo_softmax(float *x, size_t n) {
 }
 
 /* tensor.zig:30-36 */
-float lo_silu(float x) { return x / (1.0f + expf(-x)); }
-float lo_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+float lo_silu(float x) { return x / (1.0f + exp_f32(-x)); }
+float lo_sigmoid(float x) { return 1.0f / (1.0f + exp_f32(-x)); }
 
 /* tensor.zig:55-57 */
 void lo_swiglu(float *out, const float *g, const float *u, size_t n) {
@@ -305,13 +312,29 @@ static void kv_store(const lo_model *m, void *cache, size_t idx, const float *sr
     }
 }
 
-static void kv_load(const lo_model *m, const void *cache, size_t idx, float *dst, size_t n) {
-    if (m->kv_f16) {
-        const uint16_t *c = (const uint16_t *)cache + idx;
-        for (size_t i = 0; i < n; i++)
-            dst[i] = lo_f16_to_f32(c[i]);
-    } else {
-        memcpy(dst, (const float *)cache + idx, n * sizeof(float));
+/* Widening of fp16 cache values (exact), through a table of all 65536. */
+static float f16_table[65536];
+static int f16_table_ready;
+
+static void f16_table_init(void) {
+    if (f16_table_ready)
+        return;
+    for (uint32_t h = 0; h < 65536; h++)
+        f16_table[h] = lo_f16_to_f32((uint16_t)h);
+    f16_table_ready = 1;
+}
+
+/* n consecutive cache rows of one KV head (hd values at stride kvd) as f32. */
+static void kv_rows(const lo_model *m, const void *cache, size_t idx, size_t rows, size_t kvd, float *dst) {
+    size_t hd = m->head_dim;
+    for (size_t r = 0; r < rows; r++) {
+        if (m->kv_f16) {
+            const uint16_t *c = (const uint16_t *)cache + idx + r * kvd;
+            for (size_t i = 0; i < hd; i++)
+                dst[r * hd + i] = f16_table[c[i]];
+        } else {
+            memcpy(dst + r * hd, (const float *)cache + idx + r * kvd, hd * sizeof(float));
+        }
     }
 }
 
@@ -322,35 +345,48 @@ static void rope_vec(const lo_model *m, float *v, size_t pos) {
         lo_rope_norm(v, m->rope_dim, pos, m->rope_base);
 }
 
+/* Planted-mistake switch for the batch-invariant test (test infrastructure
+ * only; 0 in every other use): 1 = each lane attends over the next lane's
+ * cache, 2 = each lane writes its K/V row at its batch index instead of its
+ * position, 3 = every lane rotates q and k at lane 0's position. */
+static int batch_slip;
+void lo_set_batch_slip(int slip) { batch_slip = slip; }
+
 /* llama.zig:1127-1192: q/k/v for one lane, Q/K norm, rope, KV append and the
- * per-head attention loop, into attn_out. */
-static void attention_lane(const lo_model *m, const lo_layer *l, size_t li, lo_seq *seq, float *q,
-                           float *k, const float *v, float *attn_out, float *scores, float *tmp) {
+ * per-head attention loop, into attn_out.  The lane writes its own cache at
+ * write_pos and reads rows [0, pos] of read_seq's cache (both its own outside
+ * the planted mistakes).  kf/vf hold one KV head's rows widened to f32 (ctx x
+ * head_dim each): every query head of the group reads the same exact values
+ * the reference's f32 cache would hold. */
+static void attention_lane(const lo_model *m, const lo_layer *l, size_t li, lo_seq *seq,
+                           const lo_seq *read_seq, size_t write_pos, size_t rope_pos, float *q, float *k,
+                           const float *v, float *attn_out, float *scores, float *kf, float *vf) {
     size_t hd = m->head_dim, kvd = kv_dim(m), pos = seq->pos;
+    f16_table_init();
     lo_head_norm(q, l->q_norm, m->n_heads, hd, m->eps);
     lo_head_norm(k, l->k_norm, m->n_kv_heads, hd, m->eps);
     for (size_t h = 0; h < m->n_heads; h++)
-        rope_vec(m, q + h * hd, pos);
+        rope_vec(m, q + h * hd, rope_pos);
     for (size_t h = 0; h < m->n_kv_heads; h++)
-        rope_vec(m, k + h * hd, pos);
-    size_t base = (li * m->ctx_len + pos) * kvd;
+        rope_vec(m, k + h * hd, rope_pos);
+    size_t base = (li * m->ctx_len + write_pos) * kvd;
     kv_store(m, seq->k_cache, base, k, kvd);
     kv_store(m, seq->v_cache, base, v, kvd);
     float scale = 1.0f / sqrtf((float)hd);
     size_t q_per_kv = m->n_heads / m->n_kv_heads;
-    for (size_t h = 0; h < m->n_heads; h++) {
-        size_t kvh = h / q_per_kv;
-        const float *qh = q + h * hd;
-        for (size_t t = 0; t <= pos; t++) {
-            kv_load(m, seq->k_cache, (li * m->ctx_len + t) * kvd + kvh * hd, tmp, hd);
-            scores[t] = lo_dot_f32(qh, tmp, hd) * scale;
-        }
-        lo_softmax(scores, pos + 1);
-        float *oh = attn_out + h * hd;
-        memset(oh, 0, hd * sizeof(float));
-        for (size_t t = 0; t <= pos; t++) {
-            kv_load(m, seq->v_cache, (li * m->ctx_len + t) * kvd + kvh * hd, tmp, hd);
-            lo_axpy(oh, tmp, scores[t], hd);
+    for (size_t kvh = 0; kvh < m->n_kv_heads; kvh++) {
+        size_t row0 = (li * m->ctx_len) * kvd + kvh * hd;
+        kv_rows(m, read_seq->k_cache, row0, pos + 1, kvd, kf);
+        kv_rows(m, read_seq->v_cache, row0, pos + 1, kvd, vf);
+        for (size_t h = kvh * q_per_kv; h < (kvh + 1) * q_per_kv; h++) {
+            const float *qh = q + h * hd;
+            for (size_t t = 0; t <= pos; t++)
+                scores[t] = lo_dot_f32(qh, kf + t * hd, hd) * scale;
+            lo_softmax(scores, pos + 1);
+            float *oh = attn_out + h * hd;
+            memset(oh, 0, hd * sizeof(float));
+            for (size_t t = 0; t <= pos; t++)
+                lo_axpy(oh, vf + t * hd, scores[t], hd);
         }
     }
 }
@@ -373,7 +409,8 @@ int lo_step(const lo_model *m, lo_seq *seq, uint32_t token, float *logits) {
     float *x = (float *)malloc(dim * 4), *normed = (float *)malloc(dim * 4);
     float *q = (float *)malloc(qd * 4), *k = (float *)malloc(kvd * 4), *v = (float *)malloc(kvd * 4);
     float *att = (float *)malloc(qd * 4), *proj = (float *)malloc(dim * 4);
-    float *scores = (float *)malloc(m->ctx_len * 4), *tmp = (float *)malloc(hd * 4);
+    float *scores = (float *)malloc(m->ctx_len * 4);
+    float *kf = (float *)malloc(m->ctx_len * hd * 4), *vf = (float *)malloc(m->ctx_len * hd * 4);
     float *g = (float *)malloc(fmax * 4), *u = (float *)malloc(fmax * 4), *a = (float *)malloc(fmax * 4);
     float *acc = (float *)malloc(dim * 4);
     lo_dequant_row(m->embed.ty, x, m->embed.data, token, dim);
@@ -383,7 +420,7 @@ int lo_step(const lo_model *m, lo_seq *seq, uint32_t token, float *logits) {
         mv(&l->wq, q, normed);
         mv(&l->wk, k, normed);
         mv(&l->wv, v, normed);
-        attention_lane(m, l, li, seq, q, k, v, att, scores, tmp);
+        attention_lane(m, l, li, seq, seq, seq->pos, seq->pos, q, k, v, att, scores, kf, vf);
         mv(&l->wo, proj, att);
         lo_add(x, proj, dim);
         lo_rmsnorm(normed, x, l->ffn_norm, dim, m->eps);
@@ -410,7 +447,8 @@ int lo_step(const lo_model *m, lo_seq *seq, uint32_t token, float *logits) {
     free(att);
     free(proj);
     free(scores);
-    free(tmp);
+    free(kf);
+    free(vf);
     free(g);
     free(u);
     free(a);
@@ -435,7 +473,7 @@ int lo_decode_batch(const lo_model *m, lo_seq *seqs, const uint32_t *tokens, siz
     float *bq = (float *)malloc(n * qd * 4), *bk = (float *)malloc(n * kvd * 4);
     float *bv = (float *)malloc(n * kvd * 4), *ba = (float *)malloc(n * qd * 4);
     float *bp = (float *)malloc(n * dim * 4), *scores = (float *)malloc(m->ctx_len * 4);
-    float *tmp = (float *)malloc(hd * 4);
+    float *kf = (float *)malloc(m->ctx_len * hd * 4), *vf = (float *)malloc(m->ctx_len * hd * 4);
     float *bg = (float *)malloc(n * fmax * 4), *bu = (float *)malloc(n * fmax * 4);
     float *bact = (float *)malloc(n * fmax * 4), *normed = (float *)malloc(dim * 4);
     for (size_t t = 0; t < n; t++)
@@ -447,9 +485,13 @@ int lo_decode_batch(const lo_model *m, lo_seq *seqs, const uint32_t *tokens, siz
         lo_matmul(l->wq.ty, bq, l->wq.data, bn, n, l->wq.ne1, l->wq.ne0);
         lo_matmul(l->wk.ty, bk, l->wk.data, bn, n, l->wk.ne1, l->wk.ne0);
         lo_matmul(l->wv.ty, bv, l->wv.data, bn, n, l->wv.ne1, l->wv.ne0);
-        for (size_t t = 0; t < n; t++)
-            attention_lane(m, l, li, &seqs[t], bq + t * qd, bk + t * kvd, bv + t * kvd, ba + t * qd,
-                           scores, tmp);
+        for (size_t t = 0; t < n; t++) {
+            const lo_seq *rs = batch_slip == 1 ? &seqs[(t + 1) % n] : &seqs[t];
+            size_t wp = batch_slip == 2 ? t : seqs[t].pos;
+            size_t rp = batch_slip == 3 ? seqs[0].pos : seqs[t].pos;
+            attention_lane(m, l, li, &seqs[t], rs, wp, rp, bq + t * qd, bk + t * kvd, bv + t * kvd,
+                           ba + t * qd, scores, kf, vf);
+        }
         lo_matmul(l->wo.ty, bp, l->wo.data, ba, n, l->wo.ne1, l->wo.ne0);
         for (size_t t = 0; t < n; t++)
             lo_add(bx + t * dim, bp + t * dim, dim);
@@ -481,7 +523,8 @@ int lo_decode_batch(const lo_model *m, lo_seq *seqs, const uint32_t *tokens, siz
     free(ba);
     free(bp);
     free(scores);
-    free(tmp);
+    free(kf);
+    free(vf);
     free(bg);
     free(bu);
     free(bact);

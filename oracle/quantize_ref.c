@@ -8,7 +8,7 @@
  *    quantize_row_q6_K_ref with make_qx_quants, llama.cpp ggml-quants.c, MIT).
  *    The reference repository contains no Q4_K/Q6_K quantizer and no golden
  *    vectors for one, so these are pinned only by their own round-trip error
- *    bounds (tests/test_oracle_quant.py); every dequant/matvec parity claim is
+ *    bounds (tests/test_oracle_ggml.py); every dequant/matvec parity claim is
  *    defined on whatever bytes they emit.
  *  - splitmix64-based seeded normals/uniforms for synthetic inputs.
  */

@@ -247,3 +247,77 @@ def test_step_planted_mistakes_exceed_the_bound(oracle, arch, slips):
     for slip in slips:
         bad = _rel(got, forward64(oracle, m, tokens, slip)).max()
         assert bad > 10 * BOUND, (slip, bad)
+
+
+# ---- decodeBatch == independent single streams (llama.zig:2323-2389) -------
+
+
+def _batch_vs_single(oracle, m, n, seed, n_steps=4):
+    """Lane k first runs its own prompt of (k % 5) + 1 tokens through lo_step,
+    so the lanes sit at different positions over different contexts; its
+    cache is then copied to a batch lane.  n_steps of lo_decode_batch over all
+    lanes are compared with lo_step on each lane's single stream, fed the
+    same (greedy) tokens.  Returns (worst tolerance ratio, tokens equal)."""
+    o = oracle
+    L = o.lib()
+    vocab = m.c["vocab"]
+    cb = int(L.lo_seq_cache_bytes(C.byref(m.model)))
+    rng = np.random.default_rng(seed)
+    single, bufs = [], []
+    for k in range(n):
+        kb, vb = np.zeros(cb, np.uint8), np.zeros(cb, np.uint8)
+        s = o.Seq(kb.ctypes.data, vb.ctypes.data, 0)
+        lg = np.empty(vocab, np.float32)
+        for tok in rng.integers(0, vocab, (k % 5) + 1):
+            assert L.lo_step(C.byref(m.model), C.byref(s), int(tok), lg.ctypes.data) == 0
+        single.append((s, lg))
+        bufs += [kb, vb]
+    seqs = (o.Seq * n)()
+    copies = []
+    for k in range(n):
+        kb, vb = bufs[2 * k].copy(), bufs[2 * k + 1].copy()
+        copies += [kb, vb]
+        seqs[k].k_cache, seqs[k].v_cache, seqs[k].pos = kb.ctypes.data, vb.ctypes.data, single[k][0].pos
+    assert len({int(seqs[k].pos) for k in range(n)}) == min(n, 5)
+    worst, same = 0.0, True
+    toks = np.array([int(np.argmax(single[k][1])) for k in range(n)], np.uint32)
+    for _ in range(n_steps):
+        got = np.empty((n, vocab), np.float32)
+        assert L.lo_decode_batch(C.byref(m.model), C.cast(seqs, C.c_void_p), toks.ctypes.data, n,
+                                 got.ctypes.data) == 0
+        want = np.empty((n, vocab), np.float32)
+        for k in range(n):
+            assert L.lo_step(C.byref(m.model), C.byref(single[k][0]), int(toks[k]), want[k].ctypes.data) == 0
+        tol = np.maximum(np.abs(want), np.abs(got)) * 1e-3 + 1e-3  # the reference test's bound
+        worst = max(worst, float((np.abs(got - want) / tol).max()))
+        same &= bool(np.array_equal(np.argmax(got, axis=1), np.argmax(want, axis=1)))
+        toks = np.argmax(want, axis=1).astype(np.uint32)
+    return worst, same
+
+
+@pytest.mark.parametrize("arch", ["qwen3moe", "llama"])
+@pytest.mark.parametrize("n", [2, 3, 8, 11])
+def test_decode_batch_equals_single_streams(oracle, arch, n):
+    """lo_decode_batch over n lanes at different positions and contexts
+    equals n independent lo_step streams: every logit within the reference
+    test's max(|w|, |g|)*1e-3 + 1e-3, identical greedy tokens."""
+    m = TinyModel(oracle, arch, seed=40 + n)
+    worst, same = _batch_vs_single(oracle, m, n, seed=n)
+    assert worst <= 1.0, worst
+    assert same
+
+
+@pytest.mark.parametrize("slip,name", [(1, "cross-lane cache read"), (2, "K/V row at the batch index"),
+                                       (3, "rope at lane 0's position")])
+def test_decode_batch_planted_mistakes_break_the_invariant(oracle, slip, name):
+    """Each silent failure mode the reference's test names (llama.zig:
+    2324-2328), planted in the oracle's lo_decode_batch, breaks the
+    batch == single-streams comparison above."""
+    m = TinyModel(oracle, "qwen3moe", seed=48)
+    assert _batch_vs_single(oracle, m, 8, seed=8)[0] <= 1.0
+    oracle.lib().lo_set_batch_slip(slip)
+    try:
+        worst, _ = _batch_vs_single(oracle, m, 8, seed=8)
+    finally:
+        oracle.lib().lo_set_batch_slip(0)
+    assert worst > 10.0, (name, worst)
