@@ -1,0 +1,412 @@
+// attn_exact.hip -- GQA attention over the fp16 K/V cache in the reference's
+// own evaluation order (src/gguf/llama.zig:1162-1192), for any context length:
+//
+//   s_t = dotF32(q, k_t) * scale                      (ggml.zig:198-217)
+//   m = max s_t;  e_t = exp(s_t - m);  sum = e_0 + e_1 + ... in position order
+//   p_t = e_t * (1 / sum)                              (tensor.zig:18-28)
+//   o = 0;  o[d] = o[d] + p_t * v_t[d] in position order (axpy, ggml.zig:221-230)
+//
+// so the attention output -- and with it the int8 input of wo -- is bit-
+// identical to Loom's CPU path at every context length, which a
+// split-context (flash-decoding) merge is not.  Three launches:
+//
+//   attn_scores_kernel   per (64 positions, KV head, lane): the group's query
+//                        heads against 64 keys, dotF32 order on the VALU
+//                        (up to 4 lanes it also applies the per-head Q/K
+//                        RMSNorm and RoPE and appends the new K/V row)
+//   attn_softmax_kernel  per (query head, lane): the max, e_t, the position-
+//                        ordered sum, p_t (in place of the scores)
+//   attn_pv_kernel       per (64 value columns, KV head, lane): one lane per
+//                        (head, column) runs o = o + p_t * v_t over the whole
+//                        context from value tiles staged in LDS as f32
+//
+// The sequential sum of e_t is a dependent chain of P adds (~5.7 cycles each
+// on gfx950).  It is evaluated by speculative composition instead: the
+// context is cut into 64-position chunks; a double-precision prefix sum
+// estimates the running sum at each chunk's start; each lane of a wave runs
+// the chunk's chain from one of the 64 f32 values around that estimate
+// (consecutive bit patterns); a single pass over the chunks then follows the
+// exact running sum from chunk to chunk, reading each chunk's end from the
+// lane whose start equals it.  A start outside the window (rare) re-runs that
+// chunk serially from the exact value.  Every value is one the reference's
+// loop produces: the result is the sequential sum itself.
+#include "frame.hpp"
+#include "runtime.hpp"
+
+namespace lh {
+
+constexpr int SC_THREADS = 512;   // scores: 8 waves
+constexpr int SM_THREADS = 1024;  // softmax: 16 waves
+constexpr int PV_THREADS = 512;   // P.V: 8 waves, one query head each
+constexpr int PV_TJ = 64;         // positions per staged value tile
+constexpr int PV_VST = PV_TJ + 4; // f32 row stride of the transposed tile
+constexpr int PV_DEPTH = 4;       // value tiles requested ahead of the one in use
+
+// ---- scores -------------------------------------------------------------------------
+// Work group (chunk of 64 positions, KV head, lane).  All 512 threads load the
+// chunk's keys into padded LDS rows and the group's query heads; wave w scores
+// query heads w, w+8, ...: lane j takes position t0 + j.  fuse: the query
+// heads arrive raw and get headNorm (llama.zig:938-949, the squares summed in
+// order) and RoPE here; the chunk holding the new position normalises,
+// rotates and appends its K row and appends its V row (a full cache takes no
+// more rows), and scores against the new row from LDS.
+template <int HD>
+__global__ __launch_bounds__(SC_THREADS) void attn_scores_kernel(
+    FrameDims D, const float *__restrict__ qraw, const float *__restrict__ kraw, const float *__restrict__ vraw,
+    const float *__restrict__ q_norm, const float *__restrict__ k_norm, const float *__restrict__ rope_cs,
+    uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, const int32_t *__restrict__ pos, int li, int fuse,
+    float *__restrict__ S, int s_stride) {
+    constexpr int KS = HD + 8;                              // padded key row (halves)
+    constexpr int PR = HD / 8;                              // 16-byte pieces per row
+    constexpr int NPW = (ATT_TC * PR + SC_THREADS - 1) / SC_THREADS; // pieces per thread
+    __shared__ __align__(16) float qs[MAX_G * HD];
+    __shared__ __align__(16) uint16_t ks[ATT_TC * KS];
+    __shared__ float kn[HD], sinv[MAX_G + 1];
+    const int ch = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+    const int wave = tid >> 6, ln = tid & 63;
+    const int G = D.n_heads / D.n_kv;
+    const int p_raw = pos[t];
+    const int p = min(p_raw, D.ctx - 1);
+    const int t0 = ch * ATT_TC, nt = min(ATT_TC, p + 1 - t0);
+    if (nt <= 0)
+        return; // past the current position
+    const bool own = fuse && p_raw >= 0 && p_raw < D.ctx && p_raw >= t0 && p_raw < t0 + ATT_TC;
+    const int rp = min(max(p_raw, 0), D.ctx - 1); // rope position
+    const size_t row0 = (((size_t)t * D.n_layers + li) * D.ctx + t0) * D.kvd + (size_t)kvh * HD;
+    const float *qsrc = qraw + (size_t)t * D.qd + (size_t)kvh * G * HD;
+    const size_t kvo = (size_t)t * D.kvd + (size_t)kvh * HD;
+    uint4 pc[NPW];
+#pragma unroll
+    for (int u = 0; u < NPW; u++) {
+        const int i = tid + SC_THREADS * u;
+        pc[u] = i < ATT_TC * PR ? *(const uint4 *)(kc + row0 + (size_t)min(i / PR, nt - 1) * D.kvd + 8 * (i % PR))
+                                : make_uint4(0, 0, 0, 0);
+    }
+    float vnew = 0.0f;
+    if (own && tid < HD) {
+        kn[tid] = kraw[kvo + tid];
+        vnew = vraw[kvo + tid];
+    }
+    for (int i = tid; i < G * HD; i += SC_THREADS)
+        qs[i] = qsrc[i];
+#pragma unroll
+    for (int u = 0; u < NPW; u++) {
+        const int i = tid + SC_THREADS * u;
+        if (i < ATT_TC * PR)
+            *(uint4 *)(ks + (i / PR) * KS + 8 * (i % PR)) = pc[u];
+    }
+    __syncthreads();
+    if (fuse) {
+        // headNorm: the squares summed in the reference's order, one thread per head
+        if (q_norm && tid < G) {
+            float ss = 0.0f;
+            for (int i = 0; i < HD; i++) {
+                const float pr = qs[tid * HD + i] * qs[tid * HD + i];
+                ss = ss + pr;
+            }
+            sinv[tid] = 1.0f / sqrtf(ss / (float)HD + D.eps);
+        }
+        if (own && k_norm && tid == SC_THREADS - 64) {
+            float ss = 0.0f;
+            for (int i = 0; i < HD; i++) {
+                const float pr = kn[i] * kn[i];
+                ss = ss + pr;
+            }
+            sinv[MAX_G] = 1.0f / sqrtf(ss / (float)HD + D.eps);
+        }
+        __syncthreads();
+        if (q_norm)
+            for (int i = tid; i < G * HD; i += SC_THREADS)
+                qs[i] = (qs[i] * sinv[i / HD]) * q_norm[i % HD];
+        if (own && k_norm && tid < HD)
+            kn[tid] = (kn[tid] * sinv[MAX_G]) * k_norm[tid];
+        __syncthreads();
+        // RoPE (llama.zig:821-855) from the (cos, sin) table at the position
+        const int hr = D.rope_dim / 2;
+        const float *csp = rope_cs + (size_t)rp * hr * 2;
+        for (int i = tid; i < G * hr; i += SC_THREADS) {
+            const int g = i / hr, r = i % hr;
+            const float cs = csp[2 * r], sn = csp[2 * r + 1];
+            const int ia = D.rope_neox ? r : 2 * r, ib = D.rope_neox ? r + hr : 2 * r + 1;
+            const float a = qs[g * HD + ia], b = qs[g * HD + ib];
+            qs[g * HD + ia] = a * cs - b * sn;
+            qs[g * HD + ib] = a * sn + b * cs;
+        }
+        if (own && tid >= SC_THREADS - 64 && tid - (SC_THREADS - 64) < hr) {
+            const int r = tid - (SC_THREADS - 64);
+            const float cs = csp[2 * r], sn = csp[2 * r + 1];
+            const int ia = D.rope_neox ? r : 2 * r, ib = D.rope_neox ? r + hr : 2 * r + 1;
+            const float a = kn[ia], b = kn[ib];
+            kn[ia] = a * cs - b * sn;
+            kn[ib] = a * sn + b * cs;
+        }
+        __syncthreads();
+        if (own && tid < HD) { // the new row: to the cache and over its stale LDS copy
+            const uint16_t kh = __half_raw(__float2half(kn[tid])).x, vh = __half_raw(__float2half(vnew)).x;
+            const size_t crow = (((size_t)t * D.n_layers + li) * D.ctx + p_raw) * D.kvd + (size_t)kvh * HD;
+            kc[crow + tid] = kh;
+            vc[crow + tid] = vh;
+            ks[(p_raw - t0) * KS + tid] = kh;
+        }
+        __syncthreads();
+    }
+    const uint16_t *krow = ks + min(ln, nt - 1) * KS;
+    for (int g = wave; g < G; g += SC_THREADS / 64) {
+        const float s = dot_f32_key<HD>(qs + g * HD, krow) * D.scale;
+        if (ln < nt)
+            S[((size_t)t * D.n_heads + (size_t)kvh * G + g) * s_stride + t0 + ln] = s;
+    }
+}
+
+// ---- softmax ------------------------------------------------------------------------
+// Work group (query head, lane), 1024 threads; e[] and the chunk chain ends
+// live in LDS.
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+    for (int m = 32; m >= 1; m >>= 1)
+        v = v + __shfl_xor(v, m);
+    return v;
+}
+
+__global__ __launch_bounds__(SM_THREADS) void attn_softmax_kernel(FrameDims D, const int32_t *__restrict__ pos,
+                                                                  float *__restrict__ S, int s_stride) {
+    extern __shared__ __align__(16) float sm[]; // e[s_stride] | ends[C][64]
+    __shared__ float redf[SM_THREADS / 64];
+    __shared__ double csum[EXACT_MAX_CTX / 64 + 1];
+    __shared__ uint32_t fst[EXACT_MAX_CTX / 64 + 1];
+    __shared__ float total;
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
+    const int P = min(pos[t], D.ctx - 1) + 1;
+    const int C = (P + 63) / 64;
+    float *row = S + ((size_t)t * D.n_heads + h) * s_stride;
+    float *e = sm;
+    float *ends = sm + s_stride;
+    constexpr int NV = (EXACT_MAX_CTX + SM_THREADS - 1) / SM_THREADS;
+    // 1. m = max over the scores (order-free)
+    float sv[NV];
+    float m = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+        const int j = tid + SM_THREADS * u;
+        sv[u] = j < P ? row[j] : -INFINITY;
+        m = fmaxf(m, sv[u]);
+    }
+    m = wave_max(m);
+    if (ln == 0)
+        redf[wave] = m;
+    __syncthreads();
+    m = redf[0];
+    for (int w = 1; w < SM_THREADS / 64; w++)
+        m = fmaxf(m, redf[w]);
+    // 2. e_t = exp(s_t - m), the once-rounded double exponential
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+        const int j = tid + SM_THREADS * u;
+        if (j < P)
+            e[j] = exp_f32(sv[u] - m);
+    }
+    __syncthreads();
+    // 3. chunk sums in double: the estimate of the running sum at each chunk's start
+    for (int c = wave; c < C; c += SM_THREADS / 64) {
+        const int j = 64 * c + ln;
+        const double v = wave_sum_d(j < P ? (double)e[j] : 0.0);
+        if (ln == 0)
+            csum[c] = v;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double acc = 0.0;
+        for (int c = 0; c < C; c++) {
+            fst[c] = __float_as_uint((float)acc);
+            acc = acc + csum[c];
+        }
+    }
+    __syncthreads();
+    // 4. each chunk's chain from 64 starts around the estimate (chunk 0 from +0)
+    for (int c = wave; c < C; c += SM_THREADS / 64) {
+        const int b = c == 0 ? 0 : max((int)fst[c] + ln - 32, 0);
+        float s = __uint_as_float((uint32_t)b);
+        const int j1 = min(64 * c + 64, P);
+        for (int j = 64 * c; j < j1; j++)
+            s = s + e[j];
+        ends[c * 64 + ln] = s;
+    }
+    __syncthreads();
+    // 5. follow the exact running sum through the chunks
+    if (wave == 0) {
+        float run = ends[0];
+        for (int c = 1; c < C; c++) {
+            const int idx = (int)__float_as_uint(run) - (int)fst[c] + 32;
+            if (idx >= 0 && idx < 64) {
+                run = ends[c * 64 + idx];
+            } else { // outside the window: this chunk's chain from the exact value
+                const int j1 = min(64 * c + 64, P);
+                for (int j = 64 * c; j < j1; j++)
+                    run = run + e[j];
+            }
+        }
+        if (ln == 0)
+            total = run;
+    }
+    __syncthreads();
+    // 6. p_t = e_t * (1 / sum), in place of the scores
+    const float inv = 1.0f / total;
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+        const int j = tid + SM_THREADS * u;
+        if (j < P)
+            row[j] = e[j] * inv;
+    }
+}
+
+// ---- P.V ----------------------------------------------------------------------------
+// Work group (64 value columns, KV head, lane), 8 waves: wave w runs the
+// chains of query heads w (and w + 8 when NCH = 2), lane = column.  Value
+// tiles of 64 positions are staged transposed in LDS as f32 ([column][position],
+// converted once for the group's heads) with p beside them, double-buffered,
+// the global loads issued PV_DEPTH tiles ahead.  Positions past the context
+// enter as p = 0, v = 0: o + (+0) = o, as no position at all.
+template <int HD, int NCH>
+__global__ __launch_bounds__(PV_THREADS) void attn_pv_kernel(FrameDims D, const uint16_t *__restrict__ vc,
+                                                             const int32_t *__restrict__ pos, int li,
+                                                             const float *__restrict__ Pm, int s_stride,
+                                                             float *__restrict__ att) {
+    __shared__ __align__(16) float vt[2][64 * PV_VST];
+    __shared__ __align__(16) float pt[2][MAX_G * PV_TJ];
+    const int sl = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+    const int wave = tid >> 6, ln = tid & 63;
+    const int G = D.n_heads / D.n_kv;
+    const int P = min(pos[t], D.ctx - 1) + 1;
+    const int ntile = (P + PV_TJ - 1) / PV_TJ;
+    const int c0 = sl * 64, ncol = min(64, HD - c0);
+    // value piece: position r of the tile, 8 columns 8cg..8cg+7 (one wave per column group)
+    const int r = tid & 63, cg = tid >> 6;
+    const bool vlive = 8 * cg < ncol;
+    const uint16_t *vsrc = vc + (((size_t)t * D.n_layers + li) * D.ctx) * D.kvd + (size_t)kvh * HD + c0 + 8 * cg;
+    // p piece: head ph, positions 4*q4 .. 4*q4+3 of the tile
+    const int ph = tid >> 4, q4 = tid & 15;
+    const bool plive = ph < G;
+    const float *psrc = Pm + ((size_t)t * D.n_heads + (size_t)kvh * G + min(ph, G - 1)) * s_stride + 4 * q4;
+
+    auto load = [&](int tile, uint4 &vr, float4 &pr) {
+        const int j = tile * PV_TJ + r;
+        vr = vlive && j < P ? *(const uint4 *)(vsrc + (size_t)j * D.kvd) : make_uint4(0, 0, 0, 0);
+        const int jp = tile * PV_TJ + 4 * q4;
+        pr = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (plive && jp < P) {
+            pr = *(const float4 *)(psrc + (size_t)tile * PV_TJ);
+            if (jp + 1 >= P)
+                pr.y = 0.0f;
+            if (jp + 2 >= P)
+                pr.z = 0.0f;
+            if (jp + 3 >= P)
+                pr.w = 0.0f;
+        }
+    };
+    auto stage = [&](int buf, const uint4 &vr, const float4 &pr) {
+        if (vlive) {
+            const uint32_t w4[4] = {vr.x, vr.y, vr.z, vr.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                vt[buf][(8 * cg + i) * PV_VST + r] = half_bits_to_float((uint16_t)(w4[i >> 1] >> (16 * (i & 1))));
+        }
+        if (plive)
+            *(float4 *)(&pt[buf][ph * PV_TJ + 4 * q4]) = pr;
+    };
+
+    float o[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+        o[c] = 0.0f;
+    uint4 vr[PV_DEPTH];
+    float4 pr[PV_DEPTH];
+#pragma unroll
+    for (int d = 0; d < PV_DEPTH; d++)
+        load(d, vr[d], pr[d]);
+    for (int tb = 0; tb < ntile; tb += PV_DEPTH) {
+#pragma unroll
+        for (int d = 0; d < PV_DEPTH; d++) {
+            const int tile = tb + d;
+            if (tile >= ntile)
+                break;
+            const int buf = d & 1; // tb is a multiple of PV_DEPTH (even)
+            stage(buf, vr[d], pr[d]);
+            load(tile + PV_DEPTH, vr[d], pr[d]);
+            __syncthreads();
+            const float *vv = &vt[buf][ln * PV_VST];
+#pragma unroll
+            for (int c = 0; c < NCH; c++) {
+                const int g = wave + 8 * c;
+                if (g < G) {
+                    const float *pv = &pt[buf][g * PV_TJ];
+                    float acc = o[c];
+#pragma unroll
+                    for (int j = 0; j < PV_TJ; j += 4) {
+                        const float4 pp = *(const float4 *)(pv + j);
+                        const float4 x = *(const float4 *)(vv + j);
+                        float q;
+                        q = pp.x * x.x;
+                        acc = acc + q;
+                        q = pp.y * x.y;
+                        acc = acc + q;
+                        q = pp.z * x.z;
+                        acc = acc + q;
+                        q = pp.w * x.w;
+                        acc = acc + q;
+                    }
+                    o[c] = acc;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int g = wave + 8 * c;
+        if (g < G && ln < ncol)
+            att[(size_t)t * D.qd + ((size_t)kvh * G + g) * HD + c0 + ln] = o[c];
+    }
+}
+
+size_t exact_softmax_lds(int s_stride) { return ((size_t)s_stride + (size_t)(s_stride / 64) * 64) * 4; }
+
+template <int HD>
+static void launch_hd(const FrameDims &D, const float *q, const float *k, const float *v, const float *q_norm,
+                      const float *k_norm, const float *rope_cs, uint16_t *kc, uint16_t *vc, const int32_t *pos,
+                      int li, bool fuse, float *S, int s_stride, float *att, size_t n, hipStream_t st) {
+    const int n_chunks = (D.ctx + ATT_TC - 1) / ATT_TC;
+    const int G = D.n_heads / D.n_kv;
+    hipLaunchKernelGGL(attn_scores_kernel<HD>, dim3(n_chunks, D.n_kv, n), dim3(SC_THREADS), 0, st, D, q, k, v,
+                       q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse ? 1 : 0, S, s_stride);
+    hipLaunchKernelGGL(attn_softmax_kernel, dim3(D.n_heads, n), dim3(SM_THREADS), exact_softmax_lds(s_stride), st,
+                       D, pos, S, s_stride);
+    const dim3 pg((HD + 63) / 64, D.n_kv, n);
+    if (G <= 8)
+        hipLaunchKernelGGL((attn_pv_kernel<HD, 1>), pg, dim3(PV_THREADS), 0, st, D, vc, pos, li, S, s_stride, att);
+    else
+        hipLaunchKernelGGL((attn_pv_kernel<HD, 2>), pg, dim3(PV_THREADS), 0, st, D, vc, pos, li, S, s_stride, att);
+    note_launch();
+    note_launch();
+    note_launch();
+}
+
+bool launch_attn_exact(const FrameDims &D, const float *q, const float *k, const float *v, const float *q_norm,
+                       const float *k_norm, const float *rope_cs, uint16_t *kc, uint16_t *vc, const int32_t *pos,
+                       int li, bool fuse, float *S, int s_stride, float *att, size_t n, hipStream_t st) {
+    if (D.ctx > EXACT_MAX_CTX || s_stride % 64 || s_stride < D.ctx)
+        return false;
+    switch (D.hd) {
+    case 128:
+        launch_hd<128>(D, q, k, v, q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse, S, s_stride, att, n, st);
+        return true;
+    case 64:
+        launch_hd<64>(D, q, k, v, q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse, S, s_stride, att, n, st);
+        return true;
+    case 48:
+        launch_hd<48>(D, q, k, v, q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse, S, s_stride, att, n, st);
+        return true;
+    default:
+        return false;
+    }
+}
+
+} // namespace lh

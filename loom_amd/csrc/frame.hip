@@ -32,7 +32,7 @@
 // positions softmax's sum and P.V are a split-context merge.  Last-bit
 // differences from these can move one int8 step of a quantized matvec
 // input (the 2e-3 layer/logit tolerance).
-#include "device.hpp"
+#include "frame.hpp"
 #include "runtime.hpp"
 
 #include <cmath>
@@ -40,41 +40,6 @@
 #include <vector>
 
 namespace lh {
-
-constexpr int ATT_TC = 64;  // positions per attention work group (one per lane of a wave)
-constexpr int MAX_HD = 256; // head_dim limit
-constexpr int MAX_G = 16;   // query heads per KV head limit
-
-struct FrameDims {
-    int dim, hd, n_heads, n_kv, qd, kvd, ctx, rope_dim, rope_neox, n_layers, vocab;
-    float rope_base, eps, scale;
-};
-
-// ---- reductions ----------------------------------------------------------------
-
-__device__ inline float wave_sum_f(float v) {
-    v = v + dpp_f<0xB1>(v, v);
-    v = v + dpp_f<0x4E>(v, v);
-    v = v + dpp_f<0x141>(v, v);
-    v = v + dpp_f<0x140>(v, v);
-    v = v + dpp_f<0x142, 0xA>(v, v);
-    v = v + dpp_f<0x143, 0xC>(v, v);
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// Sum over the work group's waves (each value is already wave-uniform),
-// added in wave order.
-__device__ inline float block_sum_waves(float wave_total, float *lds) {
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0)
-        lds[wave] = wave_total;
-    __syncthreads();
-    float s = 0.0f;
-    for (int w = 0; w < nw; w++)
-        s = s + lds[w];
-    return s;
-}
 
 // ---- embedding: x[lane] = dequantRow(embed, token) (llama.zig:1122) -------------
 
@@ -281,40 +246,6 @@ __global__ __launch_bounds__(64) void qk_rope_kernel(FrameDims D, const float *_
             vc[base + i] = __half_raw(__float2half(vv[u])).x;
         }
     }
-}
-
-// ---- attention over 64 positions for one KV head group (llama.zig:1162-1192) -------
-
-// dotF32 (src/gguf/ggml.zig:198-217) of a query head (f32, LDS, read as
-// broadcasts) and a cached key row (fp16, a padded LDS row), 8 values per
-// 16-byte read: 32 accumulators over whole 32-steps, leftover 8-chunks into
-// the first 8, ((a0 + a1) + a2) + a3 per lane, the lanes summed in order
-// from -0 (HD is a multiple of 8).
-template <int HD>
-__device__ __forceinline__ float dot_f32_key(const float *a, const uint16_t *krow) {
-    float acc[32];
-#pragma unroll
-    for (int u = 0; u < 32; u++)
-        acc[u] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < HD; i += 8) {
-        const uint4 kv = *(const uint4 *)(krow + i);
-        const float4 qa = *(const float4 *)(a + i), qb = *(const float4 *)(a + i + 4);
-        const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
-        const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-        const int base = i < HD / 32 * 32 ? i % 32 : 0; // whole 32-steps, then chunks into acc[0..8)
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float k = half_bits_to_float((uint16_t)(kw[e >> 1] >> (16 * (e & 1))));
-            const float pr = qv[e] * k;
-            acc[base + e] = acc[base + e] + pr;
-        }
-    }
-    float s = -0.0f;
-#pragma unroll
-    for (int l = 0; l < 8; l++)
-        s = s + (((acc[l] + acc[8 + l]) + acc[16 + l]) + acc[24 + l]);
-    return s;
 }
 
 // Work group (chunk, kv head, lane), 8 waves.  Waves 0-3 load the chunk's
@@ -1035,6 +966,8 @@ static const float *rope_table(int ctx, int rope_dim, float base) {
 
 struct FrameWs {
     float *x, *normed, *q, *k, *v, *qrot, *part, *act, *amax_v;
+    float *S, *att; // PARITY attention: scores / p [n][n_heads][s_stride], output [n][qd]
+    int s_stride;
     uint16_t *qsplit; // the rotated queries as (f16 hi, f16 lo) planes, [2][n][qd]
     int *amax_i;
     QAct qa_dim, qa_att, qa_ffn;
@@ -1044,7 +977,7 @@ struct FrameWs {
 };
 
 static FrameWs frame_layout(char *base, size_t n, const loomhip_model *m, size_t ffn_max,
-                            int n_chunks) {
+                            int n_chunks, bool parity) {
     FrameWs w{};
     size_t off = 0;
     auto take = [&](size_t b) {
@@ -1070,6 +1003,9 @@ static FrameWs frame_layout(char *base, size_t n, const loomhip_model *m, size_t
     w.qsplit = (uint16_t *)take(n * qd * 4);
     w.part = (float *)take(n * m->n_kv_heads * (size_t)n_chunks * G * (m->head_dim + 2) * 4);
     w.act = (float *)take(n * (ffn_max ? ffn_max : 1) * 4);
+    w.s_stride = (int)((m->ctx_len + 63) / 64 * 64);
+    w.S = (float *)take(parity ? n * m->n_heads * (size_t)w.s_stride * 4 : 16);
+    w.att = (float *)take(parity ? n * qd * 4 : 16);
     w.amax_v = (float *)take(n * ARGMAX_SLICES * 4);
     w.amax_i = (int *)take(n * ARGMAX_SLICES * 4);
     w.qa_dim = qtake(dim);
@@ -1221,10 +1157,16 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         return rc;
     hipStream_t st = stream_of(stream);
     const int n_chunks = (int)((m->ctx_len + ATT_TC - 1) / ATT_TC);
-    const FrameWs probe = frame_layout(nullptr, n, m, ffn_max, n_chunks);
+    if (m->numerics != LOOMHIP_NUMERICS_PARITY && m->numerics != LOOMHIP_NUMERICS_FAST)
+        return fail(LOOMHIP_ERR_ARG, "token_frame: unknown numerics mode %d", m->numerics);
+    const bool parity = m->numerics == LOOMHIP_NUMERICS_PARITY;
+    if (parity && m->ctx_len > (size_t)EXACT_MAX_CTX)
+        return fail(LOOMHIP_DECLINED, "token_frame: PARITY attention serves contexts up to %d (ctx_len %zu)",
+                    EXACT_MAX_CTX, m->ctx_len);
+    const FrameWs probe = frame_layout(nullptr, n, m, ffn_max, n_chunks, parity);
     if (int rc = g_frame.reserve(probe.bytes))
         return rc;
-    FrameWs w = frame_layout((char *)g_frame.ptr, n, m, ffn_max, n_chunks);
+    FrameWs w = frame_layout((char *)g_frame.ptr, n, m, ffn_max, n_chunks, parity);
     w.nt = pick_nt((int)n);
     w.groups = dense_groups((int)n, w.nt, &w.n_groups); // built once per lane count, before any capture
     if (!w.groups)
@@ -1255,9 +1197,6 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     if (cmb_lds > 64 * 1024)
         return fail(LOOMHIP_DECLINED, "token_frame: context %zu exceeds the merge's LDS", m->ctx_len);
 
-    if (m->numerics != LOOMHIP_NUMERICS_PARITY && m->numerics != LOOMHIP_NUMERICS_FAST)
-        return fail(LOOMHIP_ERR_ARG, "token_frame: unknown numerics mode %d", m->numerics);
-    const bool parity = m->numerics == LOOMHIP_NUMERICS_PARITY;
     const float *rope_cs = m->rope_cs ? m->rope_cs : rope_table(D.ctx, D.rope_dim, D.rope_base);
     if (!rope_cs)
         return fail(LOOMHIP_ERR_HIP, "token_frame: rope table");
@@ -1287,6 +1226,16 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         }
         const float *qin = fuse_rope ? w.q : w.qrot;
         int ph = prof_begin(LOOMHIP_KT_ATTN, st);
+        if (parity) {
+            // the reference's own order over the whole context: scores, softmax, P.V
+            if (!launch_attn_exact(D, qin, w.k, w.v, l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li,
+                                   fuse_rope, w.S, w.s_stride, w.att, n, st))
+                return fail(LOOMHIP_ERR_ARG, "token_frame: exact attention declined");
+            prof_end(ph, st);
+            launch_quant_act(l.wo_t, w.att, D.qd, D.qd, (int)n, w.qa_att, st);
+            if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_QKV, true, 16))
+                return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
+        } else {
         const dim3 agrid(n_chunks, D.n_kv, n);
         // records of the merge: chunks of ATT_TC positions, ATT_TC_DIRECT direct
         const int span = direct ? ATT_TC_DIRECT : ATT_TC;
@@ -1323,6 +1272,7 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         note_launch();
         if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_QKV, true, 16))
             return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
+        }
         // FFN block (llama.zig:1203-1224)
         if (l.is_moe) {
             const int combine = n == 1 ? LOOMHIP_COMBINE_SELECTION_ADD : LOOMHIP_COMBINE_EXPERT_ASC;

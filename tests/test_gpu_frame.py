@@ -129,55 +129,109 @@ def test_qwen3moe_frame_greedy(lh, oracle):
     assert dev == ref
 
 
-@pytest.mark.parametrize("numerics", ["parity", "fast"])
-def test_qwen3moe_frame_prefilled_context(lh, oracle, numerics):
-    """A prefilled fp16 context (random K/V rows 0..99, as the benchmark's
-    4096-token context), then 12 steps: past 64 positions the attention is a
-    split-context merge (in FAST numerics on the matrix cores), whose last
-    bits can move one int8 step of a quantized matvec input.  Every step's
-    greedy token matches; the logits stay within 2e-3 on at least 3 steps in
-    4; one int8 step of one value moves logits by ~1e-3..2.2e-2 relative at
-    this size: within 2e-2 always in PARITY, 5e-2 in FAST."""
+def _set_numerics(dm, numerics):
     from loom_amd import NUMERICS_FAST, NUMERICS_PARITY
 
+    dm.set_numerics(NUMERICS_PARITY if numerics == "parity" else NUMERICS_FAST)
+
+
+# FAST numerics (tree-summed rmsnorm, split-context attention on the matrix
+# cores, hardware exp) are not the reference's order: a last-bit difference
+# can move one int8 step of a quantized matvec input, which moves logits by up
+# to ~1.5e-2 relative at these shapes (measured).  They are bounded here, not
+# held to north_star's 2e-3; PARITY is, and is what the benchmark reports.
+FAST_BOUND = 5e-2
+
+
+def _check(rels, numerics):
+    rels = np.asarray(rels)
+    if numerics == "parity":
+        assert rels.max() <= 2e-3, rels
+        assert (rels <= 1e-5).mean() >= 0.95, rels
+    else:
+        assert rels.max() <= FAST_BOUND, rels
+
+
+@pytest.mark.parametrize("numerics", ["parity", "fast"])
+def test_qwen3moe_frame_prefilled_context(lh, oracle, numerics):
+    """A prefilled fp16 context (random K/V rows 0..99), then 12 steps on
+    identical state: PARITY runs the reference-order attention over the whole
+    context (bit-identical but for exp's last bit), FAST the split-context
+    merge.  Every step's greedy token matches."""
     spec = _qwen_small(lh, ctx_len=128)
     dm = lh.DeviceModel.synth(spec, seed=6, keep_ggml=True)
-    dm.set_numerics(NUMERICS_PARITY if numerics == "parity" else NUMERICS_FAST)
+    _set_numerics(dm, numerics)
     om = OracleModel(oracle, dm)
     rels = _synced_steps(lh, om, dm, np.random.default_rng(1).integers(0, spec.vocab, 12),
                          prefill=100)
-    assert rels.max() <= (2e-2 if numerics == "parity" else 5e-2), rels
-    assert (rels <= 2e-3).mean() >= 0.75, rels
+    _check(rels, numerics)
 
 
-@pytest.mark.parametrize("n", [3, 6, 16])
-def test_qwen3moe_frame_batch(lh, oracle, n):
-    """decodeBatch semantics at n lanes (moeBatchUnion; n = 3 takes the
-    few-token MoE path, n = 6 the grouped one, n = 16 the matrix-core
-    matmuls for the experts and the head): per-lane logits against
-    lo_decode_batch over 6 steps on identical state."""
+def _batch_steps(lh, om, dm, n, steps, prefill, seed):
+    """n lanes over a prefilled context with staggered positions (lane i at
+    prefill - i % 7): per-lane logits against lo_decode_batch on identical
+    state for `steps` steps, the device fed the oracle's greedy tokens.
+    Returns (per lane-step max-rel, greedy tokens identical)."""
     import torch
 
-    spec = _qwen_small(lh, ctx_len=16)
-    dm = lh.DeviceModel.synth(spec, seed=7, keep_ggml=True)
-    om = OracleModel(oracle, dm)
     dec = lh.Decoder(dm, n)
+    if prefill:
+        dec.prefill_random(prefill, seed=seed, scale=0.5)
+        dec.pos.copy_(torch.tensor([prefill - (i % 7) for i in range(n)], dtype=torch.int32))
     seqs, bufs = om.new_seqs(n)
-    toks = np.random.default_rng(n).integers(0, spec.vocab, n)
-    dec.tokens.copy_(torch.from_numpy(toks.astype(np.int32)))
-    worst = []
-    for _ in range(6):
+    toks = np.random.default_rng(seed).integers(0, dm.spec.vocab, n)
+    rels, same = [], True
+    for _ in range(steps):
         _sync_oracle(dec, seqs, bufs)
+        dec.tokens.copy_(torch.from_numpy(toks.astype(np.int32)))
         dec.step()
-        want = om.decode_batch(seqs, toks)
+        want = om.step(seqs[0], int(toks[0]))[None] if n == 1 else om.decode_batch(seqs, toks)
         torch.cuda.synchronize()
         got = dec.logits.cpu().numpy()
-        worst += [maxrel(got[i], want[i]) for i in range(n)]
+        rels += [maxrel(got[i], want[i]) for i in range(n)]
         toks = np.argmax(want, axis=1)
-        assert np.array_equal(dec.tokens.cpu().numpy(), toks.astype(np.int32))
-    worst = np.array(worst)
-    assert worst.max() <= 2e-3, worst
-    assert (worst <= 1e-5).mean() >= 0.95, worst
+        same &= bool(np.array_equal(dec.tokens.cpu().numpy(), toks.astype(np.int32)))
+    return np.array(rels), same
+
+
+@pytest.mark.parametrize("numerics", ["parity", "fast"])
+@pytest.mark.parametrize("n", [3, 6, 16, 32])
+def test_qwen3moe_frame_batch(lh, oracle, n, numerics):
+    """decodeBatch semantics at n lanes (moeBatchUnion; n = 3 the few-token
+    MoE path and the fused rope, n = 6 the grouped MoE and the separate rope
+    launch, n >= 16 the matrix-core matmuls; FAST from 5 lanes the direct
+    attention over 128-position records) over a 300-position prefilled context
+    (several merge records, a partly filled last one): per-lane logits against
+    lo_decode_batch over 4 steps on identical state."""
+    spec = _qwen_small(lh, ctx_len=320)
+    dm = lh.DeviceModel.synth(spec, seed=7, keep_ggml=True)
+    _set_numerics(dm, numerics)
+    om = OracleModel(oracle, dm)
+    rels, same = _batch_steps(lh, om, dm, n, 4, 300, seed=n)
+    _check(rels, numerics)
+    if numerics == "parity":
+        assert same
+
+
+@pytest.mark.parametrize("numerics", ["parity", "fast"])
+@pytest.mark.parametrize("n", [1, 32])
+def test_qwen3moe_frame_4096_context(lh, oracle, n, numerics):
+    """The benchmark's shape: two layers at the full Qwen3-30B-A3B layer
+    shapes (128 experts top-8, vocab 4096) over a 4096-token prefilled fp16
+    context, 1 lane (llama.step) and 32 lanes (decodeBatch), 3 steps on
+    identical state.  PARITY: every logit within north_star's 2e-3 (in fact
+    bit-identical) and identical greedy tokens -- the reference's sequential
+    softmax sum and position-ordered P.V over all 4096 positions, the merge
+    tail of long contexts included."""
+    spec = lh.qwen3_30b_a3b(ctx_len=4096 + 16, n_layers=2, vocab=4096, n_expert=128)
+    dm = lh.DeviceModel.synth(spec, seed=6, keep_ggml=True)
+    _set_numerics(dm, numerics)
+    om = OracleModel(oracle, dm)
+    rels, same = _batch_steps(lh, om, dm, n, 3, 4096, seed=11 + n)
+    print(f"{numerics} n={n}: max-rel {rels.max():.2e}, steps > 2e-3: {(rels > 2e-3).sum()}/{rels.size}")
+    _check(rels, numerics)
+    if numerics == "parity":
+        assert same
 
 
 def test_frame_declines_unserved_dims(lh):
