@@ -181,6 +181,22 @@ int loomhip_moe_layer_dev(const loomhip_moe_layer *L, const float *normed, size_
                           int combine, float *out, uint32_t *ids_out, float *gates_out,
                           void *stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  loomhip_moe_layer_dev with its workspace (the quantized
+ * activations, routing tables, expert groups and partial outputs) in a fixed
+ * per-GPU device array of LOOMHIP_MOE_NOALLOC_BYTES, resolved once per device
+ * by loomhip_init; the call itself allocates nothing.  A call whose workspace
+ * would exceed the array returns LOOMHIP_ERR_ARG before launching anything
+ * (config-3 shapes: up to 128 tokens).  Every call on one GPU shares that
+ * GPU's array, so calls that overlap on one GPU (other streams, other host
+ * threads) race; nothing in it needs to start at zero.  Same kernels and
+ * results as loomhip_moe_layer_dev. */
+#define LOOMHIP_MOE_NOALLOC_BYTES ((size_t)16 << 20)
+int loomhip_moe_layer_dev_noalloc(const loomhip_moe_layer *L, const float *normed, size_t n_tok,
+                                  int combine, float *out, uint32_t *ids_out, float *gates_out,
+                                  void *stream);
+
 /* ---- whole-token decode frame --------------------------------------------- */
 
 /* Numerics of the frame's f32 reductions.  PARITY: every rmsnorm sums its

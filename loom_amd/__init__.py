@@ -192,6 +192,7 @@ def lib() -> C.CDLL:
         "loomhip_matvec_dev": (i, [i, vp, vp, vp, sz, sz, sz, vp]),
         "loomhip_dequant_dev": (i, [i, vp, vp, sz, sz, vp]),
         "loomhip_moe_layer_dev": (i, [C.POINTER(MoeLayerDesc), vp, sz, i, vp, vp, vp, vp]),
+        "loomhip_moe_layer_dev_noalloc": (i, [C.POINTER(MoeLayerDesc), vp, sz, i, vp, vp, vp, vp]),
         "loomhip_token_frame_dev": (i, [C.POINTER(ModelDesc), vp, vp, sz, vp, vp, vp, vp, vp]),
         "loomhip_host_alloc": (vp, [sz]),
         "loomhip_host_free": (None, [vp]),

@@ -10,6 +10,29 @@ namespace lh {
 static Scratch g_moe;   // per-call workspace
 static Scratch g_stage; // seam-call staging
 
+// Fixed workspace of loomhip_moe_layer_dev_noalloc: a file-scope device
+// array, one copy per GPU for the life of the process.  Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in
+// symbol): moe_noalloc_setup resolves each device's copy once, with that
+// device current, and the entry point uses that address.
+constexpr size_t MOE_NOALLOC_BYTES = LOOMHIP_MOE_NOALLOC_BYTES;
+static __device__ __align__(256) char scratch[MOE_NOALLOC_BYTES];
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static void *g_scratch_dev[NOALLOC_MAX_DEVICES];
+
+int moe_noalloc_setup(int device) {
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES)
+        return fail(LOOMHIP_ERR_INIT, "moe noalloc: device %d out of range", device);
+    if (g_scratch_dev[device])
+        return LOOMHIP_OK;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess)
+        return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_dev[device] = p;
+    return LOOMHIP_OK;
+}
+
 void moe_release_scratch() {
     g_moe.release();
     g_stage.release();
@@ -76,8 +99,11 @@ constexpr size_t DECODE_MAX_TOK = 4; // decode path up to this many tokens
 //   quant    int8 quantization of the activations
 //   down     grouped down
 //   combine  gated combine per token
+// ws/ws_cap: a caller-held workspace used instead of the grow-only one (the
+// no-allocation entry point); a call that needs more fails before launching.
 static int moe_run(const MoeRun &m, const float *normed, const float *logits_in, size_t n,
-                   int combine, float *out, uint32_t *ids_out, float *gates_out, hipStream_t st) {
+                   int combine, float *out, uint32_t *ids_out, float *gates_out, hipStream_t st,
+                   char *ws = nullptr, size_t ws_cap = 0) {
     if (int rc = moe_check(m, n))
         return rc;
     if (combine < LOOMHIP_COMBINE_SELECTION || combine > LOOMHIP_COMBINE_SELECTION_ADD)
@@ -105,9 +131,17 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     const size_t o_act = take(P * m.ffn * 4);
     const size_t o_qa = take(qbytes(P, m.ffn));
     const size_t o_y = take(decode ? 0 : P * m.dim * 4);
-    if (int rc = g_moe.reserve(off))
-        return rc;
-    char *base = (char *)g_moe.ptr;
+    char *base;
+    if (ws) {
+        if (off > ws_cap)
+            return fail(LOOMHIP_ERR_ARG, "moe_layer_dev_noalloc: %zu tokens need %zu B of workspace, the fixed "
+                        "scratch holds %zu B", n, off, ws_cap);
+        base = ws;
+    } else {
+        if (int rc = g_moe.reserve(off))
+            return rc;
+        base = (char *)g_moe.ptr;
+    }
     const QAct qx = qview(base + o_qx, n, m.dim);
     uint32_t *ids = ids_out ? ids_out : (uint32_t *)(base + o_ids);
     float *gates = gates_out ? gates_out : (float *)(base + o_gates);
@@ -279,6 +313,27 @@ int loomhip_moe_layer_dev(const loomhip_moe_layer *L, const float *normed, size_
              L->router, L->router_bias, L->sel_bias, L->gate_t, L->up_t, L->down_t, L->gate,
              L->up, L->down};
     return moe_run(m, normed, nullptr, n_tok, combine, out, ids_out, gates_out, stream_of(stream));
+}
+
+int loomhip_moe_layer_dev_noalloc(const loomhip_moe_layer *L, const float *normed, size_t n_tok,
+                                  int combine, float *out, uint32_t *ids_out, float *gates_out,
+                                  void *stream) {
+    if (int rc = require_ready())
+        return rc;
+    if (!L || !normed || !out || !L->router)
+        return fail(LOOMHIP_ERR_ARG, "moe_layer_dev_noalloc: null argument");
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES || !g_scratch_dev[dev])
+        return fail(LOOMHIP_ERR_INIT, "moe_layer_dev_noalloc: no fixed scratch resolved for device %d "
+                    "(loomhip_init sets it up)", dev);
+    MoeRun m{L->dim, L->ffn, L->n_expert, L->n_used, L->gating, L->weights_norm, L->weights_scale,
+             L->router, L->router_bias, L->sel_bias, L->gate_t, L->up_t, L->down_t, L->gate,
+             L->up, L->down};
+    return moe_run(m, normed, nullptr, n_tok, combine, out, ids_out, gates_out, stream_of(stream),
+                   (char *)g_scratch_dev[dev], MOE_NOALLOC_BYTES);
 }
 
 int loomhip_moe_route(const float *logits, const float *bias, size_t n_expert, size_t n_used,

@@ -307,6 +307,8 @@ int loomhip_init(int device) {
     if ((e = hipMemset(sy, 0, sizeof(int) * SYNC_INTS)) != hipSuccess)
         return hip_fail(e, "hipMemset sync");
     g_ctx.sync = (int *)sy;
+    if (int rc = moe_noalloc_setup(device))
+        return rc;
     g_ctx.device = device;
     g_ctx.ready = true;
     return LOOMHIP_OK;

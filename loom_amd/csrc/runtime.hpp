@@ -56,6 +56,8 @@ inline bool use_mmq(int t, int cols, int n, int group_tok, bool fused) {
 // Device group table for n vectors in groups of nt against plane 0 (cached per (n, nt)).
 const DmmvGroup *dense_groups(int n, int nt, int *count);
 void moe_release_scratch();
+// Resolves this device's copy of the no-allocation entry point's fixed scratch.
+int moe_noalloc_setup(int device);
 // The decode MoE path with its rmsnorm fused into the router launch (x = the
 // residual stream); moe_decode_fusable says whether the layer takes it.
 int moe_layer_fused_norm(const loomhip_moe_layer *L, const float *x, const float *norm_w, float eps, size_t n_tok,
