@@ -37,10 +37,9 @@ namespace lh {
 
 constexpr int SC_THREADS = 512;   // scores: 8 waves
 constexpr int SM_THREADS = 1024;  // softmax: 16 waves
-constexpr int PV_THREADS = 512;   // P.V: 8 waves, one query head each
 constexpr int PV_TJ = 64;         // positions per staged value tile
 constexpr int PV_VST = PV_TJ + 4; // f32 row stride of the transposed tile
-constexpr int PV_DEPTH = 4;       // value tiles requested ahead of the one in use
+constexpr int PV_DEPTH = 2;       // value tiles per register set (two sets; even)
 
 // ---- scores -------------------------------------------------------------------------
 // Work group (chunk of 64 positions, KV head, lane).  All 512 threads load the
@@ -162,18 +161,12 @@ __global__ __launch_bounds__(SC_THREADS) void attn_scores_kernel(
 // Work group (query head, lane), 1024 threads; e[] and the chunk chain ends
 // live in LDS.
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-    for (int m = 32; m >= 1; m >>= 1)
-        v = v + __shfl_xor(v, m);
-    return v;
-}
-
 __global__ __launch_bounds__(SM_THREADS) void attn_softmax_kernel(FrameDims D, const int32_t *__restrict__ pos,
                                                                   float *__restrict__ S, int s_stride) {
     extern __shared__ __align__(16) float sm[]; // e[s_stride] | ends[C][64]
     __shared__ float redf[SM_THREADS / 64];
-    __shared__ double csum[EXACT_MAX_CTX / 64 + 1];
-    __shared__ uint32_t fst[EXACT_MAX_CTX / 64 + 1];
+    __shared__ double csum[128];
+    __shared__ uint32_t fst[128];
     __shared__ float total;
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
     const int P = min(pos[t], D.ctx - 1) + 1;
@@ -198,58 +191,18 @@ __global__ __launch_bounds__(SM_THREADS) void attn_softmax_kernel(FrameDims D, c
     m = redf[0];
     for (int w = 1; w < SM_THREADS / 64; w++)
         m = fmaxf(m, redf[w]);
-    // 2. e_t = exp(s_t - m), the once-rounded double exponential
+    // 2. e_t = exp(s_t - m), the once-rounded double exponential; positions
+    //    past the context up to the chunk boundary hold +0 (s + 0 = s)
 #pragma unroll
     for (int u = 0; u < NV; u++) {
         const int j = tid + SM_THREADS * u;
-        if (j < P)
-            e[j] = exp_f32(sv[u] - m);
+        if (j < 64 * C)
+            e[j] = j < P ? exp_f32(sv[u] - m) : 0.0f;
     }
     __syncthreads();
-    // 3. chunk sums in double: the estimate of the running sum at each chunk's start
-    for (int c = wave; c < C; c += SM_THREADS / 64) {
-        const int j = 64 * c + ln;
-        const double v = wave_sum_d(j < P ? (double)e[j] : 0.0);
-        if (ln == 0)
-            csum[c] = v;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        double acc = 0.0;
-        for (int c = 0; c < C; c++) {
-            fst[c] = __float_as_uint((float)acc);
-            acc = acc + csum[c];
-        }
-    }
-    __syncthreads();
-    // 4. each chunk's chain from 64 starts around the estimate (chunk 0 from +0)
-    for (int c = wave; c < C; c += SM_THREADS / 64) {
-        const int b = c == 0 ? 0 : max((int)fst[c] + ln - 32, 0);
-        float s = __uint_as_float((uint32_t)b);
-        const int j1 = min(64 * c + 64, P);
-        for (int j = 64 * c; j < j1; j++)
-            s = s + e[j];
-        ends[c * 64 + ln] = s;
-    }
-    __syncthreads();
-    // 5. follow the exact running sum through the chunks
-    if (wave == 0) {
-        float run = ends[0];
-        for (int c = 1; c < C; c++) {
-            const int idx = (int)__float_as_uint(run) - (int)fst[c] + 32;
-            if (idx >= 0 && idx < 64) {
-                run = ends[c * 64 + idx];
-            } else { // outside the window: this chunk's chain from the exact value
-                const int j1 = min(64 * c + 64, P);
-                for (int j = 64 * c; j < j1; j++)
-                    run = run + e[j];
-            }
-        }
-        if (ln == 0)
-            total = run;
-    }
-    __syncthreads();
-    // 6. p_t = e_t * (1 / sum), in place of the scores
+    // 3. the position-ordered sum of e (speculative composition, exact)
+    seq_sum_nonneg<SM_THREADS / 64>(e, C, ends, csum, fst, &total);
+    // 4. p_t = e_t * (1 / sum), in place of the scores
     const float inv = 1.0f / total;
 #pragma unroll
     for (int u = 0; u < NV; u++) {
@@ -260,111 +213,135 @@ __global__ __launch_bounds__(SM_THREADS) void attn_softmax_kernel(FrameDims D, c
 }
 
 // ---- P.V ----------------------------------------------------------------------------
-// Work group (64 value columns, KV head, lane), 8 waves: wave w runs the
-// chains of query heads w (and w + 8 when NCH = 2), lane = column.  Value
-// tiles of 64 positions are staged transposed in LDS as f32 ([column][position],
-// converted once for the group's heads) with p beside them, double-buffered,
-// the global loads issued PV_DEPTH tiles ahead.  Positions past the context
-// enter as p = 0, v = 0: o + (+0) = o, as no position at all.
-template <int HD, int NCH>
-__global__ __launch_bounds__(PV_THREADS) void attn_pv_kernel(FrameDims D, const uint16_t *__restrict__ vc,
-                                                             const int32_t *__restrict__ pos, int li,
-                                                             const float *__restrict__ Pm, int s_stride,
-                                                             float *__restrict__ att) {
+// Work group (64 value columns, group of W query heads of one KV head, lane),
+// W waves: wave w runs the chain of head w of the group, lane = column.
+// Value tiles of 64 positions are staged transposed in LDS as f32
+// ([column][position], converted once for the group's heads) with p beside
+// them, double-buffered; the tiles' global loads are requested a group of
+// PV_DEPTH tiles ahead (two register sets), and inside a tile each wave reads
+// its values and p PV_AHEAD 4-position groups ahead of the chain, so the
+// chain (one multiply and one dependent add per position) waits on neither.
+// Positions past the context enter as p = 0, v = 0: o + (+0) = o, as no
+// position at all.  W = 2 puts one wave on each of two SIMDs (few lanes:
+// latency); W = 4 stages each value tile for four heads (many lanes: issue).
+constexpr int PV_AHEAD = 4;
+
+template <int HD, int W>
+__global__ __launch_bounds__(64 * W) void attn_pv_kernel(FrameDims D, const uint16_t *__restrict__ vc,
+                                                         const int32_t *__restrict__ pos, int li,
+                                                         const float *__restrict__ Pm, int s_stride,
+                                                         float *__restrict__ att) {
+    constexpr int NT = 64 * W;
+    constexpr int VPT = 512 / NT;                // 16-byte value pieces per thread per tile
+    constexpr int PPT = (16 * W + NT - 1) / NT;  // p float4 pieces per thread per tile
     __shared__ __align__(16) float vt[2][64 * PV_VST];
-    __shared__ __align__(16) float pt[2][MAX_G * PV_TJ];
-    const int sl = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
-    const int wave = tid >> 6, ln = tid & 63;
-    const int G = D.n_heads / D.n_kv;
+    __shared__ __align__(16) float pt[2][W * PV_TJ];
+    const int G = D.n_heads / D.n_kv, n_hg = (G + W - 1) / W;
+    const int sl = blockIdx.x, kvh = blockIdx.y / n_hg, hg = blockIdx.y % n_hg, t = blockIdx.z;
+    const int tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
     const int P = min(pos[t], D.ctx - 1) + 1;
     const int ntile = (P + PV_TJ - 1) / PV_TJ;
     const int c0 = sl * 64, ncol = min(64, HD - c0);
-    // value piece: position r of the tile, 8 columns 8cg..8cg+7 (one wave per column group)
-    const int r = tid & 63, cg = tid >> 6;
-    const bool vlive = 8 * cg < ncol;
-    const uint16_t *vsrc = vc + (((size_t)t * D.n_layers + li) * D.ctx) * D.kvd + (size_t)kvh * HD + c0 + 8 * cg;
-    // p piece: head ph, positions 4*q4 .. 4*q4+3 of the tile
-    const int ph = tid >> 4, q4 = tid & 15;
-    const bool plive = ph < G;
-    const float *psrc = Pm + ((size_t)t * D.n_heads + (size_t)kvh * G + min(ph, G - 1)) * s_stride + 4 * q4;
-
-    auto load = [&](int tile, uint4 &vr, float4 &pr) {
-        const int j = tile * PV_TJ + r;
-        vr = vlive && j < P ? *(const uint4 *)(vsrc + (size_t)j * D.kvd) : make_uint4(0, 0, 0, 0);
-        const int jp = tile * PV_TJ + 4 * q4;
-        pr = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (plive && jp < P) {
-            pr = *(const float4 *)(psrc + (size_t)tile * PV_TJ);
-            if (jp + 1 >= P)
-                pr.y = 0.0f;
-            if (jp + 2 >= P)
-                pr.z = 0.0f;
-            if (jp + 3 >= P)
-                pr.w = 0.0f;
+    const int g = hg * W + wave; // this wave's query head within the KV group
+    const uint16_t *vbase = vc + (((size_t)t * D.n_layers + li) * D.ctx) * D.kvd + (size_t)kvh * HD + c0;
+    const float *pbase = Pm + ((size_t)t * D.n_heads + (size_t)kvh * G) * s_stride;
+    // Every load is unconditional, from an address clamped into range (the
+    // context, the value columns, the group's heads), so the compiler counts
+    // them and waits for each tile's own loads only; what lies past the
+    // context is zeroed when the tile is staged.
+    auto load = [&](int tile, uint4 (&vr)[VPT], float4 (&pr)[PPT]) {
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            const int i = tid + NT * u, r = i & 63, cg = i >> 6;
+            const int j = min(tile * PV_TJ + r, P - 1);
+            vr[u] = *(const uint4 *)(vbase + (size_t)j * D.kvd + (8 * cg < ncol ? 8 * cg : 0));
+        }
+#pragma unroll
+        for (int u = 0; u < PPT; u++) {
+            const int i = min(tid + NT * u, 16 * W - 1), ph = min(hg * W + (i >> 4), G - 1), q4 = i & 15;
+            pr[u] = *(const float4 *)(pbase + (size_t)ph * s_stride + (size_t)min(tile, ntile - 1) * PV_TJ + 4 * q4);
         }
     };
-    auto stage = [&](int buf, const uint4 &vr, const float4 &pr) {
-        if (vlive) {
-            const uint32_t w4[4] = {vr.x, vr.y, vr.z, vr.w};
+    auto stage = [&](int buf, int tile, const uint4 (&vr)[VPT], const float4 (&pr)[PPT]) {
 #pragma unroll
-            for (int i = 0; i < 8; i++)
-                vt[buf][(8 * cg + i) * PV_VST + r] = half_bits_to_float((uint16_t)(w4[i >> 1] >> (16 * (i & 1))));
+        for (int u = 0; u < VPT; u++) {
+            const int i = tid + NT * u, r = i & 63, cg = i >> 6;
+            const bool in = tile * PV_TJ + r < P;
+            const uint32_t w4[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                vt[buf][(8 * cg + k) * PV_VST + r] = half_bits_to_float((uint16_t)(w4[k >> 1] >> (16 * (k & 1))));
         }
-        if (plive)
-            *(float4 *)(&pt[buf][ph * PV_TJ + 4 * q4]) = pr;
+#pragma unroll
+        for (int u = 0; u < PPT; u++) {
+            const int i = tid + NT * u;
+            if (i < 16 * W) {
+                const int ph = i >> 4, q4 = i & 15, jp = tile * PV_TJ + 4 * q4;
+                float4 q = pr[u];
+                q.x = jp < P ? q.x : 0.0f;
+                q.y = jp + 1 < P ? q.y : 0.0f;
+                q.z = jp + 2 < P ? q.z : 0.0f;
+                q.w = jp + 3 < P ? q.w : 0.0f;
+                *(float4 *)(&pt[buf][ph * PV_TJ + 4 * q4]) = q;
+            }
+        }
     };
-
-    float o[NCH];
-#pragma unroll
-    for (int c = 0; c < NCH; c++)
-        o[c] = 0.0f;
-    uint4 vr[PV_DEPTH];
-    float4 pr[PV_DEPTH];
-#pragma unroll
-    for (int d = 0; d < PV_DEPTH; d++)
-        load(d, vr[d], pr[d]);
-    for (int tb = 0; tb < ntile; tb += PV_DEPTH) {
+    float o = 0.0f;
+    auto group = [&](int tb, uint4 (&vr)[PV_DEPTH][VPT], float4 (&pr)[PV_DEPTH][PPT]) {
 #pragma unroll
         for (int d = 0; d < PV_DEPTH; d++) {
-            const int tile = tb + d;
-            if (tile >= ntile)
-                break;
-            const int buf = d & 1; // tb is a multiple of PV_DEPTH (even)
-            stage(buf, vr[d], pr[d]);
-            load(tile + PV_DEPTH, vr[d], pr[d]);
+            const int tile = tb + d, buf = d & 1; // tb is a multiple of PV_DEPTH (even)
+            stage(buf, tile, vr[d], pr[d]);
             __syncthreads();
-            const float *vv = &vt[buf][ln * PV_VST];
+            if (g < G && tile < ntile) { // tiles past the context skip their chain
+                const float *vv = &vt[buf][ln * PV_VST];
+                const float *pv = &pt[buf][wave * PV_TJ];
+                float4 xr[PV_AHEAD], prr[PV_AHEAD];
 #pragma unroll
-            for (int c = 0; c < NCH; c++) {
-                const int g = wave + 8 * c;
-                if (g < G) {
-                    const float *pv = &pt[buf][g * PV_TJ];
-                    float acc = o[c];
+                for (int a = 0; a < PV_AHEAD; a++) {
+                    xr[a] = *(const float4 *)(vv + 4 * a);
+                    prr[a] = *(const float4 *)(pv + 4 * a);
+                }
 #pragma unroll
-                    for (int j = 0; j < PV_TJ; j += 4) {
-                        const float4 pp = *(const float4 *)(pv + j);
-                        const float4 x = *(const float4 *)(vv + j);
-                        float q;
-                        q = pp.x * x.x;
-                        acc = acc + q;
-                        q = pp.y * x.y;
-                        acc = acc + q;
-                        q = pp.z * x.z;
-                        acc = acc + q;
-                        q = pp.w * x.w;
-                        acc = acc + q;
+                for (int gj = 0; gj < PV_TJ / 4; gj++) {
+                    const int a = gj % PV_AHEAD;
+                    const float4 x = xr[a], pp = prr[a];
+                    if (gj + PV_AHEAD < PV_TJ / 4) {
+                        xr[a] = *(const float4 *)(vv + 4 * (gj + PV_AHEAD));
+                        prr[a] = *(const float4 *)(pv + 4 * (gj + PV_AHEAD));
                     }
-                    o[c] = acc;
+                    float q;
+                    q = pp.x * x.x;
+                    o = o + q;
+                    q = pp.y * x.y;
+                    o = o + q;
+                    q = pp.z * x.z;
+                    o = o + q;
+                    q = pp.w * x.w;
+                    o = o + q;
                 }
             }
         }
-    }
+    };
+    uint4 va[PV_DEPTH][VPT], vb[PV_DEPTH][VPT];
+    float4 pa[PV_DEPTH][PPT], pb[PV_DEPTH][PPT];
 #pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        const int g = wave + 8 * c;
-        if (g < G && ln < ncol)
-            att[(size_t)t * D.qd + ((size_t)kvh * G + g) * HD + c0 + ln] = o[c];
+    for (int d = 0; d < PV_DEPTH; d++)
+        load(d, va[d], pa[d]);
+    for (int tb = 0; tb < ntile; tb += 2 * PV_DEPTH) {
+#pragma unroll
+        for (int d = 0; d < PV_DEPTH; d++)
+            load(tb + PV_DEPTH + d, vb[d], pb[d]);
+        group(tb, va, pa);
+        if (tb + PV_DEPTH >= ntile)
+            break;
+#pragma unroll
+        for (int d = 0; d < PV_DEPTH; d++)
+            load(tb + 2 * PV_DEPTH + d, va[d], pa[d]);
+        group(tb + PV_DEPTH, vb, pb);
     }
+    if (g < G && ln < ncol)
+        att[(size_t)t * D.qd + ((size_t)kvh * G + g) * HD + c0 + ln] = o;
 }
 
 size_t exact_softmax_lds(int s_stride) { return ((size_t)s_stride + (size_t)(s_stride / 64) * 64) * 4; }
@@ -379,11 +356,13 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
                        q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse ? 1 : 0, S, s_stride);
     hipLaunchKernelGGL(attn_softmax_kernel, dim3(D.n_heads, n), dim3(SM_THREADS), exact_softmax_lds(s_stride), st,
                        D, pos, S, s_stride);
-    const dim3 pg((HD + 63) / 64, D.n_kv, n);
-    if (G <= 8)
-        hipLaunchKernelGGL((attn_pv_kernel<HD, 1>), pg, dim3(PV_THREADS), 0, st, D, vc, pos, li, S, s_stride, att);
-    else
-        hipLaunchKernelGGL((attn_pv_kernel<HD, 2>), pg, dim3(PV_THREADS), 0, st, D, vc, pos, li, S, s_stride, att);
+    if (n < 8) {
+        const dim3 pg((HD + 63) / 64, D.n_kv * ((G + 1) / 2), n);
+        hipLaunchKernelGGL((attn_pv_kernel<HD, 2>), pg, dim3(128), 0, st, D, vc, pos, li, S, s_stride, att);
+    } else {
+        const dim3 pg((HD + 63) / 64, D.n_kv * ((G + 3) / 4), n);
+        hipLaunchKernelGGL((attn_pv_kernel<HD, 4>), pg, dim3(256), 0, st, D, vc, pos, li, S, s_stride, att);
+    }
     note_launch();
     note_launch();
     note_launch();

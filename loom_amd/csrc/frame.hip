@@ -54,6 +54,7 @@ __global__ void embed_kernel(int t, const uint8_t *__restrict__ w, int vocab, in
 }
 
 // ---- rmsnorm (tensor.zig:9-15) + int8 quantization for weight type QB --------------
+constexpr int EXACT_NORM_MAX_DIM = 7936; // the sequential sum's squares and chain ends fit 64 KB of LDS
 // One work group per lane; thread c owns the 32-value chunk c (dim <= 8192).
 // out_i = (x_i * scale) * w_i with scale = 1 / sqrt(ss/n + eps).  EXACT: ss
 // is the reference's sequential sum (one thread over the squares in index
@@ -68,7 +69,10 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(const float *__restrict
                                                          const float *__restrict__ w, float eps,
                                                          QAct qa, float *__restrict__ normed) {
     __shared__ float red[4];
-    __shared__ __align__(16) float sq[EXACT ? 8192 : 1];
+    __shared__ __align__(16) float sq[EXACT ? EXACT_NORM_MAX_DIM : 1];
+    __shared__ __align__(16) float ends[EXACT ? EXACT_NORM_MAX_DIM : 1];
+    __shared__ double csum[EXACT ? 128 : 1];
+    __shared__ uint32_t fst[EXACT ? 128 : 1];
     const int lane_v = blockIdx.x, c = threadIdx.x, chunks = dim / 32;
     const bool live = c < chunks;
     const int cc = live ? c : chunks - 1;
@@ -91,31 +95,24 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(const float *__restrict
     ss = live ? ss : 0.0f;
     float total;
     if constexpr (EXACT) {
-        if (live) {
+        // the squares in order, zero-padded to whole 64-value chunks, summed
+        // sequentially (speculative composition: the reference's own sum)
+        const int C = (dim + 63) / 64;
+        if (c < 2 * C) {
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                float4 p;
-                p.x = v[i].x * v[i].x;
-                p.y = v[i].y * v[i].y;
-                p.z = v[i].z * v[i].z;
-                p.w = v[i].w * v[i].w;
+                float4 p = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (live) {
+                    p.x = v[i].x * v[i].x;
+                    p.y = v[i].y * v[i].y;
+                    p.z = v[i].z * v[i].z;
+                    p.w = v[i].w * v[i].w;
+                }
                 *(float4 *)(sq + c * 32 + 4 * i) = p;
             }
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            float acc = 0.0f;
-            for (int i = 0; i < dim; i += 4) {
-                const float4 p = *(const float4 *)(sq + i);
-                acc = acc + p.x;
-                acc = acc + p.y;
-                acc = acc + p.z;
-                acc = acc + p.w;
-            }
-            red[0] = acc;
-        }
-        __syncthreads();
-        total = red[0];
+        total = seq_sum_nonneg<4>(sq, C, ends, csum, fst, &red[0]);
     } else {
         total = block_sum_waves(wave_sum_f(ss), red);
     }
@@ -1107,7 +1104,7 @@ static int frame_check(const loomhip_model *m, size_t n, size_t *ffn_max) {
     if (!m || !m->layers || n == 0 || n > 256)
         return fail(LOOMHIP_ERR_ARG, "token_frame: bad model or lane count %zu (1..256)", n);
     const size_t dim = m->dim, hd = m->head_dim, qd = m->n_heads * hd;
-    if (dim == 0 || dim % 32 || dim > 8192 || qd % 32 || (hd != 48 && hd != 64 && hd != 128) ||
+    if (dim == 0 || dim % 32 || dim > (size_t)EXACT_NORM_MAX_DIM || qd % 32 || (hd != 48 && hd != 64 && hd != 128) ||
         m->n_kv_heads == 0 || m->n_heads % m->n_kv_heads || m->n_heads / m->n_kv_heads > MAX_G ||
         m->rope_dim > hd || m->rope_dim % 2 || m->ctx_len == 0 || m->vocab == 0)
         return fail(LOOMHIP_DECLINED, "token_frame: dims not served (dim %zu, head_dim %zu, heads %zu/%zu)",
