@@ -80,13 +80,17 @@ uint64_t loomhip_take_launch_count(void);
  * every launch of the tagged kernels (the reference's LOOM_VK_KERNEL_PROF
  * timestamps, src/vulkan/device.zig:158-167,245-252).  Enabling resets the
  * totals; launches inside a stream capture are not timed. */
-#define LOOMHIP_KT_GATE_UP 0 /* grouped gate/up + SwiGLU expert kernel */
-#define LOOMHIP_KT_DOWN 1    /* grouped down expert kernel */
-#define LOOMHIP_KT_DENSE 2   /* dense dequant-fused matvec */
-#define LOOMHIP_KT_ATTN 3    /* token frame: attention over the K/V cache (partials) */
-#define LOOMHIP_KT_HEAD 4    /* token frame: output head matvec */
-#define LOOMHIP_KT_QKV 5     /* token frame: the q/k/v matvec launch and the wo matvec */
-#define LOOMHIP_KT_COUNT 6
+#define LOOMHIP_KT_GATE_UP 0      /* grouped gate/up + SwiGLU expert kernel */
+#define LOOMHIP_KT_DOWN 1         /* grouped down expert kernel */
+#define LOOMHIP_KT_DENSE 2        /* dense dequant-fused matvec */
+#define LOOMHIP_KT_ATTN 3         /* token frame, FAST: split-context attention partials */
+#define LOOMHIP_KT_HEAD 4         /* token frame: output head matvec */
+#define LOOMHIP_KT_QKV 5          /* token frame: the q/k/v matvec launch */
+#define LOOMHIP_KT_WO 6           /* token frame: the wo matvec (+ residual) */
+#define LOOMHIP_KT_ATTN_SCORES 7  /* token frame, PARITY: attention scores */
+#define LOOMHIP_KT_ATTN_SOFTMAX 8 /* token frame, PARITY: softmax (max, exp, ordered sum, p) */
+#define LOOMHIP_KT_ATTN_PV 9      /* token frame, PARITY: position-ordered P.V */
+#define LOOMHIP_KT_COUNT 10
 void loomhip_profile_kernels(int enable);
 /* Waits for the recorded events; total milliseconds and launch count of tag. */
 int loomhip_kernel_time(int tag, double *total_ms, uint64_t *launches);
@@ -343,8 +347,9 @@ typedef struct {
  * n_tok > 1: each distinct expert once per call in ascending order, its
  * tokens batched (moeBatchUnion, llama.zig:1828-1924).  More distinct
  * experts than capacity run in rounds of at most `capacity` gets.  out is
- * [n_tok][dim] (device, overwritten); ids_out/gates_out ([n_tok][n_used],
- * host) are optional.  Synchronises `stream` once per call (the ids). */
+ * [n_tok][dim] (device, overwritten; undefined after a failed call);
+ * ids_out/gates_out ([n_tok][n_used], host) are optional.  Synchronises
+ * `stream` once per call (the ids). */
 int loomhip_moe_layer_cached(const loomhip_moe_layer_ec *L, loomhip_ec *ec, const float *normed,
                              size_t n_tok, float *out, uint32_t *ids_out, float *gates_out,
                              void *stream);

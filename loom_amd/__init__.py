@@ -22,9 +22,11 @@ F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
 GATING_SOFTMAX, GATING_SIGMOID, GATING_SOFTMAX_TOPK = 1, 2, 3
 COMBINE_SELECTION, COMBINE_EXPERT_ASC, COMBINE_SELECTION_ADD = 0, 1, 2
 KT_GATE_UP, KT_DOWN, KT_DENSE, KT_ATTN, KT_HEAD, KT_QKV = 0, 1, 2, 3, 4, 5
+KT_WO, KT_ATTN_SCORES, KT_ATTN_SOFTMAX, KT_ATTN_PV = 6, 7, 8, 9
 NUMERICS_PARITY, NUMERICS_FAST = 0, 1
 KT_NAMES = {KT_GATE_UP: "gate_up", KT_DOWN: "down", KT_DENSE: "dense", KT_ATTN: "attn",
-            KT_HEAD: "head", KT_QKV: "qkvo"}
+            KT_HEAD: "head", KT_QKV: "qkv", KT_WO: "wo", KT_ATTN_SCORES: "attn_scores",
+            KT_ATTN_SOFTMAX: "attn_softmax", KT_ATTN_PV: "attn_pv"}
 
 
 class LoomHipError(RuntimeError):

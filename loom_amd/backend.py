@@ -138,11 +138,14 @@ _KERNEL_SYMBOLS = {
     "down": "moe_down_decode_kernel (n <= 4) / dmmv_kernel<T, NT, FUSED=false> / from 16 tokens "
             "mmq_kernel<T, 1, false, SBW> (grouped down)",
     "dense": "dmmv_kernel<T, NT, false> / from 16 vectors mmq_kernel<T, MT, false, SBW> (dense matvec)",
-    "attn": "attn_direct_kernel (FAST numerics, more than 4 lanes) / attn_partial_kernel (attention over "
-            "the fp16 K/V cache)",
+    "attn": "attn_direct_kernel (FAST numerics, more than 4 lanes) / attn_partial_kernel (FAST split-context "
+            "attention over the fp16 K/V cache)",
     "head": "dmmv_kernel<T, NT, false> / from 16 lanes mmq_stream_kernel<T, MT, false> (output head)",
-    "qkvo": "dmmv_seg_kernel<NT> + dmmv_kernel<T, NT, false> / from 16 lanes mmq_seg_kernel<1, SBW> (q, k, v) "
-            "+ mmq_kernel<T, 1, false, SBW> (wo)",
+    "qkv": "dmmv_seg_kernel<NT> / from 16 lanes mmq_seg_kernel<1, SBW> (q, k, v in one launch)",
+    "wo": "dmmv_kernel<T, NT, false> / from 16 lanes mmq_kernel<T, 1, false, SBW> (wo + residual)",
+    "attn_scores": "attn_scores_kernel<HD> (PARITY: dotF32-order scores)",
+    "attn_softmax": "attn_softmax_kernel (PARITY: max, exp, position-ordered sum, p)",
+    "attn_pv": "attn_pv_kernel<HD, W> (PARITY: position-ordered P.V)",
 }
 
 

@@ -352,10 +352,15 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
                       int li, bool fuse, float *S, int s_stride, float *att, size_t n, hipStream_t st) {
     const int n_chunks = (D.ctx + ATT_TC - 1) / ATT_TC;
     const int G = D.n_heads / D.n_kv;
+    int ph = prof_begin(LOOMHIP_KT_ATTN_SCORES, st);
     hipLaunchKernelGGL(attn_scores_kernel<HD>, dim3(n_chunks, D.n_kv, n), dim3(SC_THREADS), 0, st, D, q, k, v,
                        q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse ? 1 : 0, S, s_stride);
+    prof_end(ph, st);
+    ph = prof_begin(LOOMHIP_KT_ATTN_SOFTMAX, st);
     hipLaunchKernelGGL(attn_softmax_kernel, dim3(D.n_heads, n), dim3(SM_THREADS), exact_softmax_lds(s_stride), st,
                        D, pos, S, s_stride);
+    prof_end(ph, st);
+    ph = prof_begin(LOOMHIP_KT_ATTN_PV, st);
     if (n < 8) {
         const dim3 pg((HD + 63) / 64, D.n_kv * ((G + 1) / 2), n);
         hipLaunchKernelGGL((attn_pv_kernel<HD, 2>), pg, dim3(128), 0, st, D, vc, pos, li, S, s_stride, att);
@@ -363,6 +368,7 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
         const dim3 pg((HD + 63) / 64, D.n_kv * ((G + 3) / 4), n);
         hipLaunchKernelGGL((attn_pv_kernel<HD, 4>), pg, dim3(256), 0, st, D, vc, pos, li, S, s_stride, att);
     }
+    prof_end(ph, st);
     note_launch();
     note_launch();
     note_launch();

@@ -32,6 +32,8 @@ struct EcSlot {
     bool has_use = false;          // last_use has been recorded at least once
     bool open = false;                 // handed out, not yet released
     hipStream_t open_stream = nullptr; // ... on this stream (may be the null stream)
+    hipEvent_t fill = nullptr;         // recorded on the copy stream after the slot's latest fill
+    bool fill_pending = false;         // that fill may still be in flight
 };
 
 } // namespace lh
@@ -48,7 +50,6 @@ struct loomhip_ec {
     std::vector<uint64_t> access;
     std::vector<size_t> open; // slots handed out since the last release
     loomhip_ec_stats stats{};
-    hipEvent_t fill_done = nullptr;
 };
 
 namespace lh {
@@ -139,12 +140,28 @@ static int fill_slot(loomhip_ec *c, size_t s, size_t id, bool wait, hipStream_t 
         e = hipStreamWaitEvent(g_ctx.copy, sl.last_use, 0);
     if (e == hipSuccess)
         e = hipMemcpyAsync(slot_ptr(c, s), c->src[id], c->src_len[id], hipMemcpyHostToDevice, g_ctx.copy);
-    if (e == hipSuccess && wait) {
-        e = hipEventRecord(c->fill_done, g_ctx.copy);
-        if (e == hipSuccess)
-            e = hipStreamWaitEvent(consumer, c->fill_done, 0);
-    }
+    if (e == hipSuccess)
+        e = hipEventRecord(sl.fill, g_ctx.copy);
+    sl.fill_pending = e == hipSuccess;
+    if (e == hipSuccess && wait)
+        e = hipStreamWaitEvent(consumer, sl.fill, 0);
     return e == hipSuccess ? LOOMHIP_OK : hip_fail(e, "expert cache fill");
+}
+
+// A hit on a slot whose fill (a prefetch, or a miss taken on another stream)
+// may still be in flight: the consumer's stream waits for that fill.
+static int wait_fill(EcSlot &sl, hipStream_t consumer) {
+    if (!sl.fill_pending)
+        return LOOMHIP_OK;
+    hipError_t e = hipEventQuery(sl.fill);
+    if (e == hipSuccess) {
+        sl.fill_pending = false;
+        return LOOMHIP_OK;
+    }
+    if (e != hipErrorNotReady)
+        return hip_fail(e, "expert cache fill query");
+    e = hipStreamWaitEvent(consumer, sl.fill, 0);
+    return e == hipSuccess ? LOOMHIP_OK : hip_fail(e, "expert cache fill wait");
 }
 
 static void mark_open(loomhip_ec *c, size_t s, hipStream_t st) {
@@ -165,6 +182,8 @@ static int ec_get(loomhip_ec *c, size_t id, hipStream_t st, size_t *slot_out) {
     size_t s = lru_find(c, id);
     if (s != EC_NIL) {
         c->stats.lru_hits += 1;
+        if (int rc = wait_fill(c->slot[s], st))
+            return rc;
         mark_open(c, s, st);
         *slot_out = s;
         return LOOMHIP_OK;
@@ -393,6 +412,13 @@ static int moe_cached(const loomhip_moe_layer_ec &L, loomhip_ec *c, const float 
                 pair_slot[p] = (int)s;
             }
     }
+    // Every exit from here on records g_ec_tables_done after the table
+    // uploads already enqueued, so the next call waits for them before it
+    // rewrites the pinned staging; after a failed call `out` is undefined.
+    auto tables_done = [&](int rc) {
+        (void)hipEventRecord(g_ec_tables_done, st);
+        return rc;
+    };
     const size_t cap = c->capacity ? c->capacity : list.size();
     bool first_round = true;
     size_t tab_i = 0;
@@ -403,7 +429,7 @@ static int moe_cached(const loomhip_moe_layer_ec &L, loomhip_ec *c, const float 
         for (size_t i = r0; i < r1; i++) {
             size_t s;
             if (int rc = ec_get(c, L.id_base + (size_t)list[i].expert, st, &s))
-                return rc;
+                return tables_done(rc);
             plane[i - r0] = (int)s;
         }
         // tables of this round
@@ -438,7 +464,7 @@ static int moe_cached(const loomhip_moe_layer_ec &L, loomhip_ec *c, const float 
         char *dt = base + o_tab + tab_i * tab_bytes;
         e = hipMemcpyAsync(dt, ht, tab_bytes, hipMemcpyHostToDevice, st);
         if (e != hipSuccess)
-            return hip_fail(e, "moe_cached: tables");
+            return tables_done(hip_fail(e, "moe_cached: tables"));
         const int *d_src = (const int *)dt;
         const DmmvGroup *d_groups = (const DmmvGroup *)(dt + align16(P * 4));
         const int *d_first = (const int *)((const char *)d_groups + align16(P * sizeof(DmmvGroup)));
@@ -465,7 +491,7 @@ static int moe_cached(const loomhip_moe_layer_ec &L, loomhip_ec *c, const float 
             bool ok = launch_dmmv(L.gate_t, nt, true, gu, st);
             prof_end(ph, st);
             if (!ok)
-                return fail(LOOMHIP_ERR_ARG, "moe_cached: gate/up partials exceed LDS");
+                return tables_done(fail(LOOMHIP_ERR_ARG, "moe_cached: gate/up partials exceed LDS"));
             launch_quant_act(L.down_t, act, (int)L.ffn, (int)L.ffn, np, qa, st);
             DmmvParams dn{};
             dn.w = c->slab + L.down_off;
@@ -486,13 +512,13 @@ static int moe_cached(const loomhip_moe_layer_ec &L, loomhip_ec *c, const float 
             ok = launch_dmmv(L.down_t, nt, false, dn, st);
             prof_end(ph, st);
             if (!ok)
-                return fail(LOOMHIP_ERR_ARG, "moe_cached: down partials exceed LDS");
+                return tables_done(fail(LOOMHIP_ERR_ARG, "moe_cached: down partials exceed LDS"));
         }
         hipLaunchKernelGGL(ec_combine_kernel, dim3((L.dim + 255) / 256, n), dim3(256), 0, st, y, d_first,
                            d_pair, d_gate, (int)L.dim, first_round ? 1 : 0, out);
         note_launch();
         if (int rc = ec_release(c, st))
-            return rc;
+            return tables_done(rc);
         first_round = false;
         if (r1 >= list.size())
             break;
@@ -540,10 +566,11 @@ int loomhip_ec_create(size_t capacity, size_t pin_slots, size_t slot_bytes, size
     c->src_len.assign(n_ids, 0);
     c->access.assign(n_ids, 0);
     hipError_t e = hipMalloc((void **)&c->slab, c->slot_bytes * (capacity + pin_slots));
-    for (size_t s = 0; e == hipSuccess && s < c->slot.size(); s++)
+    for (size_t s = 0; e == hipSuccess && s < c->slot.size(); s++) {
         e = hipEventCreateWithFlags(&c->slot[s].last_use, hipEventDisableTiming);
-    if (e == hipSuccess)
-        e = hipEventCreateWithFlags(&c->fill_done, hipEventDisableTiming);
+        if (e == hipSuccess)
+            e = hipEventCreateWithFlags(&c->slot[s].fill, hipEventDisableTiming);
+    }
     if (e != hipSuccess) {
         loomhip_ec_destroy(c);
         return hip_fail(e, "ec_create");
@@ -556,11 +583,12 @@ void loomhip_ec_destroy(loomhip_ec *c) {
     if (!c)
         return;
     (void)hipDeviceSynchronize(); // no copy or kernel may still touch the slab
-    for (auto &s : c->slot)
+    for (auto &s : c->slot) {
         if (s.last_use)
             (void)hipEventDestroy(s.last_use);
-    if (c->fill_done)
-        (void)hipEventDestroy(c->fill_done);
+        if (s.fill)
+            (void)hipEventDestroy(s.fill);
+    }
     if (c->slab)
         (void)hipFree(c->slab);
     delete c;

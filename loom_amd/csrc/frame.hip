@@ -1016,7 +1016,7 @@ static FrameWs frame_layout(char *base, size_t n, const loomhip_model *m, size_t
 // lanes (16 for wo: more work groups for its 2048 rows; 32 for the head,
 // whose 255 MB would be read once per group).
 static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameWs &w, size_t n,
-                         QAct x, float *out, int accumulate, hipStream_t st, int tag = LOOMHIP_KT_QKV,
+                         QAct x, float *out, int accumulate, hipStream_t st, int tag = LOOMHIP_KT_DENSE,
                          bool mmq_ok = false, int mmq_group = 32) {
     DmmvParams p{};
     p.w = (const uint8_t *)wt;
@@ -1124,6 +1124,8 @@ static int frame_check(const loomhip_model *m, size_t n, size_t *ffn_max) {
         if (l.is_moe) {
             if (l.moe.dim != dim)
                 return fail(LOOMHIP_ERR_ARG, "token_frame: layer %zu MoE dim %zu != %zu", li, l.moe.dim, dim);
+            if (int rc = moe_frame_check(&l.moe, n))
+                return rc;
         } else {
             const int gq = act_block(l.ffn_gate_t);
             if (l.ffn_gate_t != l.ffn_up_t || !dmmv_supported(l.ffn_gate_t, (int)dim) ||
@@ -1222,17 +1224,16 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
             note_launch();
         }
         const float *qin = fuse_rope ? w.q : w.qrot;
-        int ph = prof_begin(LOOMHIP_KT_ATTN, st);
         if (parity) {
             // the reference's own order over the whole context: scores, softmax, P.V
             if (!launch_attn_exact(D, qin, w.k, w.v, l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li,
                                    fuse_rope, w.S, w.s_stride, w.att, n, st))
                 return fail(LOOMHIP_ERR_ARG, "token_frame: exact attention declined");
-            prof_end(ph, st);
             launch_quant_act(l.wo_t, w.att, D.qd, D.qd, (int)n, w.qa_att, st);
-            if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_QKV, true, 16))
+            if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_WO, true, 16))
                 return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
         } else {
+        const int ph = prof_begin(LOOMHIP_KT_ATTN, st);
         const dim3 agrid(n_chunks, D.n_kv, n);
         // records of the merge: chunks of ATT_TC positions, ATT_TC_DIRECT direct
         const int span = direct ? ATT_TC_DIRECT : ATT_TC;
@@ -1267,7 +1268,7 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
             hipLaunchKernelGGL(attn_combine_kernel<32>, dim3((D.qd + 255) / 256, n), dim3(1024), cmb_lds, st,
                                D, w.part, pos, n_rec, span, direct ? 1 : 0, w.qa_att);
         note_launch();
-        if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_QKV, true, 16))
+        if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_WO, true, 16))
             return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
         }
         // FFN block (llama.zig:1203-1224)

@@ -63,6 +63,8 @@ int moe_noalloc_setup(int device);
 int moe_layer_fused_norm(const loomhip_moe_layer *L, const float *x, const float *norm_w, float eps, size_t n_tok,
                          int combine, float *out, uint32_t *ids_out, hipStream_t st);
 bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok);
+// What the MoE layer would decline at n tokens, checked before any launch.
+int moe_frame_check(const loomhip_moe_layer *L, size_t n);
 void ec_release_scratch();
 
 } // namespace lh

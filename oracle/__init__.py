@@ -76,7 +76,14 @@ class MoeLayer(C.Structure):
         ("gate_exps", Tensor),
         ("up_exps", Tensor),
         ("down_exps", Tensor),
+        ("shexp_gate", Tensor),
+        ("shexp_up", Tensor),
+        ("shexp_down", Tensor),
     ]
+
+
+class ExpertRef(C.Structure):
+    _fields_ = [("gate", Tensor), ("up", Tensor), ("down", Tensor), ("weight", C.c_float)]
 
 
 class Layer(C.Structure):
@@ -164,6 +171,7 @@ def lib() -> C.CDLL:
             "lo_route": (None, [C.POINTER(RouteCfg), vp, vp, vp, vp]),
             "lo_moe_layer_token": (None, [C.POINTER(MoeLayer), vp, vp, vp, vp]),
             "lo_moe_batch_union": (None, [C.POINTER(MoeLayer), vp, vp, sz, vp, vp]),
+            "lo_moe_ffn_block": (None, [vp, sz, vp, sz, vp]),
             "lo_seq_cache_bytes": (sz, [C.POINTER(Model)]),
             "lo_step": (i, [C.POINTER(Model), C.POINTER(Seq), C.c_uint32, vp]),
             "lo_decode_batch": (i, [C.POINTER(Model), vp, vp, sz, vp]),
@@ -372,7 +380,10 @@ class MoeWeights:
 
     def __init__(self, dim, ffn, n_expert, n_used, router, gate, up, down, gate_t, up_t, down_t,
                  router_bias=None, sel_bias=None, gating=GATING_SOFTMAX, weights_norm=True,
-                 weights_scale=1.0):
+                 weights_scale=1.0, shexp=None):
+        """shexp: optional shared expert (gate, up, down, gate_t, up_t, down_t, shexp_ffn),
+        host GGML bytes of one plane each."""
+        self.shexp = shexp
         self.dim, self.ffn, self.n_expert, self.n_used = dim, ffn, n_expert, n_used
         self.router = np.ascontiguousarray(router, np.float32)
         self.gate, self.up, self.down = gate, up, down
@@ -392,6 +403,11 @@ class MoeWeights:
         L.gate_exps = Tensor(self.gate_t, self.gate.ctypes.data, self.dim, self.ffn, self.n_expert)
         L.up_exps = Tensor(self.up_t, self.up.ctypes.data, self.dim, self.ffn, self.n_expert)
         L.down_exps = Tensor(self.down_t, self.down.ctypes.data, self.ffn, self.dim, self.n_expert)
+        if self.shexp is not None:
+            g, u, d, gt, ut, dt, sf = self.shexp
+            L.shexp_gate = Tensor(gt, g.ctypes.data, self.dim, sf, 1)
+            L.shexp_up = Tensor(ut, u.ctypes.data, self.dim, sf, 1)
+            L.shexp_down = Tensor(dt, d.ctypes.data, sf, self.dim, 1)
         return L
 
 
@@ -403,6 +419,20 @@ def moe_layer_token(w: MoeWeights, normed):
     gates = np.empty(w.n_used, np.float32)
     lib().lo_moe_layer_token(C.byref(L), _p(normed), _p(acc), _p(ids), _p(gates))
     return acc, ids, gates
+
+
+def moe_ffn_block(normed, refs):
+    """backend.moeFfnBlock: refs = [(gate, up, down, gate_t, up_t, down_t, ffn, weight)],
+    host GGML bytes of one plane each; returns out[dim]."""
+    normed = np.ascontiguousarray(normed, np.float32)
+    dim = normed.size
+    arr = (ExpertRef * len(refs))()
+    for i, (g, u, d, gt, ut, dt, f, wt) in enumerate(refs):
+        arr[i] = ExpertRef(Tensor(gt, g.ctypes.data, dim, f, 1), Tensor(ut, u.ctypes.data, dim, f, 1),
+                           Tensor(dt, d.ctypes.data, f, dim, 1), wt)
+    out = np.empty(dim, np.float32)
+    lib().lo_moe_ffn_block(_p(normed), dim, C.cast(arr, C.c_void_p), len(refs), _p(out))
+    return out
 
 
 def moe_batch_union(w: MoeWeights, bnormed, bx):

@@ -130,6 +130,10 @@ typedef struct {
     const float *router_bias; /* ffn_gate_inp.bias (logit bias), nullable */
     const float *sel_bias;    /* exp_probs_b (selection-only), nullable */
     lo_tensor gate_exps, up_exps, down_exps;
+    /* the shared expert (ffn_{gate,up,down}_shexp), data NULL when absent:
+     * always on, unweighted, added after the routed sum (deepseek.zig:
+     * 1497-1502) */
+    lo_tensor shexp_gate, shexp_up, shexp_down;
 } lo_moe_layer;
 
 /* llama.moeLayer + moeRun at one token: acc = sum_sel gate * ffn(x), in
@@ -140,6 +144,16 @@ void lo_moe_layer_token(const lo_moe_layer *L, const float *normed, float *acc, 
  * visited in ascending id order; ids/gates are [n][n_used] when non-null. */
 void lo_moe_batch_union(const lo_moe_layer *L, const float *bnormed, float *bx, size_t n,
                         uint32_t *ids, float *gates);
+
+/* backend.moeFfnBlock (compute/cpu.zig:23-30, metal/backend.zig:2322-2410):
+ * out = sum over the refs, in order, of weight * denseFFN_ref(normed) (the
+ * reference's host loop acc += gate * ffn_out, deepseek.zig:1485-1487; the
+ * shared expert joins as one more ref of weight 1). */
+typedef struct {
+    lo_tensor gate, up, down; /* one plane each: [ffn][dim], [ffn][dim], [dim][ffn] */
+    float weight;
+} lo_expert_ref;
+void lo_moe_ffn_block(const float *normed, size_t dim, const lo_expert_ref *refs, size_t n, float *out);
 
 /* ---- whole-model decode (llama.zig:1111-1227, 1939-2043) ----------------- */
 typedef struct {

@@ -205,6 +205,43 @@ static void route_token(const lo_moe_layer *L, const float *normed, uint32_t *id
 }
 
 /* llama.zig:1307-1419 moeRun (local path) + denseFFN 952-958 */
+/* llama.zig:952-958 denseFFN of one plane each: gate and up matvecs, SwiGLU,
+ * down; out[dim]. */
+static void dense_ffn(const lo_tensor *gt, const lo_tensor *ut, const lo_tensor *dt, const float *x, size_t dim,
+                      float *out) {
+    size_t f = gt->ne1;
+    float *g = (float *)malloc(f * sizeof(float)), *u = (float *)malloc(f * sizeof(float));
+    float *a = (float *)malloc(f * sizeof(float));
+    lo_matvec(gt->ty, g, gt->data, x, f, dim);
+    lo_matvec(ut->ty, u, ut->data, x, f, dim);
+    lo_swiglu(a, g, u, f);
+    lo_matvec(dt->ty, out, dt->data, a, dim, f);
+    free(g);
+    free(u);
+    free(a);
+}
+
+/* acc += the shared expert's FFN of x (tensor.zig add: acc[i] + v[i]). */
+static void shared_ffn_add(const lo_moe_layer *L, const float *x, float *acc) {
+    float *o = (float *)malloc(L->dim * sizeof(float));
+    dense_ffn(&L->shexp_gate, &L->shexp_up, &L->shexp_down, x, L->dim, o);
+    lo_add(acc, o, L->dim);
+    free(o);
+}
+
+void lo_moe_ffn_block(const float *normed, size_t dim, const lo_expert_ref *refs, size_t n, float *out) {
+    float *o = (float *)malloc(dim * sizeof(float));
+    memset(out, 0, dim * sizeof(float));
+    for (size_t r = 0; r < n; r++) {
+        dense_ffn(&refs[r].gate, &refs[r].up, &refs[r].down, normed, dim, o);
+        for (size_t i = 0; i < dim; i++) {
+            float p = refs[r].weight * o[i];
+            out[i] = out[i] + p;
+        }
+    }
+    free(o);
+}
+
 void lo_moe_layer_token(const lo_moe_layer *L, const float *normed, float *acc, uint32_t *ids_out,
                         float *gates_out) {
     size_t k = L->route.n_used, dim = L->dim, f = L->ffn;
@@ -225,6 +262,8 @@ void lo_moe_layer_token(const lo_moe_layer *L, const float *normed, float *acc, 
             acc[i] = acc[i] + p;
         }
     }
+    if (L->shexp_gate.data) /* deepseek.zig:1497-1502: denseFFN(shexp), add(acc, ffn_out) */
+        shared_ffn_add(L, normed, acc);
     if (ids_out)
         memcpy(ids_out, ids, k * sizeof(uint32_t));
     if (gates_out)
@@ -279,6 +318,9 @@ void lo_moe_batch_union(const lo_moe_layer *L, const float *bnormed, float *bx, 
             }
         }
     }
+    if (L->shexp_gate.data) /* the shared expert of every lane, after its routed experts */
+        for (size_t t = 0; t < n; t++)
+            shared_ffn_add(L, bnormed + t * dim, bx + t * dim);
     if (ids_out)
         memcpy(ids_out, ids, n * k * sizeof(uint32_t));
     if (gates_out)

@@ -216,3 +216,45 @@ def test_cached_layer_matches_resident(ec_mod, oracle, n_tok, cap, pin):
     st = ec.stats
     assert (st.pin_hits, st.lru_hits, st.disk_misses) == tuple(int(c) for c in counts)
     ec.close()
+
+
+def test_hit_on_a_prefetched_slot_waits_for_its_fill(ec_mod):
+    """A prefetch fills its slot on the copy stream; a get that hits that slot
+    right away, from another (non-blocking) stream, must see the whole block:
+    the hit makes the consumer wait for the fill still in flight.  Large
+    blocks, each slot first filled with another expert's bytes, so a read
+    that ran ahead of the fill would see the wrong bytes."""
+    import torch
+
+    n_ids, slot, cap = 6, 16 << 20, 2
+    rng = np.random.default_rng(9)
+    host = ec_mod.HostBuffer(n_ids * slot)
+    host.array[:] = rng.integers(0, 256, host.nbytes, dtype=np.uint8)
+    ec = ec_mod.ExpertCache(cap, slot, n_ids)
+    for i in range(n_ids):
+        ec.set_source(i, host, i * slot, slot)
+    hip = _hip()
+    hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    side = torch.cuda.Stream()  # non-blocking with respect to the library's copy stream
+    for rnd in range(3):
+        base = 2 * (rnd % 2)
+        for i in (base, base + 1):  # occupy both slots with other experts' bytes
+            ec.get(i)
+        ec.release()
+        torch.cuda.synchronize()
+        want = [4, 5] if rnd != 1 else [5, 4]
+        ec.prefetch(want)  # both slots refilled asynchronously
+        outs = []
+        for i in want:
+            addr = ec.get(i, stream=side.cuda_stream)
+            o = torch.empty(slot, dtype=torch.uint8, device="cuda")
+            assert hip.hipMemcpyAsync(o.data_ptr(), addr, slot, 3, C.c_void_p(side.cuda_stream)) == 0
+            outs.append((i, o))
+        ec.release(stream=side.cuda_stream)
+        side.synchronize()
+        for i, o in outs:
+            assert np.array_equal(o.cpu().numpy(), host.array[i * slot:(i + 1) * slot]), (rnd, i)
+        ec.clear()
+    st = ec.stats
+    assert st.warmup_reads == 6 and st.lru_hits == 6
+    ec.close()

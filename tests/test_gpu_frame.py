@@ -245,3 +245,31 @@ def test_frame_declines_unserved_dims(lh):
     loom_amd.take_launch_count()
     assert dec.step() == loom_amd.DECLINED
     assert loom_amd.take_launch_count() == 0
+
+
+@pytest.mark.parametrize("bad", ["top17", "gate_up_types", "no_router"])
+def test_frame_declines_unserved_moe_layer(lh, bad):
+    """A MoE layer the routed path would refuse (top-k above 16, gate and up
+    of different types, no router) is caught before the frame launches
+    anything: DECLINED (ERR_ARG for a missing router), no launch, no K/V row
+    written."""
+    import loom_amd
+
+    spec = _qwen_small(lh, ctx_len=8)
+    dm = lh.DeviceModel.synth(spec, seed=1)
+    L = dm.layers[1].moe
+    if bad == "top17":
+        L.n_used = 17
+    elif bad == "gate_up_types":
+        L.up_t = loom_amd.Q6_K
+    else:
+        L.router = None
+    dec = lh.Decoder(dm, 1)
+    loom_amd.take_launch_count()
+    if bad == "no_router":
+        with pytest.raises(loom_amd.LoomHipError):
+            dec.step()
+    else:
+        assert dec.step() == loom_amd.DECLINED
+    assert loom_amd.take_launch_count() == 0
+    assert int(dec.k_cache.abs().sum().item()) == 0

@@ -270,3 +270,92 @@ def test_hottest_within_budget_kat(oracle):
     got = oracle.hottest_within_budget(np.array(kat["counts"], np.uint64), kat["expert_bytes"],
                                        kat["budget"])
     assert sorted(got) == sorted(kat["expect_ids_set"])
+
+
+# ---- shared expert and moeFfnBlock -------------------------------------------------
+
+
+def _shexp(oracle, dim, sffn, seed, t=Q4_K, down_t=Q6_K):
+    rng = np.random.default_rng(seed)
+    g = npref.pinned_scale_blocks(t, sffn, dim, rng)
+    u = npref.pinned_scale_blocks(t, sffn, dim, rng)
+    d = npref.pinned_scale_blocks(down_t, dim, sffn, rng)
+    return g, u, d, t, t, down_t, sffn
+
+
+def _ffn64(gate_t, g, u, down_t, d, x, dim, f, plane=0):
+    xq = _q256(x)
+    gt = _plane(gate_t, g, plane, f, dim) @ xq
+    ut = _plane(gate_t, u, plane, f, dim) @ xq
+    return _plane(down_t, d, plane, dim, f) @ _q256(gt / (1.0 + np.exp(-gt)) * ut)
+
+
+@pytest.mark.parametrize("slip", [None, "no_shared", "shared_weighted", "shared_before_norm"])
+def test_moe_layer_with_shared_expert_against_float64(oracle, slip):
+    """deepseek.zig:1485-1502: acc = sum over the selected experts of gate *
+    FFN_e(x), then acc += FFN_shared(x) (unweighted, wider).  Against a
+    float64 forward within 2e-3; the planted slips (shared expert dropped,
+    scaled by the last gate, fed a scaled input) miss by far
+    more."""
+    dim, ffn, sffn, E, k = 256, 256, 512, 8, 2
+    w = _layer(oracle, dim, ffn, E, k, seed=15)
+    w.shexp = _shexp(oracle, dim, sffn, seed=16)
+    g, u, d, gt_, _, dt_, _ = w.shexp
+    worst = 0.0
+    for s in range(4):
+        x = oracle.normal(dim, 500 + s, 0.0, 1.0)
+        got, ids, gates = oracle.moe_layer_token(w, x)
+        want = np.zeros(dim)
+        for e, gg in zip(ids, gates):
+            want += float(gg) * _ffn64(w.gate_t, w.gate, w.up, w.down_t, w.down, x, dim, ffn, plane=e)
+        sh = _ffn64(gt_, g, u, dt_, d, x, dim, sffn)
+        if slip is None:
+            want += sh
+        elif slip == "shared_weighted":
+            want += float(gates[-1]) * sh
+        elif slip == "shared_before_norm":
+            want += _ffn64(gt_, g, u, dt_, d, 3.0 * x, dim, sffn)
+        worst = max(worst, float(np.abs(got - want).max() / np.abs(want).max()))
+    if slip is None:
+        assert worst < 2e-3, worst
+    else:
+        assert worst > 2e-2, (slip, worst)
+
+
+def test_moe_batch_union_shared_expert_matches_per_token(oracle):
+    """The batched layer adds each lane's shared expert after its routed
+    experts: per lane within the reference's batch bound of moeRun + shared."""
+    dim, ffn, sffn, E, k, n = 256, 256, 512, 16, 4, 5
+    w = _layer(oracle, dim, ffn, E, k, seed=17)
+    w.shexp = _shexp(oracle, dim, sffn, seed=18)
+    xs = np.stack([oracle.normal(dim, 600 + i, 0.0, 1.0) for i in range(n)])
+    resid = np.zeros((n, dim), np.float32)
+    got, _, _ = oracle.moe_batch_union(w, xs, resid)
+    for i in range(n):
+        acc, _, _ = oracle.moe_layer_token(w, xs[i])
+        assert np.all(np.abs(got[i] - acc) <= 1e-3 * np.abs(acc).max() + 1e-3)
+
+
+def test_moe_ffn_block_against_float64(oracle):
+    """backend.moeFfnBlock (compute/cpu.zig:23-30; metal/backend.zig:2322-2410):
+    out = sum over the refs in order of weight * FFN_ref(x), the shared expert
+    as a ref of weight 1 and its own width.  Float64 forward within 2e-3;
+    weights applied to the wrong refs miss."""
+    dim, ffn, sffn, E = 256, 256, 512, 6
+    w = _layer(oracle, dim, ffn, E, 2, seed=19)
+    from oracle import row_bytes
+
+    gb, db = ffn * row_bytes(w.gate_t, dim), dim * row_bytes(w.down_t, ffn)
+    g_, u_, d_, gt_, ut_, dt_, _ = _shexp(oracle, dim, sffn, seed=20)
+    weights = [0.4, 0.25, 0.2, 0.15]
+    refs = [(w.gate[e * gb:(e + 1) * gb], w.up[e * gb:(e + 1) * gb], w.down[e * db:(e + 1) * db],
+             w.gate_t, w.up_t, w.down_t, ffn, wt) for e, wt in zip([3, 0, 5, 1], weights)]
+    refs.append((g_, u_, d_, gt_, ut_, dt_, sffn, 1.0))
+    x = oracle.normal(dim, 700, 0.0, 1.0)
+    got = oracle.moe_ffn_block(x, refs)
+    parts = [_ffn64(w.gate_t, w.gate, w.up, w.down_t, w.down, x, dim, ffn, plane=e) for e in [3, 0, 5, 1]]
+    sh = _ffn64(gt_, g_, u_, dt_, d_, x, dim, sffn)
+    want = sum(wt * p for wt, p in zip(weights, parts)) + sh
+    assert np.abs(got - want).max() / np.abs(want).max() < 2e-3
+    wrong = sum(wt * p for wt, p in zip(weights[::-1], parts)) + sh
+    assert np.abs(got - wrong).max() / np.abs(wrong).max() > 2e-2
