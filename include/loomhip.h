@@ -151,13 +151,42 @@ int loomhip_moe_route(const float *logits, const float *bias, size_t n_expert, s
  * 455-551) generalised to n_tok tokens: router logits in, the routed experts'
  * gate/up/SwiGLU/down and gated combine out.  gate/up/down are whole 3D
  * tensors in GGML layout ([n_expert][ffn][dim] and [n_expert][dim][ffn]).
+ * shexp (the seam's `shexp: ?[3]WeightRef` and `shexp_ffn`): the shared
+ * expert's three GGML tensors ([shexp_ffn][dim] x2, [dim][shexp_ffn]), or
+ * shexp_gate_w NULL; its FFN is added after the routed sum, in the same
+ * submission (src/vulkan/backend.zig:527-548).
  * combine = LOOMHIP_COMBINE_*.  out is [n_tok][dim] (overwritten for
  * SELECTION, accumulated into for EXPERT_ASC). */
 int loomhip_moe_ffn_routed(const float *normed, size_t n_tok, size_t dim, const float *logits,
                            const float *sel_bias, size_t n_expert, size_t n_used, int gating,
                            int weights_norm, float weights_scale, int gate_t, const void *gate_w,
-                           int up_t, const void *up_w, int down_t, const void *down_w, size_t ffn,
-                           int combine, float *out);
+                           int up_t, const void *up_w, int down_t, const void *down_w,
+                           int shexp_gate_t, const void *shexp_gate_w, int shexp_up_t,
+                           const void *shexp_up_w, int shexp_down_t, const void *shexp_down_w,
+                           size_t ffn, size_t shexp_ffn, int combine, float *out);
+
+/* backend.moeFfnBlock (src/compute/cpu.zig:23-30 ExpertRef / moeFfnBlock;
+ * the Metal form src/metal/backend.zig:2322-2410): one MoE layer's selected
+ * experts -- the shared one joining as one more ref of weight 1 and its own
+ * width (src/gguf/deepseek.zig:1405-1440) -- as host GGML slices of one plane
+ * each ([ffn][dim] gate and up, [dim][ffn] down), with their router weights.
+ * out[dim] = sum over the refs, in order, of weight * FFN(normed).  Each
+ * slice resolves to a slot of a library-held HBM LRU (keyed by pointer,
+ * length, type and shape; misses copied in, repacked where the device layout
+ * differs), so the slices must stay valid and unchanged while cached, as the
+ * expert Source's stablePointers promises.  1..16 refs; DECLINED otherwise
+ * or on an unserved type or shape, before anything is recorded. */
+typedef struct {
+    int gate_t, up_t, down_t;
+    const void *gate, *up, *down; /* host GGML bytes */
+    float weight;
+    size_t ffn;
+} loomhip_expert_ref;
+int loomhip_moe_ffn_block(const float *normed, size_t dim, const loomhip_expert_ref *experts, size_t n_experts,
+                          float *out);
+/* Hit / miss counters of moe_ffn_block's HBM LRU (tensor slices) and the
+ * bytes its misses copied in. */
+int loomhip_moe_ffn_block_stats(uint64_t *hits, uint64_t *misses, uint64_t *bytes_read);
 
 /* ---- device-resident hot path ------------------------------------------- */
 
@@ -179,6 +208,14 @@ typedef struct {
     const float *sel_bias;    /* [n_expert] selection-only bias or NULL */
     int gate_t, up_t, down_t;
     const void *gate, *up, *down; /* device-layout, plane per expert */
+    /* The shared expert (ffn_{gate,up,down}_shexp, src/gguf/deepseek.zig:
+     * 1354-1358): one device-layout plane each, [shexp_ffn][dim] x2 and
+     * [dim][shexp_ffn]; always on and unweighted, its FFN added after the
+     * routed sum (deepseek.zig:1497-1502).  shexp_gate NULL: none.  Served
+     * with the SELECTION and EXPERT_ASC combines. */
+    int shexp_gate_t, shexp_up_t, shexp_down_t;
+    const void *shexp_gate, *shexp_up, *shexp_down;
+    size_t shexp_ffn;
 } loomhip_moe_layer;
 
 int loomhip_moe_layer_dev(const loomhip_moe_layer *L, const float *normed, size_t n_tok,
@@ -338,6 +375,11 @@ typedef struct {
     int gate_t, down_t;
     size_t id_base;
     size_t gate_off, up_off, down_off;
+    /* the shared expert, resident in HBM (device layout), as in
+     * loomhip_moe_layer; shexp_gate NULL: none */
+    int shexp_gate_t, shexp_up_t, shexp_down_t;
+    const void *shexp_gate, *shexp_up, *shexp_down;
+    size_t shexp_ffn;
 } loomhip_moe_layer_ec;
 
 /* moe.moeFFN's routed part (src/engine/moe.zig:97-124) on the device with

@@ -53,6 +53,13 @@ class MoeLayerDesc(C.Structure):
         ("gate", C.c_void_p),
         ("up", C.c_void_p),
         ("down", C.c_void_p),
+        ("shexp_gate_t", C.c_int),
+        ("shexp_up_t", C.c_int),
+        ("shexp_down_t", C.c_int),
+        ("shexp_gate", C.c_void_p),
+        ("shexp_up", C.c_void_p),
+        ("shexp_down", C.c_void_p),
+        ("shexp_ffn", C.c_size_t),
     ]
 
 
@@ -138,6 +145,28 @@ class MoeLayerEcDesc(C.Structure):
         ("gate_off", C.c_size_t),
         ("up_off", C.c_size_t),
         ("down_off", C.c_size_t),
+        ("shexp_gate_t", C.c_int),
+        ("shexp_up_t", C.c_int),
+        ("shexp_down_t", C.c_int),
+        ("shexp_gate", C.c_void_p),
+        ("shexp_up", C.c_void_p),
+        ("shexp_down", C.c_void_p),
+        ("shexp_ffn", C.c_size_t),
+    ]
+
+
+class ExpertRefDesc(C.Structure):
+    """Mirror of ``loomhip_expert_ref`` in include/loomhip.h."""
+
+    _fields_ = [
+        ("gate_t", C.c_int),
+        ("up_t", C.c_int),
+        ("down_t", C.c_int),
+        ("gate", C.c_void_p),
+        ("up", C.c_void_p),
+        ("down", C.c_void_p),
+        ("weight", C.c_float),
+        ("ffn", C.c_size_t),
     ]
 
 
@@ -190,7 +219,7 @@ def lib() -> C.CDLL:
         "loomhip_dequant_row": (i, [i, vp, vp, sz, sz]),
         "loomhip_moe_route": (i, [vp, vp, sz, sz, i, i, f, vp, vp]),
         "loomhip_moe_ffn_routed": (i, [vp, sz, sz, vp, vp, sz, sz, i, i, f, i, vp, i, vp, i, vp,
-                                       sz, i, vp]),
+                                       i, vp, i, vp, i, vp, sz, sz, i, vp]),
         "loomhip_matvec_dev": (i, [i, vp, vp, vp, sz, sz, sz, vp]),
         "loomhip_dequant_dev": (i, [i, vp, vp, sz, sz, vp]),
         "loomhip_moe_layer_dev": (i, [C.POINTER(MoeLayerDesc), vp, sz, i, vp, vp, vp, vp]),
@@ -209,6 +238,8 @@ def lib() -> C.CDLL:
         "loomhip_ec_access_counts": (i, [vp, vp, sz]),
         "loomhip_ec_clear": (i, [vp]),
         "loomhip_moe_layer_cached": (i, [C.POINTER(MoeLayerEcDesc), vp, vp, sz, vp, vp, vp, vp]),
+        "loomhip_moe_ffn_block": (i, [vp, sz, C.POINTER(ExpertRefDesc), sz, vp]),
+        "loomhip_moe_ffn_block_stats": (i, [C.POINTER(u64), C.POINTER(u64), C.POINTER(u64)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

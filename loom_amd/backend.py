@@ -109,10 +109,12 @@ def moeFfnBlockRouted(normed: np.ndarray, logits: np.ndarray, bias, gate_w: Weig
     """src/compute/cpu.zig:68 moeFfnBlockRouted, generalised to n_tok tokens.
 
     ``normed`` is [n_tok][dim], ``logits`` [n_tok][n_expert]; ``out`` [n_tok][dim]
-    receives the gated sum (SELECTION) or has it added (EXPERT_ASC).  A shared
-    expert is declined (no config on this path has one)."""
+    receives the gated sum (SELECTION) or has it added (EXPERT_ASC).  ``shexp``
+    is None or the shared expert's three WeightRefs (gate, up, down) of width
+    ``shexp_ffn``, whose FFN is added after the routed sum."""
+    sg = su = sd = WeightRef(0, None)
     if shexp is not None:
-        return False
+        sg, su, sd = shexp
     normed = np.ascontiguousarray(normed, np.float32)
     logits = np.ascontiguousarray(logits, np.float32)
     dim = normed.size // n_tok
@@ -122,8 +124,44 @@ def moeFfnBlockRouted(normed: np.ndarray, logits: np.ndarray, bias, gate_w: Weig
         _p(normed), n_tok, dim, _p(logits), _p(b), cfg.n_expert, cfg.n_used,
         GATING_SIGMOID if cfg.gating_sigmoid else GATING_SOFTMAX, int(cfg.weights_norm),
         cfg.weights_scale, gate_w.ty, _p(gate_w.data), up_w.ty, _p(up_w.data), down_w.ty,
-        _p(down_w.data), ffn, combine, _p(out))
+        _p(down_w.data), sg.ty, _p(sg.data), su.ty, _p(su.data), sd.ty, _p(sd.data), ffn, shexp_ffn,
+        combine, _p(out))
     return _served(rc, "moeFfnBlockRouted")
+
+
+@dataclass
+class ExpertRef:
+    """src/compute/cpu.zig:23 ExpertRef: one expert's gate/up/down slices
+    (GGML bytes of one plane each), its router weight and hidden width."""
+
+    gate: WeightRef
+    up: WeightRef
+    down: WeightRef
+    weight: float
+    ffn: int
+
+
+def moeFfnBlock(normed: np.ndarray, experts: list, out: np.ndarray) -> bool:
+    """src/compute/cpu.zig:27 moeFfnBlock: out = sum over experts, in order, of
+    weight * FFN(normed); each slice is resolved to the library's HBM LRU.
+    False when declined (the caller runs its own loop)."""
+    from . import ExpertRefDesc
+
+    normed = np.ascontiguousarray(normed, np.float32)
+    assert out.dtype == np.float32 and out.size == normed.size
+    arr = (ExpertRefDesc * max(1, len(experts)))()
+    for i, e in enumerate(experts):
+        arr[i] = ExpertRefDesc(e.gate.ty, e.up.ty, e.down.ty, _p(e.gate.data), _p(e.up.data), _p(e.down.data),
+                               float(e.weight), e.ffn)
+    rc = lib().loomhip_moe_ffn_block(_p(normed), normed.size, arr, len(experts), _p(out))
+    return _served(rc, "moeFfnBlock")
+
+
+def moeFfnBlockStats() -> tuple:
+    """(hits, misses, bytes_read) of moeFfnBlock's HBM LRU."""
+    h, m, b = C.c_uint64(), C.c_uint64(), C.c_uint64()
+    check(lib().loomhip_moe_ffn_block_stats(C.byref(h), C.byref(m), C.byref(b)), "moe_ffn_block_stats")
+    return h.value, m.value, b.value
 
 
 def profileKernels(enable: bool) -> None:
@@ -235,13 +273,21 @@ class MoeLayer:
 
     def __init__(self, dim, ffn, n_expert, n_used, router, gate, up, down, gate_t, up_t, down_t,
                  router_bias=None, sel_bias=None, gating=GATING_SOFTMAX, weights_norm=True,
-                 weights_scale=1.0):
-        self.keep = (router, gate, up, down, router_bias, sel_bias)
+                 weights_scale=1.0, shexp=None):
+        """shexp: None or the shared expert (gate, up, down device tensors, gate_t, up_t,
+        down_t, shexp_ffn)."""
+        self.keep = (router, gate, up, down, router_bias, sel_bias, shexp)
         self.desc = MoeLayerDesc(dim, ffn, n_expert, n_used, gating, int(weights_norm),
                                  weights_scale, router.data_ptr(),
                                  None if router_bias is None else router_bias.data_ptr(),
                                  None if sel_bias is None else sel_bias.data_ptr(), gate_t, up_t,
                                  down_t, gate.data_ptr(), up.data_ptr(), down.data_ptr())
+        if shexp is not None:
+            sg, su, sd, sgt, sut, sdt, sf = shexp
+            d = self.desc
+            d.shexp_gate_t, d.shexp_up_t, d.shexp_down_t = sgt, sut, sdt
+            d.shexp_gate, d.shexp_up, d.shexp_down = sg.data_ptr(), su.data_ptr(), sd.data_ptr()
+            d.shexp_ffn = sf
         self.dim, self.ffn, self.n_expert, self.n_used = dim, ffn, n_expert, n_used
 
     def __call__(self, normed, out, combine=COMBINE_SELECTION, ids=None, gates=None) -> int:
@@ -252,7 +298,8 @@ class MoeLayer:
 
 
 __all__ = [
-    "COMBINE_EXPERT_ASC", "COMBINE_SELECTION", "DECLINED", "F32", "MAX_BATCH", "MoeLayer",
+    "COMBINE_EXPERT_ASC", "COMBINE_SELECTION", "DECLINED", "ExpertRef", "F32", "MAX_BATCH", "MoeLayer",
+    "moeFfnBlock", "moeFfnBlockStats",
     "RoutedCfg", "WeightRef", "clearWeightCache", "dequantRow", "matmul", "matvec", "moeFfnBlockRouted",
     "moeRoute", "parallelBegin", "parallelEnd", "registerWeights", "takeCmdBufCount",
 ]

@@ -297,6 +297,11 @@ static int moe_cached(const loomhip_moe_layer_ec &L, loomhip_ec *c, const float 
                     L.id_base + E, c->n_ids);
     if (c->capacity == 0 && c->n_pinned == 0)
         return fail(LOOMHIP_ERR_ARG, "moe_cached: empty cache");
+    const DenseFfn sh{L.shexp_gate_t, L.shexp_up_t, L.shexp_down_t, L.shexp_gate, L.shexp_up, L.shexp_down,
+                      L.shexp_ffn};
+    if (sh.gate)
+        if (int rc = dense_ffn_check(sh, L.dim))
+            return rc;
     const int nt = n == 1 ? 1 : pick_nt((int)n);
 
     // device workspace
@@ -524,7 +529,10 @@ static int moe_cached(const loomhip_moe_layer_ec &L, loomhip_ec *c, const float 
             break;
     }
     e = hipEventRecord(g_ec_tables_done, st);
-    return e == hipSuccess ? LOOMHIP_OK : hip_fail(e, "moe_cached: event");
+    if (e != hipSuccess)
+        return hip_fail(e, "moe_cached: event");
+    // the shared expert (resident), after the routed sum (deepseek.zig:1497-1502)
+    return sh.gate ? dense_ffn_add(sh, normed, n, L.dim, out, st, true) : LOOMHIP_OK;
 }
 
 } // namespace lh

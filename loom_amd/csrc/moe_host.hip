@@ -9,6 +9,7 @@ namespace lh {
 
 static Scratch g_moe;   // per-call workspace
 static Scratch g_stage; // seam-call staging
+static Scratch g_sh;    // the shared expert's workspace
 
 // Fixed workspace of loomhip_moe_layer_dev_noalloc: a file-scope device
 // array, one copy per GPU for the life of the process.  Host code never
@@ -36,6 +37,7 @@ int moe_noalloc_setup(int device) {
 void moe_release_scratch() {
     g_moe.release();
     g_stage.release();
+    g_sh.release();
 }
 
 struct MoeRun {
@@ -47,7 +49,98 @@ struct MoeRun {
     const void *gate, *up, *down;
     const float *norm_w = nullptr; // decode path: rmsnorm the input first (normed = residual x)
     float norm_eps = 0.0f;
+    DenseFfn sh{}; // the shared expert (sh.gate null: none)
 };
+
+static size_t qbytes(size_t nvec, size_t cols) {
+    return align16(nvec * cols) + align16(nvec * (cols / 32) * 4) + align16(nvec * (cols / 16) * 4);
+}
+
+static QAct qview(char *base, size_t nvec, size_t cols) {
+    QAct q;
+    q.q = (int8_t *)base;
+    q.d = (float *)(base + align16(nvec * cols));
+    q.s = (int32_t *)((char *)q.d + align16(nvec * (cols / 32) * 4));
+    return q;
+}
+
+// ---- the shared expert: a dense SwiGLU FFN added after the routed sum ----------------
+// out[t] = out[t] + down . swiglu(gate . x_t, up . x_t) (add; else out[t] =
+// the FFN's output): the reference's
+// denseFFN (llama.zig:952-958) of ffn_{gate,up,down}_shexp, then
+// backend.add(acc, ffn_out) (deepseek.zig:1497-1502).  One plane each, device
+// layout; the fused gate/up launch, the activations' quantization and the
+// down matvec with its residual-add epilogue, all bit-identical to the CPU
+// kernels.
+
+int dense_ffn_check(const DenseFfn &f, size_t dim) {
+    if (!f.gate || !f.up || !f.down || f.ffn == 0)
+        return fail(LOOMHIP_ERR_ARG, "shared expert: missing tensor or width");
+    if (f.gate_t != f.up_t || !dmmv_supported(f.gate_t, (int)dim) || !dmmv_supported(f.down_t, (int)f.ffn) ||
+        f.ffn % 32 || (act_block(f.gate_t) == 256 && dim % 256) || (act_block(f.down_t) == 256 && f.ffn % 256))
+        return fail(LOOMHIP_DECLINED, "shared expert: types %d/%d/%d at dim %zu / ffn %zu not served", f.gate_t,
+                    f.up_t, f.down_t, dim, f.ffn);
+    return LOOMHIP_OK;
+}
+
+int dense_ffn_add(const DenseFfn &f, const float *x, size_t n, size_t dim, float *out, hipStream_t st, bool add) {
+    if (int rc = dense_ffn_check(f, dim))
+        return rc;
+    const size_t need = qbytes(n, dim) + align16(n * f.ffn * 4) + qbytes(n, f.ffn);
+    if (int rc = g_sh.reserve(need))
+        return rc;
+    char *base = (char *)g_sh.ptr;
+    const QAct qx = qview(base, n, dim);
+    float *act = (float *)(base + qbytes(n, dim));
+    const QAct qa = qview(base + qbytes(n, dim) + align16(n * f.ffn * 4), n, f.ffn);
+    const int nt = pick_nt((int)n);
+    int ng = 0;
+    const DmmvGroup *groups = dense_groups((int)n, nt, &ng);
+    if (!groups)
+        return fail(LOOMHIP_ERR_HIP, "shared expert: group table");
+    launch_quant_act(f.gate_t, x, (int)dim, (int)dim, (int)n, qx, st);
+    DmmvParams p{};
+    p.w = (const uint8_t *)f.gate;
+    p.w2 = (const uint8_t *)f.up;
+    p.rows = (int)f.ffn;
+    p.cols = (int)dim;
+    p.xq = qx.q;
+    p.xd = qx.d;
+    p.xs = qx.s;
+    p.pair_src = g_ctx.iota;
+    p.pair_dst = g_ctx.iota;
+    p.groups = groups;
+    p.n_groups = ng;
+    p.out = act;
+    p.out_stride = (int)f.ffn;
+    p.rpw = dmmv_pick_rpw(f.gate_t, (int)dim, (int)f.ffn, ng, nt, true);
+    if (!launch_dmmv(f.gate_t, nt, true, p, st))
+        return fail(LOOMHIP_ERR_ARG, "shared expert: gate/up partials exceed LDS");
+    launch_quant_act(f.down_t, act, (int)f.ffn, (int)f.ffn, (int)n, qa, st);
+    DmmvParams d{};
+    d.w = (const uint8_t *)f.down;
+    d.rows = (int)dim;
+    d.cols = (int)f.ffn;
+    d.xq = qa.q;
+    d.xd = qa.d;
+    d.xs = qa.s;
+    d.pair_src = g_ctx.iota;
+    d.pair_dst = g_ctx.iota;
+    d.groups = groups;
+    d.n_groups = ng;
+    d.out = out;
+    d.out_stride = (int)dim;
+    d.accumulate = add ? 1 : 0; // add: out = out + value
+    d.rpw = dmmv_pick_rpw(f.down_t, (int)f.ffn, (int)dim, ng, nt, false);
+    if (!launch_dmmv(f.down_t, nt, false, d, st))
+        return fail(LOOMHIP_ERR_ARG, "shared expert: down partials exceed LDS");
+    return LOOMHIP_OK;
+}
+
+static DenseFfn shexp_of(const loomhip_moe_layer *L) {
+    return DenseFfn{L->shexp_gate_t, L->shexp_up_t, L->shexp_down_t, L->shexp_gate, L->shexp_up, L->shexp_down,
+                    L->shexp_ffn};
+}
 
 static int moe_check(const MoeRun &m, size_t n) {
     if (!gate_supported((int)n, (int)m.E, (int)m.k))
@@ -60,19 +153,9 @@ static int moe_check(const MoeRun &m, size_t n) {
                     m.dim, m.ffn, m.gate_t, m.down_t);
     if (m.dim % 32 || m.ffn % 32)
         return fail(LOOMHIP_DECLINED, "moe: dims must be multiples of 32");
+    if (m.sh.gate)
+        return dense_ffn_check(m.sh, m.dim);
     return LOOMHIP_OK;
-}
-
-static size_t qbytes(size_t nvec, size_t cols) {
-    return align16(nvec * cols) + align16(nvec * (cols / 32) * 4) + align16(nvec * (cols / 16) * 4);
-}
-
-static QAct qview(char *base, size_t nvec, size_t cols) {
-    QAct q;
-    q.q = (int8_t *)base;
-    q.d = (float *)(base + align16(nvec * cols));
-    q.s = (int32_t *)((char *)q.d + align16(nvec * (cols / 32) * 4));
-    return q;
 }
 
 static int moe_nt(size_t n, size_t k, size_t E) {
@@ -108,6 +191,9 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
         return rc;
     if (combine < LOOMHIP_COMBINE_SELECTION || combine > LOOMHIP_COMBINE_SELECTION_ADD)
         return fail(LOOMHIP_ERR_ARG, "moe: unknown combine mode %d", combine);
+    if (m.sh.gate && (combine == LOOMHIP_COMBINE_SELECTION_ADD || m.norm_w))
+        return fail(LOOMHIP_DECLINED, "moe: a shared expert is served with the SELECTION and EXPERT_ASC combines "
+                    "on a normalised input");
     const size_t P = n * m.k;
     const bool decode = n <= DECODE_MAX_TOK && decode_supported(m.gate_t, m.down_t, (int)m.ffn);
     // matrix cores for the expert matmuls from MMQ_MIN_TOK tokens on, groups
@@ -211,7 +297,7 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
         launch_router_small(gp, st);
         if (!launch_moe_decode(m.gate_t, m.down_t, dp, (int)n, st, LOOMHIP_KT_GATE_UP, LOOMHIP_KT_DOWN))
             return fail(LOOMHIP_ERR_ARG, "moe: decode kernels declined the shape");
-        return LOOMHIP_OK;
+        return m.sh.gate ? dense_ffn_add(m.sh, normed, n, m.dim, out, st, true) : LOOMHIP_OK;
     }
 
     if (m.norm_w)
@@ -278,7 +364,7 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
         return fail(LOOMHIP_ERR_ARG, "moe: down partials exceed LDS");
 
     launch_combine(y, gates, ids, b.pair_of, (int)n, (int)m.k, (int)m.dim, combine, out, st);
-    return LOOMHIP_OK;
+    return m.sh.gate ? dense_ffn_add(m.sh, normed, n, m.dim, out, st, true) : LOOMHIP_OK;
 }
 
 // Everything moe_run would decline or refuse for this layer at n tokens,
@@ -290,8 +376,11 @@ int moe_frame_check(const loomhip_moe_layer *L, size_t n) {
     MoeRun m{L->dim, L->ffn, L->n_expert, L->n_used, L->gating, L->weights_norm, L->weights_scale,
              L->router, L->router_bias, L->sel_bias, L->gate_t, L->up_t, L->down_t, L->gate,
              L->up, L->down};
+    m.sh = shexp_of(L);
     if (int rc = moe_check(m, n))
         return rc;
+    if (m.sh.gate) // the frame adds its MoE output to the residual, acc = routed + shared is not formed
+        return fail(LOOMHIP_DECLINED, "token_frame: a shared expert is not served inside the frame");
     if (n <= DECODE_MAX_TOK && decode_supported(m.gate_t, m.down_t, (int)m.ffn) &&
         decode_down_lds(m.down_t, (int)m.ffn, (int)m.k, 1) > 64 * 1024)
         return fail(LOOMHIP_DECLINED, "moe: ffn %zu x top-%zu exceeds the decode LDS budget", m.ffn, m.k);
@@ -329,6 +418,7 @@ int loomhip_moe_layer_dev(const loomhip_moe_layer *L, const float *normed, size_
     MoeRun m{L->dim, L->ffn, L->n_expert, L->n_used, L->gating, L->weights_norm, L->weights_scale,
              L->router, L->router_bias, L->sel_bias, L->gate_t, L->up_t, L->down_t, L->gate,
              L->up, L->down};
+    m.sh = shexp_of(L);
     return moe_run(m, normed, nullptr, n_tok, combine, out, ids_out, gates_out, stream_of(stream));
 }
 
@@ -346,6 +436,9 @@ int loomhip_moe_layer_dev_noalloc(const loomhip_moe_layer *L, const float *norme
     if (dev < 0 || dev >= NOALLOC_MAX_DEVICES || !g_scratch_dev[dev])
         return fail(LOOMHIP_ERR_INIT, "moe_layer_dev_noalloc: no fixed scratch resolved for device %d "
                     "(loomhip_init sets it up)", dev);
+    if (L->shexp_gate)
+        return fail(LOOMHIP_ERR_ARG, "moe_layer_dev_noalloc: the shared expert's workspace is allocated; "
+                    "use loomhip_moe_layer_dev");
     MoeRun m{L->dim, L->ffn, L->n_expert, L->n_used, L->gating, L->weights_norm, L->weights_scale,
              L->router, L->router_bias, L->sel_bias, L->gate_t, L->up_t, L->down_t, L->gate,
              L->up, L->down};
@@ -403,17 +496,28 @@ int loomhip_moe_route(const float *logits, const float *bias, size_t n_expert, s
 int loomhip_moe_ffn_routed(const float *normed, size_t n_tok, size_t dim, const float *logits,
                            const float *sel_bias, size_t n_expert, size_t n_used, int gating,
                            int weights_norm, float weights_scale, int gate_t, const void *gate_w,
-                           int up_t, const void *up_w, int down_t, const void *down_w, size_t ffn,
-                           int combine, float *out) {
+                           int up_t, const void *up_w, int down_t, const void *down_w,
+                           int shexp_gate_t, const void *shexp_gate_w, int shexp_up_t,
+                           const void *shexp_up_w, int shexp_down_t, const void *shexp_down_w,
+                           size_t ffn, size_t shexp_ffn, int combine, float *out) {
     if (int rc = require_ready())
         return rc;
     if (!normed || !logits || !gate_w || !up_w || !down_w || !out)
         return fail(LOOMHIP_ERR_ARG, "moe_ffn_routed: null argument");
+    if (shexp_gate_w && (!shexp_up_w || !shexp_down_w || shexp_ffn == 0))
+        return fail(LOOMHIP_ERR_ARG, "moe_ffn_routed: incomplete shared expert");
     MoeRun m{dim, ffn, n_expert, n_used, gating, weights_norm, weights_scale, nullptr, nullptr,
              nullptr, gate_t, up_t, down_t, nullptr, nullptr, nullptr};
+    // the shared expert's shapes and types, checked with the rest (its
+    // pointers stand in until the upload below resolves them)
+    if (shexp_gate_w)
+        m.sh = DenseFfn{shexp_gate_t, shexp_up_t, shexp_down_t, shexp_gate_w, shexp_up_w, shexp_down_w, shexp_ffn};
     // Decline before touching the device (src/vulkan/backend.zig:462-489).
     if (int rc = moe_check(m, n_tok))
         return rc;
+    if (m.sh.gate && combine == LOOMHIP_COMBINE_SELECTION_ADD)
+        return fail(LOOMHIP_DECLINED, "moe_ffn_routed: a shared expert is served with the SELECTION and "
+                    "EXPERT_ASC combines");
     void *dg, *du, *dd;
     int rc;
     if ((rc = upload_weights(gate_t, gate_w, ffn, dim, n_expert, &dg)) ||
@@ -423,6 +527,16 @@ int loomhip_moe_ffn_routed(const float *normed, size_t n_tok, size_t dim, const 
     m.gate = dg;
     m.up = du;
     m.down = dd;
+    if (m.sh.gate) {
+        void *sg, *su, *sd;
+        if ((rc = upload_weights(shexp_gate_t, shexp_gate_w, shexp_ffn, dim, 1, &sg)) ||
+            (rc = upload_weights(shexp_up_t, shexp_up_w, shexp_ffn, dim, 1, &su)) ||
+            (rc = upload_weights(shexp_down_t, shexp_down_w, dim, shexp_ffn, 1, &sd)))
+            return rc;
+        m.sh.gate = sg;
+        m.sh.up = su;
+        m.sh.down = sd;
+    }
     const size_t nb = align16(n_tok * dim * 4), lb = align16(n_tok * n_expert * 4);
     if ((rc = g_stage.reserve(2 * nb + 2 * lb)))
         return rc;

@@ -327,6 +327,7 @@ void loomhip_shutdown(void) {
     g_ctx.ostage.release();
     moe_release_scratch();
     ec_release_scratch();
+    block_release_cache();
     prof_drain();
     for (hipEvent_t e : g_prof_pool)
         (void)hipEventDestroy(e);

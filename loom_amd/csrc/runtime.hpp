@@ -56,6 +56,17 @@ inline bool use_mmq(int t, int cols, int n, int group_tok, bool fused) {
 // Device group table for n vectors in groups of nt against plane 0 (cached per (n, nt)).
 const DmmvGroup *dense_groups(int n, int nt, int *count);
 void moe_release_scratch();
+// A dense SwiGLU FFN of one plane per tensor (device layout): the shared
+// expert of a routed MoE layer.  dense_ffn_add: out[t] (+)= down . swiglu(gate .
+// x_t, up . x_t) for n vectors (add: a residual-add epilogue), bit-identical
+// to the CPU kernels.
+struct DenseFfn {
+    int gate_t, up_t, down_t;
+    const void *gate, *up, *down; // gate null: none
+    size_t ffn;
+};
+int dense_ffn_check(const DenseFfn &f, size_t dim);
+int dense_ffn_add(const DenseFfn &f, const float *x, size_t n, size_t dim, float *out, hipStream_t st, bool add);
 // Resolves this device's copy of the no-allocation entry point's fixed scratch.
 int moe_noalloc_setup(int device);
 // The decode MoE path with its rmsnorm fused into the router launch (x = the
@@ -66,5 +77,6 @@ bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok);
 // What the MoE layer would decline at n tokens, checked before any launch.
 int moe_frame_check(const loomhip_moe_layer *L, size_t n);
 void ec_release_scratch();
+void block_release_cache();
 
 } // namespace lh

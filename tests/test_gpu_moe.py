@@ -215,3 +215,140 @@ def test_moe_layer_dev_gatings_and_down_types(be, oracle, down_t, ffn, gi, n):
     got = out.cpu().numpy()
     for i in range(n):
         assert _maxrel(got[i] - resid[i], want[i] - resid[i]) <= 2e-3, i
+
+
+# ---- config 5's block: the shared expert, and moeFfnBlock -------------------------
+
+
+def _c5_layer(oracle, E, k, seed, dim=7168, ffn=2048, sffn=2048):
+    """Config 5's routed block at its shapes (hidden 7168, expert ffn 2048,
+    Q4_K, sigmoid gating with renorm) over E experts, plus the shared expert
+    of width sffn."""
+    rng = np.random.default_rng(seed)
+    w = make_layer(oracle, dim, ffn, E, k, seed, gate_t=Q4_K, down_t=Q4_K)
+    w.gating = oracle.GATING_SIGMOID
+    sg = npref.pinned_scale_blocks(Q4_K, sffn, dim, rng)
+    su = npref.pinned_scale_blocks(Q4_K, sffn, dim, rng)
+    sd = npref.pinned_scale_blocks(Q4_K, dim, sffn, rng)
+    w.shexp = (sg, su, sd, Q4_K, Q4_K, Q4_K, sffn)
+    return w
+
+
+def test_moe_ffn_routed_with_shared_expert(be, oracle):
+    """backend.moeFfnBlockRouted with `shexp` (src/compute/cpu.zig:68;
+    src/vulkan/backend.zig:527-548): the shared expert's FFN added after the
+    routed sum in one submission, at config 5's shapes; against the oracle's
+    moeRun + shared expert (deepseek.zig:1485-1502) within 2e-3, ids exact."""
+    from loom_amd.backend import RoutedCfg, WeightRef
+
+    w = _c5_layer(oracle, E=16, k=8, seed=51)
+    sg, su, sd, _, _, _, sffn = w.shexp
+    for s in range(2):
+        normed = oracle.normal(w.dim, 900 + s, 0.0, 1.0)
+        logits = oracle.matvec(F32, w.router.view(np.uint8).ravel(), normed, w.n_expert, w.dim)
+        out = np.empty(w.dim, np.float32)
+        be.takeCmdBufCount()
+        ok = be.moeFfnBlockRouted(normed, logits, None, WeightRef(Q4_K, w.gate), WeightRef(Q4_K, w.up),
+                                  WeightRef(Q4_K, w.down),
+                                  (WeightRef(Q4_K, sg), WeightRef(Q4_K, su), WeightRef(Q4_K, sd)),
+                                  w.ffn, sffn, RoutedCfg(w.n_expert, w.n_used, True, True, 1.0), out)
+        assert ok
+        assert be.takeCmdBufCount() >= 6  # the routed chain and the shared expert's launches
+        want, _, _ = oracle.moe_layer_token(w, normed)
+        assert _maxrel(out, want) <= 2e-3, _maxrel(out, want)
+        # the same block without the shared expert differs by that expert's output
+        w2 = oracle.MoeWeights(w.dim, w.ffn, w.n_expert, w.n_used, w.router, w.gate, w.up, w.down, Q4_K, Q4_K,
+                               Q4_K, gating=oracle.GATING_SIGMOID)
+        routed, _, _ = oracle.moe_layer_token(w2, normed)
+        assert _maxrel(out, routed) > 2e-2
+
+
+@pytest.mark.parametrize("n", [1, 4, 16])
+def test_moe_layer_dev_shared_expert(be, oracle, n):
+    """loomhip_moe_layer_dev with the layer's shared expert: n = 1 in
+    selection order (moeRun), n > 1 ascending-expert (moeBatchUnion), the
+    shared expert of every token after its routed experts."""
+    import torch
+
+    from loom_amd import COMBINE_EXPERT_ASC, COMBINE_SELECTION
+
+    w = _c5_layer(oracle, E=16, k=8, seed=52)
+    sg, su, sd, _, _, _, sffn = w.shexp
+
+    def dev(raw, rows, cols, planes=1):
+        return be.repack_dev(Q4_K, torch.from_numpy(raw).cuda(), rows, cols, planes)
+
+    layer = be.MoeLayer(w.dim, w.ffn, w.n_expert, w.n_used, torch.from_numpy(w.router).cuda(),
+                        dev(w.gate, w.ffn, w.dim, w.n_expert), dev(w.up, w.ffn, w.dim, w.n_expert),
+                        dev(w.down, w.dim, w.ffn, w.n_expert), Q4_K, Q4_K, Q4_K, gating=oracle.GATING_SIGMOID,
+                        shexp=(dev(sg, sffn, w.dim), dev(su, sffn, w.dim), dev(sd, w.dim, sffn), Q4_K, Q4_K, Q4_K,
+                               sffn))
+    xs = np.stack([oracle.normal(w.dim, 950 + i, 0.0, 1.0) for i in range(n)])
+    resid = np.stack([oracle.normal(w.dim, 980 + i, 0.0, 1.0) for i in range(n)])
+    out = torch.from_numpy(resid.copy()).cuda() if n > 1 else torch.zeros(1, w.dim, device="cuda")
+    layer(torch.from_numpy(xs).cuda(), out, COMBINE_SELECTION if n == 1 else COMBINE_EXPERT_ASC)
+    got = out.cpu().numpy()
+    if n == 1:
+        want, _, _ = oracle.moe_layer_token(w, xs[0])
+        assert _maxrel(got[0], want) <= 2e-3
+    else:
+        want, _, _ = oracle.moe_batch_union(w, xs, resid)
+        for i in range(n):
+            assert _maxrel(got[i], want[i]) <= 2e-3, (i, _maxrel(got[i], want[i]))
+
+
+def test_moe_ffn_block_matches_oracle_and_caches(be, oracle):
+    """backend.moeFfnBlock (src/compute/cpu.zig:23-30): the selected experts'
+    slices with their gates plus the shared expert at weight 1, at config 5's
+    shapes.  Every expert's FFN is the CPU kernels' bit for bit and the sum
+    runs in list order, so the result is bit-identical to the oracle's
+    moeFfnBlock; a second call with the same slices is served from the HBM
+    LRU (hits only, same bits)."""
+    from loom_amd.backend import ExpertRef, WeightRef
+    from oracle import row_bytes
+
+    w = _c5_layer(oracle, E=8, k=6, seed=53)
+    sg, su, sd, _, _, _, sffn = w.shexp
+    gb, db = w.ffn * row_bytes(Q4_K, w.dim), w.dim * row_bytes(Q4_K, w.ffn)
+    sel = [5, 1, 7, 2, 0, 6]
+    gates = [0.3, 0.2, 0.15, 0.15, 0.1, 0.1]
+    refs = [ExpertRef(WeightRef(Q4_K, w.gate[e * gb:(e + 1) * gb]), WeightRef(Q4_K, w.up[e * gb:(e + 1) * gb]),
+                      WeightRef(Q4_K, w.down[e * db:(e + 1) * db]), g, w.ffn) for e, g in zip(sel, gates)]
+    refs.append(ExpertRef(WeightRef(Q4_K, sg), WeightRef(Q4_K, su), WeightRef(Q4_K, sd), 1.0, sffn))
+    normed = oracle.normal(w.dim, 990, 0.0, 1.0)
+    want = oracle.moe_ffn_block(normed, [(r.gate.data, r.up.data, r.down.data, Q4_K, Q4_K, Q4_K, r.ffn, r.weight)
+                                         for r in refs])
+    h0, m0, _ = be.moeFfnBlockStats()
+    out = np.empty(w.dim, np.float32)
+    be.takeCmdBufCount()
+    assert be.moeFfnBlock(normed, refs, out)
+    assert be.takeCmdBufCount() >= 3 * len(refs)
+    assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
+    h1, m1, _ = be.moeFfnBlockStats()
+    assert m1 - m0 <= 3 * len(refs)
+    out2 = np.empty(w.dim, np.float32)
+    assert be.moeFfnBlock(normed, refs, out2)
+    h2, m2, _ = be.moeFfnBlockStats()
+    assert (h2 - h1, m2 - m1) == (3 * len(refs), 0)
+    assert np.array_equal(out2.view(np.uint32), want.view(np.uint32))
+
+
+def test_moe_ffn_block_declines(be, oracle):
+    """More than 16 refs, or a type the kernels do not serve, decline before
+    anything is recorded (the caller then runs its own loop)."""
+    import loom_amd
+    from loom_amd.backend import ExpertRef, WeightRef
+
+    dim, ffn = 512, 256
+    rng = np.random.default_rng(3)
+    g = npref.pinned_scale_blocks(Q4_K, ffn, dim, rng)
+    d = npref.pinned_scale_blocks(Q6_K, dim, ffn, rng)
+    ref = ExpertRef(WeightRef(Q4_K, g), WeightRef(Q4_K, g), WeightRef(Q6_K, d), 0.5, ffn)
+    out = np.empty(dim, np.float32)
+    x = oracle.normal(dim, 1, 0.0, 1.0)
+    loom_amd.take_launch_count()
+    assert not be.moeFfnBlock(x, [ref] * 17, out)
+    bad = ExpertRef(WeightRef(F32, g), WeightRef(F32, g), WeightRef(Q6_K, d), 0.5, ffn)
+    assert not be.moeFfnBlock(x, [ref, bad], out)
+    assert loom_amd.take_launch_count() == 0
+    assert be.moeFfnBlock(x, [ref], out)  # the served form runs
