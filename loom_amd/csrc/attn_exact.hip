@@ -344,6 +344,166 @@ __global__ __launch_bounds__(64 * W) void attn_pv_kernel(FrameDims D, const uint
         att[(size_t)t * D.qd + ((size_t)kvh * G + g) * HD + c0 + ln] = o;
 }
 
+// ---- P.V for few lanes: the chain fed by producer waves ----------------------------
+// With few lanes there are too few chains to fill the chip, and each chain's
+// time is what counts: a wave that also multiplies, converts and stages
+// spends two or more issue slots per position.  Here a work group (64 value
+// columns, query head, lane) has one consumer wave, lane = column, whose
+// loop is only o = o + x_t over products x_t read from LDS four positions at
+// a time, and PVS_NP producer waves that write x_t = p_t * v_t for the
+// consumer two tiles ahead, 32 positions of each tile apiece.  The product
+// is formed as fma(p, v, +0) on the f16 value directly (v_fma_mix_f32): the
+// same rounding as p * v in f32,
+// except that an exact zero comes out +0 -- and o, which starts at +0 and
+// only ever receives sums, reads o + (+0) = o + (-0) = o either way.
+// Each wave passes one barrier per tile; the consumer reads only positions
+// below P, so what the producers write past the context is never used.
+constexpr int PVS_NP = 3;                // producer waves per work group
+constexpr int PVS_TJ = 32 * PVS_NP;      // positions per tile, 32 per producer
+constexpr int PVS_SETS = 4;              // tiles of value loads in flight per producer
+constexpr int PVS_STR = 4 * ((PVS_TJ / 4 + 15) / 16 * 16 + 1); // f32 stride of a column's products:
+                                         // a whole number of 16-byte slots, 1 mod 16
+constexpr int PVS_NBUF = 3;              // product tiles: the consumer's, and two ahead
+constexpr int PVS_AHEAD = 8;             // consumer float4 reads in flight (divides a tile's groups, so
+                                         // the ring carries the next tile's first reads in the slots
+                                         // it starts from)
+static_assert((PVS_TJ / 4) % PVS_AHEAD == 0, "the read ring must wrap at tile boundaries");
+
+// The LDS row of column c (0..63): bits 1, 2, 3 of c flipped by bits 3, 4, 5.
+// Rows are a whole number of 16-byte slots apart, 1 mod 16, so a slot's bank
+// group is (row + position group) mod 16; the permutation makes both access
+// patterns hit 16 different groups per quarter-wave: the consumer's (c = 16 q
+// + i, i = 0..15; one position group) and a producer store's (c = 8 cq + k,
+// cq = 0..7, at position groups g and g + 1).
+__device__ __forceinline__ int pv_row(int c) { return c ^ ((c >> 2) & 14); }
+
+template <int HD>
+__global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameDims D, const uint16_t *__restrict__ vc,
+                                                                         const int32_t *__restrict__ pos, int li,
+                                                                         const float *__restrict__ Pm, int s_stride,
+                                                                         float *__restrict__ att) {
+    constexpr int PP = PVS_TJ / PVS_NP; // positions per producer per tile
+    __shared__ __align__(16) float prod[PVS_NBUF][64 * PVS_STR];
+    __shared__ __align__(16) float pst[PVS_NP][PP];
+    const int ncb = (HD + 63) / 64;
+    // XCD-aware order: consecutive work items share an XCD (work groups are
+    // dealt to the 8 XCDs round robin), so one KV head's values stay in few L2s
+    const int nwg = ncb * D.n_heads, lin = blockIdx.x;
+    const int wi = (nwg % 8 == 0) ? (lin % 8) * (nwg / 8) + lin / 8 : lin;
+    const int sl = wi % ncb, h = wi / ncb, t = blockIdx.z;
+    const int wave = threadIdx.x >> 6, ln = threadIdx.x & 63;
+    const int G = D.n_heads / D.n_kv, kvh = h / G;
+    const int P = min(pos[t], D.ctx - 1) + 1;
+    const int ntile = (P + PVS_TJ - 1) / PVS_TJ;
+    const int ntp = (ntile + PVS_SETS - 1) / PVS_SETS * PVS_SETS; // tiles the loops run (padded)
+    const int c0 = sl * 64, ncol = min(64, HD - c0);
+    if (wave == 0) { // consumer
+        float o = 0.0f;
+        lds_barrier(); // tiles 0 and 1 are in
+        const int crow = pv_row(ln) * PVS_STR;
+        const float4 *src0 = (const float4 *)&prod[0][crow];
+        float4 xr[PVS_AHEAD];
+#pragma unroll
+        for (int a = 0; a < PVS_AHEAD; a++)
+            xr[a] = src0[a];
+        for (int k = 0; k < ntp; k++) {
+            const int nk = min(PVS_TJ, P - k * PVS_TJ);
+            const float4 *nxt = (const float4 *)&prod[(k + 1) % PVS_NBUF][crow];
+            if (nk == PVS_TJ) {
+                const float4 *src = (const float4 *)&prod[k % PVS_NBUF][crow];
+#pragma unroll
+                for (int gj = 0; gj < PVS_TJ / 4; gj++) {
+                    const int a = gj % PVS_AHEAD;
+                    const float4 x = xr[a];
+                    // the ring runs on into the next tile, complete since the last barrier;
+                    // the scheduler keeps each read ahead of the adds it must not wait for
+                    xr[a] = gj + PVS_AHEAD < PVS_TJ / 4 ? src[gj + PVS_AHEAD] : nxt[gj + PVS_AHEAD - PVS_TJ / 4];
+                    __builtin_amdgcn_sched_barrier(0);
+                    o = o + x.x;
+                    o = o + x.y;
+                    o = o + x.z;
+                    o = o + x.w;
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else if (nk > 0) { // the partial last tile
+                const float *src = &prod[k % PVS_NBUF][crow];
+                for (int j = 0; j < nk; j++)
+                    o = o + src[j];
+            }
+            lds_barrier();
+        }
+        if (ln < ncol)
+            att[(size_t)t * D.qd + (size_t)h * HD + c0 + ln] = o;
+    } else { // producer wave - 1: positions [PP (wave - 1), PP wave) of each tile
+        // lane (row group rg, column octet cq): eight columns of four
+        // positions, 4 rg + [0, 4) of the producer's 32; a dwordx4 load per
+        // position brings the eight values, and the 8 consecutive lanes of
+        // one row read 128 contiguous bytes of it.  Offsets are 32-bit byte
+        // offsets from the layer's (uniform) base, clamped to row P - 1.
+        // Column c's products live in LDS row pv_row(c).
+        const int pw = wave - 1, rg = ln >> 3, cq = ln & 7;
+        const int cqc = min(cq, ncol / 8 - 1);
+        const char *vb0 = (const char *)(vc + (((size_t)t * D.n_layers + li) * D.ctx) * D.kvd + (size_t)kvh * HD);
+        const uint32_t rowb = (uint32_t)D.kvd * 2, colb = (uint32_t)(c0 + 8 * cqc) * 2;
+        const uint32_t lim = (uint32_t)(P - 1) * rowb + colb;
+        const float *pb = Pm + ((size_t)t * D.n_heads + h) * s_stride;
+        const int r0 = PP * pw + 4 * rg; // first position of this lane within a tile
+        int rw[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            rw[k] = pv_row(8 * cq + k) * PVS_STR + r0;
+        uint4 hv[PVS_SETS][4];
+        float pp[PVS_SETS];
+        auto load = [&](int tile, uint4 (&v)[4], float &p) {
+            const uint32_t o = (uint32_t)(tile * PVS_TJ + r0) * rowb + colb;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                v[j] = *(const uint4 *)(vb0 + min(o + (uint32_t)j * rowb, lim));
+            p = pb[min(tile * PVS_TJ + PP * pw + (ln & (PP - 1)), P - 1)];
+        };
+        auto produce = [&](int tile, const uint4 (&v)[4], float p) {
+            float *dst = prod[tile % PVS_NBUF];
+            if (ln < PP)
+                pst[pw][ln] = p;
+            const float4 q = *(const float4 *)&pst[pw][4 * rg];
+            const uint32_t w[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w},
+                                      {v[1].x, v[1].y, v[1].z, v[1].w},
+                                      {v[2].x, v[2].y, v[2].z, v[2].w},
+                                      {v[3].x, v[3].y, v[3].z, v[3].w}};
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int d = k >> 1, sh = 16 * (k & 1);
+                float4 a;
+                a.x = __builtin_fmaf(q.x, half_bits_to_float(w[0][d] >> sh), 0.0f);
+                a.y = __builtin_fmaf(q.y, half_bits_to_float(w[1][d] >> sh), 0.0f);
+                a.z = __builtin_fmaf(q.z, half_bits_to_float(w[2][d] >> sh), 0.0f);
+                a.w = __builtin_fmaf(q.w, half_bits_to_float(w[3][d] >> sh), 0.0f);
+                *(float4 *)&dst[rw[k]] = a;
+            }
+        };
+#pragma unroll
+        for (int d = 0; d < PVS_SETS; d++)
+            load(d, hv[d], pp[d]);
+        produce(0, hv[0], pp[0]);
+        load(PVS_SETS, hv[0], pp[0]);
+        produce(1, hv[1], pp[1]);
+        load(PVS_SETS + 1, hv[1], pp[1]);
+        lds_barrier();
+        // iteration k: tile k + 2 into buffer (k + 2) % NBUF from register set
+        // (k + 2) % SETS, whose loads went out SETS - 1 tiles ago; then the
+        // loads of tile k + 2 + SETS into the same set
+        for (int kb = 0; kb < ntp; kb += PVS_SETS) {
+#pragma unroll
+            for (int d = 0; d < PVS_SETS; d++) {
+                const int tile = kb + d + 2, set = (d + 2) % PVS_SETS;
+                produce(tile, hv[set], pp[set]);
+                load(tile + PVS_SETS, hv[set], pp[set]);
+                lds_barrier();
+            }
+        }
+    }
+}
+
 size_t exact_softmax_lds(int s_stride) { return ((size_t)s_stride + (size_t)(s_stride / 64) * 64) * 4; }
 
 template <int HD>
@@ -361,7 +521,11 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
                        D, pos, S, s_stride);
     prof_end(ph, st);
     ph = prof_begin(LOOMHIP_KT_ATTN_PV, st);
-    if (n < 8) {
+    if (n <= 4) {
+        const dim3 pg(((HD + 63) / 64) * D.n_heads, 1, n);
+        hipLaunchKernelGGL((attn_pv_split_kernel<HD>), pg, dim3(64 * (1 + PVS_NP)), 0, st, D, vc, pos, li, S,
+                           s_stride, att);
+    } else if (n < 8) {
         const dim3 pg((HD + 63) / 64, D.n_kv * ((G + 1) / 2), n);
         hipLaunchKernelGGL((attn_pv_kernel<HD, 2>), pg, dim3(128), 0, st, D, vc, pos, li, S, s_stride, att);
     } else {
