@@ -76,7 +76,7 @@ def parse():
                     help="0 = the reference's default, host cores - 2 (capped at the box's share)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cache", action="store_true", help="skip the config-5 expert-cache streaming run")
-    ap.add_argument("--cache-steps", type=int, default=1024, help="config-5 decode steps at batch 1")
+    ap.add_argument("--cache-steps", type=int, default=1024, help="config-5 decode steps at batch 1 and at 64")
     ap.add_argument("--sweep", action="store_true",
                     help="config 2 instead: the dequant-fused matvec alone, GB/s per type x shape x vectors")
     ap.add_argument("--moe-layer", action="store_true",
@@ -486,13 +486,14 @@ def bench_moe_layer(args):
             "results": res}
 
 
-C5_DIM, C5_FFN, C5_E, C5_K, C5_SLOTS = 7168, 2048, 256, 8, 64
+C5_DIM, C5_FFN, C5_E, C5_K, C5_SLOTS, C5_SFFN = 7168, 2048, 256, 8, 64, 2048
 
 
 def _c5_layer():
     """Config 5's routed block: 256 experts of Q4_K gate/up [2048][7168] and
-    down [7168][2048] (24,772,608 B each) in pinned host memory, the f32
-    router with a Zipf(1.1) logit bias, sigmoid top-8 with renorm."""
+    down [7168][2048] (24,772,608 B each) in pinned host memory, the shared
+    expert (Q4_K, width 2048) resident in HBM, the f32 router with a
+    Zipf(1.1) logit bias, sigmoid top-8 with renorm."""
     import torch
 
     from loom_amd import GATING_SIGMOID, Q4_K, MoeLayerEcDesc, plane_bytes
@@ -518,15 +519,28 @@ def _c5_layer():
     ranks = torch.randperm(C5_E, generator=g, device="cuda").float() + 1
     z = -1.1 * torch.log(ranks)
     bias = (z - z.mean()).contiguous()
+    sh = [be.repack_dev(Q4_K, be.synth_ggml_dev(Q4_K, r, c, 1, 7000 + i, 0.02), r, c, 1)
+          for i, (r, c) in enumerate(((C5_SFFN, C5_DIM), (C5_SFFN, C5_DIM), (C5_DIM, C5_SFFN)))]
     desc = MoeLayerEcDesc(C5_DIM, C5_FFN, C5_E, C5_K, GATING_SIGMOID, 1, 1.0, router.data_ptr(),
-                          bias.data_ptr(), None, Q4_K, Q4_K, 0, 0, gb, 2 * gb)
-    return host, slot, gb, desc, (router, bias)
+                          bias.data_ptr(), None, Q4_K, Q4_K, 0, 0, gb, 2 * gb,
+                          Q4_K, Q4_K, Q4_K, sh[0].data_ptr(), sh[1].data_ptr(), sh[2].data_ptr(), C5_SFFN)
+    return host, slot, gb, desc, (router, bias, sh)
+
+
+def _c5_gets(ids, b):
+    """The cache accesses of one call in get order: one token, moeFFN's
+    selection order; more, each distinct expert once, ascending."""
+    return list(ids[0]) if b == 1 else sorted(set(int(v) for v in ids.ravel()))
 
 
 def bench_cache(args):
-    """Config 5: the routed block decoding with its experts streamed from
-    pinned host memory through a 64-slot HBM LRU (loomhip_moe_layer_cached);
-    tok/s, hit rate and bytes over each link at batch 1 and 64."""
+    """Config 5: the routed block (and its resident shared expert) decoding
+    with its experts streamed from pinned host memory through a 64-slot HBM
+    LRU (loomhip_moe_layer_cached); tok/s, hit rate and bytes over each link
+    at batch 1 and 64 over args.cache_steps steps each.  The access trace of
+    each run is kept for the oracle's replay (cpu leg).  A second batch-1 run
+    prefetches, after each step, the most-accessed experts not resident
+    (up to 4; loomhip_ec_prefetch), so their fills overlap the next step."""
     import torch
 
     from loom_amd.expert_cache import ExpertCache
@@ -538,7 +552,6 @@ def bench_cache(args):
     for e in range(C5_E):
         ec.set_source(e, host, e * slot, slot)
     # the fill rate alone: 64 distinct misses
-    out1 = torch.empty(1, C5_DIM, device="cuda")
     torch.cuda.synchronize()
     s0 = ec.stats
     t0 = time.perf_counter()
@@ -548,44 +561,84 @@ def bench_cache(args):
     torch.cuda.synchronize()
     fill_s = time.perf_counter() - t0
     fill_gbs = (ec.stats.bytes_read - s0.bytes_read) / fill_s / 1e9
-    ec.clear()
     res = {"fill_GBs": round(fill_gbs, 2)}
+    traces = {}
     g = torch.Generator(device="cuda").manual_seed(77)
-    for b, steps in ((1, args.cache_steps), (64, max(4, args.cache_steps // 32))):
-        warm = 16 if b == 1 else 2
+    for b, steps, prefetch in ((1, args.cache_steps, False), (64, args.cache_steps, False),
+                               (1, args.cache_steps, True)):
+        ec.clear()
+        warm = 16
         x = torch.randn(warm + steps, b, C5_DIM, generator=g, device="cuda")
         out = torch.empty(b, C5_DIM, device="cuda")
+        warm_trace = []
         for i in range(warm):
-            ec.moe_layer(desc, x[i], out, b)
+            ids, _ = ec.moe_layer(desc, x[i], out, b, want_ids=True)
+            warm_trace += _c5_gets(ids, b)
         torch.cuda.synchronize()
         s0 = ec.stats
+        trace = []
+        resident = None
         t0 = time.perf_counter()
         for i in range(warm, warm + steps):
-            ec.moe_layer(desc, x[i], out, b)
+            ids, _ = ec.moe_layer(desc, x[i], out, b, want_ids=True)
+            trace += _c5_gets(ids, b)
+            if prefetch:  # the hottest experts (access counts) not resident, ahead of the next step
+                acc = ec.access_counts()
+                hot = [int(e) for e in np.argsort(-acc, kind="stable")[:C5_SLOTS - 8]]
+                resident = set(trace[-C5_SLOTS:]) if resident is None else resident | set(trace[-8:])
+                ec.prefetch([e for e in hot if e not in resident][:4])
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
         s1 = ec.stats
         hits = (s1.pin_hits - s0.pin_hits) + (s1.lru_hits - s0.lru_hits)
         miss = s1.disk_misses - s0.disk_misses
-        res[f"b{b}"] = {
+        key = f"b{b}" + ("_prefetch" if prefetch else "")
+        res[key] = {
             "steps": steps, "tok_s": round(b * steps / dt, 2), "ms_per_step": round(dt / steps * 1e3, 3),
             "hit_rate": round(hits / max(1, hits + miss), 4), "gets_per_step": round((hits + miss) / steps, 2),
             "misses_per_step": round(miss / steps, 2),
             "host_link_GBs": round((s1.bytes_read - s0.bytes_read) / dt / 1e9, 2),
             "hbm_hit_bytes_per_step": int(hits * slot / steps),
         }
-        log(f"config 5 batch {b}: {res[f'b{b}']}")
+        if prefetch:
+            res[key]["prefetched_per_step"] = round((s1.warmup_reads - s0.warmup_reads) / steps, 2)
+        else:
+            # the state the trace starts from is the warm-up's: replayed with it
+            traces[key] = {"warm": warm_trace, "trace": trace,
+                           "counts": (s1.pin_hits - s0.pin_hits, s1.lru_hits - s0.lru_hits, miss)}
+        log(f"config 5 {key}: {res[key]}")
     ec.close()
-    return res, host, gb, keep
+    return res, host, gb, keep, traces
 
 
-def cpu_baseline_c5(host, gb, keep, threads, seconds):
-    """Loom's CPU MoE block (the oracle's moeRun restatement, row-parallel
-    pool) on the same 256 experts, read from the pinned host copy."""
+def cache_replay_check(traces):
+    """SURVEY's config-5 bar: the hit/miss counts equal the oracle's replay of
+    the same access trace exactly (ExpertCache.get order: pinned, LRU, miss;
+    src/engine/expert_cache.zig:230-249).  The runs start from an empty cache
+    (cleared before their warm-up), so the replay runs the warm-up's accesses
+    and the timed ones; only the timed ones are compared."""
     import oracle as o
 
     o.build()
-    router, bias = (t.cpu().numpy() for t in keep)
+    out = {}
+    for key, t in traces.items():
+        warm, _ = o.cache_replay(C5_SLOTS, np.asarray(t["warm"], np.uint32), n_ids=C5_E)
+        full, _ = o.cache_replay(C5_SLOTS, np.asarray(t["warm"] + t["trace"], np.uint32), n_ids=C5_E)
+        timed = [int(f - w) for f, w in zip(full, warm)]
+        dev = [int(v) for v in t["counts"]]
+        out[key] = {"device": dev, "oracle": timed, "accesses": len(t["trace"]), "match": dev == timed}
+    return out
+
+
+def cpu_baseline_c5(host, gb, keep, threads, seconds):
+    """Loom's CPU MoE block (the oracle's moeRun restatement and the shared
+    expert, row-parallel pool) on the same 256 experts, read from the pinned
+    host copy."""
+    import oracle as o
+
+    o.build()
+    router, bias = (t.cpu().numpy() for t in keep[:2])
+    sg, su, sd = (t.cpu().numpy() for t in keep[2])  # Q4_K: the device layout is GGML's
     slot = host.nbytes // C5_E
     db = slot - 2 * gb
     a = host.array.reshape(C5_E, slot)
@@ -593,7 +646,7 @@ def cpu_baseline_c5(host, gb, keep, threads, seconds):
     up = np.ascontiguousarray(a[:, gb:2 * gb])
     down = np.ascontiguousarray(a[:, 2 * gb:2 * gb + db])
     w = o.MoeWeights(C5_DIM, C5_FFN, C5_E, C5_K, router, gate, up, down, 12, 12, 12, router_bias=bias,
-                     gating=o.GATING_SIGMOID, weights_norm=True)
+                     gating=o.GATING_SIGMOID, weights_norm=True, shexp=(sg, su, sd, 12, 12, 12, C5_SFFN))
     rng = np.random.default_rng(9)
     with o.Pool(threads):
         o.moe_layer_token(w, rng.standard_normal(C5_DIM).astype(np.float32))
@@ -604,8 +657,10 @@ def cpu_baseline_c5(host, gb, keep, threads, seconds):
             n += 1
         dt = (time.perf_counter() - t0) / n
     return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} tokens through the config-5 routed block (moeRun order) with all 256 experts "
-                      f"in host memory ({dt * 1e3:.1f} ms/token)"}
+            "sample": f"{n} tokens through the config-5 routed block (moeRun order) and its shared expert "
+                      f"with all 256 experts in host memory ({dt * 1e3:.1f} ms/token)"}
+
+
 
 
 def main():
@@ -698,15 +753,17 @@ def main():
         log(f"cpu baseline: {cores} threads, {args.cpu_seconds} s sample")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, cores, args.ctx)
     if not args.no_cache:
-        c5, host, gb, keep = bench_cache(args)
+        c5, host, gb, keep, traces = bench_cache(args)
         line["expert_cache"] = {
             "workload": f"config 5: DeepSeek-V3-class routed block, hidden {C5_DIM}, {C5_E} experts top-{C5_K} "
-                        "(sigmoid, renorm, Zipf(1.1) logit bias), expert ffn 2048, Q4_K gate/up/down "
-                        "(24,772,608 B per expert), 6.34 GB pinned host backing store, "
-                        f"{C5_SLOTS}-slot HBM LRU (1.59 GB); synthetic hidden states",
+                        "(sigmoid, renorm, Zipf(1.1) logit bias) plus 1 shared expert (ffn 2048, resident), "
+                        "expert ffn 2048, Q4_K gate/up/down (24,772,608 B per expert), 6.34 GB pinned host "
+                        f"backing store, {C5_SLOTS}-slot HBM LRU (1.59 GB); synthetic hidden states; the MLA "
+                        "attention of the block is not included",
             **c5}
         if not args.no_cpu:
             line["expert_cache"]["cpu_baseline"] = cpu_baseline_c5(host, gb, keep, cores, args.cpu_seconds / 3)
+            line["expert_cache"]["oracle_replay"] = cache_replay_check(traces)
         host.free()
     print(json.dumps(line), flush=True)
 

@@ -163,17 +163,14 @@ __global__ __launch_bounds__(SC_THREADS) void attn_scores_kernel(
 
 __global__ __launch_bounds__(SM_THREADS) void attn_softmax_kernel(FrameDims D, const int32_t *__restrict__ pos,
                                                                   float *__restrict__ S, int s_stride) {
-    extern __shared__ __align__(16) float sm[]; // e[s_stride] | ends[C][64]
+    extern __shared__ __align__(16) float sm[]; // e[s_stride]
     __shared__ float redf[SM_THREADS / 64];
-    __shared__ double csum[128];
-    __shared__ uint32_t fst[128];
-    __shared__ float total;
+    __shared__ SeqSumLds seq;
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
     const int P = min(pos[t], D.ctx - 1) + 1;
     const int C = (P + 63) / 64;
     float *row = S + ((size_t)t * D.n_heads + h) * s_stride;
     float *e = sm;
-    float *ends = sm + s_stride;
     constexpr int NV = (EXACT_MAX_CTX + SM_THREADS - 1) / SM_THREADS;
     // 1. m = max over the scores (order-free)
     float sv[NV];
@@ -201,7 +198,7 @@ __global__ __launch_bounds__(SM_THREADS) void attn_softmax_kernel(FrameDims D, c
     }
     __syncthreads();
     // 3. the position-ordered sum of e (speculative composition, exact)
-    seq_sum_nonneg<SM_THREADS / 64>(e, C, ends, csum, fst, &total);
+    const float total = seq_sum_nonneg<SM_THREADS / 64>(e, P, seq);
     // 4. p_t = e_t * (1 / sum), in place of the scores
     const float inv = 1.0f / total;
 #pragma unroll
@@ -504,7 +501,7 @@ __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameD
     }
 }
 
-size_t exact_softmax_lds(int s_stride) { return ((size_t)s_stride + (size_t)(s_stride / 64) * 64) * 4; }
+size_t exact_softmax_lds(int s_stride) { return (size_t)s_stride * 4; }
 
 template <int HD>
 static void launch_hd(const FrameDims &D, const float *q, const float *k, const float *v, const float *q_norm,

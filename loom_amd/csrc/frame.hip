@@ -54,36 +54,40 @@ __global__ void embed_kernel(int t, const uint8_t *__restrict__ w, int vocab, in
 }
 
 // ---- rmsnorm (tensor.zig:9-15) + int8 quantization for weight type QB --------------
-constexpr int EXACT_NORM_MAX_DIM = 7936; // the sequential sum's squares and chain ends fit 64 KB of LDS
-// One work group per lane; thread c owns the 32-value chunk c (dim <= 8192).
-// out_i = (x_i * scale) * w_i with scale = 1 / sqrt(ss/n + eps).  EXACT: ss
-// is the reference's sequential sum (one thread over the squares in index
-// order, ~dim dependent adds); otherwise per chunk in order, then across
-// chunks as a fixed tree.  The exact form is used where the input is an
-// embedding row: its values sit on a few quantization levels, so int8
-// rounding of the normed vector meets exact .5 ties that a one-ulp
-// difference in the scale would flip.  qa (QB = 32 or 256) and normed are
-// each optional.
+constexpr int EXACT_NORM_MAX_DIM = 7936; // the squares and the sequential sum's LDS fit 64 KB
+// One work group per lane; thread c < dim / 32 owns the 32-value chunk c
+// (dim <= 8192).  out_i = (x_i * scale) * w_i with scale = 1 / sqrt(ss/n +
+// eps).  EXACT: ss is the reference's sequential sum of the squares in index
+// order (seq_sum_nonneg, over 16 waves: the chunk chains are what takes the
+// time, so the group has 1024 threads); otherwise per chunk in order, then
+// across chunks as a fixed tree (256 threads).  qa (QB = 32 or 256) and
+// normed are each optional.
+constexpr int norm_threads(bool exact) { return exact ? 1024 : 256; }
+
 template <int QB, bool EXACT>
-__global__ __launch_bounds__(256) void norm_quant_kernel(const float *__restrict__ x, int dim,
-                                                         const float *__restrict__ w, float eps,
-                                                         QAct qa, float *__restrict__ normed) {
+__global__ __launch_bounds__(norm_threads(EXACT)) void norm_quant_kernel(const float *__restrict__ x, int dim,
+                                                                        const float *__restrict__ w, float eps,
+                                                                        QAct qa, float *__restrict__ normed) {
     __shared__ float red[4];
     __shared__ __align__(16) float sq[EXACT ? EXACT_NORM_MAX_DIM : 1];
-    __shared__ __align__(16) float ends[EXACT ? EXACT_NORM_MAX_DIM : 1];
-    __shared__ double csum[EXACT ? 128 : 1];
-    __shared__ uint32_t fst[EXACT ? 128 : 1];
+    __shared__ SeqSumLds seq;
     const int lane_v = blockIdx.x, c = threadIdx.x, chunks = dim / 32;
     const bool live = c < chunks;
     const int cc = live ? c : chunks - 1;
     const float *xv = x + (size_t)lane_v * dim + (size_t)cc * 32;
     float4 v[8], gw[8]; // the norm weights are requested with x, not after the reduction
+    if (c < 256) {
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-        v[i] = *(const float4 *)(xv + 4 * i);
+        for (int i = 0; i < 8; i++)
+            v[i] = *(const float4 *)(xv + 4 * i);
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-        gw[i] = *(const float4 *)(w + (size_t)cc * 32 + 4 * i);
+        for (int i = 0; i < 8; i++)
+            gw[i] = *(const float4 *)(w + (size_t)cc * 32 + 4 * i);
+    } else { // the sum's helper threads (EXACT) own no chunk
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            v[i] = gw[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -112,7 +116,7 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(const float *__restrict
             }
         }
         __syncthreads();
-        total = seq_sum_nonneg<4>(sq, C, ends, csum, fst, &red[0]);
+        total = seq_sum_nonneg<norm_threads(EXACT) / 64>(sq, dim, seq);
     } else {
         total = block_sum_waves(wave_sum_f(ss), red);
     }
@@ -1081,13 +1085,13 @@ template <bool EXACT>
 static void launch_norm_t(int qb, const float *x, int dim, const float *w, float eps, QAct qa,
                           float *normed, size_t n, hipStream_t st) {
     if (qb == 256)
-        hipLaunchKernelGGL((norm_quant_kernel<256, EXACT>), dim3(n), dim3(256), 0, st, x, dim, w, eps, qa,
+        hipLaunchKernelGGL((norm_quant_kernel<256, EXACT>), dim3(n), dim3(norm_threads(EXACT)), 0, st, x, dim, w, eps, qa,
                            normed);
     else if (qb == 32)
-        hipLaunchKernelGGL((norm_quant_kernel<32, EXACT>), dim3(n), dim3(256), 0, st, x, dim, w, eps, qa,
+        hipLaunchKernelGGL((norm_quant_kernel<32, EXACT>), dim3(n), dim3(norm_threads(EXACT)), 0, st, x, dim, w, eps, qa,
                            normed);
     else
-        hipLaunchKernelGGL((norm_quant_kernel<0, EXACT>), dim3(n), dim3(256), 0, st, x, dim, w, eps,
+        hipLaunchKernelGGL((norm_quant_kernel<0, EXACT>), dim3(n), dim3(norm_threads(EXACT)), 0, st, x, dim, w, eps,
                            QAct{}, normed);
     note_launch();
 }

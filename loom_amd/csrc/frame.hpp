@@ -79,88 +79,163 @@ __device__ __forceinline__ float dot_f32_key(const float *a, const uint16_t *kro
 // ---- the sequential sum of non-negative values, by speculative composition ----
 // The reference sums softmax's exponentials and rmsnorm's squares in index
 // order (tensor.zig:12,22-25): a chain of n dependent f32 adds.  Here the n
-// values (LDS, zero-padded to whole 64-value chunks) are cut into chunks of
-// 64; a double prefix sum estimates the running sum at each chunk's start;
-// each lane of a wave runs the chunk's chain from one of the 64 f32 values
-// around that estimate (consecutive bit patterns; chunk 0 from +0, the
-// reference's start); one wave then follows the exact running sum through
-// the chunks, taking each chunk's end from the lane whose start equals the
-// running sum, or re-running the chunk from the exact value when the window
-// missed it.  Every value produced is one the reference's loop produces, so
-// the result is the sequential sum itself.  All NW waves of the work group
-// call it; C = n/64 <= 128; ends holds 64 floats per chunk, csum C doubles,
-// fst C words, out one float (all LDS).  Adding +0 to a sum of non-negative
-// values leaves it unchanged, which makes the zero padding exact.
-__device__ __forceinline__ double wave_sum_d(double v) {
-    for (int m = 32; m >= 1; m >>= 1)
-        v = v + __shfl_xor(v, m);
-    return v;
+// values (LDS, zero-padded to a multiple of 64) are cut into at most
+// SEQ_MAX_CHUNKS chunks of L values (L a multiple of 64); a double-precision
+// prefix sum estimates the running sum at each chunk's start; each lane of a
+// wave runs the chunk's chain from one of the 64 f32 values around that
+// estimate (consecutive bit patterns; chunk 0 from +0, the reference's
+// start); wave 0 then follows the exact running sum through the chunks,
+// taking each chunk's end from the lane whose start equals the running sum,
+// or re-running the chunk from the exact value when the window missed it.
+// Every value produced is one the reference's loop produces, so the result
+// is the sequential sum itself.  Adding +0 to a sum of non-negative values
+// leaves it unchanged, which makes the zero padding exact.  All NW waves of
+// the work group call it.
+constexpr int SEQ_MAX_CHUNKS = 32;
+
+struct SeqSumLds {
+    float ends[SEQ_MAX_CHUNKS * 64]; // chunk c's end from start lane l
+    int nx[SEQ_MAX_CHUNKS * 64];     // the lane of chunk c + 1's window holding it (0x100: none;
+                                     // the last chunk: l itself)
+    double wtot[16];                 // the estimates' per-wave totals
+    uint32_t fst[SEQ_MAX_CHUNKS];    // estimated start (f32 bits) of chunk c
+    float out;
+};
+
+// DPP move of a double's two halves; out-of-row lanes and rows outside
+// ROW_MASK read +0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ inline double dpp_d0(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, ROW_MASK, 0xF, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, ROW_MASK, 0xF, true);
+    return __longlong_as_double(((long long)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// Inclusive prefix sum over the wave: row_shr 1, 2, 4, 8 within each row of
+// 16 lanes, then row_bcast 15 and 31 carry the row totals upward.
+__device__ inline double wave_scan_d(double x) {
+    x = x + dpp_d0<0x111>(x);
+    x = x + dpp_d0<0x112>(x);
+    x = x + dpp_d0<0x114>(x);
+    x = x + dpp_d0<0x118>(x);
+    x = x + dpp_d0<0x142, 0xA>(x);
+    x = x + dpp_d0<0x143, 0xC>(x);
+    return x;
 }
 
 template <int NW>
-__device__ float seq_sum_nonneg(const float *v, int C, float *ends, double *csum, uint32_t *fst, float *out) {
-    const int wave = threadIdx.x >> 6, ln = threadIdx.x & 63;
-    for (int c = wave; c < C; c += NW) {
-        const double s = wave_sum_d((double)v[64 * c + ln]);
-        if (ln == 0)
-            csum[c] = s;
-    }
+__device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds &s) {
+    constexpr int NT = 64 * NW;
+    const int tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
+    const int n64 = (n + 63) & ~63;
+    const int L = 64 * ((n64 / 64 + SEQ_MAX_CHUNKS - 1) / SEQ_MAX_CHUNKS);
+    const int C = (n64 + L - 1) / L;
+    int K = 1; // values per thread in the estimates: a power of two, so it divides L
+    while (K * NT < n64)
+        K *= 2;
+    // 1. the estimates: an exclusive prefix sum in double at every chunk start
+    const int j0 = tid * K;
+    double own = 0.0;
+    for (int j = j0; j < min(j0 + K, n64); j++)
+        own = own + (double)v[j];
+    const double inc = wave_scan_d(own);
+    if (ln == 63)
+        s.wtot[wave] = inc;
     __syncthreads();
-    if (wave == 0) { // exclusive prefix of the chunk sums: the estimates (their order is free)
-        const double ca = ln < C ? csum[ln] : 0.0, cb = 64 + ln < C ? csum[64 + ln] : 0.0;
-        double a = ca, b = cb;
-        for (int o = 1; o < 64; o <<= 1) {
-            const double ta = __shfl_up(a, o), tb = __shfl_up(b, o);
-            if (ln >= o) {
-                a = a + ta;
-                b = b + tb;
+    double ex = inc - own;
+    for (int w = 0; w < wave; w++)
+        ex = ex + s.wtot[w];
+    if (j0 < n64 && j0 % L == 0)
+        s.fst[j0 / L] = __float_as_uint((float)ex);
+    __syncthreads();
+    // 2. every chunk's chain from 64 starts around its estimate; the values
+    //    are read four float4 ahead of the adds
+    for (int c = wave; c < C; c += NW) {
+        const int b = c == 0 ? 0 : max((int)s.fst[c] + ln - 32, 0);
+        const int ng = min(L, n64 - c * L) / 4; // a multiple of 16
+        const float4 *src = (const float4 *)(v + c * L);
+        float r = __uint_as_float((uint32_t)b);
+        float4 ring[4];
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+            ring[a] = src[a];
+        for (int g = 0; g < ng; g += 4) {
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                const float4 x = ring[a];
+                ring[a] = src[min(g + a + 4, ng - 1)];
+                __builtin_amdgcn_sched_barrier(0);
+                r = r + x.x;
+                r = r + x.y;
+                r = r + x.z;
+                r = r + x.w;
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        b = b + __shfl(a, 63);
-        if (ln < C)
-            fst[ln] = __float_as_uint((float)(a - ca));
-        if (64 + ln < C)
-            fst[64 + ln] = __float_as_uint((float)(b - cb));
+        s.ends[c * 64 + ln] = r;
+        const int n = c + 1 < C ? __float_as_int(r) - (int)s.fst[c + 1] + 32 : ln; // the last: itself
+        s.nx[c * 64 + ln] = (unsigned)n < 64u ? n : 0x100 | (n & 63);
     }
     __syncthreads();
-    for (int c = wave; c < C; c += NW) {
-        const int b = c == 0 ? 0 : max((int)fst[c] + ln - 32, 0);
-        float4 ev[16];
-#pragma unroll
-        for (int k = 0; k < 16; k++)
-            ev[k] = *(const float4 *)(v + 64 * c + 4 * k);
-        float s = __uint_as_float((uint32_t)b);
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            s = s + ev[k].x;
-            s = s + ev[k].y;
-            s = s + ev[k].z;
-            s = s + ev[k].w;
-        }
-        ends[c * 64 + ln] = s;
-    }
-    __syncthreads();
+    // 3. the exact running sum through the chunks: lane i of chunk c has
+    //    stored n_c(i), the lane of chunk c + 1's window that holds its end
+    //    (flag 0x100: outside the window), so the exact path is a chain of
+    //    lane reads idx = n_c(idx) from chunk 0 (which ran from +0 in every
+    //    lane).  A flagged step leaves the chain; the chunks are then
+    //    followed serially from the start (rare).
     if (wave == 0) {
-        const uint32_t fa = ln < C ? fst[ln] : 0u, fb = 64 + ln < C ? fst[64 + ln] : 0u;
-        float run = ends[0];
-        float cur = C > 1 ? ends[64 + ln] : 0.0f;
-        for (int c = 1; c < C; c++) {
-            const float nxt = c + 1 < C ? ends[(c + 1) * 64 + ln] : 0.0f;
-            const int f = (int)(c < 64 ? __builtin_amdgcn_readlane(fa, c) : __builtin_amdgcn_readlane(fb, c - 64));
-            const int idx = __builtin_amdgcn_readfirstlane((int)__float_as_uint(run) - f + 32);
-            if (idx >= 0 && idx < 64) {
-                run = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur), idx));
-            } else { // outside the window: this chunk's chain from the exact value
-                for (int j = 64 * c; j < 64 * c + 64; j++)
-                    run = run + v[j];
+        const int fa = ln < C ? (int)s.fst[ln] : 0;
+        int idx = 0;
+        int flags = 0;
+        int ea[8], eb[8]; // eight chunks a batch, the next batch in flight
+        auto load = [&](int (&e)[8], int cb) { // past the last chunk, its row: the identity
+#pragma unroll
+            for (int a = 0; a < 8; a++)
+                e[a] = s.nx[min(cb + a, C - 1) * 64 + ln];
+        };
+        auto follow = [&](const int (&e)[8]) {
+#pragma unroll
+            for (int a = 0; a < 8; a++) {
+                idx = __builtin_amdgcn_readlane(e[a], idx);
+                flags |= idx;
             }
-            cur = nxt;
+        };
+        load(ea, 0);
+#pragma unroll
+        for (int cb = 0; cb < SEQ_MAX_CHUNKS; cb += 16) {
+            load(eb, cb + 8);
+            __builtin_amdgcn_sched_barrier(0);
+            follow(ea);
+            __builtin_amdgcn_sched_barrier(0);
+            if (cb + 16 < SEQ_MAX_CHUNKS)
+                load(ea, cb + 16);
+            __builtin_amdgcn_sched_barrier(0);
+            follow(eb);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        int run;
+        if (!(flags & 0x100)) {
+            run = __builtin_amdgcn_readfirstlane(__float_as_int(s.ends[(C - 1) * 64 + (idx & 63)]));
+        } else { // some start fell outside its window: every chunk in turn
+            run = __builtin_amdgcn_readfirstlane(__float_as_int(s.ends[0]));
+            for (int c = 1; c < C; c++) {
+                const int i = run - __builtin_amdgcn_readlane(fa, c) + 32;
+                if ((unsigned)i < 64u) {
+                    run = __builtin_amdgcn_readfirstlane(__float_as_int(s.ends[c * 64 + i]));
+                } else {
+                    float r = __int_as_float(run);
+                    for (int j = c * L; j < min(c * L + L, n64); j++)
+                        r = r + v[j];
+                    run = __builtin_amdgcn_readfirstlane(__float_as_int(r));
+                }
+            }
         }
         if (ln == 0)
-            *out = run;
+            s.out = __int_as_float(run);
     }
     __syncthreads();
-    return *out;
+    return s.out;
 }
 
 // ---- the reference-order attention (attn_exact.hip), PARITY numerics --------
@@ -169,7 +244,7 @@ __device__ float seq_sum_nonneg(const float *v, int C, float *ends, double *csum
 // one softmax launch per (head, lane), one P.V launch per (64 columns, KV
 // head, lane).  S is [n][n_heads][s_stride] f32 (scores, then p in place),
 // att the f32 attention output [n][n_heads * head_dim].
-constexpr int EXACT_MAX_CTX = 7936; // the softmax's LDS: e[ctx] + 64 chain ends per 64 positions
+constexpr int EXACT_MAX_CTX = 7936; // the softmax's e[] and the sequential sum's LDS in 64 KB
 size_t exact_softmax_lds(int s_stride);
 bool launch_attn_exact(const FrameDims &D, const float *q, const float *k, const float *v, const float *q_norm,
                        const float *k_norm, const float *rope_cs, uint16_t *kc, uint16_t *vc, const int32_t *pos,
