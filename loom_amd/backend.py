@@ -183,7 +183,8 @@ _KERNEL_SYMBOLS = {
     "wo": "dmmv_kernel<T, NT, false> / from 16 lanes mmq_kernel<T, 1, false, SBW> (wo + residual)",
     "attn_scores": "attn_scores_kernel<HD> (PARITY: dotF32-order scores)",
     "attn_softmax": "attn_softmax_kernel (PARITY: max, exp, position-ordered sum, p)",
-    "attn_pv": "attn_pv_kernel<HD, W> (PARITY: position-ordered P.V)",
+    "attn_pv": "attn_pv_split_kernel<HD> (up to 4 lanes) / attn_pv_kernel<HD, W> (PARITY: position-ordered "
+               "P.V)",
 }
 
 

@@ -158,15 +158,15 @@ __global__ __launch_bounds__(SC_THREADS) void attn_scores_kernel(
 }
 
 // ---- softmax ------------------------------------------------------------------------
-// Work group (query head, lane), 1024 threads; e[] and the chunk chain ends
-// live in LDS.
+// Work group (query head, lane), 1024 threads; e[] and the sequential sum's
+// state live in LDS.
 
 __global__ __launch_bounds__(SM_THREADS) void attn_softmax_kernel(FrameDims D, const int32_t *__restrict__ pos,
                                                                   float *__restrict__ S, int s_stride) {
     extern __shared__ __align__(16) float sm[]; // e[s_stride]
     __shared__ float redf[SM_THREADS / 64];
     __shared__ SeqSumLds seq;
-    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
+    const int h = blockIdx.x, t = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
     const int P = min(pos[t], D.ctx - 1) + 1;
     const int C = (P + 63) / 64;
     float *row = S + ((size_t)t * D.n_heads + h) * s_stride;
@@ -514,7 +514,7 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
                        q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse ? 1 : 0, S, s_stride);
     prof_end(ph, st);
     ph = prof_begin(LOOMHIP_KT_ATTN_SOFTMAX, st);
-    hipLaunchKernelGGL(attn_softmax_kernel, dim3(D.n_heads, n), dim3(SM_THREADS), exact_softmax_lds(s_stride), st,
+    hipLaunchKernelGGL(attn_softmax_kernel, dim3(D.n_heads, 1, n), dim3(SM_THREADS), exact_softmax_lds(s_stride), st,
                        D, pos, S, s_stride);
     prof_end(ph, st);
     ph = prof_begin(LOOMHIP_KT_ATTN_PV, st);

@@ -151,11 +151,9 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
     __syncthreads();
     // 2. every chunk's chain from 64 starts around its estimate; the values
     //    are read four float4 ahead of the adds
-    for (int c = wave; c < C; c += NW) {
-        const int b = c == 0 ? 0 : max((int)s.fst[c] + ln - 32, 0);
+    auto chain = [&](float r, int c) {
         const int ng = min(L, n64 - c * L) / 4; // a multiple of 16
         const float4 *src = (const float4 *)(v + c * L);
-        float r = __uint_as_float((uint32_t)b);
         float4 ring[4];
 #pragma unroll
         for (int a = 0; a < 4; a++)
@@ -173,6 +171,11 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        return r;
+    };
+    for (int c = wave; c < C; c += NW) {
+        const int b = c == 0 ? 0 : max((int)s.fst[c] + ln - 32, 0);
+        const float r = chain(__uint_as_float((uint32_t)b), c);
         s.ends[c * 64 + ln] = r;
         const int n = c + 1 < C ? __float_as_int(r) - (int)s.fst[c + 1] + 32 : ln; // the last: itself
         s.nx[c * 64 + ln] = (unsigned)n < 64u ? n : 0x100 | (n & 63);
@@ -223,11 +226,8 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
                 const int i = run - __builtin_amdgcn_readlane(fa, c) + 32;
                 if ((unsigned)i < 64u) {
                     run = __builtin_amdgcn_readfirstlane(__float_as_int(s.ends[c * 64 + i]));
-                } else {
-                    float r = __int_as_float(run);
-                    for (int j = c * L; j < min(c * L + L, n64); j++)
-                        r = r + v[j];
-                    run = __builtin_amdgcn_readfirstlane(__float_as_int(r));
+                } else { // the chain from the exact value (every lane the same)
+                    run = __builtin_amdgcn_readfirstlane(__float_as_int(chain(__int_as_float(run), c)));
                 }
             }
         }
