@@ -158,55 +158,42 @@ __global__ __launch_bounds__(SC_THREADS) void attn_scores_kernel(
 }
 
 // ---- softmax ------------------------------------------------------------------------
-// Work group (query head, lane), 1024 threads; e[] and the sequential sum's
-// state live in LDS.
+// Work group (query head, lane): the max, e_t, the position-ordered sum of e
+// (the speculative composition), p_t.  NT = 1024 for few lanes (the launch
+// has few groups, and each group's latency is the step's); 256 for many, so
+// that four groups share a CU and the whole launch runs in one round.
 
-__global__ __launch_bounds__(SM_THREADS) void attn_softmax_kernel(FrameDims D, const int32_t *__restrict__ pos,
-                                                                  float *__restrict__ S, int s_stride) {
-    extern __shared__ __align__(16) float sm[]; // e[s_stride]
-    __shared__ float redf[SM_THREADS / 64];
+template <int NT>
+__global__ __launch_bounds__(NT) void attn_softmax_kernel(FrameDims D, const int32_t *__restrict__ pos,
+                                                          float *__restrict__ S, int s_stride) {
+    extern __shared__ __align__(16) float e[]; // e[s_stride]
+    __shared__ float redf[NT / 64];
     __shared__ SeqSumLds seq;
     const int h = blockIdx.x, t = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
     const int P = min(pos[t], D.ctx - 1) + 1;
     const int C = (P + 63) / 64;
     float *row = S + ((size_t)t * D.n_heads + h) * s_stride;
-    float *e = sm;
-    constexpr int NV = (EXACT_MAX_CTX + SM_THREADS - 1) / SM_THREADS;
     // 1. m = max over the scores (order-free)
-    float sv[NV];
     float m = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < NV; u++) {
-        const int j = tid + SM_THREADS * u;
-        sv[u] = j < P ? row[j] : -INFINITY;
-        m = fmaxf(m, sv[u]);
-    }
+    for (int j = tid; j < P; j += NT)
+        m = fmaxf(m, row[j]);
     m = wave_max(m);
     if (ln == 0)
         redf[wave] = m;
     __syncthreads();
     m = redf[0];
-    for (int w = 1; w < SM_THREADS / 64; w++)
+    for (int w = 1; w < NT / 64; w++)
         m = fmaxf(m, redf[w]);
-    // 2. e_t = exp(s_t - m), the once-rounded double exponential; positions
-    //    past the context up to the chunk boundary hold +0 (s + 0 = s)
-#pragma unroll
-    for (int u = 0; u < NV; u++) {
-        const int j = tid + SM_THREADS * u;
-        if (j < 64 * C)
-            e[j] = j < P ? exp_f32(sv[u] - m) : 0.0f;
-    }
+    // 2. e_t = exp(s_t - m), rounded once to f32 from a double exponential;
+    //    positions past the context up to the next multiple of 64 hold +0
+    for (int j = tid; j < 64 * C; j += NT)
+        e[j] = j < P ? exp_f32(row[j] - m) : 0.0f;
     __syncthreads();
-    // 3. the position-ordered sum of e (speculative composition, exact)
-    const float total = seq_sum_nonneg<SM_THREADS / 64>(e, P, seq);
+    // 3. the position-ordered sum of e (speculative composition, exact);
     // 4. p_t = e_t * (1 / sum), in place of the scores
-    const float inv = 1.0f / total;
-#pragma unroll
-    for (int u = 0; u < NV; u++) {
-        const int j = tid + SM_THREADS * u;
-        if (j < P)
-            row[j] = e[j] * inv;
-    }
+    const float inv = 1.0f / seq_sum_nonneg<NT / 64>(e, P, seq);
+    for (int j = tid; j < P; j += NT)
+        row[j] = e[j] * inv;
 }
 
 // ---- P.V ----------------------------------------------------------------------------
@@ -514,8 +501,12 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
                        q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse ? 1 : 0, S, s_stride);
     prof_end(ph, st);
     ph = prof_begin(LOOMHIP_KT_ATTN_SOFTMAX, st);
-    hipLaunchKernelGGL(attn_softmax_kernel, dim3(D.n_heads, 1, n), dim3(SM_THREADS), exact_softmax_lds(s_stride), st,
-                       D, pos, S, s_stride);
+    if (n <= 4)
+        hipLaunchKernelGGL((attn_softmax_kernel<SM_THREADS>), dim3(D.n_heads, 1, n), dim3(SM_THREADS),
+                           exact_softmax_lds(s_stride), st, D, pos, S, s_stride);
+    else
+        hipLaunchKernelGGL((attn_softmax_kernel<256>), dim3(D.n_heads, 1, n), dim3(256), exact_softmax_lds(s_stride),
+                           st, D, pos, S, s_stride);
     prof_end(ph, st);
     ph = prof_begin(LOOMHIP_KT_ATTN_PV, st);
     if (n <= 4) {
