@@ -114,8 +114,8 @@ size_t loomhip_ggml_bytes(int t, size_t rows, size_t cols);
  * re-uploads).  Returns LOOMHIP_OK and the device pointer in *dev_out. */
 int loomhip_register_weights(int t, const void *host, size_t rows, size_t cols, size_t planes,
                              void **dev_out);
-/* Drop every cached upload (tests recycle host addresses,
- * src/vulkan/backend.zig:159-172). */
+/* Drop every cached upload, moe_ffn_block's HBM tier and the registered
+ * arenas (tests recycle host addresses, src/vulkan/backend.zig:159-172). */
 void loomhip_clear_weight_cache(void);
 /* Bytes currently resident through the cache (backend.materializeArenas). */
 size_t loomhip_resident_bytes(void);
@@ -171,11 +171,13 @@ int loomhip_moe_ffn_routed(const float *normed, size_t n_tok, size_t dim, const 
  * width (src/gguf/deepseek.zig:1405-1440) -- as host GGML slices of one plane
  * each ([ffn][dim] gate and up, [dim][ffn] down), with their router weights.
  * out[dim] = sum over the refs, in order, of weight * FFN(normed).  Each
- * slice resolves to a slot of a library-held HBM LRU (keyed by pointer,
- * length, type and shape; misses copied in, repacked where the device layout
- * differs), so the slices must stay valid and unchanged while cached, as the
- * expert Source's stablePointers promises.  1..16 refs; DECLINED otherwise
- * or on an unserved type or shape, before anything is recorded. */
+ * slice is copied into a slot of a library-held HBM LRU (repacked where the
+ * device layout differs): a slice inside a registered arena stays there
+ * across calls (keyed by pointer, length, type and shape), any other slice --
+ * a Source RAM-cache slot whose bytes change on refill -- is copied on every
+ * call.  Slices need only stay valid during the call (the Source's
+ * stablePointers).  1..16 refs; DECLINED otherwise or on an unserved type or
+ * shape, before anything is recorded. */
 typedef struct {
     int gate_t, up_t, down_t;
     const void *gate, *up, *down; /* host GGML bytes */
@@ -184,9 +186,23 @@ typedef struct {
 } loomhip_expert_ref;
 int loomhip_moe_ffn_block(const float *normed, size_t dim, const loomhip_expert_ref *experts, size_t n_experts,
                           float *out);
+/* Source.prefetchAsync for the HBM tier (src/p2p/expert_fetch.zig:385-400):
+ * the refs' arena slices not resident start their copies on the library's
+ * copy stream and return at once; the moe_ffn_block call that uses them waits
+ * for each fill on the device.  Slices outside the arenas are skipped (their
+ * bytes may change before use), as are refs wider than the cache's slots. */
+int loomhip_moe_ffn_block_prefetch(size_t dim, const loomhip_expert_ref *experts, size_t n_experts);
 /* Hit / miss counters of moe_ffn_block's HBM LRU (tensor slices) and the
- * bytes its misses copied in. */
+ * bytes its misses and prefetches copied in. */
 int loomhip_moe_ffn_block_stats(uint64_t *hits, uint64_t *misses, uint64_t *bytes_read);
+/* backend.registerArena (src/compute/cpu.zig:33-36; src/metal/backend.zig:
+ * 744-760): a read-only host region (the model's mapping) whose bytes stay
+ * fixed while registered; moe_ffn_block keeps its slices in HBM across calls.
+ * Registering a covered region again is OK; DECLINED past 16 regions. */
+int loomhip_register_arena(const void *mem, size_t len);
+/* backend.materializeArenas (src/compute/cpu.zig:38-45): the registered
+ * arena bytes (page-rounded). */
+size_t loomhip_materialize_arenas(void);
 
 /* ---- device-resident hot path ------------------------------------------- */
 

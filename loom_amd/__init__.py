@@ -240,6 +240,9 @@ def lib() -> C.CDLL:
         "loomhip_moe_layer_cached": (i, [C.POINTER(MoeLayerEcDesc), vp, vp, sz, vp, vp, vp, vp]),
         "loomhip_moe_ffn_block": (i, [vp, sz, C.POINTER(ExpertRefDesc), sz, vp]),
         "loomhip_moe_ffn_block_stats": (i, [C.POINTER(u64), C.POINTER(u64), C.POINTER(u64)]),
+        "loomhip_moe_ffn_block_prefetch": (i, [sz, C.POINTER(ExpertRefDesc), sz]),
+        "loomhip_register_arena": (i, [vp, sz]),
+        "loomhip_materialize_arenas": (sz, []),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

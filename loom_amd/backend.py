@@ -141,20 +141,42 @@ class ExpertRef:
     ffn: int
 
 
-def moeFfnBlock(normed: np.ndarray, experts: list, out: np.ndarray) -> bool:
-    """src/compute/cpu.zig:27 moeFfnBlock: out = sum over experts, in order, of
-    weight * FFN(normed); each slice is resolved to the library's HBM LRU.
-    False when declined (the caller runs its own loop)."""
+def _refs(experts: list):
     from . import ExpertRefDesc
 
-    normed = np.ascontiguousarray(normed, np.float32)
-    assert out.dtype == np.float32 and out.size == normed.size
     arr = (ExpertRefDesc * max(1, len(experts)))()
     for i, e in enumerate(experts):
         arr[i] = ExpertRefDesc(e.gate.ty, e.up.ty, e.down.ty, _p(e.gate.data), _p(e.up.data), _p(e.down.data),
                                float(e.weight), e.ffn)
-    rc = lib().loomhip_moe_ffn_block(_p(normed), normed.size, arr, len(experts), _p(out))
+    return arr
+
+
+def moeFfnBlock(normed: np.ndarray, experts: list, out: np.ndarray) -> bool:
+    """src/compute/cpu.zig:27 moeFfnBlock: out = sum over experts, in order, of
+    weight * FFN(normed); each slice is copied into the library's HBM LRU
+    (kept across calls when it lies in a registered arena).  False when
+    declined (the caller runs its own loop)."""
+    normed = np.ascontiguousarray(normed, np.float32)
+    assert out.dtype == np.float32 and out.size == normed.size
+    rc = lib().loomhip_moe_ffn_block(_p(normed), normed.size, _refs(experts), len(experts), _p(out))
     return _served(rc, "moeFfnBlock")
+
+
+def moeFfnBlockPrefetch(dim: int, experts: list) -> None:
+    """Source.prefetchAsync for the HBM tier (src/p2p/expert_fetch.zig:390):
+    start the copies of the refs' arena slices; returns at once."""
+    check(lib().loomhip_moe_ffn_block_prefetch(dim, _refs(experts), len(experts)), "moe_ffn_block_prefetch")
+
+
+def registerArena(mem: np.ndarray) -> bool:
+    """src/compute/cpu.zig:33 registerArena: a read-only host region whose
+    bytes stay fixed (the model's mapping); False when declined."""
+    return _served(lib().loomhip_register_arena(_p(mem), mem.nbytes), "registerArena")
+
+
+def materializeArenas() -> int:
+    """src/compute/cpu.zig:38 materializeArenas: the registered arena bytes."""
+    return int(lib().loomhip_materialize_arenas())
 
 
 def moeFfnBlockStats() -> tuple:

@@ -377,7 +377,10 @@ int loomhip_register_weights(int t, const void *host, size_t rows, size_t cols, 
     return upload_weights(t, host, rows, cols, planes, dev_out);
 }
 
-void loomhip_clear_weight_cache(void) { clear_weight_cache(); }
+void loomhip_clear_weight_cache(void) {
+    clear_weight_cache();
+    block_release_cache();
+}
 
 size_t loomhip_resident_bytes(void) { return g_resident; }
 

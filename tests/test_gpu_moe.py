@@ -302,8 +302,11 @@ def test_moe_ffn_block_matches_oracle_and_caches(be, oracle):
     slices with their gates plus the shared expert at weight 1, at config 5's
     shapes.  Every expert's FFN is the CPU kernels' bit for bit and the sum
     runs in list order, so the result is bit-identical to the oracle's
-    moeFfnBlock; a second call with the same slices is served from the HBM
-    LRU (hits only, same bits)."""
+    moeFfnBlock.  Slices outside any registered arena are copied on every call
+    -- a Source RAM-cache slot refilled in place (src/p2p/expert_fetch.zig:
+    270-321) gives the new bytes' result, not a stale one; once the weights'
+    arena is registered (cpu.zig:33 registerArena) a second call is served
+    from the HBM tier (hits only, same bits)."""
     from loom_amd.backend import ExpertRef, WeightRef
     from oracle import row_bytes
 
@@ -312,25 +315,57 @@ def test_moe_ffn_block_matches_oracle_and_caches(be, oracle):
     gb, db = w.ffn * row_bytes(Q4_K, w.dim), w.dim * row_bytes(Q4_K, w.ffn)
     sel = [5, 1, 7, 2, 0, 6]
     gates = [0.3, 0.2, 0.15, 0.15, 0.1, 0.1]
-    refs = [ExpertRef(WeightRef(Q4_K, w.gate[e * gb:(e + 1) * gb]), WeightRef(Q4_K, w.up[e * gb:(e + 1) * gb]),
-                      WeightRef(Q4_K, w.down[e * db:(e + 1) * db]), g, w.ffn) for e, g in zip(sel, gates)]
-    refs.append(ExpertRef(WeightRef(Q4_K, sg), WeightRef(Q4_K, su), WeightRef(Q4_K, sd), 1.0, sffn))
-    normed = oracle.normal(w.dim, 990, 0.0, 1.0)
-    want = oracle.moe_ffn_block(normed, [(r.gate.data, r.up.data, r.down.data, Q4_K, Q4_K, Q4_K, r.ffn, r.weight)
-                                         for r in refs])
-    h0, m0, _ = be.moeFfnBlockStats()
-    out = np.empty(w.dim, np.float32)
-    be.takeCmdBufCount()
-    assert be.moeFfnBlock(normed, refs, out)
-    assert be.takeCmdBufCount() >= 3 * len(refs)
-    assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
-    h1, m1, _ = be.moeFfnBlockStats()
-    assert m1 - m0 <= 3 * len(refs)
-    out2 = np.empty(w.dim, np.float32)
-    assert be.moeFfnBlock(normed, refs, out2)
-    h2, m2, _ = be.moeFfnBlockStats()
-    assert (h2 - h1, m2 - m1) == (3 * len(refs), 0)
-    assert np.array_equal(out2.view(np.uint32), want.view(np.uint32))
+
+    def refs_of(sel):
+        r = [ExpertRef(WeightRef(Q4_K, w.gate[e * gb:(e + 1) * gb]), WeightRef(Q4_K, w.up[e * gb:(e + 1) * gb]),
+                       WeightRef(Q4_K, w.down[e * db:(e + 1) * db]), g, w.ffn) for e, g in zip(sel, gates)]
+        r.append(ExpertRef(WeightRef(Q4_K, sg), WeightRef(Q4_K, su), WeightRef(Q4_K, sd), 1.0, sffn))
+        return r
+
+    def want_of(refs):
+        return oracle.moe_ffn_block(normed, [(r.gate.data, r.up.data, r.down.data, Q4_K, Q4_K, Q4_K, r.ffn,
+                                              r.weight) for r in refs])
+
+    def run(refs):
+        out = np.empty(w.dim, np.float32)
+        h0, m0, _ = be.moeFfnBlockStats()
+        assert be.moeFfnBlock(normed, refs, out)
+        h1, m1, _ = be.moeFfnBlockStats()
+        return out, (h1 - h0, m1 - m0)
+
+    be.clearWeightCache()
+    try:
+        refs = refs_of(sel)
+        normed = oracle.normal(w.dim, 990, 0.0, 1.0)
+        want = want_of(refs)
+        be.takeCmdBufCount()
+        out, (h, m) = run(refs)
+        assert be.takeCmdBufCount() >= 3 * len(refs)
+        assert np.array_equal(out.view(np.uint32), want.view(np.uint32)) and (h, m) == (0, 3 * len(refs))
+        # no arena: the same slices are copied again, and a slot refilled in place reads its new bytes
+        w.gate[5 * gb:6 * gb] = w.gate[3 * gb:4 * gb]
+        w.up[5 * gb:6 * gb] = w.up[3 * gb:4 * gb]
+        w.down[5 * db:6 * db] = w.down[3 * db:4 * db]
+        want2 = want_of(refs)
+        assert not np.array_equal(want2, want)
+        out, (h, m) = run(refs)
+        assert np.array_equal(out.view(np.uint32), want2.view(np.uint32)) and (h, m) == (0, 3 * len(refs))
+        # the weights' arena: kept across calls
+        for a in (w.gate, w.up, w.down, sg, su, sd):
+            assert be.registerArena(a)
+        assert be.materializeArenas() >= w.gate.nbytes + w.up.nbytes + w.down.nbytes
+        out, (h, m) = run(refs)
+        assert np.array_equal(out.view(np.uint32), want2.view(np.uint32)) and m == 3 * len(refs)
+        out, (h, m) = run(refs)
+        assert np.array_equal(out.view(np.uint32), want2.view(np.uint32)) and (h, m) == (3 * len(refs), 0)
+        # prefetchAsync of the next selection: its copies run on the copy stream, the call waits for them
+        refs3 = refs_of([4, 3, 0, 1, 2, 7])
+        be.moeFfnBlockPrefetch(w.dim, refs3)
+        out, (h, m) = run(refs3)
+        assert np.array_equal(out.view(np.uint32), want_of(refs3).view(np.uint32))
+        assert (h, m) == (3 * len(refs3), 0)
+    finally:
+        be.clearWeightCache()  # the arenas end with this test's arrays
 
 
 def test_moe_ffn_block_declines(be, oracle):
