@@ -256,14 +256,16 @@ int loomhip_moe_layer_dev_noalloc(const loomhip_moe_layer *L, const float *norme
 
 /* ---- whole-token decode frame --------------------------------------------- */
 
-/* Numerics of the frame's f32 reductions.  PARITY: every rmsnorm sums its
- * squares in the reference's sequential order (tensor.zig:9-15), so with
- * the matvecs, the attention within 64 positions and the per-head norms
- * already in the reference's order the step is bit-identical to the CPU
- * path wherever exp agrees (a sliver of inputs) -- at ~dim dependent adds per
- * norm.  FAST: rmsnorm sums as a fixed tree (the embedding row's excepted);
- * last-bit differences may then move one int8 step of a quantized matvec
- * input (the 2e-3 logit tolerance). */
+/* Numerics of the frame's f32 reductions.  PARITY: every reduction in the
+ * reference's own order -- rmsnorm's squares and softmax's exponentials
+ * summed sequentially (tensor.zig:9-28, evaluated by speculative
+ * composition), the scores in dotF32's order, P.V position by position
+ * (ggml.zig:221-230) -- so, with the matvecs already exact, the step is
+ * bit-identical to the CPU path at any context up to 7936 positions wherever
+ * exp agrees (a sliver of inputs).  FAST: rmsnorm sums as a fixed tree (the
+ * embedding row's excepted) and split-context attention on the matrix cores;
+ * last-bit differences then move int8 steps of quantized matvec inputs, and
+ * logits by up to ~2e-2 relative at a 4096-token context. */
 #define LOOMHIP_NUMERICS_PARITY 0
 #define LOOMHIP_NUMERICS_FAST 1
 
@@ -318,6 +320,12 @@ typedef struct {
 int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int32_t *pos, size_t n,
                             uint16_t *k_cache, uint16_t *v_cache, float *logits, uint32_t *next,
                             void *stream);
+/* The checks loomhip_token_frame_dev makes before it launches anything, for
+ * n lanes: OK when the frame serves the model, DECLINED (or ERR_ARG) with the
+ * reason in loomhip_last_error otherwise.  What the HIP arm's
+ * gpuLayersSupported (src/gguf/llama.zig:985-1009) asks once at load, since
+ * a frame must never decline halfway through a token. */
+int loomhip_frame_check(const loomhip_model *m, size_t n);
 
 /* ---- expert cache: pinned host memory -> HBM LRU ----------------------------
  * The tiers of ExpertCache (src/engine/expert_cache.zig:150-249) with HBM as

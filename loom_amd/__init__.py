@@ -225,6 +225,7 @@ def lib() -> C.CDLL:
         "loomhip_moe_layer_dev": (i, [C.POINTER(MoeLayerDesc), vp, sz, i, vp, vp, vp, vp]),
         "loomhip_moe_layer_dev_noalloc": (i, [C.POINTER(MoeLayerDesc), vp, sz, i, vp, vp, vp, vp]),
         "loomhip_token_frame_dev": (i, [C.POINTER(ModelDesc), vp, vp, sz, vp, vp, vp, vp, vp]),
+        "loomhip_frame_check": (i, [C.POINTER(ModelDesc), sz]),
         "loomhip_host_alloc": (vp, [sz]),
         "loomhip_host_free": (None, [vp]),
         "loomhip_ec_create": (i, [sz, sz, sz, sz, C.POINTER(vp)]),

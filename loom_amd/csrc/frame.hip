@@ -1139,6 +1139,11 @@ static int frame_check(const loomhip_model *m, size_t n, size_t *ffn_max) {
             *ffn_max = l.ffn > *ffn_max ? l.ffn : *ffn_max;
         }
     }
+    if (m->numerics != LOOMHIP_NUMERICS_PARITY && m->numerics != LOOMHIP_NUMERICS_FAST)
+        return fail(LOOMHIP_ERR_ARG, "token_frame: unknown numerics mode %d", m->numerics);
+    if (m->numerics == LOOMHIP_NUMERICS_PARITY && m->ctx_len > (size_t)EXACT_MAX_CTX)
+        return fail(LOOMHIP_DECLINED, "token_frame: PARITY attention serves contexts up to %d (ctx_len %zu)",
+                    EXACT_MAX_CTX, m->ctx_len);
     return LOOMHIP_OK;
 }
 
@@ -1147,6 +1152,13 @@ static int frame_check(const loomhip_model *m, size_t n, size_t *ffn_max) {
 using namespace lh;
 
 extern "C" {
+
+int loomhip_frame_check(const loomhip_model *m, size_t n) {
+    if (int rc = require_ready())
+        return rc;
+    size_t ffn_max = 0;
+    return frame_check(m, n, &ffn_max);
+}
 
 int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int32_t *pos, size_t n,
                             uint16_t *k_cache, uint16_t *v_cache, float *logits, uint32_t *next,
@@ -1160,12 +1172,7 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         return rc;
     hipStream_t st = stream_of(stream);
     const int n_chunks = (int)((m->ctx_len + ATT_TC - 1) / ATT_TC);
-    if (m->numerics != LOOMHIP_NUMERICS_PARITY && m->numerics != LOOMHIP_NUMERICS_FAST)
-        return fail(LOOMHIP_ERR_ARG, "token_frame: unknown numerics mode %d", m->numerics);
     const bool parity = m->numerics == LOOMHIP_NUMERICS_PARITY;
-    if (parity && m->ctx_len > (size_t)EXACT_MAX_CTX)
-        return fail(LOOMHIP_DECLINED, "token_frame: PARITY attention serves contexts up to %d (ctx_len %zu)",
-                    EXACT_MAX_CTX, m->ctx_len);
     const FrameWs probe = frame_layout(nullptr, n, m, ffn_max, n_chunks, parity);
     if (int rc = g_frame.reserve(probe.bytes))
         return rc;

@@ -19,7 +19,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import (GATING_SOFTMAX, NUMERICS_PARITY, Q4_0, Q4_K, Q6_K, LayerDesc, ModelDesc,
-               MoeLayerDesc, check, lib)
+               MoeLayerDesc, check, lib, OK)
 from .backend import _ptr, _stream, repack_dev, synth_ggml_dev
 
 
@@ -112,6 +112,13 @@ class DeviceModel:
         NUMERICS_FAST (tree sums)."""
         self.numerics = mode
         self.desc.numerics = mode
+
+    def frame_check(self, n: int = 1) -> bool:
+        """gpuLayersSupported (src/gguf/llama.zig:985-1009) for the HIP arm:
+        True when the frame serves this model at n lanes -- the checks the
+        frame call makes before launching anything, asked once at load."""
+        rc = lib().loomhip_frame_check(C.byref(self.desc), n)
+        return rc == OK
 
     # ---- construction ----------------------------------------------------
     @classmethod

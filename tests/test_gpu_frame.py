@@ -240,9 +240,11 @@ def test_frame_declines_unserved_dims(lh):
 
     spec = lh.stories15m(ctx_len=8)
     dm = lh.DeviceModel.synth(spec, seed=1)
+    assert dm.frame_check(1) and dm.frame_check(32)
     dm.desc.head_dim = 300  # > 256
     dec = lh.Decoder(dm, 1)
     loom_amd.take_launch_count()
+    assert not dm.frame_check(1)  # gpuLayersSupported's answer at load
     assert dec.step() == loom_amd.DECLINED
     assert loom_amd.take_launch_count() == 0
 
@@ -266,6 +268,7 @@ def test_frame_declines_unserved_moe_layer(lh, bad):
         L.router = None
     dec = lh.Decoder(dm, 1)
     loom_amd.take_launch_count()
+    assert not dm.frame_check(1)
     if bad == "no_router":
         with pytest.raises(loom_amd.LoomHipError):
             dec.step()
