@@ -327,6 +327,85 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
  * a frame must never decline halfway through a token. */
 int loomhip_frame_check(const loomhip_model *m, size_t n);
 
+/* ---- GGUF v3 files (src/gguf/gguf.zig) ------------------------------------
+ * gguf.zig:251-332 parse: the header, the metadata key/values and the tensor
+ * table, with the whole file mapped read-only so a tensor's bytes are a
+ * pointer into it (the data section starts at the first general.alignment
+ * boundary after the table; tensor offsets are relative to it).  Malformed
+ * files return LOOMHIP_ERR_ARG with the reference's error name first in
+ * loomhip_last_error (NotGguf, UnsupportedGgufVersion, TruncatedGguf,
+ * UnknownValueType, ArrayNestingTooDeep, BadTensorDims, BadAlignment). */
+typedef struct loomhip_gguf loomhip_gguf;
+int loomhip_gguf_open(const char *path, loomhip_gguf **out);
+void loomhip_gguf_close(loomhip_gguf *g);
+typedef struct {
+    uint32_t version;
+    uint64_t alignment, n_tensors, n_kv, data_offset, file_size;
+    const uint8_t *base; /* the mapped file */
+} loomhip_gguf_info;
+int loomhip_gguf_get_info(const loomhip_gguf *g, loomhip_gguf_info *info);
+/* Tensor i (gguf.zig:36-47 TensorInfo): dims[0] is the row length (unused
+ * dims read 1); nbytes is its GGML size for F32/F16/Q4_0/Q8_0/Q4_K/Q6_K (0
+ * for other types), data its bytes in the mapping (NULL when unknown or
+ * outside the file). */
+typedef struct {
+    const char *name;
+    uint32_t n_dims;
+    uint64_t dims[8];
+    uint32_t ggml_type;
+    uint64_t offset, nbytes;
+    const void *data;
+} loomhip_gguf_tensor;
+int loomhip_gguf_get_tensor(const loomhip_gguf *g, size_t i, loomhip_gguf_tensor *t);
+/* Parsed.findTensor (gguf.zig:139-144); DECLINED when absent. */
+int loomhip_gguf_find_tensor(const loomhip_gguf *g, const char *name, size_t *index);
+/* Key/value i (gguf.zig:49-71 MetaValue / MetaKV): kind 0 int (i), 1 uint
+ * (u), 2 float (f), 3 bool (u), 4 string (s, s_len), 5 string array (strs,
+ * count), 6 f32 array (f32s), 7 i32 array (i32s), 8 array of another element
+ * type (elem_type, count; contents skipped); type is the file's value type;
+ * [span_start, span_end) the pair's bytes in the file. */
+typedef struct {
+    const char *key;
+    uint32_t type;
+    int kind;
+    int64_t i;
+    uint64_t u;
+    double f;
+    const char *s;
+    size_t s_len;
+    uint32_t elem_type;
+    uint64_t count;
+    const char *const *strs;
+    const float *f32s;
+    const int32_t *i32s;
+    uint64_t span_start, span_end;
+} loomhip_gguf_kv;
+int loomhip_gguf_get_kv(const loomhip_gguf *g, size_t i, loomhip_gguf_kv *kv);
+/* Parsed.getUint / getFloat / getString / getBool (gguf.zig:97-137), with
+ * the same coercions; DECLINED when the key is absent or of another kind. */
+int loomhip_gguf_get_uint(const loomhip_gguf *g, const char *key, uint64_t *v);
+int loomhip_gguf_get_float(const loomhip_gguf *g, const char *key, double *v);
+int loomhip_gguf_get_string(const loomhip_gguf *g, const char *key, const char **s, size_t *len);
+int loomhip_gguf_get_bool(const loomhip_gguf *g, const char *key, int *v);
+
+/* A GGUF v3 writer laid out as the reference's fixture writers lay theirs
+ * out (gguf.zig:643-912): key/values in call order, then tensor infos in call
+ * order with offsets aligned to `alignment`, zero padding to the data
+ * section and between tensors.  writer_kv: a GGUF value type (0-12) with
+ * its scalar bytes at value, a string value[0..len), or an array of
+ * elem_type with len elements at value (strings: len NUL-terminated const
+ * char * pointers).  writer_tensor copies the bytes (checked against the
+ * shape for known types).  finish writes the file and frees the writer;
+ * abort only frees it. */
+typedef struct loomhip_gguf_writer loomhip_gguf_writer;
+int loomhip_gguf_writer_begin(uint64_t alignment, loomhip_gguf_writer **out);
+int loomhip_gguf_writer_kv(loomhip_gguf_writer *w, const char *key, uint32_t type, const void *value,
+                           uint64_t len, uint32_t elem_type);
+int loomhip_gguf_writer_tensor(loomhip_gguf_writer *w, const char *name, uint32_t n_dims, const uint64_t *dims,
+                               uint32_t ggml_type, const void *data, uint64_t nbytes);
+int loomhip_gguf_writer_finish(loomhip_gguf_writer *w, const char *path);
+void loomhip_gguf_writer_abort(loomhip_gguf_writer *w);
+
 /* ---- expert cache: pinned host memory -> HBM LRU ----------------------------
  * The tiers of ExpertCache (src/engine/expert_cache.zig:150-249) with HBM as
  * the cache and pinned host memory as the backing store that readBlock

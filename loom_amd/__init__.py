@@ -243,6 +243,22 @@ def lib() -> C.CDLL:
         "loomhip_moe_ffn_block_stats": (i, [C.POINTER(u64), C.POINTER(u64), C.POINTER(u64)]),
         "loomhip_moe_ffn_block_prefetch": (i, [sz, C.POINTER(ExpertRefDesc), sz]),
         "loomhip_register_arena": (i, [vp, sz]),
+        # GGUF (structs from loom_amd.gguf, passed by reference as void *)
+        "loomhip_gguf_open": (i, [C.c_char_p, vp]),
+        "loomhip_gguf_close": (None, [vp]),
+        "loomhip_gguf_get_info": (i, [vp, vp]),
+        "loomhip_gguf_get_tensor": (i, [vp, sz, vp]),
+        "loomhip_gguf_find_tensor": (i, [vp, C.c_char_p, vp]),
+        "loomhip_gguf_get_kv": (i, [vp, sz, vp]),
+        "loomhip_gguf_get_uint": (i, [vp, C.c_char_p, vp]),
+        "loomhip_gguf_get_float": (i, [vp, C.c_char_p, vp]),
+        "loomhip_gguf_get_string": (i, [vp, C.c_char_p, vp, vp]),
+        "loomhip_gguf_get_bool": (i, [vp, C.c_char_p, vp]),
+        "loomhip_gguf_writer_begin": (i, [u64, vp]),
+        "loomhip_gguf_writer_kv": (i, [vp, C.c_char_p, C.c_uint32, vp, u64, C.c_uint32]),
+        "loomhip_gguf_writer_tensor": (i, [vp, C.c_char_p, C.c_uint32, vp, C.c_uint32, vp, u64]),
+        "loomhip_gguf_writer_finish": (i, [vp, C.c_char_p]),
+        "loomhip_gguf_writer_abort": (None, [vp]),
         "loomhip_materialize_arenas": (sz, []),
     }
     for name, (res, args) in sig.items():

@@ -18,8 +18,8 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import (GATING_SOFTMAX, NUMERICS_PARITY, Q4_0, Q4_K, Q6_K, LayerDesc, ModelDesc,
-               MoeLayerDesc, check, lib, OK)
+from . import (GATING_SIGMOID, GATING_SOFTMAX, NUMERICS_PARITY, Q4_0, Q4_K, Q6_K, Q8_0, LayerDesc,
+               ModelDesc, MoeLayerDesc, check, lib, OK)
 from .backend import _ptr, _stream, repack_dev, synth_ggml_dev
 
 
@@ -169,6 +169,107 @@ class DeviceModel:
         m._build_desc()
         return m
 
+    @classmethod
+    def from_gguf(cls, g, ctx_len: int | None = None, keep_ggml: bool = False) -> "DeviceModel":
+        """llama.zig:335-420 load, for the architectures the frame serves
+        (llama: NORM rope; qwen3moe: NEOX rope and per-head q/k RMSNorm),
+        from a loom_amd.gguf.GgufFile: the configuration from the metadata
+        with load's defaults, every matrix's GGML bytes uploaded and
+        repacked to the device layout (each layer keeps its own types), the
+        norms, routers and selection bias as f32 (routeCfgFromMeta,
+        src/gguf/moe.zig:63-97, for the gating)."""
+        import torch
+
+        arch = g.get_string("general.architecture")
+        if arch not in ("llama", "qwen3moe"):
+            raise ValueError(f"UnsupportedArchitecture: {arch} (the frame serves llama and qwen3moe)")
+
+        def u(key, default=None):
+            v = g.get_uint(f"{arch}.{key}")
+            return default if v is None else int(v)
+
+        def fl(key, default):
+            v = g.get_float(f"{arch}.{key}")
+            return default if v is None else float(v)
+
+        dim, n_heads = u("embedding_length"), u("attention.head_count")
+        if not dim or not n_heads:
+            raise ValueError("BadConfig: embedding_length / attention.head_count")
+        head_dim = u("attention.key_length", dim // n_heads)
+        n_layers = u("block_count") - u("nextn_predict_layers", 0)
+        n_expert, n_used = u("expert_count", 0), u("expert_used_count", 0)
+        ffn = u("feed_forward_length", 0)
+        moe_ffn = u("expert_feed_forward_length", 0) or (ffn // n_used if n_expert and n_used else 0)
+        norm = g.get_bool(f"{arch}.expert_weights_norm")
+
+        def tensor(name):
+            t = g.find_tensor(name)
+            if t is None:
+                raise ValueError(f"missing tensor {name}")
+            return t
+
+        embd = tensor("token_embd.weight")
+        out = g.find_tensor("output.weight") or embd  # tied embeddings
+        first_moe = tensor("blk.0.ffn_gate_exps.weight") if n_expert else None
+        spec = ModelSpec(dim=dim, head_dim=head_dim, n_layers=n_layers, n_heads=n_heads,
+                         n_kv_heads=u("attention.head_count_kv", n_heads), vocab=embd.dims[1],
+                         ctx_len=ctx_len or u("context_length", 2048), rope_dim=u("rope.dimension_count", head_dim),
+                         rope_base=fl("rope.freq_base", 10000.0), eps=fl("attention.layer_norm_rms_epsilon", 1e-5),
+                         rope_neox=arch == "qwen3moe", qk_norm=g.find_tensor("blk.0.attn_q_norm.weight") is not None,
+                         embed_t=embd.ggml_type, output_t=out.ggml_type,
+                         wq_t=tensor("blk.0.attn_q.weight").ggml_type, wk_t=tensor("blk.0.attn_k.weight").ggml_type,
+                         wv_t=tensor("blk.0.attn_v.weight").ggml_type,
+                         wo_t=tensor("blk.0.attn_output.weight").ggml_type, ffn=ffn, n_expert=n_expert,
+                         n_used=n_used, moe_ffn=moe_ffn,
+                         moe_gate_t=first_moe.ggml_type if first_moe else Q4_K,
+                         router_bias=g.find_tensor("blk.0.exp_probs_b.bias") is not None,
+                         gating=GATING_SIGMOID if u("expert_gating_func", 1) == 2 else GATING_SOFTMAX,
+                         weights_norm=True if norm is None else norm,
+                         weights_scale=fl("expert_weights_scale", 1.0))
+        m = cls(spec)
+
+        def quant(key, t, rows, cols, planes=1):
+            if t.ggml_type not in (Q4_0, Q8_0, Q4_K, Q6_K) or t.data is None:
+                raise ValueError(f"{t.name}: GGML type {t.ggml_type} is not served")
+            gb = torch.from_numpy(np.array(t.data, copy=True)).cuda()
+            m.tensors[key] = _Tensor(t.ggml_type, rows, cols, planes, repack_dev(t.ggml_type, gb, rows, cols, planes),
+                                     gb if keep_ggml else None)
+
+        def f32(key, t, n):
+            if t.ggml_type != 0 or t.nbytes != 4 * n:
+                raise ValueError(f"{t.name}: expected {n} f32 values")
+            m.f32[key] = torch.from_numpy(np.array(t.data.view(np.float32), copy=True)).cuda()
+
+        m.f32["ones_dim"] = torch.ones(dim, dtype=torch.float32, device="cuda")
+        m.f32["ones_hd"] = torch.ones(head_dim, dtype=torch.float32, device="cuda")
+        quant("embed", embd, spec.vocab, dim)
+        quant("output", out, spec.vocab, dim)
+        f32("out_norm", tensor("output_norm.weight"), dim)
+        for li in range(n_layers):
+            b, p = f"blk.{li}.", f"l{li}."
+            f32(p + "attn_norm", tensor(b + "attn_norm.weight"), dim)
+            f32(p + "ffn_norm", tensor(b + "ffn_norm.weight"), dim)
+            if spec.qk_norm:
+                f32(p + "q_norm", tensor(b + "attn_q_norm.weight"), head_dim)
+                f32(p + "k_norm", tensor(b + "attn_k_norm.weight"), head_dim)
+            quant(p + "wq", tensor(b + "attn_q.weight"), spec.qd, dim)
+            quant(p + "wk", tensor(b + "attn_k.weight"), spec.kvd, dim)
+            quant(p + "wv", tensor(b + "attn_v.weight"), spec.kvd, dim)
+            quant(p + "wo", tensor(b + "attn_output.weight"), dim, spec.qd)
+            if n_expert:
+                f32(p + "router", tensor(b + "ffn_gate_inp.weight"), n_expert * dim)
+                if spec.router_bias:
+                    f32(p + "router_bias", tensor(b + "exp_probs_b.bias"), n_expert)
+                quant(p + "gate", tensor(b + "ffn_gate_exps.weight"), moe_ffn, dim, n_expert)
+                quant(p + "up", tensor(b + "ffn_up_exps.weight"), moe_ffn, dim, n_expert)
+                quant(p + "down", tensor(b + "ffn_down_exps.weight"), dim, moe_ffn, n_expert)
+            else:
+                quant(p + "ffn_gate", tensor(b + "ffn_gate.weight"), ffn, dim)
+                quant(p + "ffn_up", tensor(b + "ffn_up.weight"), ffn, dim)
+                quant(p + "ffn_down", tensor(b + "ffn_down.weight"), dim, ffn)
+        m._build_desc()
+        return m
+
     def _ptr(self, name):
         t = self.tensors.get(name)
         return None if t is None else t.dev.data_ptr()
@@ -180,32 +281,34 @@ class DeviceModel:
     def _build_desc(self):
         s = self.spec
         layers = (LayerDesc * s.n_layers)()
+        ty = lambda name: self.tensors[name].t  # noqa: E731
         for li in range(s.n_layers):
             p = f"l{li}."
             L = layers[li]
-            L.attn_norm = L.ffn_norm = self._f("ones_dim")
-            L.q_norm = L.k_norm = self._f("ones_hd") if s.qk_norm else None
-            L.wq_t, L.wk_t, L.wv_t, L.wo_t = s.wq_t, s.wk_t, s.wv_t, s.wo_t
+            L.attn_norm = self._f(p + "attn_norm") or self._f("ones_dim")
+            L.ffn_norm = self._f(p + "ffn_norm") or self._f("ones_dim")
+            L.q_norm = (self._f(p + "q_norm") or self._f("ones_hd")) if s.qk_norm else None
+            L.k_norm = (self._f(p + "k_norm") or self._f("ones_hd")) if s.qk_norm else None
+            L.wq_t, L.wk_t, L.wv_t, L.wo_t = (ty(p + n) for n in ("wq", "wk", "wv", "wo"))
             L.wq, L.wk, L.wv, L.wo = (self._ptr(p + n) for n in ("wq", "wk", "wv", "wo"))
             if s.n_expert:
                 L.is_moe = 1
                 L.moe = MoeLayerDesc(s.dim, s.moe_ffn, s.n_expert, s.n_used, s.gating,
                                      int(s.weights_norm), s.weights_scale, self._f(p + "router"),
-                                     self._f(p + "router_bias"), None, s.moe_gate_t, s.moe_gate_t,
-                                     s.moe_down_t, self._ptr(p + "gate"), self._ptr(p + "up"),
+                                     self._f(p + "router_bias"), None, ty(p + "gate"), ty(p + "up"),
+                                     ty(p + "down"), self._ptr(p + "gate"), self._ptr(p + "up"),
                                      self._ptr(p + "down"))
             else:
                 L.is_moe = 0
-                L.ffn_gate_t = L.ffn_up_t = s.ffn_gate_t
-                L.ffn_down_t = s.ffn_down_t
+                L.ffn_gate_t, L.ffn_up_t, L.ffn_down_t = (ty(p + n) for n in ("ffn_gate", "ffn_up", "ffn_down"))
                 L.ffn_gate, L.ffn_up, L.ffn_down = (self._ptr(p + n)
                                                     for n in ("ffn_gate", "ffn_up", "ffn_down"))
                 L.ffn = s.ffn
         self.layers = layers
         self.desc = ModelDesc(s.dim, s.head_dim, s.n_layers, s.n_heads, s.n_kv_heads, s.vocab,
                               s.ctx_len, s.rope_dim, s.rope_base, s.eps, int(s.rope_neox),
-                              s.embed_t, self._ptr("embed"), self._f("ones_dim"), s.output_t,
-                              self._ptr("output"), C.cast(layers, C.POINTER(LayerDesc)), None,
+                              ty("embed"), self._ptr("embed"), self._f("out_norm") or self._f("ones_dim"),
+                              ty("output"), self._ptr("output"), C.cast(layers, C.POINTER(LayerDesc)), None,
                               self.numerics, None)
 
     def weight_bytes(self) -> int:

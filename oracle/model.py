@@ -35,12 +35,18 @@ class OracleModel:
             return o.Tensor(t.t, host(name).ctypes.data, cols, rows, planes)
 
         ones_dim, ones_hd = f32("ones_dim"), f32("ones_hd")
+
+        def norm(name, ones):  # the model's own norm weights where it has them
+            return f32(name).ctypes.data if name in dm.f32 else ones.ctypes.data
+
         layers = (o.Layer * s.n_layers)()
         for li in range(s.n_layers):
             p = f"l{li}."
             L = layers[li]
-            L.attn_norm = L.ffn_norm = ones_dim.ctypes.data
-            L.q_norm = L.k_norm = ones_hd.ctypes.data if s.qk_norm else None
+            L.attn_norm = norm(p + "attn_norm", ones_dim)
+            L.ffn_norm = norm(p + "ffn_norm", ones_dim)
+            L.q_norm = norm(p + "q_norm", ones_hd) if s.qk_norm else None
+            L.k_norm = norm(p + "k_norm", ones_hd) if s.qk_norm else None
             L.wq = tensor(p + "wq", s.qd, s.dim)
             L.wk = tensor(p + "wk", s.kvd, s.dim)
             L.wv = tensor(p + "wv", s.kvd, s.dim)
@@ -65,7 +71,7 @@ class OracleModel:
         self.layers = layers
         self.model = o.Model(s.dim, s.head_dim, s.n_layers, s.n_heads, s.n_kv_heads, s.vocab,
                              s.ctx_len, s.rope_dim, s.rope_base, s.eps, int(s.rope_neox), 1,
-                             tensor("embed", s.vocab, s.dim), ones_dim.ctypes.data,
+                             tensor("embed", s.vocab, s.dim), norm("out_norm", ones_dim),
                              tensor("output", s.vocab, s.dim), C.cast(layers, C.c_void_p))
         self.cache_bytes = int(o.lib().lo_seq_cache_bytes(C.byref(self.model)))
 
