@@ -82,12 +82,21 @@ def _greedy(lh, om, dm, prompt, n_gen):
     return dev_toks, ref_toks
 
 
-def test_stories15m_greedy_64(lh, oracle):
-    """Config 1 at full size: the stories15M shape with Q4_0 weights (llama
-    architecture, NORM rope, dense SwiGLU), a seeded 16-token prompt, 64
-    greedy tokens identical to the oracle's."""
-    spec = lh.stories15m(ctx_len=96)
-    dm = lh.DeviceModel.synth(spec, seed=3, keep_ggml=True)
+def test_stories15m_greedy_64(lh, oracle, tmp_path):
+    """Config 1 at full size and by its input recipe: the stories15M shape
+    (llama architecture, NORM rope, dense SwiGLU) with every matrix N(0,
+    0.02) through the reference's Q4_0 rule (ggml.zig:1861), written as a
+    GGUF file and loaded from it; a seeded 16-token prompt, then 64 greedy
+    tokens identical to the oracle's."""
+    from loom_amd import gguf
+    from recipes import stories15m_gguf
+
+    path = str(tmp_path / "stories15m.gguf")
+    stories15m_gguf(path, seed=3)
+    with gguf.GgufFile(path) as g:
+        dm = lh.DeviceModel.from_gguf(g, ctx_len=96, keep_ggml=True)
+    spec = dm.spec
+    assert (spec.dim, spec.n_layers, spec.n_heads, spec.head_dim, spec.vocab) == (288, 6, 6, 48, 32000)
     om = OracleModel(oracle, dm)
     prompt = np.random.default_rng(16).integers(0, spec.vocab, 16)
     dev, ref = _greedy(lh, om, dm, prompt, 64)

@@ -70,11 +70,21 @@ def test_route_kats_on_device(be, oracle):
 
 
 def make_layer(oracle, dim, ffn, n_expert, n_used, seed, gate_t=Q4_K, down_t=Q6_K,
-               router_bias=False):
+               router_bias=False, recipe=False):
+    """recipe: the expert planes by config 3's input recipe (N(0, 0.02)
+    through the oracle's GGUF quantizers); otherwise random blocks with
+    pinned scales (every quant level exercised)."""
     rng = np.random.default_rng(seed)
-    gate = npref.pinned_scale_blocks(gate_t, ffn, dim, rng, planes=n_expert)
-    up = npref.pinned_scale_blocks(gate_t, ffn, dim, rng, planes=n_expert)
-    down = npref.pinned_scale_blocks(down_t, dim, ffn, rng, planes=n_expert)
+    if recipe:
+        import recipes
+
+        gate = recipes.planes(gate_t, ffn, dim, n_expert, seed * 3 + 1)
+        up = recipes.planes(gate_t, ffn, dim, n_expert, seed * 3 + 2)
+        down = recipes.planes(down_t, dim, ffn, n_expert, seed * 3 + 3)
+    else:
+        gate = npref.pinned_scale_blocks(gate_t, ffn, dim, rng, planes=n_expert)
+        up = npref.pinned_scale_blocks(gate_t, ffn, dim, rng, planes=n_expert)
+        down = npref.pinned_scale_blocks(down_t, dim, ffn, rng, planes=n_expert)
     router = oracle.normal(n_expert * dim, seed + 1, 0.0, 1.0 / np.sqrt(dim)).reshape(n_expert, dim)
     rb = None
     if router_bias:  # Zipf(1.1) popularity as a logit bias (config 3)
@@ -88,7 +98,7 @@ def make_layer(oracle, dim, ffn, n_expert, n_used, seed, gate_t=Q4_K, down_t=Q6_
 def test_moe_ffn_routed_single_token(be, oracle, dim, ffn, E, k):
     from loom_amd.backend import RoutedCfg, WeightRef
 
-    w = make_layer(oracle, dim, ffn, E, k, seed=dim + E)
+    w = make_layer(oracle, dim, ffn, E, k, seed=dim + E, recipe=dim == 2048)
     normed = oracle.normal(dim, 99, 0.0, 1.0)
     logits = oracle.matvec(F32, w.router.view(np.uint8).ravel(), normed, E, dim)
     out = np.empty(dim, np.float32)
@@ -118,11 +128,12 @@ def _dev_layer(be, w):
 
 @pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 8, 32, 128])
 def test_moe_layer_dev_matches_oracle(be, oracle, n):
-    """Config-3 shape: hidden 2048, 128 experts top-8, ffn 768, Q4_K gate/up,
-    Q6_K down, f32 router with a Zipf(1.1) logit bias."""
+    """Config 3 by its recipe: hidden 2048, 128 experts top-8, ffn 768, Q4_K
+    gate/up and Q6_K down from N(0, 0.02) weights, f32 router with a
+    Zipf(1.1) logit bias."""
     import torch
 
-    w = make_layer(oracle, 2048, 768, 128, 8, seed=3, router_bias=True)
+    w = make_layer(oracle, 2048, 768, 128, 8, seed=3, router_bias=True, recipe=True)
     layer = _dev_layer(be, w)
     xs = np.stack([oracle.normal(2048, 500 + i, 0.0, 1.0) for i in range(n)])
     normed = torch.from_numpy(xs).cuda()
