@@ -182,6 +182,34 @@ def test_moe_layer_dev_wide_hidden(be, oracle, n):
         assert _maxrel(got[i] - resid[i], want[i] - resid[i]) <= 2e-3, i
 
 
+@pytest.mark.parametrize("n", [5, 7, 9, 16, 17, 31, 33, 47, 64, 65, 100, 127, 128, 129, 200, 256])
+def test_moe_gate_handoff_at_many_lane_counts(be, oracle, n):
+    """The batched gate kernel hands its per-chunk results from work group
+    to work group inside the launch (agent-scope stores, a completion
+    counter whose last arrival reads them back).  Every lane count from the
+    batched path's smallest to the largest served, partial last chunks
+    included, three launches each with fresh inputs: ids bit-exact and
+    outputs within 2e-3 of moeBatchUnion every time."""
+    import torch
+
+    dim, ffn, E, k = 512, 256, 32, 4
+    w = make_layer(oracle, dim, ffn, E, k, seed=91, router_bias=True)
+    layer = _dev_layer(be, w)
+    for rep in range(3):
+        xs = np.stack([oracle.normal(dim, 10_000 * rep + n * 7 + i, 0.0, 1.0) for i in range(n)])
+        resid = np.zeros((n, dim), np.float32)
+        out = torch.zeros((n, dim), dtype=torch.float32, device="cuda")
+        ids = torch.empty((n, k), dtype=torch.int32, device="cuda")
+        gates = torch.empty((n, k), dtype=torch.float32, device="cuda")
+        layer(torch.from_numpy(xs).cuda(), out, combine=be.COMBINE_EXPERT_ASC, ids=ids, gates=gates)
+        want, wid, wg = oracle.moe_batch_union(w, xs, resid)
+        torch.cuda.synchronize()
+        assert np.array_equal(ids.cpu().numpy().astype(np.uint32), wid), (n, rep)
+        assert np.all(np.abs(gates.cpu().numpy() - wg) <= 1e-6), (n, rep)
+        got = out.cpu().numpy()
+        assert max(_maxrel(got[i], want[i]) for i in range(n)) <= 2e-3, (n, rep)
+
+
 Q8_0, Q4_0 = 8, 2
 
 # (gating, weights_norm, weights_scale, selection bias): the routing variants
