@@ -206,7 +206,7 @@ def rocprof_us(tag, b):
     count; None where the table has no entry."""
     names = {"attn_pv": ("lh::attn_pv_split_kernel<128>" if b <= 4 else
                          "lh::attn_pv_kernel<128, 2>" if b < 8 else "lh::attn_pv_kernel<128, 4>"),
-             "attn_softmax": "lh::attn_softmax_kernel",
+             "attn_softmax": "lh::attn_softmax_kernel<1024>" if b <= 4 else "lh::attn_softmax_kernel<256>",
              "attn_scores": "lh::attn_scores_kernel<128>",
              "attn": "lh::attn_partial_kernel<128>" if b <= 4 else "lh::attn_direct_kernel<128, 128>"}
     try:

@@ -184,10 +184,11 @@ __global__ __launch_bounds__(NT) void attn_softmax_kernel(FrameDims D, const int
     m = redf[0];
     for (int w = 1; w < NT / 64; w++)
         m = fmaxf(m, redf[w]);
-    // 2. e_t = exp(s_t - m), rounded once to f32 from a double exponential;
+    // 2. e_t = exp(s_t - m), rounded once to f32 from a double exponential
+    //    (the polynomial form: this loop is exp's heaviest user);
     //    positions past the context up to the next multiple of 64 hold +0
     for (int j = tid; j < 64 * C; j += NT)
-        e[j] = j < P ? exp_f32(row[j] - m) : 0.0f;
+        e[j] = j < P ? exp_f32_poly(row[j] - m) : 0.0f;
     __syncthreads();
     // 3. the position-ordered sum of e (speculative composition, exact);
     // 4. p_t = e_t * (1 / sum), in place of the scores

@@ -77,18 +77,26 @@ __device__ inline float half_bits_to_float(uint32_t bits16) {
     return __half2float(__half(r));
 }
 
-// exp(x) rounded once to f32 from a double-precision exponential: x = k ln2
-// + r (Cody-Waite: ln 2 split into a double and its remainder, both applied
-// by FMA, |r| <= ln2/2), exp(r) by its Taylor series through r^13/13!
-// (truncation below 5e-18 relative) in Horner form with FMA, scaled by 2^k.
-// The double result is within about 1e-16 relative, so after the one f32
-// rounding it is the correctly rounded f32 exp except when exp(x) lies
-// within a few double ulps of an f32 rounding midpoint; on the host the same
-// steps agree with (float)exp((double)x) on every f32 input checked (every
-// seventh bit pattern in [-110, 90]).  Inputs at or below -104 round to +0,
-// above 88.8 to +inf.  About twenty double operations: a tenth of the
-// library's double exp, which the softmax evaluates at every position.
-__device__ inline float exp_f32(float xf) {
+// exp(x) rounded once to f32: the library's double-precision exponential
+// (far below half an f32 ulp of error) then one rounding, so the result is
+// the correctly rounded f32 exp except when exp(x) lies within a double ulp
+// of an f32 rounding midpoint.  The CPU path's expf is itself within 0.502
+// ulp, so the two agree on all but a sliver of inputs.
+__device__ inline float exp_f32(float x) { return (float)exp((double)x); }
+
+// The same once-rounded exponential in about twenty double operations (a
+// tenth of the library's), for the attention softmax, which evaluates it at
+// every position: x = k ln2 + r (Cody-Waite: ln 2 split into a double and its
+// remainder, both applied by FMA, |r| <= ln2/2), exp(r) by its Taylor series
+// through r^13/13! (truncation below 5e-18 relative) in Horner form with FMA,
+// scaled by 2^k.  The double result is within about 1e-16 relative, so after
+// the f32 rounding it is the correctly rounded f32 exp except within a few
+// double ulps of an f32 rounding midpoint; on the host the same steps equal
+// (float)exp((double)x) on every f32 input checked (every seventh bit pattern
+// in [-110, 90]).  Inputs at or below -104 round to +0, above 88.8 to +inf.
+// Its constants take 26 VGPRs where the compiler hoists them, so kernels
+// short of registers keep exp_f32.
+__device__ inline float exp_f32_poly(float xf) {
     if (!(xf > -104.0f))
         return xf != xf ? xf : 0.0f;
     if (xf > 88.8f)
