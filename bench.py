@@ -50,6 +50,10 @@ DOWN_BYTES = 1_290_240     # one expert's Q6_K [2048][768] plane
 ROUTER_BYTES = N_EXPERT * DIM * 4
 ATTN_W_BYTES = 4_718_592 + 589_824 + 860_160 + 4_718_592  # wq, wk (Q4_K), wv (Q6_K), wo (Q4_K)
 HEAD_BYTES = 151936 * 8 * 210  # Q6_K [151936][2048]
+# Latency of a dependent f32 add on gfx950 (in-kernel clock64 over a chain of
+# adds, the split P.V kernel's probe) and the engine clock it was measured at.
+ADD_LATENCY_CYCLES = 5.75
+CLOCK_HZ = 2.4e9
 # Largest per-step logit max-rel of FAST numerics against the CPU path at the
 # 4096-token context (32 lanes), measured by the GPU parity test named in the
 # output line.
@@ -247,6 +251,14 @@ def roofline(r, b, ctx, layers):
                         "frac": round(ops / avg_s / VALU_LANE_OPS, 4)}
         if prof:
             roof["valu"]["frac_rocprof"] = round(ops / (prof / 1e6) / VALU_LANE_OPS, 4)
+        # every output column is one chain of ctx + 1 dependent f32 adds in
+        # position order: its latency floors the launch whatever the bytes
+        floor_s = (ctx + 1) * ADD_LATENCY_CYCLES / CLOCK_HZ
+        roof["chain"] = {"adds_in_order": ctx + 1, "add_latency_cycles": ADD_LATENCY_CYCLES,
+                         "clock_GHz": CLOCK_HZ / 1e9, "floor_us": round(floor_s * 1e6, 2),
+                         "frac": round(floor_s / avg_s, 4)}
+        if prof:
+            roof["chain"]["frac_rocprof"] = round(floor_s / (prof / 1e6), 4)
     return roof, per_kernel
 
 
