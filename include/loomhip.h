@@ -90,7 +90,12 @@ uint64_t loomhip_take_launch_count(void);
 #define LOOMHIP_KT_ATTN_SCORES 7  /* token frame, PARITY: attention scores */
 #define LOOMHIP_KT_ATTN_SOFTMAX 8 /* token frame, PARITY: softmax (max, exp, ordered sum, p) */
 #define LOOMHIP_KT_ATTN_PV 9      /* token frame, PARITY: position-ordered P.V */
-#define LOOMHIP_KT_COUNT 10
+#define LOOMHIP_KT_MLA_ABSORB 10  /* MLA: qa = W_k^T q_nope */
+#define LOOMHIP_KT_MLA_SCORES 11  /* MLA: scores over the compressed cache */
+#define LOOMHIP_KT_MLA_SOFTMAX 12 /* MLA: softmax (ordered sum) */
+#define LOOMHIP_KT_MLA_WSUM 13    /* MLA: o = sum_t p_t c_t in position order */
+#define LOOMHIP_KT_MLA_WV 14      /* MLA: W_v (quantize + grouped matvec) */
+#define LOOMHIP_KT_COUNT 15
 void loomhip_profile_kernels(int enable);
 /* Waits for the recorded events; total milliseconds and launch count of tag. */
 int loomhip_kernel_time(int tag, double *total_ms, uint64_t *launches);
@@ -326,6 +331,64 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
  * gpuLayersSupported (src/gguf/llama.zig:985-1009) asks once at load, since
  * a frame must never decline halfway through a token. */
 int loomhip_frame_check(const loomhip_model *m, size_t n);
+
+/* ---- MLA attention over the compressed cache (src/gguf/deepseek.zig) ------
+ * The seam's mlaInit / mlaAppend / hasMlaCache / mlaReadCache / mlaSetWk /
+ * mlaAttnHeads (src/compute/backend.zig:162-169,193-197; the CPU arm
+ * declines, src/compute/cpu.zig:47-96; the Vulkan arm
+ * src/vulkan/backend.zig:589-771).  The cache holds, per layer and
+ * position, the normalised latent c_kv (kvr floats) and the rotated shared
+ * rope key (rope floats), f32 as the engine's own cache
+ * (deepseek.zig:523-524).  Attention follows the host head loop
+ * (deepseek.zig:988-1047) in its own order: absorb qa = sum_r q_nope[r] W_k[r]
+ * (axpy order), s_t = (dotF32(qa, c_t) + dotF32(q_rope, kr_t)) * scale, the
+ * exact softmax, o = sum_t p_t c_t (axpy order), out = matvec(W_v, o) -- so
+ * o and out are bit-identical to the CPU path.  Slices are (pointer, length)
+ * pairs; a length that does not match the cache declines, as the Vulkan arm. */
+
+/* mlaInit: records the cache shape (allocated on first use); DECLINED for a
+ * context over 7,936 positions, kvr over 4096 or rope over 512. */
+int loomhip_mla_init(size_t layers, size_t ctx_len, size_t kvr, size_t rope);
+/* hasMlaCache: 1 when the device cache exists (allocating it), else 0. */
+int loomhip_has_mla_cache(void);
+/* mlaAppend: one position's rows into layer li of the device cache. */
+int loomhip_mla_append(size_t li, size_t pos, const float *c_kv, size_t c_len, const float *k_rope,
+                       size_t r_len);
+/* mlaReadCache: one position's rows back (after the compute stream drains). */
+int loomhip_mla_read_cache(size_t li, size_t pos, float *c_kv, size_t c_len, float *k_rope, size_t r_len);
+/* mlaSetWk: layers in order, as the reference requires.  The device keeps no
+ * f32 copy: the absorb dequantizes kv_b's W_k rows in the kernel (the same
+ * values at 1/7 of the bytes), so this only validates the order. */
+int loomhip_mla_set_wk(size_t li, const float *wk_f32, size_t n);
+/* mlaAttnHeads: every head's attention at position pos of layer li, W_v
+ * applied: out [n_heads][vd].  kv_b is the fused GGML tensor (rows h*(nope+vd)
+ * .. +nope: head h's W_k, the next vd rows its W_v; Q4_0/Q8_0/Q4_K/Q6_K),
+ * split per head into the device layout on first use and kept, keyed by its
+ * host pointer. */
+int loomhip_mla_attn_heads(size_t li, size_t pos, const float *q_nope, size_t qn_len, const float *q_rope,
+                           size_t qr_len, int kvb_type, const uint8_t *kv_b, size_t kvb_len, float *out,
+                           size_t out_len, size_t n_heads, size_t nope, size_t vd, float scale);
+
+/* Device-resident form (no seam counterpart): the same attention over a
+ * caller-held cache, stream-ordered.  wk / wv: kv_b split per head into
+ * W_k planes [n_heads][nope][kvr] and W_v planes [n_heads][vd][kvr] of the
+ * device layout (loomhip_mla_split_kvb_dev). */
+typedef struct {
+    int kvb_type;
+    const void *wk, *wv;
+    size_t n_heads, nope, vd, kvr, rope;
+    float scale;
+} loomhip_mla_attn;
+/* kv_b (GGML bytes on the device) into wk (plane_bytes(t, nope, kvr) *
+ * n_heads) and wv (plane_bytes(t, vd, kvr) * n_heads). */
+int loomhip_mla_split_kvb_dev(int t, const void *kv_b, size_t n_heads, size_t nope, size_t vd, size_t kvr,
+                              void *wk, void *wv, void *stream);
+/* c_kv [>= seq][kvr], k_rope [>= seq][rope]: one layer's rows; q_nope
+ * [n_heads][nope], q_rope [n_heads][rope] (rope applied); out [n_heads][vd];
+ * o_lat (nullable) receives o [n_heads][kvr].  Capturable once an eager call
+ * has sized the workspace for this seq. */
+int loomhip_mla_attn_dev(const loomhip_mla_attn *a, const float *c_kv, const float *k_rope, size_t seq,
+                         const float *q_nope, const float *q_rope, float *out, float *o_lat, void *stream);
 
 /* ---- GGUF v3 files (src/gguf/gguf.zig) ------------------------------------
  * gguf.zig:251-332 parse: the header, the metadata key/values and the tensor

@@ -23,10 +23,13 @@ GATING_SOFTMAX, GATING_SIGMOID, GATING_SOFTMAX_TOPK = 1, 2, 3
 COMBINE_SELECTION, COMBINE_EXPERT_ASC, COMBINE_SELECTION_ADD = 0, 1, 2
 KT_GATE_UP, KT_DOWN, KT_DENSE, KT_ATTN, KT_HEAD, KT_QKV = 0, 1, 2, 3, 4, 5
 KT_WO, KT_ATTN_SCORES, KT_ATTN_SOFTMAX, KT_ATTN_PV = 6, 7, 8, 9
+KT_MLA_ABSORB, KT_MLA_SCORES, KT_MLA_SOFTMAX, KT_MLA_WSUM, KT_MLA_WV = 10, 11, 12, 13, 14
 NUMERICS_PARITY, NUMERICS_FAST = 0, 1
 KT_NAMES = {KT_GATE_UP: "gate_up", KT_DOWN: "down", KT_DENSE: "dense", KT_ATTN: "attn",
             KT_HEAD: "head", KT_QKV: "qkv", KT_WO: "wo", KT_ATTN_SCORES: "attn_scores",
-            KT_ATTN_SOFTMAX: "attn_softmax", KT_ATTN_PV: "attn_pv"}
+            KT_ATTN_SOFTMAX: "attn_softmax", KT_ATTN_PV: "attn_pv", KT_MLA_ABSORB: "mla_absorb",
+            KT_MLA_SCORES: "mla_scores", KT_MLA_SOFTMAX: "mla_softmax", KT_MLA_WSUM: "mla_wsum",
+            KT_MLA_WV: "mla_wv"}
 
 
 class LoomHipError(RuntimeError):
@@ -155,6 +158,22 @@ class MoeLayerEcDesc(C.Structure):
     ]
 
 
+class MlaAttnDesc(C.Structure):
+    """Mirror of ``loomhip_mla_attn`` in include/loomhip.h."""
+
+    _fields_ = [
+        ("kvb_type", C.c_int),
+        ("wk", C.c_void_p),
+        ("wv", C.c_void_p),
+        ("n_heads", C.c_size_t),
+        ("nope", C.c_size_t),
+        ("vd", C.c_size_t),
+        ("kvr", C.c_size_t),
+        ("rope", C.c_size_t),
+        ("scale", C.c_float),
+    ]
+
+
 class ExpertRefDesc(C.Structure):
     """Mirror of ``loomhip_expert_ref`` in include/loomhip.h."""
 
@@ -260,6 +279,14 @@ def lib() -> C.CDLL:
         "loomhip_gguf_writer_finish": (i, [vp, C.c_char_p]),
         "loomhip_gguf_writer_abort": (None, [vp]),
         "loomhip_materialize_arenas": (sz, []),
+        "loomhip_mla_init": (i, [sz, sz, sz, sz]),
+        "loomhip_has_mla_cache": (i, []),
+        "loomhip_mla_append": (i, [sz, sz, vp, sz, vp, sz]),
+        "loomhip_mla_read_cache": (i, [sz, sz, vp, sz, vp, sz]),
+        "loomhip_mla_set_wk": (i, [sz, vp, sz]),
+        "loomhip_mla_attn_heads": (i, [sz, sz, vp, sz, vp, sz, i, vp, sz, vp, sz, sz, sz, sz, f]),
+        "loomhip_mla_split_kvb_dev": (i, [i, vp, sz, sz, sz, sz, vp, vp, vp]),
+        "loomhip_mla_attn_dev": (i, [C.POINTER(MlaAttnDesc), vp, vp, sz, vp, vp, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -22,7 +22,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import (COMBINE_EXPERT_ASC, COMBINE_SELECTION, DECLINED, F32, GATING_SIGMOID,
-               GATING_SOFTMAX, OK, MoeLayerDesc, check, lib, take_launch_count)
+               GATING_SOFTMAX, OK, MlaAttnDesc, MoeLayerDesc, check, lib, take_launch_count)
 
 MAX_BATCH = 256  # tokens per grouped MoE launch (the reference caps batching at 8)
 
@@ -207,6 +207,11 @@ _KERNEL_SYMBOLS = {
     "attn_softmax": "attn_softmax_kernel (PARITY: max, exp, position-ordered sum, p)",
     "attn_pv": "attn_pv_split_kernel<HD> (up to 4 lanes) / attn_pv_kernel<HD, W> (PARITY: position-ordered "
                "P.V)",
+    "mla_absorb": "mla_absorb_kernel (MLA: qa = W_k^T q_nope in axpy order)",
+    "mla_scores": "mla_scores_kernel (MLA: dotF32-order scores over the compressed cache)",
+    "mla_softmax": "mla_softmax_kernel<1024> (MLA: max, exp, position-ordered sum, p)",
+    "mla_wsum": "mla_wsum_kernel (MLA: o = sum_t p_t c_t in position order)",
+    "mla_wv": "quant_act_kernel + dmmv_kernel<T, 1, false> (MLA: W_v per head)",
 }
 
 
@@ -290,6 +295,70 @@ def dequant_dev(t: int, out, w, rows: int, cols: int) -> int:
                  "dequant_dev")
 
 
+# ---- MLA attention over the compressed cache (src/compute/backend.zig:162-169,
+# 193-197; src/gguf/deepseek.zig:851-1048) ----------------------------------
+
+
+def mlaInit(layers: int, ctx_len: int, kvr: int, rope: int) -> bool:
+    """backend.mlaInit: record the compressed cache's shape; False declines."""
+    return _served(lib().loomhip_mla_init(layers, ctx_len, kvr, rope), "mlaInit")
+
+
+def hasMlaCache() -> bool:
+    return bool(lib().loomhip_has_mla_cache())
+
+
+def mlaAppend(li: int, pos: int, c_kv: np.ndarray, k_rope: np.ndarray) -> bool:
+    """backend.mlaAppend: mirror one position's rows into the device cache."""
+    c_kv = np.ascontiguousarray(c_kv, np.float32)
+    k_rope = np.ascontiguousarray(k_rope, np.float32)
+    return _served(lib().loomhip_mla_append(li, pos, _p(c_kv), c_kv.size, _p(k_rope), k_rope.size), "mlaAppend")
+
+
+def mlaReadCache(li: int, pos: int, c_kv: np.ndarray, k_rope: np.ndarray) -> bool:
+    return _served(lib().loomhip_mla_read_cache(li, pos, _p(c_kv), c_kv.size, _p(k_rope), k_rope.size),
+                   "mlaReadCache")
+
+
+def mlaSetWk(li: int, wk_f32: np.ndarray) -> bool:
+    wk_f32 = np.ascontiguousarray(wk_f32, np.float32)
+    return _served(lib().loomhip_mla_set_wk(li, _p(wk_f32), wk_f32.size), "mlaSetWk")
+
+
+def mlaAttnHeads(li: int, pos: int, q_nope: np.ndarray, q_rope: np.ndarray, kv_b: WeightRef, out: np.ndarray,
+                 n_heads: int, nope: int, v_head_dim: int, scale: float) -> bool:
+    """backend.mlaAttnHeads: every head's attention over the device cache with
+    W_v applied, into out [n_heads * v_head_dim]; False declines."""
+    q_nope = np.ascontiguousarray(q_nope, np.float32)
+    q_rope = np.ascontiguousarray(q_rope, np.float32)
+    rc = lib().loomhip_mla_attn_heads(li, pos, _p(q_nope), q_nope.size, _p(q_rope), q_rope.size, kv_b.ty,
+                                      _p(kv_b.data), kv_b.data.nbytes, _p(out), out.size, n_heads, nope,
+                                      v_head_dim, scale)
+    return _served(rc, "mlaAttnHeads")
+
+
+class MlaAttn:
+    """Device-resident MLA attention of one layer: kv_b (GGML bytes, a torch
+    uint8 device tensor) split per head into W_k / W_v planes once."""
+
+    def __init__(self, kvb_type: int, kv_b_ggml, n_heads: int, nope: int, vd: int, kvr: int, rope: int,
+                 scale: float):
+        import torch
+
+        self.wk = torch.empty(plane_bytes(kvb_type, nope, kvr) * n_heads, dtype=torch.uint8, device="cuda")
+        self.wv = torch.empty(plane_bytes(kvb_type, vd, kvr) * n_heads, dtype=torch.uint8, device="cuda")
+        check(lib().loomhip_mla_split_kvb_dev(kvb_type, _ptr(kv_b_ggml), n_heads, nope, vd, kvr, _ptr(self.wk),
+                                              _ptr(self.wv), _stream()), "mla_split_kvb_dev")
+        self.desc = MlaAttnDesc(kvb_type, self.wk.data_ptr(), self.wv.data_ptr(), n_heads, nope, vd, kvr, rope,
+                                scale)
+        self.n_heads, self.nope, self.vd, self.kvr, self.rope = n_heads, nope, vd, kvr, rope
+
+    def __call__(self, c_kv, k_rope, seq: int, q_nope, q_rope, out, o_lat=None) -> int:
+        return check(lib().loomhip_mla_attn_dev(C.byref(self.desc), _ptr(c_kv), _ptr(k_rope), seq, _ptr(q_nope),
+                                                _ptr(q_rope), _ptr(out), _ptr(o_lat), _stream()),
+                     "mla_attn_dev")
+
+
 class MoeLayer:
     """Device-resident MoE layer (weights are torch uint8 tensors in the
     device layout, one plane per expert)."""
@@ -321,7 +390,8 @@ class MoeLayer:
 
 
 __all__ = [
-    "COMBINE_EXPERT_ASC", "COMBINE_SELECTION", "DECLINED", "ExpertRef", "F32", "MAX_BATCH", "MoeLayer",
+    "COMBINE_EXPERT_ASC", "COMBINE_SELECTION", "DECLINED", "ExpertRef", "F32", "MAX_BATCH", "MlaAttn", "MoeLayer",
+    "hasMlaCache", "mlaAppend", "mlaAttnHeads", "mlaInit", "mlaReadCache", "mlaSetWk",
     "moeFfnBlock", "moeFfnBlockStats",
     "RoutedCfg", "WeightRef", "clearWeightCache", "dequantRow", "matmul", "matvec", "moeFfnBlockRouted",
     "moeRoute", "parallelBegin", "parallelEnd", "registerWeights", "takeCmdBufCount",

@@ -169,32 +169,9 @@ __global__ __launch_bounds__(NT) void attn_softmax_kernel(FrameDims D, const int
     extern __shared__ __align__(16) float e[]; // e[s_stride]
     __shared__ float redf[NT / 64];
     __shared__ SeqSumLds seq;
-    const int h = blockIdx.x, t = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
+    const int h = blockIdx.x, t = blockIdx.z;
     const int P = min(pos[t], D.ctx - 1) + 1;
-    const int C = (P + 63) / 64;
-    float *row = S + ((size_t)t * D.n_heads + h) * s_stride;
-    // 1. m = max over the scores (order-free)
-    float m = -INFINITY;
-    for (int j = tid; j < P; j += NT)
-        m = fmaxf(m, row[j]);
-    m = wave_max(m);
-    if (ln == 0)
-        redf[wave] = m;
-    __syncthreads();
-    m = redf[0];
-    for (int w = 1; w < NT / 64; w++)
-        m = fmaxf(m, redf[w]);
-    // 2. e_t = exp(s_t - m), rounded once to f32 from a double exponential
-    //    (the polynomial form: this loop is exp's heaviest user);
-    //    positions past the context up to the next multiple of 64 hold +0
-    for (int j = tid; j < 64 * C; j += NT)
-        e[j] = j < P ? exp_f32_poly(row[j] - m) : 0.0f;
-    __syncthreads();
-    // 3. the position-ordered sum of e (speculative composition, exact);
-    // 4. p_t = e_t * (1 / sum), in place of the scores
-    const float inv = 1.0f / seq_sum_nonneg<NT / 64>(e, P, seq);
-    for (int j = tid; j < P; j += NT)
-        row[j] = e[j] * inv;
+    softmax_row_exact<NT>(S + ((size_t)t * D.n_heads + h) * s_stride, P, e, redf, seq);
 }
 
 // ---- P.V ----------------------------------------------------------------------------

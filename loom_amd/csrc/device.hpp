@@ -13,13 +13,8 @@ constexpr int MAX_E = 256, MAX_K = 16, MAX_TOK = 256; // routing limits
 // f32 arithmetic in the reference's two-rounding form (src/gguf/ggml.zig:
 // 1342-1374 Q4_K, 1420-1471 Q6_K, 1834-1849 Q4_0/Q8_0); value (r, c) of a
 // rows x cols matrix.
-__device__ inline float dequant_value(int t, const uint8_t *__restrict__ w, size_t rows, size_t cols,
-                                      size_t r, size_t c) {
-    const int be = block_elems(t);
-    const size_t nb = cols / be;
-    const size_t unit = r * nb + c / be;
-    const size_t U = rows * nb;
-    const int e = (int)(c % be);
+// Value e of block `unit` of a quantized plane of U blocks (device layout).
+__device__ inline float dequant_unit(int t, const uint8_t *__restrict__ w, size_t U, size_t unit, int e) {
     if (t == LH_Q4_K) {
         const uint8_t *blk = w + unit * 144;
         const float d = half_bits_to_float(blk[0] | (blk[1] << 8));
@@ -63,9 +58,18 @@ __device__ inline float dequant_value(int t, const uint8_t *__restrict__ w, size
         const int nib = e < 16 ? (qs[e] & 0xF) : (qs[e - 16] >> 4);
         return (float)(nib - 8) * half_bits_to_float(dp[unit]);
     }
+    return 0.0f;
+}
+
+__device__ inline float dequant_value(int t, const uint8_t *__restrict__ w, size_t rows, size_t cols,
+                                      size_t r, size_t c) {
     if (t == LH_F16)
         return half_bits_to_float(((const uint16_t *)w)[r * cols + c]);
-    return ((const float *)w)[r * cols + c];
+    if (t == LH_F32)
+        return ((const float *)w)[r * cols + c];
+    const int be = block_elems(t);
+    const size_t nb = cols / be;
+    return dequant_unit(t, w, rows * nb, r * nb + c / be, (int)(c % be));
 }
 
 // ---- wave-level int8 activation quantizers ------------------------------------

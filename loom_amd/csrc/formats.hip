@@ -78,6 +78,22 @@ void launch_repack(int t, const void *src, void *dst, size_t rows, size_t cols, 
     note_launch();
 }
 
+// Planes whose GGML rows start src_plane bytes apart (a per-head slice of a
+// fused tensor): the same per-block copy, plane by plane.
+void launch_repack_strided(int t, const void *src, size_t src_plane, void *dst, size_t rows, size_t cols,
+                           size_t planes, hipStream_t st) {
+    const size_t U = rows * (cols / block_elems(t));
+    const size_t sp = ggml_bytes(t, rows, cols), dp = plane_bytes(t, rows, cols);
+    if (t == LH_Q4_K || t == LH_F32 || t == LH_F16) {
+        (void)hipMemcpy2DAsync(dst, dp, src, src_plane, sp, planes, hipMemcpyDeviceToDevice, st);
+        return;
+    }
+    const size_t n = U * planes;
+    hipLaunchKernelGGL(repack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, t,
+                       (const uint8_t *)src, (uint8_t *)dst, U, src_plane, dp, planes);
+    note_launch();
+}
+
 // ---- synthetic weights ------------------------------------------------------
 // Counter-based hash per (seed, plane, unit, word): deterministic and
 // independent of launch shape.

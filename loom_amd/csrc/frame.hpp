@@ -244,6 +244,34 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
 // one softmax launch per (head, lane), one P.V launch per (64 columns, KV
 // head, lane).  S is [n][n_heads][s_stride] f32 (scores, then p in place),
 // att the f32 attention output [n][n_heads * head_dim].
+// softmax (tensor.zig:18-28) of one row of P scores in place, in the
+// reference's order: m = max (order-free), e_t = exp(s_t - m) rounded once
+// from a double exponential (the polynomial form: this loop is exp's heaviest
+// user), the position-ordered sum of e (speculative composition, exact),
+// p_t = e_t * (1 / sum).  e holds 64 * ceil(P / 64) floats of LDS (positions
+// past P read +0); all NT threads of the work group call it.
+template <int NT>
+__device__ __forceinline__ void softmax_row_exact(float *row, int P, float *e, float *redf, SeqSumLds &seq) {
+    const int tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
+    const int C = (P + 63) / 64;
+    float m = -INFINITY;
+    for (int j = tid; j < P; j += NT)
+        m = fmaxf(m, row[j]);
+    m = wave_max(m);
+    if (ln == 0)
+        redf[wave] = m;
+    __syncthreads();
+    m = redf[0];
+    for (int w = 1; w < NT / 64; w++)
+        m = fmaxf(m, redf[w]);
+    for (int j = tid; j < 64 * C; j += NT)
+        e[j] = j < P ? exp_f32_poly(row[j] - m) : 0.0f;
+    __syncthreads();
+    const float inv = 1.0f / seq_sum_nonneg<NT / 64>(e, P, seq);
+    for (int j = tid; j < P; j += NT)
+        row[j] = e[j] * inv;
+}
+
 constexpr int EXACT_MAX_CTX = 7936; // the softmax's e[] and the sequential sum's LDS in 64 KB
 size_t exact_softmax_lds(int s_stride);
 bool launch_attn_exact(const FrameDims &D, const float *q, const float *k, const float *v, const float *q_norm,

@@ -69,6 +69,8 @@ void launch_quant_act(int wtype, const float *x, int cols, int x_stride, int nve
 void launch_dequant(int t, const void *w, size_t rows, size_t cols, float *out, hipStream_t st);
 void launch_repack(int t, const void *src, void *dst, size_t rows, size_t cols, size_t planes,
                    hipStream_t st);
+void launch_repack_strided(int t, const void *src, size_t src_plane, void *dst, size_t rows, size_t cols,
+                           size_t planes, hipStream_t st);
 void launch_synth(int t, void *dst, size_t rows, size_t cols, size_t planes, uint64_t seed,
                   float stddev, hipStream_t st);
 

@@ -328,6 +328,7 @@ void loomhip_shutdown(void) {
     moe_release_scratch();
     ec_release_scratch();
     block_release_cache();
+    mla_release();
     prof_drain();
     for (hipEvent_t e : g_prof_pool)
         (void)hipEventDestroy(e);

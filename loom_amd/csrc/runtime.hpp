@@ -78,5 +78,6 @@ bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok);
 int moe_frame_check(const loomhip_moe_layer *L, size_t n);
 void ec_release_scratch();
 void block_release_cache();
+void mla_release();
 
 } // namespace lh

@@ -184,6 +184,8 @@ def lib() -> C.CDLL:
             "lo_lru_clear": (None, [vp]),
             "lo_cache_replay": (None, [sz, vp, sz, vp, sz, vp, vp]),
             "lo_hottest_within_budget": (sz, [vp, sz, sz, C.c_uint64, vp]),
+            "lo_rope_yarn": (None, [vp, sz, sz, f, f, f]),
+            "lo_mla_attn_heads": (None, [vp, vp, sz, sz, sz, vp, vp, i, vp, sz, sz, sz, f, vp, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -348,6 +350,31 @@ def rope(vec, rope_dim, pos, base, neox):
     v = np.array(vec, np.float32)
     (lib().lo_rope_neox if neox else lib().lo_rope_norm)(_p(v), rope_dim, pos, base)
     return v
+
+
+def rope_yarn(vec, pos, base, factor=0.0, orig_ctx=0.0):
+    """deepseek.zig:581-629 ropeApply (NORM pairs; YaRN when factor > 1)."""
+    v = np.array(vec, np.float32)
+    lib().lo_rope_yarn(_p(v), v.size, pos, base, factor, orig_ctx)
+    return v
+
+
+def mla_attn_heads(c_kv, k_rope, seq, q_nope, q_rope, kvb_type, kv_b, n_heads, nope, vd, scale):
+    """deepseek.zig:988-1047: (out [n_heads][vd], o_lat [n_heads][kvr]) from
+    one layer's cache rows c_kv [>= seq][kvr] and k_rope [>= seq][rope]."""
+    c_kv = np.ascontiguousarray(c_kv, np.float32)
+    k_rope = np.ascontiguousarray(k_rope, np.float32)
+    kvr, rope = c_kv.shape[-1], k_rope.shape[-1]
+    q_nope = np.ascontiguousarray(q_nope, np.float32)
+    q_rope = np.ascontiguousarray(q_rope, np.float32)
+    kv_b = np.ascontiguousarray(kv_b, np.uint8)
+    assert q_nope.size == n_heads * nope and q_rope.size == n_heads * rope
+    assert kv_b.size >= n_heads * (nope + vd) * row_bytes(kvb_type, kvr)
+    out = np.empty(n_heads * vd, np.float32)
+    o_lat = np.empty(n_heads * kvr, np.float32)
+    lib().lo_mla_attn_heads(_p(c_kv), _p(k_rope), seq, kvr, rope, _p(q_nope), _p(q_rope), kvb_type, _p(kv_b),
+                            n_heads, nope, vd, scale, _p(out), _p(o_lat))
+    return out, o_lat
 
 
 def head_norm(vec, w, n_heads, hd, eps):

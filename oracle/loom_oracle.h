@@ -213,6 +213,16 @@ void lo_cache_replay(size_t capacity, const uint8_t *pinned, size_t n_ids, const
 size_t lo_hottest_within_budget(const uint64_t *access_count, size_t n, size_t expert_bytes,
                                 uint64_t budget, size_t *out_ids);
 
+/* ---- MLA attention over the compressed cache (gguf/deepseek.zig) ------- */
+/* deepseek.zig:581-629 ropeApply: NORM pairs, YaRN when factor > 1. */
+void lo_rope_yarn(float *vec, size_t n, size_t pos, float base, float factor, float orig_ctx);
+/* deepseek.zig:988-1047 host head loop (fused kv_b): absorb, scores,
+ * softmax, weighted sum of c_t, W_v.  out [n_heads][vd]; o_lat (nullable)
+ * [n_heads][kvr]. */
+void lo_mla_attn_heads(const float *c_kv, const float *k_rope, size_t seq, size_t kvr, size_t rope,
+                       const float *q_nope, const float *q_rope, int kvb_type, const uint8_t *kv_b,
+                       size_t n_heads, size_t nope, size_t vd, float scale, float *out, float *o_lat);
+
 #ifdef __cplusplus
 }
 #endif

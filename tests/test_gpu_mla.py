@@ -1,0 +1,112 @@
+"""MLA attention on the device (loom_amd/csrc/mla.hip) against the oracle's
+host head loop (oracle/mla_ref.c, deepseek.zig:988-1047): the compressed
+output o and the head outputs bit-identical, through the seam (mlaInit /
+mlaAppend / mlaAttnHeads, the reference's own device-test layout of
+vulkan/backend.zig:1432-1546: layer 1 of 2 with decoy rows in layer 0) and
+through the device-resident entry point at config 5's per-head shape
+(DeepSeek-V3: 128 heads, nope 128, rope 64, kv_lora 512, v 128) up to a
+4096-position context."""
+import numpy as np
+import pytest
+
+from mla_case import make_case
+
+pytestmark = pytest.mark.gpu
+
+Q4_0, Q8_0, Q4_K, Q6_K, F32 = 2, 8, 12, 14, 0
+
+
+@pytest.fixture(scope="module")
+def lh():
+    import loom_amd
+    from loom_amd import backend
+
+    loom_amd.init(0)
+    return backend
+
+
+def _vulkan_kvb(rng, n_heads, stride, kvr):
+    """The reference test's kv_b: random Q8_0 bytes with every block's d set
+    to 0x2C00 (0.0625), vulkan/backend.zig:1459-1463."""
+    from oracle import row_bytes
+
+    kvb = rng.integers(0, 256, n_heads * stride * row_bytes(Q8_0, kvr), dtype=np.uint8)
+    kvb.reshape(-1, 34)[:, 0] = 0x00
+    kvb.reshape(-1, 34)[:, 1] = 0x2C
+    return kvb
+
+
+def test_seam_mla_attn_heads_matches_the_host_loop(lh, oracle):
+    """mlaInit(2 layers) / mlaAppend (decoys in layer 0) / mlaAttnHeads at
+    layer 1: out bit-identical to the oracle; mlaReadCache returns the rows;
+    mlaSetWk in order only; one launch count moved."""
+    import loom_amd
+
+    n_heads, nope, vd, kvr, rope, ctx, seq, li, scale = 4, 32, 16, 64, 16, 64, 5, 1, 0.25
+    rng = np.random.default_rng(0x1207A)
+    kvb = _vulkan_kvb(rng, n_heads, nope + vd, kvr)
+    assert lh.mlaInit(2, ctx, kvr, rope)
+    assert lh.hasMlaCache()
+    assert lh.mlaSetWk(0, np.zeros(8, np.float32)) and lh.mlaSetWk(1, np.zeros(8, np.float32))
+    assert not lh.mlaSetWk(3, np.zeros(8, np.float32))  # out of order: declined
+    c_rows = ((rng.random((seq, kvr)) - 0.5) * 2).astype(np.float32)
+    r_rows = ((rng.random((seq, rope)) - 0.5) * 2).astype(np.float32)
+    for t in range(seq):
+        assert lh.mlaAppend(0, t, ((rng.random(kvr) - 0.5) * 2).astype(np.float32),
+                            ((rng.random(rope) - 0.5) * 2).astype(np.float32))
+        assert lh.mlaAppend(li, t, c_rows[t], r_rows[t])
+    assert not lh.mlaAppend(li, 0, c_rows[0][:-1], r_rows[0])  # wrong length: declined
+    back_c, back_r = np.empty(kvr, np.float32), np.empty(rope, np.float32)
+    assert lh.mlaReadCache(li, 3, back_c, back_r)
+    assert np.array_equal(back_c, c_rows[3]) and np.array_equal(back_r, r_rows[3])
+    q_nope = ((rng.random(n_heads * nope) - 0.5) * 2).astype(np.float32)
+    q_rope = ((rng.random(n_heads * rope) - 0.5) * 2).astype(np.float32)
+    got = np.full(n_heads * vd, np.nan, np.float32)
+    loom_amd.take_launch_count()
+    assert lh.mlaAttnHeads(li, seq - 1, q_nope, q_rope, lh.WeightRef(Q8_0, kvb), got, n_heads, nope, vd, scale)
+    assert loom_amd.take_launch_count() > 0
+    want, _ = oracle.mla_attn_heads(c_rows, r_rows, seq, q_nope, q_rope, Q8_0, kvb, n_heads, nope, vd, scale)
+    assert np.array_equal(got, want), np.abs(got - want).max()
+    # the same call again (kv_b split cached) and past the cache: declined
+    assert lh.mlaAttnHeads(li, seq - 1, q_nope, q_rope, lh.WeightRef(Q8_0, kvb), got, n_heads, nope, vd, scale)
+    assert np.array_equal(got, want)
+    assert not lh.mlaAttnHeads(li, ctx, q_nope, q_rope, lh.WeightRef(Q8_0, kvb), got, n_heads, nope, vd, scale)
+    assert not lh.mlaAttnHeads(li, 2, q_nope[:-1], q_rope, lh.WeightRef(Q8_0, kvb), got, n_heads, nope, vd, scale)
+    f32 = lh.WeightRef(F32, np.zeros(n_heads * (nope + vd) * kvr * 4, np.uint8))
+    assert not lh.mlaAttnHeads(li, 2, q_nope, q_rope, f32, got, n_heads, nope, vd, scale)
+    assert not lh.mlaInit(2, 8192, kvr, rope)  # past the exact softmax's context: declined
+
+
+CASES = [
+    # (type, heads, nope, vd, kvr, rope, seqs)
+    (Q4_K, 128, 128, 128, 512, 64, (1, 17, 300, 4096)),  # config 5's MLA shape
+    (Q6_K, 128, 128, 128, 512, 64, (301,)),
+    (Q8_0, 20, 32, 16, 96, 20, (1, 7, 65)),  # heads past a 32-tile, a 3-step kvr, a rope tail of 4
+    (Q4_0, 36, 16, 24, 64, 16, (33, 130)),
+]
+
+
+@pytest.mark.parametrize("t,H,nope,vd,kvr,rope,seqs", CASES, ids=["q4_k_cfg5", "q6_k_cfg5", "q8_0_ragged", "q4_0"])
+def test_device_mla_attention_is_bit_identical(lh, oracle, t, H, nope, vd, kvr, rope, seqs):
+    import torch
+
+    ctx = max(seqs)
+    case = make_case(oracle, t, H, nope, vd, kvr, rope, ctx, seed=H * 7 + kvr + t)
+    kvb_dev = torch.from_numpy(case.kv_b).cuda()
+    mla = lh.MlaAttn(t, kvb_dev, H, nope, vd, kvr, rope, case.scale)
+    c = torch.from_numpy(case.c_kv).cuda()
+    r = torch.from_numpy(case.k_rope).cuda()
+    qn = torch.from_numpy(case.q_nope).cuda()
+    qr = torch.from_numpy(case.q_rope).cuda()
+    out = torch.full((H * vd,), float("nan"), device="cuda")
+    olat = torch.full((H * kvr,), float("nan"), device="cuda")
+    for seq in seqs:
+        print(f"mla t={t} H={H} kvr={kvr} rope={rope} seq={seq}", flush=True)
+        mla(c, r, seq, qn, qr, out, olat)
+        want, want_lat = oracle.mla_attn_heads(case.c_kv, case.k_rope, seq, case.q_nope, case.q_rope, t, case.kv_b,
+                                               H, nope, vd, case.scale)
+        torch.cuda.synchronize()
+        got_lat = olat.cpu().numpy()
+        assert np.array_equal(got_lat, want_lat), (seq, np.abs(got_lat - want_lat).max())
+        got = out.cpu().numpy()
+        assert np.array_equal(got, want), (seq, np.abs(got - want).max())
