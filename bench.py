@@ -85,6 +85,9 @@ def parse():
                     help="config 2 instead: the dequant-fused matvec alone, GB/s per type x shape x vectors")
     ap.add_argument("--moe-layer", action="store_true",
                     help="config 3 instead: one MoE layer at token batches 1, 8, 32 and 128")
+    ap.add_argument("--mla", action="store_true",
+                    help="config 5's MLA attention alone: 61 layers at contexts 1024, 2048, 4096")
+    ap.add_argument("--no-mla", action="store_true", help="skip the MLA attention run of the default bench")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="first copy MB megabytes device to device three times: the known-size kernel that "
                          "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -500,6 +503,140 @@ def bench_moe_layer(args):
             "results": res}
 
 
+# Config 5's attention: DeepSeek-V3 MLA, 128 heads, q/k nope 128, rope 64,
+# kv_lora 512, v 128, Q4_K kv_b, 61 layers.
+MLA_LAYERS, MLA_H, MLA_NOPE, MLA_ROPE, MLA_KVR, MLA_VD = 61, 128, 128, 64, 512, 128
+
+
+def mla_launch_bytes(tag, S):
+    """Algorithmic bytes of one launch of an MLA kernel at context S: what it
+    must read and write once (W_k / W_v as Q4_K planes, the f32 latent and
+    rope rows, q, the score rows)."""
+    H, nope, rope, kvr, vd = MLA_H, MLA_NOPE, MLA_ROPE, MLA_KVR, MLA_VD
+    q4k = lambda rows: rows * kvr // 256 * 144  # noqa: E731
+    return {"mla_absorb": q4k(H * nope) + H * nope * 4 + H * kvr * 4,
+            "mla_scores": S * (kvr + rope) * 4 + H * (kvr + rope) * 4 + H * S * 4,
+            "mla_softmax": 2 * H * S * 4,
+            "mla_wsum": S * kvr * 4 + H * S * 4 + H * kvr * 4,
+            "mla_wv": q4k(H * vd) + H * kvr * 4 + H * vd * 4}[tag]
+
+
+def mla_launch_ops(tag, S):
+    """VALU lane-ops of the ordered f32 work (one multiply and one add per
+    term): the scores' dot products, the weighted sum, the absorb."""
+    H = MLA_H
+    return {"mla_scores": 2 * H * S * (MLA_KVR + MLA_ROPE), "mla_wsum": 2 * H * S * MLA_KVR,
+            "mla_absorb": 2 * H * MLA_NOPE * MLA_KVR}.get(tag)
+
+
+def bench_mla(args, seqs, cpu=True):
+    """Config 5's MLA attention (loomhip_mla_attn_dev) over 61 layers, each
+    with its own Q4_K kv_b (9.4 MB) and its own f32 latent cache (2,304 B per
+    position), replayed from a HIP graph: one step = one token's attention in
+    every layer at context S (batch 1).  Per-kernel HIP-event times come from
+    an eager pass; the CPU column times the oracle's host head loop on one
+    layer."""
+    import torch
+
+    from loom_amd import Q4_K
+    from loom_amd import backend as be
+
+    H, nope, rope, kvr, vd, L = MLA_H, MLA_NOPE, MLA_ROPE, MLA_KVR, MLA_VD, MLA_LAYERS
+    scale = float(1.0 / np.sqrt(nope + rope))
+    smax = max(seqs)
+    g = torch.Generator(device="cuda").manual_seed(61)
+    layers = []
+    for li in range(L):
+        kvb = be.synth_ggml_dev(Q4_K, H * (nope + vd), kvr, 1, 500 + li, float(1 / np.sqrt(kvr)))
+        layers.append((be.MlaAttn(Q4_K, kvb, H, nope, vd, kvr, rope, scale),
+                       torch.randn(smax, kvr, generator=g, device="cuda"),
+                       torch.randn(smax, rope, generator=g, device="cuda")))
+        del kvb
+    qn = torch.randn(H * nope, generator=g, device="cuda")
+    qr = torch.randn(H * rope, generator=g, device="cuda")
+    out = torch.empty(H * vd, device="cuda")
+    res = []
+    for S in seqs:
+        def step():
+            for m, c, r in layers:
+                m(c, r, S, qn, qr, out)
+        step()  # sizes the workspace before the capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(2):
+            graph.replay()
+        st = torch.cuda.current_stream()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = max(5, min(args.steps, 20))
+        torch.cuda.synchronize()
+        ev0.record(st)
+        for _ in range(n):
+            graph.replay()
+        ev1.record(st)
+        torch.cuda.synchronize()
+        ms = ev0.elapsed_time(ev1) / n
+        del graph
+        be.profileKernels(True)
+        for _ in range(2):
+            torch.cuda._sleep(50_000_000)
+            step()
+            torch.cuda.synchronize()
+        stats = be.kernelStats()
+        be.profileKernels(False)
+        kern = {}
+        for k, v in stats.items():
+            avg_s = v["ms"] / v["count"] / 1e3
+            e = {"avg_us": round(avg_s * 1e6, 2), "launches": v["count"],
+                 "GBs": round(mla_launch_bytes(k, S) / avg_s / 1e9, 1)}
+            ops = mla_launch_ops(k, S)
+            if ops:
+                e["valu_Tops"] = round(ops / avg_s / 1e12, 2)
+                e["valu_frac"] = round(ops / avg_s / VALU_LANE_OPS, 4)
+            kern[k] = e
+        dom = max(stats, key=lambda k: stats[k]["ms"])
+        avg_s = stats[dom]["ms"] / stats[dom]["count"] / 1e3
+        ops = mla_launch_ops(dom, S)
+        roof = {"bound": "valu", "kernel": stats[dom]["name"], "tag": dom, "avg_launch_us": round(avg_s * 1e6, 2)}
+        if ops:
+            roof.update({"achieved": round(ops / avg_s / 1e12, 2), "peak": round(VALU_LANE_OPS / 1e12, 1),
+                         "unit": "T lane-ops/s (f32 multiply, add: the order the reference fixes)",
+                         "frac": round(ops / avg_s / VALU_LANE_OPS, 4), "lane_ops_per_launch": int(ops)})
+        if dom == "mla_wsum":
+            floor_s = S * ADD_LATENCY_CYCLES / CLOCK_HZ
+            roof["chain"] = {"adds_in_order": S, "floor_us": round(floor_s * 1e6, 2), "frac": round(floor_s / avg_s, 4)}
+        r = {"ctx": S, "us_per_layer": round(ms * 1e3 / L, 2), "ms_per_token": round(ms, 3),
+             "layers_per_s": round(L / (ms / 1e3), 1), "kernels": kern, "roofline": roof}
+        log(f"mla ctx {S}: {ms * 1e3 / L:.2f} us per layer ({ms:.3f} ms per token over {L} layers), kernels {kern}")
+        res.append(r)
+    if cpu:
+        import oracle
+        from loom_amd import Q4_K as T
+
+        rng = np.random.default_rng(5)
+        S = smax
+        w = (rng.standard_normal((H * (nope + vd), kvr)) / np.sqrt(kvr)).astype(np.float32)
+        kvb_h = oracle.quantize(T, w)
+        c_h = rng.standard_normal((S, kvr)).astype(np.float32)
+        r_h = rng.standard_normal((S, rope)).astype(np.float32)
+        qn_h = rng.standard_normal(H * nope).astype(np.float32)
+        qr_h = rng.standard_normal(H * rope).astype(np.float32)
+        t0 = time.perf_counter()
+        oracle.mla_attn_heads(c_h, r_h, S, qn_h, qr_h, T, kvb_h, H, nope, vd, scale)
+        dt = time.perf_counter() - t0
+        res[-1]["cpu_baseline"] = {"value": round(dt * 1e6, 1), "unit": "us per layer", "cores": 1, "kind": "port",
+                                   "sample": f"the oracle's host head loop (deepseek.zig:988-1047) on one layer "
+                                             f"at context {S}"}
+        log(f"mla cpu: {dt * 1e3:.1f} ms per layer at context {S}")
+    del layers
+    torch.cuda.empty_cache()
+    return {"workload": f"config 5 attention: DeepSeek-V3 MLA over {L} layers, {H} heads, nope {nope}, rope {rope}, "
+                        f"kv_lora {kvr}, v {vd}, Q4_K kv_b, f32 latent cache, batch 1, seeded random weights and "
+                        "cache rows, HIP graph", "numerics": "the reference's order (bit-identical to the CPU path)",
+            "results": res}
+
+
 C5_DIM, C5_FFN, C5_E, C5_K, C5_SLOTS, C5_SFFN = 7168, 2048, 256, 8, 64, 2048
 
 
@@ -689,6 +826,11 @@ def main():
     from loom_amd.frame import DeviceModel, qwen3_30b_a3b
 
     loom_amd.init(0)
+    if args.mla:
+        line = {"metric": "MLA attention: us per layer and ms per token (config 5's attention)", "n_gpus": 1,
+                "data": "synthetic", "dtype": "f32", **bench_mla(args, (1024, 2048, 4096), cpu=not args.no_cpu)}
+        print(json.dumps(line), flush=True)
+        return
     if args.sweep or args.moe_layer:
         line = bench_sweep(args) if args.sweep else bench_moe_layer(args)
         print(json.dumps(line), flush=True)
@@ -779,6 +921,8 @@ def main():
             line["expert_cache"]["cpu_baseline"] = cpu_baseline_c5(host, gb, keep, cores, args.cpu_seconds / 3)
             line["expert_cache"]["oracle_replay"] = cache_replay_check(traces)
         host.free()
+    if not args.no_mla:
+        line["mla"] = bench_mla(args, (args.ctx,), cpu=not args.no_cpu)
     print(json.dumps(line), flush=True)
 
 

@@ -13,14 +13,55 @@ constexpr int MAX_E = 256, MAX_K = 16, MAX_TOK = 256; // routing limits
 // f32 arithmetic in the reference's two-rounding form (src/gguf/ggml.zig:
 // 1342-1374 Q4_K, 1420-1471 Q6_K, 1834-1849 Q4_0/Q8_0); value (r, c) of a
 // rows x cols matrix.
-// Value e of block `unit` of a quantized plane of U blocks (device layout).
-__device__ inline float dequant_unit(int t, const uint8_t *__restrict__ w, size_t U, size_t unit, int e) {
+// Every value of these formats is a * q - b with an integer q and one f32
+// pair (a, b) per scale group of a block: Q4_K a = d*sc, b = dmin*m (32
+// values per group), Q6_K a = d*sc, q = qv - 32, b = 0 (16 per group), Q8_0
+// and Q4_0 a = d, b = 0 (the block).  a * q rounds once and - b once: the
+// reference's two roundings ((d*sc)*q - dmin*m; s*(q-32); q*d), and - 0
+// leaves every value (-0 included) as it is.
+
+// Scale group of value e within its block.
+__device__ inline int dq_group(int t, int e) {
+    if (t == LH_Q4_K)
+        return e / 32;
+    if (t == LH_Q6_K)
+        return 8 * (e / 128) + (e % 32) / 16 + 2 * ((e % 128) / 32);
+    return 0;
+}
+
+// Groups per block.
+__host__ __device__ inline constexpr int dq_groups(int t) { return t == LH_Q4_K ? 8 : t == LH_Q6_K ? 16 : 1; }
+
+// The integer q of value e of block `unit` of a plane of U blocks (device layout).
+__device__ inline int dq_q(int t, const uint8_t *__restrict__ w, size_t U, size_t unit, int e) {
+    if (t == LH_Q4_K) {
+        const int g = e / 32, l = e % 32;
+        const uint8_t byte = w[unit * 144 + 16 + 32 * (g / 2) + l];
+        return (g & 1) ? (byte >> 4) : (byte & 0xF);
+    }
+    if (t == LH_Q6_K) {
+        const int h = e / 128, r128 = e % 128, quarter = r128 / 32, l = r128 % 32;
+        const uint8_t qlb = w[unit * 128 + 64 * h + l + ((quarter & 1) ? 32 : 0)];
+        const uint8_t qhb = w[U * 128 + unit * 64 + 32 * h + l];
+        const int nib = (quarter < 2) ? (qlb & 0xF) : (qlb >> 4);
+        return (nib | (((qhb >> (2 * quarter)) & 3) << 4)) - 32;
+    }
+    if (t == LH_Q8_0)
+        return ((const int8_t *)w)[unit * 32 + e];
+    if (t == LH_Q4_0) {
+        const uint8_t *qs = w + unit * 16;
+        return (e < 16 ? (qs[e] & 0xF) : (qs[e - 16] >> 4)) - 8;
+    }
+    return 0;
+}
+
+// The pair (a, b) of scale group g of block `unit`.
+__device__ inline float2 dq_pair(int t, const uint8_t *__restrict__ w, size_t U, size_t unit, int g) {
     if (t == LH_Q4_K) {
         const uint8_t *blk = w + unit * 144;
         const float d = half_bits_to_float(blk[0] | (blk[1] << 8));
         const float dmin = half_bits_to_float(blk[2] | (blk[3] << 8));
         const uint8_t *s = blk + 4;
-        const int g = e / 32, l = e % 32;
         int sc, m;
         if (g < 4) {
             sc = s[g] & 63;
@@ -29,36 +70,28 @@ __device__ inline float dequant_unit(int t, const uint8_t *__restrict__ w, size_
             sc = (s[g + 4] & 0xF) | ((s[g - 4] >> 6) << 4);
             m = (s[g + 4] >> 4) | ((s[g] >> 6) << 4);
         }
-        const uint8_t byte = blk[16 + 32 * (g / 2) + l];
-        const int qv = (g & 1) ? (byte >> 4) : (byte & 0xF);
-        const float d1 = d * (float)sc, m1 = dmin * (float)m;
-        return d1 * (float)qv - m1;
+        return make_float2(d * (float)sc, dmin * (float)m);
     }
     if (t == LH_Q6_K) {
-        const uint8_t *ql = w + unit * 128, *qh = w + U * 128 + unit * 64;
         const int8_t *sc = (const int8_t *)(w + U * 192 + unit * 16);
-        const uint16_t *dp = (const uint16_t *)(w + U * 208);
-        const float d = half_bits_to_float(dp[unit]);
-        const int h = e / 128, r128 = e % 128, quarter = r128 / 32, l = r128 % 32;
-        const uint8_t qlb = ql[64 * h + l + ((quarter & 1) ? 32 : 0)];
-        const uint8_t qhb = qh[32 * h + l];
-        const int nib = (quarter < 2) ? (qlb & 0xF) : (qlb >> 4);
-        const int qv = nib | (((qhb >> (2 * quarter)) & 3) << 4);
-        const float s = d * (float)sc[8 * h + l / 16 + 2 * quarter];
-        return s * ((float)qv - 32.0f);
+        const float d = half_bits_to_float(((const uint16_t *)(w + U * 208))[unit]);
+        return make_float2(d * (float)sc[g], 0.0f);
     }
-    if (t == LH_Q8_0) {
-        const int8_t *qs = (const int8_t *)(w + unit * 32);
-        const uint16_t *dp = (const uint16_t *)(w + U * 32);
-        return (float)qs[e] * half_bits_to_float(dp[unit]);
-    }
-    if (t == LH_Q4_0) {
-        const uint8_t *qs = w + unit * 16;
-        const uint16_t *dp = (const uint16_t *)(w + U * 16);
-        const int nib = e < 16 ? (qs[e] & 0xF) : (qs[e - 16] >> 4);
-        return (float)(nib - 8) * half_bits_to_float(dp[unit]);
-    }
-    return 0.0f;
+    if (t == LH_Q8_0)
+        return make_float2(half_bits_to_float(((const uint16_t *)(w + U * 32))[unit]), 0.0f);
+    if (t == LH_Q4_0)
+        return make_float2(half_bits_to_float(((const uint16_t *)(w + U * 16))[unit]), 0.0f);
+    return make_float2(0.0f, 0.0f);
+}
+
+__device__ inline float dq_apply(float2 ab, int q) {
+    const float v = ab.x * (float)q;
+    return v - ab.y;
+}
+
+// Value e of block `unit` of a quantized plane of U blocks (device layout).
+__device__ inline float dequant_unit(int t, const uint8_t *__restrict__ w, size_t U, size_t unit, int e) {
+    return dq_apply(dq_pair(t, w, U, unit, dq_group(t, e)), dq_q(t, w, U, unit, e));
 }
 
 __device__ inline float dequant_value(int t, const uint8_t *__restrict__ w, size_t rows, size_t cols,

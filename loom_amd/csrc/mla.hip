@@ -37,23 +37,70 @@ constexpr int MLA_MAX_ROPE = 512;
 
 // ---- absorb -----------------------------------------------------------------
 // qa[h][c] = chain over r of q_nope[h][r] * W_k[h][r][c] (product rounded,
-// then added), from +0; W_k plane h holds nope rows of kvr values.
-__global__ __launch_bounds__(64) void mla_absorb_kernel(int t, const uint8_t *__restrict__ wk, size_t plane,
-                                                        const float *__restrict__ q_nope, int nope, int kvr,
-                                                        int nb, int be_log2, float *__restrict__ qa) {
-    const int h = blockIdx.y, c = blockIdx.x * 64 + threadIdx.x;
-    if (c >= kvr)
-        return;
+// then added), from +0.  Work group (256 latent columns, head h): the
+// scale-group pairs (a, b) of the head's W_k rows over those columns go to
+// LDS first; each thread then runs its column's chain, the rows' integer q
+// loaded a batch ahead, value = a * q - b (the dequant's own rounding).
+constexpr int MA_THREADS = 256;
+constexpr int MA_SLOTS = 16;      // scale groups in 256 columns, at most (Q6_K)
+constexpr int MA_MAX_NOPE = 256;
+constexpr int MA_BATCH = 32;      // rows of q per load batch
+
+template <int T>
+__global__ __launch_bounds__(MA_THREADS) void mla_absorb_kernel(const uint8_t *__restrict__ wk, size_t plane,
+                                                                const float *__restrict__ q_nope, int nope, int kvr,
+                                                                float *__restrict__ qa) {
+    constexpr int BE = block_elems(T), GPB = dq_groups(T);
+    __shared__ float2 pairs[MA_MAX_NOPE * MA_SLOTS];
+    __shared__ float qn[MA_MAX_NOPE];
+    const int h = blockIdx.y, c0 = blockIdx.x * MA_THREADS, tid = threadIdx.x;
+    const int nb = kvr / BE;
     const uint8_t *w = wk + (size_t)h * plane;
-    const float *q = q_nope + (size_t)h * nope;
     const size_t U = (size_t)nope * nb;
-    const int cb = c >> be_log2, e = c & ((1 << be_log2) - 1);
-    float acc = 0.0f;
-    for (int r = 0; r < nope; r++) {
-        const float p = q[r] * dequant_unit(t, w, U, (size_t)r * nb + cb, e);
-        acc = acc + p;
+    const int b0 = c0 / BE, nslots = (min(MA_THREADS, kvr - c0) + BE - 1) / BE * GPB;
+    for (int i = tid; i < nope * nslots; i += MA_THREADS) {
+        const int r = i / nslots, sl = i % nslots;
+        pairs[r * MA_SLOTS + sl] = dq_pair(T, w, U, (size_t)r * nb + b0 + sl / GPB, sl % GPB);
     }
-    qa[(size_t)h * kvr + c] = acc;
+    for (int i = tid; i < nope; i += MA_THREADS)
+        qn[i] = q_nope[(size_t)h * nope + i];
+    const int c = min(c0 + tid, kvr - 1), cb = c / BE, e = c % BE;
+    const int slot = (cb - b0) * GPB + dq_group(T, e);
+    int qa_[MA_BATCH], qb_[MA_BATCH];
+    auto load = [&](int (&q)[MA_BATCH], int r0) {
+#pragma unroll
+        for (int u = 0; u < MA_BATCH; u++)
+            q[u] = dq_q(T, w, U, (size_t)min(r0 + u, nope - 1) * nb + cb, e);
+    };
+    float acc = 0.0f;
+    auto run = [&](const int (&q)[MA_BATCH], int r0) {
+        if (r0 + MA_BATCH <= nope) {
+#pragma unroll
+            for (int u = 0; u < MA_BATCH; u++) {
+                const float p = qn[r0 + u] * dq_apply(pairs[(r0 + u) * MA_SLOTS + slot], q[u]);
+                acc = acc + p;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < MA_BATCH; u++)
+                if (r0 + u < nope) {
+                    const float p = qn[r0 + u] * dq_apply(pairs[(r0 + u) * MA_SLOTS + slot], q[u]);
+                    acc = acc + p;
+                }
+        }
+    };
+    load(qa_, 0);
+    load(qb_, MA_BATCH);
+    __syncthreads();
+    for (int r0 = 0; r0 < nope; r0 += 2 * MA_BATCH) {
+        run(qa_, r0);
+        load(qa_, r0 + 2 * MA_BATCH);
+        if (r0 + MA_BATCH < nope)
+            run(qb_, r0 + MA_BATCH);
+        load(qb_, r0 + 3 * MA_BATCH);
+    }
+    if (c0 + tid < kvr)
+        qa[(size_t)h * kvr + c0 + tid] = acc;
 }
 
 // ---- scores -----------------------------------------------------------------
@@ -187,38 +234,136 @@ __global__ __launch_bounds__(NT) void mla_softmax_kernel(float *__restrict__ S, 
 
 // ---- weighted sum of the cached rows ------------------------------------------
 // o[h][c] = chain over t of p[h][t] * c_kv[t][c] (product rounded, then
-// added), from +0.  Wave = head, lane = latent column; the four waves of a
-// work group share the cached rows through L1.
-constexpr int MW_UNROLL = 16;
+// added), from +0.  Wave = head, lane = latent column: a work group's four
+// waves take four heads over the same 64 columns, and the work groups of one
+// column tile are ntile apart in launch order (with kvr 512 each tile's rows
+// stay in one XCD's L2: work groups go round-robin over the 8 XCDs).  The
+// rows come through LDS in tiles of MW_TP positions: loaded MW_AHEAD tiles
+// ahead with 16-byte loads, stored transposed (row = column, each 4-position
+// chunk at chunk q ^ (column >> 4), which keeps the stores and the 16-byte
+// reads free of bank conflicts) into one of 3 buffers.  Each tile begins with
+// one wait for its own values (read the tile before) and then issues the next
+// tile's LDS reads and its p loads (scalar: p is uniform over the wave), so
+// they are in flight while this tile's products and adds run.
+constexpr int MW_TP = 32;
+constexpr int MW_AHEAD = 2;
+constexpr int MW_NB = 3;
+constexpr int MW_RS = MW_TP + 4;          // f32 row stride of a transposed tile
+constexpr int MW_NF = MW_TP * 16 / 256;   // 16-byte loads per thread per tile
+static_assert(MW_AHEAD % 2 == 0, "the value registers alternate with the tile's parity");
+typedef const __attribute__((address_space(4))) float const_f32;
 __global__ __launch_bounds__(256) void mla_wsum_kernel(const float *__restrict__ S, int s_stride,
                                                        const float *__restrict__ c_kv, int seq, int H, int kvr,
-                                                       float *__restrict__ o_lat) {
-    const int wave = threadIdx.x >> 6, ln = threadIdx.x & 63;
-    const int h = blockIdx.y * 4 + wave, c = blockIdx.x * 64 + ln;
-    if (h >= H)
-        return;
-    const float *p = S + (size_t)h * s_stride;
-    const float *col = c_kv + min(c, kvr - 1);
+                                                       int ntile, float *__restrict__ o_lat) {
+    __shared__ __align__(16) float tl[MW_NB][64 * MW_RS];
+    const int id = blockIdx.x, tile = id % ntile, hg = id / ntile;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), ln = tid & 63;
+    const int h = hg * 4 + wave, hc = min(h, H - 1);
+    const int c = tile * 64 + ln;
+    const_f32 *pr = (const_f32 *)(S + (size_t)hc * s_stride);
+    const int ntl = (seq + MW_TP - 1) / MW_TP;
+    // rows past seq read row seq - 1, columns past kvr read columns kvr - 4 ..
+    // (their results are not stored)
+    auto gload = [&](int k, float4 (&r)[MW_NF]) {
+#pragma unroll
+        for (int j = 0; j < MW_NF; j++) {
+            const int f = tid + 256 * j, pos = f / 16, c4 = f % 16;
+            const int tt = min(k * MW_TP + pos, seq - 1);
+            const int cc = min(tile * 64 + 4 * c4, kvr - 4);
+            r[j] = *(const float4 *)(c_kv + (size_t)tt * kvr + cc);
+        }
+    };
+    auto lstore = [&](int buf, const float4 (&r)[MW_NF]) {
+#pragma unroll
+        for (int j = 0; j < MW_NF; j++) {
+            const int f = tid + 256 * j, pos = f / 16, c4 = f % 16;
+            const int q = pos >> 2, w = pos & 3;
+            const float vals[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int row = 4 * c4 + e;
+                tl[buf][row * MW_RS + 4 * (q ^ (row >> 4)) + w] = vals[e];
+            }
+        }
+    };
+    auto lread = [&](int k, float4 (&x)[MW_TP / 4]) {
+        const float *src = tl[k % MW_NB] + ln * MW_RS;
+#pragma unroll
+        for (int q = 0; q < MW_TP / 4; q++)
+            x[q] = *(const float4 *)(src + 4 * (q ^ (ln >> 4)));
+    };
+    // p of tile k (a tile starting past the row also starts past seq: its
+    // values are never used)
+    auto pload = [&](float (&p)[MW_TP], int k) {
+        const int base = min(k * MW_TP, s_stride - MW_TP);
+#pragma unroll
+        for (int u = 0; u < MW_TP; u++)
+            p[u] = pr[base + u];
+    };
     float acc = 0.0f;
-    int t = 0;
-    for (; t + MW_UNROLL <= seq; t += MW_UNROLL) {
-        float v[MW_UNROLL], w[MW_UNROLL];
+    auto tilek = [&](int k, const float4 (&xc)[MW_TP / 4], const float (&pc)[MW_TP], float4 (&xn)[MW_TP / 4],
+                     float (&pn)[MW_TP], float4 (&r)[MW_NF]) {
+        __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this tile's values and p
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + 1 < ntl)
+            lread(k + 1, xn);
+        pload(pn, k + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        const int tb = k * MW_TP;
+        if (tb + MW_TP <= seq) {
 #pragma unroll
-        for (int u = 0; u < MW_UNROLL; u++) {
-            v[u] = col[(size_t)(t + u) * kvr];
-            w[u] = p[t + u];
+            for (int q = 0; q < MW_TP / 4; q++) {
+                const float xs[4] = {xc[q].x, xc[q].y, xc[q].z, xc[q].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float m = pc[4 * q + e] * xs[e];
+                    acc = acc + m;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < MW_TP / 4; q++) {
+                const float xs[4] = {xc[q].x, xc[q].y, xc[q].z, xc[q].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (tb + 4 * q + e < seq) {
+                        const float m = pc[4 * q + e] * xs[e];
+                        acc = acc + m;
+                    }
+            }
         }
+        __builtin_amdgcn_sched_barrier(0);
+        // tile k + 2 (in r) into the buffer tile k - 1 left; tile k + 2 + AHEAD's loads go out
+        lstore((k + 2) % MW_NB, r);
+        gload(k + 2 + MW_AHEAD, r);
+        __syncthreads();
+    };
+    float4 rg[MW_AHEAD][MW_NF];
+    float4 xa[MW_TP / 4], xb[MW_TP / 4];
+    float pa[MW_TP], pb[MW_TP];
+    gload(0, rg[0]);
+    lstore(0, rg[0]);
+    gload(1, rg[0]);
+    lstore(1, rg[0]);
 #pragma unroll
-        for (int u = 0; u < MW_UNROLL; u++) {
-            const float x = w[u] * v[u];
-            acc = acc + x;
+    for (int a = 0; a < MW_AHEAD; a++)
+        gload(2 + a, rg[a]);
+    __syncthreads();
+    lread(0, xa);
+    pload(pa, 0);
+    for (int k0 = 0; k0 < ntl; k0 += MW_AHEAD) {
+#pragma unroll
+        for (int a = 0; a < MW_AHEAD; a++) {
+            const int k = k0 + a;
+            if (k < ntl) {
+                if (a & 1)
+                    tilek(k, xb, pb, xa, pa, rg[a]);
+                else
+                    tilek(k, xa, pa, xb, pb, rg[a]);
+            }
         }
     }
-    for (; t < seq; t++) {
-        const float x = p[t] * col[(size_t)t * kvr];
-        acc = acc + x;
-    }
-    if (c < kvr)
+    if (h < H && c < kvr)
         o_lat[(size_t)h * kvr + c] = acc;
 }
 
@@ -272,6 +417,8 @@ static int mla_check(const loomhip_mla_attn *a, size_t seq) {
         return fail(LOOMHIP_ERR_ARG, "mla: null weights");
     if (a->n_heads == 0 || a->nope == 0 || a->vd == 0 || a->kvr == 0 || a->rope == 0)
         return fail(LOOMHIP_ERR_ARG, "mla: empty shape");
+    if (a->nope > (size_t)MA_MAX_NOPE)
+        return fail(LOOMHIP_DECLINED, "mla: nope %zu over %d", a->nope, MA_MAX_NOPE);
     if (seq == 0 || seq > (size_t)MLA_MAX_CTX)
         return fail(LOOMHIP_DECLINED, "mla: context %zu outside 1..%d", seq, MLA_MAX_CTX);
     if (a->kvr > (size_t)MLA_MAX_KVR || a->rope > (size_t)MLA_MAX_ROPE || a->n_heads > (size_t)IOTA_LEN)
@@ -297,15 +444,28 @@ static int mla_attn_impl(const loomhip_mla_attn *a, const float *c_kv, const flo
         return fail(LOOMHIP_ERR_HIP, "mla: head group table");
     float *qa = (float *)g_mla.qa.ptr, *S = (float *)g_mla.S.ptr;
     float *ol = o_lat ? o_lat : (float *)g_mla.olat.ptr;
-    const int be = block_elems(t);
-    int be_log2 = 0;
-    while ((1 << be_log2) < be)
-        be_log2++;
     // 1. absorb
     int ph = prof_begin(LOOMHIP_KT_MLA_ABSORB, st);
-    hipLaunchKernelGGL(mla_absorb_kernel, dim3((unsigned)((kvr + 63) / 64), (unsigned)H), dim3(64), 0, st, t,
-                       (const uint8_t *)a->wk, plane_bytes(t, a->nope, kvr), q_nope, (int)a->nope, (int)kvr,
-                       (int)(kvr / be), be_log2, qa);
+    {
+        const dim3 g((unsigned)((kvr + MA_THREADS - 1) / MA_THREADS), (unsigned)H);
+        const size_t pl = plane_bytes(t, a->nope, kvr);
+        const uint8_t *wk = (const uint8_t *)a->wk;
+        const int nope = (int)a->nope;
+        switch (t) {
+        case LH_Q4_K:
+            hipLaunchKernelGGL((mla_absorb_kernel<LH_Q4_K>), g, dim3(MA_THREADS), 0, st, wk, pl, q_nope, nope, (int)kvr, qa);
+            break;
+        case LH_Q6_K:
+            hipLaunchKernelGGL((mla_absorb_kernel<LH_Q6_K>), g, dim3(MA_THREADS), 0, st, wk, pl, q_nope, nope, (int)kvr, qa);
+            break;
+        case LH_Q8_0:
+            hipLaunchKernelGGL((mla_absorb_kernel<LH_Q8_0>), g, dim3(MA_THREADS), 0, st, wk, pl, q_nope, nope, (int)kvr, qa);
+            break;
+        default:
+            hipLaunchKernelGGL((mla_absorb_kernel<LH_Q4_0>), g, dim3(MA_THREADS), 0, st, wk, pl, q_nope, nope, (int)kvr, qa);
+            break;
+        }
+    }
     note_launch();
     prof_end(ph, st);
     // 2. scores
@@ -323,8 +483,11 @@ static int mla_attn_impl(const loomhip_mla_attn *a, const float *c_kv, const flo
     prof_end(ph, st);
     // 4. weighted sum
     ph = prof_begin(LOOMHIP_KT_MLA_WSUM, st);
-    hipLaunchKernelGGL(mla_wsum_kernel, dim3((unsigned)((kvr + 63) / 64), (unsigned)((H + 3) / 4)), dim3(256), 0, st,
-                       S, (int)s_stride, c_kv, (int)seq, (int)H, (int)kvr, ol);
+    {
+        const int ntile = (int)((kvr + 63) / 64);
+        hipLaunchKernelGGL(mla_wsum_kernel, dim3((unsigned)(ntile * ((H + 3) / 4))), dim3(256), 0, st, S,
+                           (int)s_stride, c_kv, (int)seq, (int)H, (int)kvr, ntile, ol);
+    }
     note_launch();
     prof_end(ph, st);
     // 5. W_v: quantize every head's o and run the grouped matvec, plane = head
