@@ -87,6 +87,7 @@ def parse():
                     help="config 3 instead: one MoE layer at token batches 1, 8, 32 and 128")
     ap.add_argument("--mla", action="store_true",
                     help="config 5's MLA attention alone: 61 layers at contexts 1024, 2048, 4096")
+    ap.add_argument("--mla-ctx", default="1024,2048,4096", help="contexts of the --mla run")
     ap.add_argument("--no-mla", action="store_true", help="skip the MLA attention run of the default bench")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="first copy MB megabytes device to device three times: the known-size kernel that "
@@ -828,7 +829,7 @@ def main():
     loom_amd.init(0)
     if args.mla:
         line = {"metric": "MLA attention: us per layer and ms per token (config 5's attention)", "n_gpus": 1,
-                "data": "synthetic", "dtype": "f32", **bench_mla(args, (1024, 2048, 4096), cpu=not args.no_cpu)}
+                "data": "synthetic", "dtype": "f32", **bench_mla(args, tuple(int(v) for v in args.mla_ctx.split(",") if v), cpu=not args.no_cpu)}
         print(json.dumps(line), flush=True)
         return
     if args.sweep or args.moe_layer:

@@ -229,7 +229,10 @@ __global__ __launch_bounds__(NT) void mla_softmax_kernel(float *__restrict__ S, 
     extern __shared__ __align__(16) float e[]; // e[s_stride]
     __shared__ float redf[NT / 64];
     __shared__ SeqSumLds sq;
-    softmax_row_exact<NT>(S + (size_t)blockIdx.x * s_stride, seq, e, redf, sq);
+    float *row = S + (size_t)blockIdx.x * s_stride;
+    softmax_row_exact<NT>(row, seq, e, redf, sq);
+    for (int j = seq + threadIdx.x; j < s_stride; j += NT) // the weighted sum's padding
+        row[j] = 0.0f;
 }
 
 // ---- weighted sum of the cached rows ------------------------------------------
@@ -244,7 +247,10 @@ __global__ __launch_bounds__(NT) void mla_softmax_kernel(float *__restrict__ S, 
 // reads free of bank conflicts) into one of 3 buffers.  Each tile begins with
 // one wait for its own values (read the tile before) and then issues the next
 // tile's LDS reads and its p loads (scalar: p is uniform over the wave), so
-// they are in flight while this tile's products and adds run.
+// they are in flight while this tile's products and adds run.  The last tile
+// runs whole: past seq both p (the softmax writes +0 up to the row's end) and
+// the rows (loaded as +0) are zero, and o + (+-0) is o (o starts at +0 and a
+// sum of products never reaches -0 from there), so the padding is exact.
 constexpr int MW_TP = 32;
 constexpr int MW_AHEAD = 2;
 constexpr int MW_NB = 3;
@@ -268,9 +274,10 @@ __global__ __launch_bounds__(256) void mla_wsum_kernel(const float *__restrict__
 #pragma unroll
         for (int j = 0; j < MW_NF; j++) {
             const int f = tid + 256 * j, pos = f / 16, c4 = f % 16;
-            const int tt = min(k * MW_TP + pos, seq - 1);
+            const int tt = k * MW_TP + pos;
             const int cc = min(tile * 64 + 4 * c4, kvr - 4);
-            r[j] = *(const float4 *)(c_kv + (size_t)tt * kvr + cc);
+            const float4 v = *(const float4 *)(c_kv + (size_t)min(tt, seq - 1) * kvr + cc);
+            r[j] = tt < seq ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
     };
     auto lstore = [&](int buf, const float4 (&r)[MW_NF]) {
@@ -309,27 +316,13 @@ __global__ __launch_bounds__(256) void mla_wsum_kernel(const float *__restrict__
             lread(k + 1, xn);
         pload(pn, k + 1);
         __builtin_amdgcn_sched_barrier(0);
-        const int tb = k * MW_TP;
-        if (tb + MW_TP <= seq) {
 #pragma unroll
-            for (int q = 0; q < MW_TP / 4; q++) {
-                const float xs[4] = {xc[q].x, xc[q].y, xc[q].z, xc[q].w};
+        for (int q = 0; q < MW_TP / 4; q++) {
+            const float xs[4] = {xc[q].x, xc[q].y, xc[q].z, xc[q].w};
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float m = pc[4 * q + e] * xs[e];
-                    acc = acc + m;
-                }
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < MW_TP / 4; q++) {
-                const float xs[4] = {xc[q].x, xc[q].y, xc[q].z, xc[q].w};
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (tb + 4 * q + e < seq) {
-                        const float m = pc[4 * q + e] * xs[e];
-                        acc = acc + m;
-                    }
+            for (int e = 0; e < 4; e++) {
+                const float m = pc[4 * q + e] * xs[e];
+                acc = acc + m;
             }
         }
         __builtin_amdgcn_sched_barrier(0);
