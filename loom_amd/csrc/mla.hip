@@ -37,67 +37,86 @@ constexpr int MLA_MAX_ROPE = 512;
 
 // ---- absorb -----------------------------------------------------------------
 // qa[h][c] = chain over r of q_nope[h][r] * W_k[h][r][c] (product rounded,
-// then added), from +0.  Work group (256 latent columns, head h): the
-// scale-group pairs (a, b) of the head's W_k rows over those columns go to
-// LDS first; each thread then runs its column's chain, the rows' integer q
-// loaded a batch ahead, value = a * q - b (the dequant's own rounding).
+// then added), from +0.  Work group (256 latent columns, head h), rows in
+// chunks of MA_ROWS: the chunk's blocks of the head's W_k over those columns
+// are copied into LDS with 16-byte loads as a compact plane of the same
+// device layout (U' = rows x blocks), the scale-group pairs (a, b) of every
+// row are decoded from it once, then each thread runs its column's chain with
+// value = a * q - b (the dequant's own rounding).
 constexpr int MA_THREADS = 256;
-constexpr int MA_SLOTS = 16;      // scale groups in 256 columns, at most (Q6_K)
+constexpr int MA_SLOTS = 16;     // scale groups in 256 columns, at most (Q6_K)
+constexpr int MA_ROWS = 128;     // rows per LDS chunk
 constexpr int MA_MAX_NOPE = 256;
-constexpr int MA_BATCH = 32;      // rows of q per load batch
+constexpr int MA_STAGE = MA_ROWS * 8 * 34 + 64; // bytes of the largest chunk (Q8_0: 8 blocks of 34 bytes a row)
+
+// The arrays of a block in the device layout: (offset of the array in units
+// of U, bytes per block).  The d arrays (2 bytes a block) come last.
+template <int T>
+__device__ constexpr int ma_arrays() { return T == LH_Q4_K ? 1 : T == LH_Q6_K ? 4 : 2; }
+template <int T>
+__device__ constexpr int ma_off(int a) {
+    return T == LH_Q4_K ? 0 : T == LH_Q6_K ? (a == 0 ? 0 : a == 1 ? 128 : a == 2 ? 192 : 208)
+                                          : (a == 0 ? 0 : T == LH_Q8_0 ? 32 : 16);
+}
+template <int T>
+__device__ constexpr int ma_bytes(int a) {
+    return T == LH_Q4_K ? 144 : T == LH_Q6_K ? (a == 0 ? 128 : a == 1 ? 64 : a == 2 ? 16 : 2)
+                                            : (a == 0 ? (T == LH_Q8_0 ? 32 : 16) : 2);
+}
 
 template <int T>
 __global__ __launch_bounds__(MA_THREADS) void mla_absorb_kernel(const uint8_t *__restrict__ wk, size_t plane,
                                                                 const float *__restrict__ q_nope, int nope, int kvr,
                                                                 float *__restrict__ qa) {
     constexpr int BE = block_elems(T), GPB = dq_groups(T);
-    __shared__ float2 pairs[MA_MAX_NOPE * MA_SLOTS];
+    __shared__ __align__(16) uint8_t stage[MA_STAGE];
+    __shared__ float2 pairs[MA_ROWS * MA_SLOTS];
     __shared__ float qn[MA_MAX_NOPE];
     const int h = blockIdx.y, c0 = blockIdx.x * MA_THREADS, tid = threadIdx.x;
     const int nb = kvr / BE;
     const uint8_t *w = wk + (size_t)h * plane;
     const size_t U = (size_t)nope * nb;
-    const int b0 = c0 / BE, nslots = (min(MA_THREADS, kvr - c0) + BE - 1) / BE * GPB;
-    for (int i = tid; i < nope * nslots; i += MA_THREADS) {
-        const int r = i / nslots, sl = i % nslots;
-        pairs[r * MA_SLOTS + sl] = dq_pair(T, w, U, (size_t)r * nb + b0 + sl / GPB, sl % GPB);
-    }
+    const int b0 = c0 / BE, nblk = (min(MA_THREADS, kvr - c0) + BE - 1) / BE, nslots = nblk * GPB;
     for (int i = tid; i < nope; i += MA_THREADS)
         qn[i] = q_nope[(size_t)h * nope + i];
-    const int c = min(c0 + tid, kvr - 1), cb = c / BE, e = c % BE;
-    const int slot = (cb - b0) * GPB + dq_group(T, e);
-    int qa_[MA_BATCH], qb_[MA_BATCH];
-    auto load = [&](int (&q)[MA_BATCH], int r0) {
-#pragma unroll
-        for (int u = 0; u < MA_BATCH; u++)
-            q[u] = dq_q(T, w, U, (size_t)min(r0 + u, nope - 1) * nb + cb, e);
-    };
+    const int c = min(c0 + tid, kvr - 1), cb = c / BE - b0, e = c % BE;
+    const int slot = cb * GPB + dq_group(T, e);
     float acc = 0.0f;
-    auto run = [&](const int (&q)[MA_BATCH], int r0) {
-        if (r0 + MA_BATCH <= nope) {
+    for (int r0 = 0; r0 < nope; r0 += MA_ROWS) {
+        const int rows = min(MA_ROWS, nope - r0);
+        const int Uc = rows * nblk; // blocks of the compact plane
+        __syncthreads();            // the previous chunk's reads are done
 #pragma unroll
-            for (int u = 0; u < MA_BATCH; u++) {
-                const float p = qn[r0 + u] * dq_apply(pairs[(r0 + u) * MA_SLOTS + slot], q[u]);
-                acc = acc + p;
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < MA_BATCH; u++)
-                if (r0 + u < nope) {
-                    const float p = qn[r0 + u] * dq_apply(pairs[(r0 + u) * MA_SLOTS + slot], q[u]);
-                    acc = acc + p;
+        for (int a = 0; a < ma_arrays<T>(); a++) {
+            const int bb = ma_bytes<T>(a);
+            const uint8_t *src = w + (size_t)ma_off<T>(a) * U;
+            uint8_t *dst = stage + ma_off<T>(a) * Uc;
+            if (bb >= 16) {
+                const int per_row = nblk * bb / 16; // 16-byte pieces of a row's blocks
+                for (int i = tid; i < rows * per_row; i += MA_THREADS) {
+                    const int r = i / per_row, k = i % per_row;
+                    *(uint4 *)(dst + (size_t)r * nblk * bb + 16 * k) =
+                        *(const uint4 *)(src + ((size_t)(r0 + r) * nb + b0) * bb + 16 * k);
                 }
+            } else {
+                for (int i = tid; i < rows * nblk; i += MA_THREADS) {
+                    const int r = i / nblk, k = i % nblk;
+                    ((uint16_t *)dst)[i] = ((const uint16_t *)src)[(size_t)(r0 + r) * nb + b0 + k];
+                }
+            }
         }
-    };
-    load(qa_, 0);
-    load(qb_, MA_BATCH);
-    __syncthreads();
-    for (int r0 = 0; r0 < nope; r0 += 2 * MA_BATCH) {
-        run(qa_, r0);
-        load(qa_, r0 + 2 * MA_BATCH);
-        if (r0 + MA_BATCH < nope)
-            run(qb_, r0 + MA_BATCH);
-        load(qb_, r0 + 3 * MA_BATCH);
+        __syncthreads();
+        for (int i = tid; i < rows * nslots; i += MA_THREADS) {
+            const int r = i / nslots, sl = i % nslots;
+            pairs[r * MA_SLOTS + sl] = dq_pair(T, stage, (size_t)Uc, (size_t)r * nblk + sl / GPB, sl % GPB);
+        }
+        __syncthreads();
+#pragma unroll 16
+        for (int r = 0; r < rows; r++) {
+            const int q = dq_q(T, stage, (size_t)Uc, (size_t)r * nblk + cb, e);
+            const float p = qn[r0 + r] * dq_apply(pairs[r * MA_SLOTS + slot], q);
+            acc = acc + p;
+        }
     }
     if (c0 + tid < kvr)
         qa[(size_t)h * kvr + c0 + tid] = acc;
