@@ -390,6 +390,33 @@ int loomhip_mla_split_kvb_dev(int t, const void *kv_b, size_t n_heads, size_t no
 int loomhip_mla_attn_dev(const loomhip_mla_attn *a, const float *c_kv, const float *k_rope, size_t seq,
                          const float *q_nope, const float *q_rope, float *out, float *o_lat, void *stream);
 
+/* mlaLayerTail (src/compute/cpu.zig:63; Vulkan src/vulkan/backend.zig:773):
+ * the rest of an MLA layer after its attention head, one submission: the
+ * attention above (cache layer li, position pos), x = x + attn_output . heads,
+ * normed = rmsnorm(x) * ffn_norm (the squares summed in order), the routed
+ * MoE from router logits router . normed (f32 router; router_bias is the
+ * selection-only bias, exp_probs_b) in selection order plus the shared
+ * expert (shexp_gate NULL: none), x = x + that sum -- the engine's own
+ * sequence (deepseek.zig:1044-1046, 1325-1387), bit-identical to it.  x [dim]
+ * is read and written.  gating/weights_norm/weights_scale: RoutedCfg. */
+int loomhip_mla_layer_tail(size_t li, size_t pos, float *x, size_t dim, const float *q_nope, size_t qn_len,
+                           const float *q_rope, size_t qr_len, int kvb_type, const uint8_t *kv_b, size_t kvb_len,
+                           int attn_out_type, const uint8_t *attn_out, const float *ffn_norm, float eps,
+                           int router_type, const uint8_t *router, const float *router_bias, int gate_type,
+                           const uint8_t *gate, int up_type, const uint8_t *up, int down_type, const uint8_t *down,
+                           int shexp_gate_type, const uint8_t *shexp_gate, int shexp_up_type,
+                           const uint8_t *shexp_up, int shexp_down_type, const uint8_t *shexp_down, size_t ffn,
+                           size_t shexp_ffn, size_t n_expert, size_t n_used, int gating, int weights_norm,
+                           float weights_scale, size_t n_heads, size_t nope, size_t vd, float scale);
+/* Device-resident form (no seam counterpart): the same tail over a
+ * caller-held cache and device weights (attn_out [dim][n_heads * vd] device
+ * layout, ffn_norm [dim] f32, moe the layer's device MoE -- for a DeepSeek
+ * layer its sel_bias is exp_probs_b), x [dim] in place, stream-ordered. */
+int loomhip_mla_layer_tail_dev(const loomhip_mla_attn *a, const float *c_kv, const float *k_rope, size_t seq,
+                               const float *q_nope, const float *q_rope, int attn_out_type, const void *attn_out,
+                               const float *ffn_norm, float eps, const loomhip_moe_layer *moe, float *x,
+                               void *stream);
+
 /* ---- GGUF v3 files (src/gguf/gguf.zig) ------------------------------------
  * gguf.zig:251-332 parse: the header, the metadata key/values and the tensor
  * table, with the whole file mapped read-only so a tensor's bytes are a

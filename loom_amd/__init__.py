@@ -287,6 +287,10 @@ def lib() -> C.CDLL:
         "loomhip_mla_attn_heads": (i, [sz, sz, vp, sz, vp, sz, i, vp, sz, vp, sz, sz, sz, sz, f]),
         "loomhip_mla_split_kvb_dev": (i, [i, vp, sz, sz, sz, sz, vp, vp, vp]),
         "loomhip_mla_attn_dev": (i, [C.POINTER(MlaAttnDesc), vp, vp, sz, vp, vp, vp, vp, vp]),
+        "loomhip_mla_layer_tail": (i, [sz, sz, vp, sz, vp, sz, vp, sz, i, vp, sz, i, vp, vp, f, i, vp, vp, i, vp, i,
+                                       vp, i, vp, i, vp, i, vp, i, vp, sz, sz, sz, sz, i, i, f, sz, sz, sz, f]),
+        "loomhip_mla_layer_tail_dev": (i, [C.POINTER(MlaAttnDesc), vp, vp, sz, vp, vp, i, vp, vp, f,
+                                           C.POINTER(MoeLayerDesc), vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

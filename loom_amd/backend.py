@@ -337,6 +337,32 @@ def mlaAttnHeads(li: int, pos: int, q_nope: np.ndarray, q_rope: np.ndarray, kv_b
     return _served(rc, "mlaAttnHeads")
 
 
+def mlaLayerTail(li: int, pos: int, x: np.ndarray, q_nope: np.ndarray, q_rope: np.ndarray, kv_b: WeightRef,
+                 attn_out_w: WeightRef, ffn_norm: np.ndarray, eps: float, router_w: WeightRef, router_bias,
+                 gate_w: WeightRef, up_w: WeightRef, down_w: WeightRef, shexp, ffn: int, shexp_ffn: int,
+                 cfg: RoutedCfg, n_heads: int, nope: int, v_head_dim: int, scale: float) -> bool:
+    """backend.mlaLayerTail (src/compute/cpu.zig:63): attention over the device
+    cache, the output projection and residual, the FFN norm, the routed MoE
+    with the shared expert and its residual, one submission; x [dim] in place.
+    False declines."""
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    q_nope = np.ascontiguousarray(q_nope, np.float32)
+    q_rope = np.ascontiguousarray(q_rope, np.float32)
+    ffn_norm = np.ascontiguousarray(ffn_norm, np.float32)
+    b = None if router_bias is None else np.ascontiguousarray(router_bias, np.float32)
+    sg = su = sd = WeightRef(0, None)
+    if shexp is not None:
+        sg, su, sd = shexp
+    rc = lib().loomhip_mla_layer_tail(
+        li, pos, _p(x), x.size, _p(q_nope), q_nope.size, _p(q_rope), q_rope.size, kv_b.ty, _p(kv_b.data),
+        kv_b.data.nbytes, attn_out_w.ty, _p(attn_out_w.data), _p(ffn_norm), eps, router_w.ty, _p(router_w.data), _p(b),
+        gate_w.ty, _p(gate_w.data), up_w.ty, _p(up_w.data), down_w.ty, _p(down_w.data), sg.ty, _p(sg.data), su.ty,
+        _p(su.data), sd.ty, _p(sd.data), ffn, shexp_ffn, cfg.n_expert, cfg.n_used,
+        GATING_SIGMOID if cfg.gating_sigmoid else GATING_SOFTMAX, int(cfg.weights_norm), cfg.weights_scale, n_heads,
+        nope, v_head_dim, scale)
+    return _served(rc, "mlaLayerTail")
+
+
 class MlaAttn:
     """Device-resident MLA attention of one layer: kv_b (GGML bytes, a torch
     uint8 device tensor) split per head into W_k / W_v planes once."""
@@ -357,6 +383,14 @@ class MlaAttn:
         return check(lib().loomhip_mla_attn_dev(C.byref(self.desc), _ptr(c_kv), _ptr(k_rope), seq, _ptr(q_nope),
                                                 _ptr(q_rope), _ptr(out), _ptr(o_lat), _stream()),
                      "mla_attn_dev")
+
+    def tail(self, c_kv, k_rope, seq: int, q_nope, q_rope, attn_out_t: int, attn_out, ffn_norm, eps: float,
+             moe: "MoeLayer", x) -> int:
+        """The whole layer after the attention head on the device (x in place)."""
+        return check(lib().loomhip_mla_layer_tail_dev(C.byref(self.desc), _ptr(c_kv), _ptr(k_rope), seq,
+                                                      _ptr(q_nope), _ptr(q_rope), attn_out_t, _ptr(attn_out),
+                                                      _ptr(ffn_norm), eps, C.byref(moe.desc), _ptr(x), _stream()),
+                     "mla_layer_tail_dev")
 
 
 class MoeLayer:
@@ -391,7 +425,7 @@ class MoeLayer:
 
 __all__ = [
     "COMBINE_EXPERT_ASC", "COMBINE_SELECTION", "DECLINED", "ExpertRef", "F32", "MAX_BATCH", "MlaAttn", "MoeLayer",
-    "hasMlaCache", "mlaAppend", "mlaAttnHeads", "mlaInit", "mlaReadCache", "mlaSetWk",
+    "hasMlaCache", "mlaAppend", "mlaAttnHeads", "mlaInit", "mlaLayerTail", "mlaReadCache", "mlaSetWk",
     "moeFfnBlock", "moeFfnBlockStats",
     "RoutedCfg", "WeightRef", "clearWeightCache", "dequantRow", "matmul", "matvec", "moeFfnBlockRouted",
     "moeRoute", "parallelBegin", "parallelEnd", "registerWeights", "takeCmdBufCount",

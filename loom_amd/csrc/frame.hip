@@ -1104,6 +1104,16 @@ static void launch_norm(int qb, const float *x, int dim, const float *w, float e
         launch_norm_t<false>(qb, x, dim, w, eps, qa, normed, n, st);
 }
 
+// tensor.rmsnorm (core/tensor.zig:9-15) of n rows of dim values with the
+// squares summed in index order: the norm the reference's FFN input takes.
+int rmsnorm_exact_dev(const float *x, int dim, const float *w, float eps, float *normed, size_t n, hipStream_t st) {
+    if (dim <= 0 || dim % 32 || dim > EXACT_NORM_MAX_DIM)
+        return fail(LOOMHIP_DECLINED, "rmsnorm: dim %d not served (a multiple of 32 up to %d)", dim,
+                    EXACT_NORM_MAX_DIM);
+    launch_norm(0, x, dim, w, eps, QAct{}, normed, n, st, true);
+    return LOOMHIP_OK;
+}
+
 static int frame_check(const loomhip_model *m, size_t n, size_t *ffn_max) {
     if (!m || !m->layers || n == 0 || n > 256)
         return fail(LOOMHIP_ERR_ARG, "token_frame: bad model or lane count %zu (1..256)", n);

@@ -394,7 +394,7 @@ struct Mla {
     size_t layers = 0, ctx = 0, kvr = 0, rope = 0;
     bool want = false;
     size_t wk_layers = 0;
-    Scratch qa, S, olat, act, kvb_stage;
+    Scratch qa, S, olat, act, kvb_stage, tail, act2;
     std::unordered_map<size_t, void *> vgroups; // per head count: groups {h, h, 1}
     std::unordered_map<const void *, KvbSplit> kvb;
 };
@@ -543,11 +543,132 @@ static int mla_split(int t, const void *src, size_t H, size_t nope, size_t vd, s
     return LOOMHIP_OK;
 }
 
+// x[i] = x[i] + y[i] (tensor.zig:50-52)
+__global__ void mla_add_kernel(float *__restrict__ x, const float *__restrict__ y, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        x[i] = x[i] + y[i];
+}
+
+// out = out + W . x for one vector: the matvec (int8 activations, ggml.zig:
+// 602) with the residual add as its epilogue (tensor.zig:50-52).
+static int matvec_add(int t, const void *w, const float *x, int rows, int cols, float *out, hipStream_t st) {
+    const size_t qbytes = align16(cols) + align16((size_t)cols / 32 * 4) + align16((size_t)cols / 16 * 4);
+    if (int rc = reserve_on(g_mla.act2, qbytes, st))
+        return rc;
+    QAct q;
+    q.q = (int8_t *)g_mla.act2.ptr;
+    q.d = (float *)((char *)g_mla.act2.ptr + align16(cols));
+    q.s = (int32_t *)((char *)q.d + align16((size_t)cols / 32 * 4));
+    launch_quant_act(t, x, cols, cols, 1, q, st);
+    int ng = 0;
+    const DmmvGroup *g = dense_groups(1, 1, &ng);
+    if (!g)
+        return fail(LOOMHIP_ERR_HIP, "mla: dense group table");
+    DmmvParams p{};
+    p.w = (const uint8_t *)w;
+    p.w2 = nullptr;
+    p.plane_bytes = plane_bytes(t, rows, cols);
+    p.rows = rows;
+    p.cols = cols;
+    p.xq = q.q;
+    p.xd = q.d;
+    p.xs = q.s;
+    p.pair_src = g_ctx.iota;
+    p.pair_dst = g_ctx.iota;
+    p.groups = g;
+    p.n_groups_dev = nullptr;
+    p.n_groups = ng;
+    p.out = out;
+    p.out_stride = rows;
+    p.rpw = dmmv_pick_rpw(t, cols, rows, ng, 1, false);
+    p.accumulate = 1;
+    p.ident_n = 0;
+    if (!launch_dmmv(t, 1, false, p, st))
+        return fail(LOOMHIP_DECLINED, "mla: attn_output partials exceed LDS for %d columns", cols);
+    return LOOMHIP_OK;
+}
+
+// The whole layer after the attention head (the seam's mlaLayerTail,
+// cpu.zig:63; the engine's own sequence, deepseek.zig:1044-1046 and
+// 1325-1387): attention with W_v, x = x + attn_output . heads, normed =
+// rmsnorm(x) * ffn_norm, acc = the routed experts in selection order plus
+// the shared expert, x = x + acc.  Every check runs before the first launch.
+static int mla_tail_impl(const loomhip_mla_attn *a, const float *c_kv, const float *k_rope, size_t seq,
+                         const float *q_nope, const float *q_rope, int out_t, const void *attn_out,
+                         const float *ffn_norm, float eps, const loomhip_moe_layer *moe, float *x, hipStream_t st) {
+    if (int rc = mla_check(a, seq))
+        return rc;
+    if (!moe || !attn_out || !ffn_norm || !x)
+        return fail(LOOMHIP_ERR_ARG, "mla_layer_tail: null pointer");
+    const size_t hv = a->n_heads * a->vd, dim = moe->dim;
+    if (out_t == LH_F32 || out_t == LH_F16 || !dmmv_supported(out_t, (int)hv))
+        return fail(LOOMHIP_DECLINED, "mla_layer_tail: attn_output type %d with %zu columns not served", out_t, hv);
+    if (dim == 0 || dim % 32 || dim > 7936)
+        return fail(LOOMHIP_DECLINED, "mla_layer_tail: dim %zu not served", dim);
+    if (int rc = moe_layer_check(moe, 1, true))
+        return rc;
+    if (int rc = reserve_on(g_mla.tail, align16(hv * 4) + 2 * align16(dim * 4), st))
+        return rc;
+    float *head = (float *)g_mla.tail.ptr;
+    float *normed = (float *)((char *)g_mla.tail.ptr + align16(hv * 4));
+    float *acc = (float *)((char *)normed + align16(dim * 4));
+    int rc;
+    if ((rc = mla_attn_impl(a, c_kv, k_rope, seq, q_nope, q_rope, head, nullptr, st)) ||
+        (rc = matvec_add(out_t, attn_out, head, (int)dim, (int)hv, x, st)) ||
+        (rc = rmsnorm_exact_dev(x, (int)dim, ffn_norm, eps, normed, 1, st)) ||
+        (rc = loomhip_moe_layer_dev(moe, normed, 1, LOOMHIP_COMBINE_SELECTION, acc, nullptr, nullptr, st)))
+        return rc;
+    hipLaunchKernelGGL(mla_add_kernel, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0, st, x, acc, (int)dim);
+    note_launch();
+    return LOOMHIP_OK;
+}
+
+// kv_b split per head into the device layout once per host tensor (keyed by
+// its pointer, re-split when the tensor behind it changes).
+static int kvb_cached(int t, const uint8_t *kv_b, size_t kvb_len, size_t n_heads, size_t nope, size_t vd, size_t kvr,
+                      hipStream_t st, KvbSplit **out) {
+    KvbSplit &ks = g_mla.kvb[kv_b];
+    if (ks.t == t && ks.len == kvb_len && ks.H == n_heads && ks.nope == nope && ks.vd == vd && ks.kvr == kvr) {
+        *out = &ks;
+        return LOOMHIP_OK;
+    }
+    (void)hipStreamSynchronize(st);
+    if (ks.wk)
+        (void)hipFree(ks.wk);
+    if (ks.wv)
+        (void)hipFree(ks.wv);
+    ks = KvbSplit{};
+    void *wk = nullptr, *wv = nullptr;
+    hipError_t e = hipMalloc(&wk, plane_bytes(t, nope, kvr) * n_heads);
+    if (e == hipSuccess)
+        e = hipMalloc(&wv, plane_bytes(t, vd, kvr) * n_heads);
+    int rc = e == hipSuccess ? reserve_on(g_mla.kvb_stage, kvb_len, st) : hip_fail(e, "hipMalloc kv_b split");
+    if (rc == LOOMHIP_OK) {
+        e = hipMemcpy(g_mla.kvb_stage.ptr, kv_b, kvb_len, hipMemcpyHostToDevice);
+        rc = e == hipSuccess ? mla_split(t, g_mla.kvb_stage.ptr, n_heads, nope, vd, kvr, wk, wv, st)
+                             : hip_fail(e, "kv_b upload");
+    }
+    if (rc == LOOMHIP_OK && (e = hipStreamSynchronize(st)) != hipSuccess)
+        rc = hip_fail(e, "kv_b split");
+    if (rc != LOOMHIP_OK) {
+        if (wk)
+            (void)hipFree(wk);
+        if (wv)
+            (void)hipFree(wv);
+        g_mla.kvb.erase(kv_b);
+        return rc;
+    }
+    ks = KvbSplit{t, kvb_len, n_heads, nope, vd, kvr, wk, wv};
+    *out = &ks;
+    return LOOMHIP_OK;
+}
+
 static int ensure_cache() {
+    if (!g_mla.want) // as the Vulkan arm: a declined mlaInit leaves no usable cache
+        return fail(LOOMHIP_DECLINED, "mla: no cache shape (mlaInit)");
     if (g_mla.cache)
         return LOOMHIP_OK;
-    if (!g_mla.want)
-        return fail(LOOMHIP_DECLINED, "mla: no cache shape (mlaInit)");
     const size_t n = g_mla.layers * g_mla.ctx * (g_mla.kvr + g_mla.rope);
     void *d = nullptr;
     hipError_t e = hipMalloc(&d, n * 4);
@@ -586,6 +707,8 @@ void mla_release() {
     g_mla.olat.release();
     g_mla.act.release();
     g_mla.kvb_stage.release();
+    g_mla.tail.release();
+    g_mla.act2.release();
 }
 
 } // namespace lh
@@ -706,37 +829,9 @@ int loomhip_mla_attn_heads(size_t li, size_t pos, const float *q_nope, size_t qn
         kvb_len != n_heads * (nope + vd) * ggml_bytes(kvb_type, 1, kvr))
         return fail(LOOMHIP_DECLINED, "mla_attn_heads: kv_b type %d / %zu bytes not served", kvb_type, kvb_len);
     hipStream_t st = g_ctx.compute;
-    // kv_b split per head into the device layout once per host tensor
-    KvbSplit &ks = g_mla.kvb[kv_b];
-    if (ks.t != kvb_type || ks.len != kvb_len || ks.H != n_heads || ks.nope != nope || ks.vd != vd || ks.kvr != kvr) {
-        (void)hipStreamSynchronize(st);
-        if (ks.wk)
-            (void)hipFree(ks.wk);
-        if (ks.wv)
-            (void)hipFree(ks.wv);
-        ks = KvbSplit{};
-        void *wk = nullptr, *wv = nullptr;
-        hipError_t e = hipMalloc(&wk, plane_bytes(kvb_type, nope, kvr) * n_heads);
-        if (e == hipSuccess)
-            e = hipMalloc(&wv, plane_bytes(kvb_type, vd, kvr) * n_heads);
-        int rc = e == hipSuccess ? reserve_on(g_mla.kvb_stage, kvb_len, st) : hip_fail(e, "hipMalloc kv_b split");
-        if (rc == LOOMHIP_OK) {
-            e = hipMemcpy(g_mla.kvb_stage.ptr, kv_b, kvb_len, hipMemcpyHostToDevice);
-            rc = e == hipSuccess ? mla_split(kvb_type, g_mla.kvb_stage.ptr, n_heads, nope, vd, kvr, wk, wv, st)
-                                 : hip_fail(e, "kv_b upload");
-        }
-        if (rc == LOOMHIP_OK && (e = hipStreamSynchronize(st)) != hipSuccess)
-            rc = hip_fail(e, "kv_b split");
-        if (rc != LOOMHIP_OK) {
-            if (wk)
-                (void)hipFree(wk);
-            if (wv)
-                (void)hipFree(wv);
-            g_mla.kvb.erase(kv_b);
-            return rc;
-        }
-        ks = KvbSplit{kvb_type, kvb_len, n_heads, nope, vd, kvr, wk, wv};
-    }
+    KvbSplit *ks = nullptr;
+    if (int rc = kvb_cached(kvb_type, kv_b, kvb_len, n_heads, nope, vd, kvr, st, &ks))
+        return rc;
     const size_t qn = n_heads * nope, qr = n_heads * rope;
     int rc = g_ctx.xstage.reserve((qn + qr) * 4);
     if (rc || (rc = g_ctx.ostage.reserve(out_len * 4)))
@@ -747,7 +842,7 @@ int loomhip_mla_attn_heads(size_t li, size_t pos, const float *q_nope, size_t qn
         e = hipMemcpyAsync(dq + qn, q_rope, qr * 4, hipMemcpyHostToDevice, st);
     if (e != hipSuccess)
         return hip_fail(e, "mla_attn_heads upload");
-    const loomhip_mla_attn a{kvb_type, ks.wk, ks.wv, n_heads, nope, vd, kvr, rope, scale};
+    const loomhip_mla_attn a{kvb_type, ks->wk, ks->wv, n_heads, nope, vd, kvr, rope, scale};
     rc = mla_attn_impl(&a, cache_c(li, 0), cache_r(li, 0), seq, dq, dq + qn, (float *)g_ctx.ostage.ptr, nullptr, st);
     if (rc)
         return rc;
@@ -755,6 +850,125 @@ int loomhip_mla_attn_heads(size_t li, size_t pos, const float *q_nope, size_t qn
     if (e == hipSuccess)
         e = hipStreamSynchronize(st);
     return e == hipSuccess ? LOOMHIP_OK : hip_fail(e, "mla_attn_heads");
+}
+
+int loomhip_mla_layer_tail_dev(const loomhip_mla_attn *a, const float *c_kv, const float *k_rope, size_t seq,
+                               const float *q_nope, const float *q_rope, int attn_out_type, const void *attn_out,
+                               const float *ffn_norm, float eps, const loomhip_moe_layer *moe, float *x,
+                               void *stream) {
+    if (int rc = require_ready())
+        return rc;
+    std::lock_guard<std::mutex> lk(g_mla.mu);
+    if (!c_kv || !k_rope || !q_nope || !q_rope)
+        return fail(LOOMHIP_ERR_ARG, "mla_layer_tail_dev: null pointer");
+    return mla_tail_impl(a, c_kv, k_rope, seq, q_nope, q_rope, attn_out_type, attn_out, ffn_norm, eps, moe, x,
+                         stream_of(stream));
+}
+
+int loomhip_mla_layer_tail(size_t li, size_t pos, float *x, size_t dim, const float *q_nope, size_t qn_len,
+                           const float *q_rope, size_t qr_len, int kvb_type, const uint8_t *kv_b, size_t kvb_len,
+                           int attn_out_type, const uint8_t *attn_out, const float *ffn_norm, float eps,
+                           int router_type, const uint8_t *router, const float *router_bias, int gate_type,
+                           const uint8_t *gate, int up_type, const uint8_t *up, int down_type, const uint8_t *down,
+                           int shexp_gate_type, const uint8_t *shexp_gate, int shexp_up_type,
+                           const uint8_t *shexp_up, int shexp_down_type, const uint8_t *shexp_down, size_t ffn,
+                           size_t shexp_ffn, size_t n_expert, size_t n_used, int gating, int weights_norm,
+                           float weights_scale, size_t n_heads, size_t nope, size_t vd, float scale) {
+    if (int rc = require_ready())
+        return rc;
+    std::lock_guard<std::mutex> lk(g_mla.mu);
+    if (int rc = ensure_cache())
+        return rc;
+    const size_t kvr = g_mla.kvr, rope = g_mla.rope, seq = pos + 1, hv = n_heads * vd;
+    if (li >= g_mla.layers || seq > g_mla.ctx)
+        return fail(LOOMHIP_DECLINED, "mla_layer_tail: layer %zu / position %zu outside the cache", li, pos);
+    if (!x || !q_nope || !q_rope || !kv_b || !attn_out || !ffn_norm || !router || !gate || !up || !down ||
+        qn_len != n_heads * nope || qr_len != n_heads * rope)
+        return fail(LOOMHIP_DECLINED, "mla_layer_tail: missing tensor or slice lengths that do not match");
+    if (router_type != LH_F32)
+        return fail(LOOMHIP_DECLINED, "mla_layer_tail: router type %d (f32 served)", router_type);
+    if (shexp_gate && (!shexp_up || !shexp_down || shexp_ffn == 0))
+        return fail(LOOMHIP_DECLINED, "mla_layer_tail: incomplete shared expert");
+    if (kvb_type == LH_F32 || kvb_type == LH_F16 || !dmmv_supported(kvb_type, (int)kvr) ||
+        kvb_len != n_heads * (nope + vd) * ggml_bytes(kvb_type, 1, kvr))
+        return fail(LOOMHIP_DECLINED, "mla_layer_tail: kv_b type %d / %zu bytes not served", kvb_type, kvb_len);
+    // the MoE half's shapes and types, checked before anything is uploaded
+    loomhip_moe_layer m{};
+    m.dim = dim;
+    m.ffn = ffn;
+    m.n_expert = n_expert;
+    m.n_used = n_used;
+    m.gating = gating;
+    m.weights_norm = weights_norm;
+    m.weights_scale = weights_scale;
+    m.gate_t = gate_type;
+    m.up_t = up_type;
+    m.down_t = down_type;
+    m.router = (const float *)router;
+    m.gate = gate;
+    m.up = up;
+    m.down = down;
+    if (shexp_gate) {
+        m.shexp_gate_t = shexp_gate_type;
+        m.shexp_up_t = shexp_up_type;
+        m.shexp_down_t = shexp_down_type;
+        m.shexp_gate = shexp_gate;
+        m.shexp_up = shexp_up;
+        m.shexp_down = shexp_down;
+        m.shexp_ffn = shexp_ffn;
+    }
+    if (int rc = moe_layer_check(&m, 1, true))
+        return rc;
+    if (attn_out_type == LH_F32 || attn_out_type == LH_F16 || !dmmv_supported(attn_out_type, (int)hv))
+        return fail(LOOMHIP_DECLINED, "mla_layer_tail: attn_output type %d with %zu columns not served",
+                    attn_out_type, hv);
+    hipStream_t st = g_ctx.compute;
+    KvbSplit *ks = nullptr;
+    void *d_out, *d_norm, *d_router, *d_bias = nullptr, *d_gate, *d_up, *d_down;
+    int rc;
+    if ((rc = kvb_cached(kvb_type, kv_b, kvb_len, n_heads, nope, vd, kvr, st, &ks)) ||
+        (rc = upload_weights(attn_out_type, attn_out, dim, hv, 1, &d_out)) ||
+        (rc = upload_weights(LH_F32, ffn_norm, 1, dim, 1, &d_norm)) ||
+        (rc = upload_weights(LH_F32, router, n_expert, dim, 1, &d_router)) ||
+        (router_bias && (rc = upload_weights(LH_F32, router_bias, 1, n_expert, 1, &d_bias))) ||
+        (rc = upload_weights(gate_type, gate, ffn, dim, n_expert, &d_gate)) ||
+        (rc = upload_weights(up_type, up, ffn, dim, n_expert, &d_up)) ||
+        (rc = upload_weights(down_type, down, dim, ffn, n_expert, &d_down)))
+        return rc;
+    m.router = (const float *)d_router;
+    m.sel_bias = (const float *)d_bias;
+    m.gate = d_gate;
+    m.up = d_up;
+    m.down = d_down;
+    if (shexp_gate) {
+        void *sg, *su, *sd;
+        if ((rc = upload_weights(shexp_gate_type, shexp_gate, shexp_ffn, dim, 1, &sg)) ||
+            (rc = upload_weights(shexp_up_type, shexp_up, shexp_ffn, dim, 1, &su)) ||
+            (rc = upload_weights(shexp_down_type, shexp_down, dim, shexp_ffn, 1, &sd)))
+            return rc;
+        m.shexp_gate = sg;
+        m.shexp_up = su;
+        m.shexp_down = sd;
+    }
+    const size_t qn = n_heads * nope, qr = n_heads * rope;
+    if ((rc = g_ctx.xstage.reserve((qn + qr + dim) * 4)))
+        return rc;
+    float *dq = (float *)g_ctx.xstage.ptr, *dx = dq + qn + qr;
+    hipError_t e = hipMemcpyAsync(dq, q_nope, qn * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(dq + qn, q_rope, qr * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(dx, x, dim * 4, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess)
+        return hip_fail(e, "mla_layer_tail upload");
+    const loomhip_mla_attn a{kvb_type, ks->wk, ks->wv, n_heads, nope, vd, kvr, rope, scale};
+    if ((rc = mla_tail_impl(&a, cache_c(li, 0), cache_r(li, 0), seq, dq, dq + qn, attn_out_type, d_out,
+                            (const float *)d_norm, eps, &m, dx, st)))
+        return rc;
+    e = hipMemcpyAsync(x, dx, dim * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(st);
+    return e == hipSuccess ? LOOMHIP_OK : hip_fail(e, "mla_layer_tail");
 }
 
 } // extern "C"

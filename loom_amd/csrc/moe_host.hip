@@ -370,22 +370,24 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
 // Everything moe_run would decline or refuse for this layer at n tokens,
 // checked before the token frame launches anything (the frame's layers are
 // resolved up front, src/vulkan/backend.zig:462-489).
-int moe_frame_check(const loomhip_moe_layer *L, size_t n) {
+int moe_layer_check(const loomhip_moe_layer *L, size_t n, bool shexp_ok) {
     if (!L->router || !L->gate || !L->up || !L->down)
-        return fail(LOOMHIP_ERR_ARG, "token_frame: MoE layer without router or expert tensors");
+        return fail(LOOMHIP_ERR_ARG, "moe: layer without router or expert tensors");
     MoeRun m{L->dim, L->ffn, L->n_expert, L->n_used, L->gating, L->weights_norm, L->weights_scale,
              L->router, L->router_bias, L->sel_bias, L->gate_t, L->up_t, L->down_t, L->gate,
              L->up, L->down};
     m.sh = shexp_of(L);
     if (int rc = moe_check(m, n))
         return rc;
-    if (m.sh.gate) // the frame adds its MoE output to the residual, acc = routed + shared is not formed
+    if (m.sh.gate && !shexp_ok) // the frame adds its MoE output to the residual, acc = routed + shared is not formed
         return fail(LOOMHIP_DECLINED, "token_frame: a shared expert is not served inside the frame");
     if (n <= DECODE_MAX_TOK && decode_supported(m.gate_t, m.down_t, (int)m.ffn) &&
         decode_down_lds(m.down_t, (int)m.ffn, (int)m.k, 1) > 64 * 1024)
         return fail(LOOMHIP_DECLINED, "moe: ffn %zu x top-%zu exceeds the decode LDS budget", m.ffn, m.k);
     return LOOMHIP_OK;
 }
+
+int moe_frame_check(const loomhip_moe_layer *L, size_t n) { return moe_layer_check(L, n, false); }
 
 int moe_layer_fused_norm(const loomhip_moe_layer *L, const float *x, const float *norm_w, float eps, size_t n_tok,
                          int combine, float *out, uint32_t *ids_out, hipStream_t st) {

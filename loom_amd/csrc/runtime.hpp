@@ -76,8 +76,13 @@ int moe_layer_fused_norm(const loomhip_moe_layer *L, const float *x, const float
 bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok);
 // What the MoE layer would decline at n tokens, checked before any launch.
 int moe_frame_check(const loomhip_moe_layer *L, size_t n);
+// The same checks for a caller that forms acc = routed + shared itself
+// (shexp_ok) before adding it to the residual.
+int moe_layer_check(const loomhip_moe_layer *L, size_t n, bool shexp_ok);
 void ec_release_scratch();
 void block_release_cache();
 void mla_release();
+// The exact rmsnorm (squares summed in order) of n rows into normed.
+int rmsnorm_exact_dev(const float *x, int dim, const float *w, float eps, float *normed, size_t n, hipStream_t st);
 
 } // namespace lh

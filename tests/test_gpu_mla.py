@@ -110,3 +110,61 @@ def test_device_mla_attention_is_bit_identical(lh, oracle, t, H, nope, vd, kvr, 
         assert np.array_equal(got_lat, want_lat), (seq, np.abs(got_lat - want_lat).max())
         got = out.cpu().numpy()
         assert np.array_equal(got, want), (seq, np.abs(got - want).max())
+
+
+def test_seam_mla_layer_tail_matches_the_engine_sequence(lh, oracle):
+    """mlaLayerTail (src/compute/cpu.zig:63) on a DeepSeek-V3-shaped layer at
+    reduced width (dim 1024, 16 heads of nope 128 / rope 64 / v 128, kv_lora
+    512; 16 experts top-4 of ffn 256 with sigmoid gating, exp_probs_b as the
+    selection bias, renormalised gates scaled by 2.5, a shared expert of ffn
+    512; Q4_K, Q6_K down): x after the layer is bit-identical to the engine's
+    own sequence run by the oracle -- the head loop, matvec(attn_output) and
+    the residual add, rmsnorm, moeLayer with the shared expert, the second
+    residual add (deepseek.zig:1044-1046, 1325-1387) -- and a second call
+    with the kv_b split cached matches again."""
+    import loom_amd
+    from recipes import planes
+
+    dim, H, nope, vd, kvr, rope, ctx, seq = 1024, 16, 128, 128, 512, 64, 64, 37
+    E, k, ffn, sffn = 16, 4, 256, 512
+    case = make_case(oracle, Q4_K, H, nope, vd, kvr, rope, ctx, seed=41)
+    rng = np.random.default_rng(42)
+    attn_out = planes(Q4_K, dim, H * vd, 1, 51)
+    gate, up, down = planes(Q4_K, ffn, dim, E, 52), planes(Q4_K, ffn, dim, E, 53), planes(Q6_K, dim, ffn, E, 54)
+    sg, su, sd = planes(Q4_K, sffn, dim, 1, 55), planes(Q4_K, sffn, dim, 1, 56), planes(Q6_K, dim, sffn, 1, 57)
+    router = (rng.standard_normal((E, dim)) / np.sqrt(dim)).astype(np.float32)
+    sel_bias = (0.1 * rng.standard_normal(E)).astype(np.float32)
+    ffn_norm = (1.0 + 0.05 * rng.standard_normal(dim)).astype(np.float32)
+    x0 = rng.standard_normal(dim).astype(np.float32)
+    eps = 1e-6
+    assert lh.mlaInit(1, ctx, kvr, rope)
+    for t in range(seq):
+        assert lh.mlaAppend(0, t, case.c_kv[t], case.k_rope[t])
+    cfg = lh.RoutedCfg(E, k, True, True, 2.5)
+    WR = lh.WeightRef
+    args = (case.q_nope, case.q_rope, WR(Q4_K, case.kv_b), WR(Q4_K, attn_out), ffn_norm, eps,
+            WR(F32, router.view(np.uint8).ravel()), sel_bias, WR(Q4_K, gate), WR(Q4_K, up), WR(Q6_K, down),
+            (WR(Q4_K, sg), WR(Q4_K, su), WR(Q6_K, sd)), ffn, sffn, cfg, H, nope, vd, case.scale)
+    # the engine's sequence on the oracle
+    heads, _ = oracle.mla_attn_heads(case.c_kv, case.k_rope, seq, case.q_nope, case.q_rope, Q4_K, case.kv_b, H,
+                                     nope, vd, case.scale)
+    x1 = x0 + oracle.matvec(Q4_K, attn_out, heads, dim, H * vd)
+    normed = oracle.rmsnorm(x1, ffn_norm, eps)
+    w = oracle.MoeWeights(dim, ffn, E, k, router, gate, up, down, Q4_K, Q4_K, Q6_K, sel_bias=sel_bias,
+                          gating=oracle.GATING_SIGMOID, weights_norm=True, weights_scale=2.5,
+                          shexp=(sg, su, sd, Q4_K, Q4_K, Q6_K, sffn))
+    acc, _, _ = oracle.moe_layer_token(w, normed)
+    want = x1 + acc
+    for _ in range(2):
+        x = x0.copy()
+        loom_amd.take_launch_count()
+        assert lh.mlaLayerTail(0, seq - 1, x, *args), loom_amd.last_error()
+        assert loom_amd.take_launch_count() > 0
+        assert np.array_equal(x, want), np.abs(x - want).max()
+    # declines: a quantized router, a position past the cache
+    x = x0.copy()
+    bad = list(args)
+    bad[6] = WR(Q4_K, planes(Q4_K, E, dim, 1, 58))
+    assert not lh.mlaLayerTail(0, seq - 1, x, *bad)
+    assert not lh.mlaLayerTail(0, ctx, x, *args)
+    assert np.array_equal(x, x0)
