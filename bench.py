@@ -530,7 +530,89 @@ def mla_launch_ops(tag, S):
             "mla_absorb": 2 * H * MLA_NOPE * MLA_KVR}.get(tag)
 
 
-def bench_mla(args, seqs, cpu=True):
+def bench_mla_layer(args, S, scale, attn_layers):
+    """Config 5's whole block at context S, batch 1: loomhip_mla_layer_tail_dev
+    = MLA attention, the Q4_K output projection [7168][16384] and residual,
+    the exact FFN norm, the routed MoE (256 HBM-resident Q4_K experts of
+    24,772,608 B, sigmoid top-8 with renorm, Zipf(1.1) logit bias) plus the
+    shared expert and the residual.  Three distinct layers rotated, each with
+    its own experts (6.4 GB a layer); one step = the three layers, replayed
+    from a HIP graph."""
+    import torch
+
+    from loom_amd import GATING_SIGMOID, Q4_K
+    from loom_amd import backend as be
+
+    H, vd, D, F, E, K = MLA_H, MLA_VD, C5_DIM, C5_FFN, C5_E, C5_K
+    g = torch.Generator(device="cuda").manual_seed(71)
+    built = []
+    for i, (m, c, r) in enumerate(attn_layers):
+        wo = be.repack_dev(Q4_K, be.synth_ggml_dev(Q4_K, D, H * vd, 1, 900 + i, 0.02), D, H * vd, 1)
+        ex = [be.repack_dev(Q4_K, be.synth_ggml_dev(Q4_K, rows, cols, E, 910 + 10 * i + k, 0.02), rows, cols, E)
+              for k, (rows, cols) in enumerate(((F, D), (F, D), (D, F)))]
+        sh = [be.repack_dev(Q4_K, be.synth_ggml_dev(Q4_K, rows, cols, 1, 950 + 10 * i + k, 0.02), rows, cols, 1)
+              for k, (rows, cols) in enumerate(((C5_SFFN, D), (C5_SFFN, D), (D, C5_SFFN)))]
+        router = (torch.randn(E, D, generator=g, device="cuda") / np.sqrt(D)).contiguous()
+        ranks = torch.randperm(E, generator=g, device="cuda").float() + 1
+        z = -1.1 * torch.log(ranks)
+        bias = (z - z.mean()).contiguous()
+        moe = be.MoeLayer(D, F, E, K, router, ex[0], ex[1], ex[2], Q4_K, Q4_K, Q4_K, router_bias=bias,
+                          gating=GATING_SIGMOID, weights_norm=True, weights_scale=2.5,
+                          shexp=(sh[0], sh[1], sh[2], Q4_K, Q4_K, Q4_K, C5_SFFN))
+        norm = (1.0 + 0.05 * torch.randn(D, generator=g, device="cuda")).contiguous()
+        built.append((m, c, r, wo, norm, moe))
+    qn = torch.randn(H * MLA_NOPE, generator=g, device="cuda")
+    qr = torch.randn(H * MLA_ROPE, generator=g, device="cuda")
+    x = torch.randn(D, generator=g, device="cuda")
+    x0 = x.clone()
+
+    def step():
+        for m, c, r, wo, norm, moe in built:
+            if m.tail(c, r, S, qn, qr, Q4_K, wo, norm, 1e-6, moe, x) != 0:
+                from loom_amd import last_error
+                raise RuntimeError(f"mla_layer_tail_dev declined: {last_error()}")
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    n = max(5, min(args.steps, 20))
+    x.copy_(x0)
+    graph.replay()
+    st = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(st)
+    for _ in range(n):
+        x.copy_(x0)  # keep the residual stream at its scale
+        graph.replay()
+    ev1.record(st)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / n
+    per_layer_us = ms * 1e3 / len(built)
+    moe_bytes = K * C5_EXPERT_BYTES + 3 * plane_bytes_q4k(C5_SFFN, D) + E * D * 4
+    byts = mla_launch_bytes("mla_absorb", S) + mla_launch_bytes("mla_scores", S) + \
+        mla_launch_bytes("mla_wsum", S) + mla_launch_bytes("mla_wv", S) + plane_bytes_q4k(D, H * vd) + moe_bytes
+    log(f"mla layer (attention + projection + norm + routed MoE + shared expert) ctx {S}: {per_layer_us:.1f} us "
+        f"per layer")
+    del graph, built
+    torch.cuda.empty_cache()
+    return {"us_per_layer": round(per_layer_us, 2), "ctx": S, "layers_rotated": len(attn_layers),
+            "bytes_per_layer": int(byts), "GBs": round(byts / (per_layer_us / 1e6) / 1e9, 1),
+            "entry_point": "loomhip_mla_layer_tail_dev",
+            "workload": "config 5 block: MLA attention (128 heads, kv_lora 512, rope 64) + Q4_K wo [7168][16384] "
+                        "+ exact rmsnorm + 256 resident Q4_K experts top-8 (sigmoid, renorm, scale 2.5, Zipf(1.1) "
+                        "logit bias) + shared expert (ffn 2048)"}
+
+
+def plane_bytes_q4k(rows, cols):
+    return rows * cols // 256 * 144
+
+
+C5_EXPERT_BYTES = 24_772_608
+
+
+def bench_mla(args, seqs, cpu=True, tail=True):
     """Config 5's MLA attention (loomhip_mla_attn_dev) over 61 layers, each
     with its own Q4_K kv_b (9.4 MB) and its own f32 latent cache (2,304 B per
     position), replayed from a HIP graph: one step = one token's attention in
@@ -611,6 +693,8 @@ def bench_mla(args, seqs, cpu=True):
              "layers_per_s": round(L / (ms / 1e3), 1), "kernels": kern, "roofline": roof}
         log(f"mla ctx {S}: {ms * 1e3 / L:.2f} us per layer ({ms:.3f} ms per token over {L} layers), kernels {kern}")
         res.append(r)
+    if tail:
+        res[-1]["layer"] = bench_mla_layer(args, smax, scale, layers[:3])
     if cpu:
         import oracle
         from loom_amd import Q4_K as T
