@@ -90,3 +90,36 @@ def test_mla_single_position_is_the_value_row(oracle):
     _, olat = oracle.mla_attn_heads(case.c_kv, case.k_rope, 1, case.q_nope, case.q_rope, Q8_0, case.kv_b,
                                     4, 32, 16, case.scale)
     assert np.array_equal(olat.reshape(4, 64), np.tile(case.c_kv[0], (4, 1)))
+
+
+def test_rope_yarn_regimes(oracle):
+    """deepseek.zig:581-613: factor <= 1 is the plain NORM rope (the same
+    expressions as llama.zig's ropeNorm, bit for bit); position 0 is the
+    identity; pairs below the ramp's low end rotate by pos * base^(-2i/d)
+    (extrapolated), pairs above its high end by that angle / factor
+    (interpolated), each pair keeps its length; with DeepSeek-V3's rope
+    (64 dims, base 10000, factor 40, original context 4096) the ramp runs
+    over pairs 10 .. 23."""
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal(64).astype(np.float32)
+    for pos in (0, 1, 17, 4095):
+        assert np.array_equal(oracle.rope_yarn(v, pos, 10000.0, 1.0, 4096.0), oracle.rope(v, 64, pos, 10000.0, False))
+    assert np.array_equal(oracle.rope_yarn(v, 0, 10000.0, 40.0, 4096.0), v)
+    d, base, factor, orig = 64, 10000.0, 40.0, 4096.0
+    corr = lambda beta: d * np.log(orig / (beta * 2 * np.pi)) / (2 * np.log(base))  # noqa: E731
+    low, high = max(0.0, np.floor(corr(32.0))), min(d - 1.0, np.ceil(corr(1.0)))
+    assert (low, high) == (10.0, 23.0)
+    for pos in (1, 300, 4095):
+        got = oracle.rope_yarn(v, pos, base, factor, orig).astype(np.float64)
+        for i in range(d // 2):
+            a, b = float(v[2 * i]), float(v[2 * i + 1])
+            assert abs(np.hypot(got[2 * i], got[2 * i + 1]) - np.hypot(a, b)) < 1e-5 * (1 + np.hypot(a, b))
+            theta = pos * base ** (-2 * i / d)
+            if i <= low:
+                ang = theta
+            elif i >= high:
+                ang = theta / factor
+            else:
+                continue
+            want = (a * np.cos(ang) - b * np.sin(ang), a * np.sin(ang) + b * np.cos(ang))
+            assert abs(got[2 * i] - want[0]) < 2e-3 and abs(got[2 * i + 1] - want[1]) < 2e-3, (pos, i)
