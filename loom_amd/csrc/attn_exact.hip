@@ -309,19 +309,26 @@ __global__ __launch_bounds__(64 * W) void attn_pv_kernel(FrameDims D, const uint
 // ---- P.V for few lanes: the chain fed by producer waves ----------------------------
 // With few lanes there are too few chains to fill the chip, and each chain's
 // time is what counts: a wave that also multiplies, converts and stages
-// spends two or more issue slots per position.  Here a work group (64 value
-// columns, query head, lane) has one consumer wave, lane = column, whose
-// loop is only o = o + x_t over products x_t read from LDS four positions at
-// a time, and PVS_NP producer waves that write x_t = p_t * v_t for the
-// consumer two tiles ahead, 32 positions of each tile apiece.  The product
+// spends two or more issue slots per position.  Here a work group (32 value
+// columns, query head, lane) has one consumer wave, lane = column (lanes 32
+// and up shadow 0..31 and store nothing), whose loop is only o = o + x_t
+// over products x_t read from LDS four positions at a time, and PVS_NP
+// producer waves that write x_t = p_t * v_t for the consumer two tiles
+// ahead, 64 positions of each tile apiece.  The consumer's chain costs the
+// same per position whatever its lane count; the narrower group halves
+// each producer's share of the products per position.  The product
 // is formed as fma(p, v, +0) on the f16 value directly (v_fma_mix_f32): the
 // same rounding as p * v in f32,
 // except that an exact zero comes out +0 -- and o, which starts at +0 and
 // only ever receives sums, reads o + (+0) = o + (-0) = o either way.
 // Each wave passes one barrier per tile; the consumer reads only positions
-// below P, so what the producers write past the context is never used.
+// below P, so what the producers write past the context is never used.  The
+// consumer's barrier waits for none of its own reads: the ones in flight at
+// a barrier read the next tile's buffer, which the producers only rewrite
+// two barriers later; the producers' barrier waits for their stores.
 constexpr int PVS_NP = 3;                // producer waves per work group
-constexpr int PVS_TJ = 32 * PVS_NP;      // positions per tile, 32 per producer
+constexpr int PVS_COLS = 32;             // value columns per work group
+constexpr int PVS_TJ = 64 * PVS_NP;      // positions per tile, 64 per producer
 constexpr int PVS_SETS = 4;              // tiles of value loads in flight per producer
 constexpr int PVS_STR = 4 * ((PVS_TJ / 4 + 15) / 16 * 16 + 1); // f32 stride of a column's products:
                                          // a whole number of 16-byte slots, 1 mod 16
@@ -331,13 +338,12 @@ constexpr int PVS_AHEAD = 8;             // consumer float4 reads in flight (div
                                          // it starts from)
 static_assert((PVS_TJ / 4) % PVS_AHEAD == 0, "the read ring must wrap at tile boundaries");
 
-// The LDS row of column c (0..63): bits 1, 2, 3 of c flipped by bits 3, 4, 5.
-// Rows are a whole number of 16-byte slots apart, 1 mod 16, so a slot's bank
-// group is (row + position group) mod 16; the permutation makes both access
-// patterns hit 16 different groups per quarter-wave: the consumer's (c = 16 q
-// + i, i = 0..15; one position group) and a producer store's (c = 8 cq + k,
-// cq = 0..7, at position groups g and g + 1).
-__device__ __forceinline__ int pv_row(int c) { return c ^ ((c >> 2) & 14); }
+// Column c's products are LDS row c.  Rows are a whole number of 16-byte
+// slots apart, 1 mod 16, so slot (c, g) -- position group g of column c --
+// sits in bank group (c + g) mod 16.  The consumer reads one g across
+// consecutive columns, a producer store one c across 16 consecutive g:
+// every 8 and every 16 consecutive lanes of either access hit distinct bank
+// groups.
 
 template <int HD>
 __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameDims D, const uint16_t *__restrict__ vc,
@@ -345,9 +351,8 @@ __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameD
                                                                          const float *__restrict__ Pm, int s_stride,
                                                                          float *__restrict__ att) {
     constexpr int PP = PVS_TJ / PVS_NP; // positions per producer per tile
-    __shared__ __align__(16) float prod[PVS_NBUF][64 * PVS_STR];
-    __shared__ __align__(16) float pst[PVS_NP][PP];
-    const int ncb = (HD + 63) / 64;
+    __shared__ __align__(16) float prod[PVS_NBUF][PVS_COLS * PVS_STR];
+    const int ncb = (HD + PVS_COLS - 1) / PVS_COLS;
     // XCD-aware order: consecutive work items share an XCD (work groups are
     // dealt to the 8 XCDs round robin), so one KV head's values stay in few L2s
     const int nwg = ncb * D.n_heads, lin = blockIdx.x;
@@ -358,11 +363,11 @@ __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameD
     const int P = min(pos[t], D.ctx - 1) + 1;
     const int ntile = (P + PVS_TJ - 1) / PVS_TJ;
     const int ntp = (ntile + PVS_SETS - 1) / PVS_SETS * PVS_SETS; // tiles the loops run (padded)
-    const int c0 = sl * 64, ncol = min(64, HD - c0);
+    const int c0 = sl * PVS_COLS, ncol = min(PVS_COLS, HD - c0);
     if (wave == 0) { // consumer
         float o = 0.0f;
         lds_barrier(); // tiles 0 and 1 are in
-        const int crow = pv_row(ln) * PVS_STR;
+        const int crow = (ln % PVS_COLS) * PVS_STR;
         const float4 *src0 = (const float4 *)&prod[0][crow];
         float4 xr[PVS_AHEAD];
 #pragma unroll
@@ -374,17 +379,26 @@ __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameD
             if (nk == PVS_TJ) {
                 const float4 *src = (const float4 *)&prod[k % PVS_NBUF][crow];
 #pragma unroll
-                for (int gj = 0; gj < PVS_TJ / 4; gj++) {
+                for (int gj = 0; gj < PVS_TJ / 4; gj += 2) {
                     const int a = gj % PVS_AHEAD;
-                    const float4 x = xr[a];
-                    // the ring runs on into the next tile, complete since the last barrier;
-                    // the scheduler keeps each read ahead of the adds it must not wait for
+                    // one wait for two groups: the reads of both are the oldest in flight
+                    __builtin_amdgcn_s_waitcnt(0xC07F & ~(0xF << 8) | ((PVS_AHEAD - 2) << 8));
+                    const float4 x0 = xr[a], x1 = xr[a + 1];
+                    __builtin_amdgcn_sched_barrier(0);
                     xr[a] = gj + PVS_AHEAD < PVS_TJ / 4 ? src[gj + PVS_AHEAD] : nxt[gj + PVS_AHEAD - PVS_TJ / 4];
                     __builtin_amdgcn_sched_barrier(0);
-                    o = o + x.x;
-                    o = o + x.y;
-                    o = o + x.z;
-                    o = o + x.w;
+                    o = o + x0.x;
+                    o = o + x0.y;
+                    o = o + x0.z;
+                    o = o + x0.w;
+                    __builtin_amdgcn_sched_barrier(0);
+                    xr[a + 1] = gj + 1 + PVS_AHEAD < PVS_TJ / 4 ? src[gj + 1 + PVS_AHEAD]
+                                                                : nxt[gj + 1 + PVS_AHEAD - PVS_TJ / 4];
+                    __builtin_amdgcn_sched_barrier(0);
+                    o = o + x1.x;
+                    o = o + x1.y;
+                    o = o + x1.z;
+                    o = o + x1.w;
                     __builtin_amdgcn_sched_barrier(0);
                 }
             } else if (nk > 0) { // the partial last tile
@@ -392,42 +406,47 @@ __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameD
                 for (int j = 0; j < nk; j++)
                     o = o + src[j];
             }
-            lds_barrier();
+            // no wait for the reads in flight (the next tile's); the memory
+            // clobber keeps every LDS access on its side of the barrier
+            __builtin_amdgcn_sched_barrier(0);
+            __asm__ volatile("s_barrier" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (ln < ncol)
             att[(size_t)t * D.qd + (size_t)h * HD + c0 + ln] = o;
     } else { // producer wave - 1: positions [PP (wave - 1), PP wave) of each tile
         // lane (row group rg, column octet cq): eight columns of four
-        // positions, 4 rg + [0, 4) of the producer's 32; a dwordx4 load per
-        // position brings the eight values, and the 8 consecutive lanes of
-        // one row read 128 contiguous bytes of it.  Offsets are 32-bit byte
-        // offsets from the layer's (uniform) base, clamped to row P - 1.
-        // Column c's products live in LDS row pv_row(c).
-        const int pw = wave - 1, rg = ln >> 3, cq = ln & 7;
+        // positions, 4 rg + [0, 4) of the producer's 64; a dwordx4 load per
+        // position brings the eight values, so each load instruction reads
+        // 64 contiguous bytes of 16 rows.  Offsets are 32-bit byte offsets
+        // from the layer's (uniform) base, clamped to row P - 1.
+        static_assert(PP == 64 && PVS_COLS == 32, "lane = (16 row groups of 4 positions, 4 column octets)");
+        const int pw = wave - 1, rg = ln & 15, cq = ln >> 4;
         const int cqc = min(cq, ncol / 8 - 1);
         const char *vb0 = (const char *)(vc + (((size_t)t * D.n_layers + li) * D.ctx) * D.kvd + (size_t)kvh * HD);
         const uint32_t rowb = (uint32_t)D.kvd * 2, colb = (uint32_t)(c0 + 8 * cqc) * 2;
         const uint32_t lim = (uint32_t)(P - 1) * rowb + colb;
+        // p of the lane's four positions as one float4, clamped to the last
+        // whole quad holding position P - 1 (inside the row: s_stride is a
+        // multiple of 64 and at least P)
         const float *pb = Pm + ((size_t)t * D.n_heads + h) * s_stride;
+        const int p4 = (P - 1) & ~3;
         const int r0 = PP * pw + 4 * rg; // first position of this lane within a tile
         int rw[8];
 #pragma unroll
         for (int k = 0; k < 8; k++)
-            rw[k] = pv_row(8 * cq + k) * PVS_STR + r0;
+            rw[k] = (8 * cq + k) * PVS_STR + r0;
         uint4 hv[PVS_SETS][4];
-        float pp[PVS_SETS];
-        auto load = [&](int tile, uint4 (&v)[4], float &p) {
+        float4 pp[PVS_SETS];
+        auto load = [&](int tile, uint4 (&v)[4], float4 &p) {
             const uint32_t o = (uint32_t)(tile * PVS_TJ + r0) * rowb + colb;
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 v[j] = *(const uint4 *)(vb0 + min(o + (uint32_t)j * rowb, lim));
-            p = pb[min(tile * PVS_TJ + PP * pw + (ln & (PP - 1)), P - 1)];
+            p = *(const float4 *)(pb + min(tile * PVS_TJ + r0, p4));
         };
-        auto produce = [&](int tile, const uint4 (&v)[4], float p) {
+        auto produce = [&](int tile, const uint4 (&v)[4], const float4 &q) {
             float *dst = prod[tile % PVS_NBUF];
-            if (ln < PP)
-                pst[pw][ln] = p;
-            const float4 q = *(const float4 *)&pst[pw][4 * rg];
             const uint32_t w[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w},
                                       {v[1].x, v[1].y, v[1].z, v[1].w},
                                       {v[2].x, v[2].y, v[2].z, v[2].w},
@@ -458,9 +477,13 @@ __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameD
 #pragma unroll
             for (int d = 0; d < PVS_SETS; d++) {
                 const int tile = kb + d + 2, set = (d + 2) % PVS_SETS;
+                // pinned in place: products of later tiles hoisted above
+                // this barrier would wait for loads meant to stay in flight
+                __builtin_amdgcn_sched_barrier(0);
                 produce(tile, hv[set], pp[set]);
                 load(tile + PVS_SETS, hv[set], pp[set]);
                 lds_barrier();
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
@@ -488,7 +511,7 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
     prof_end(ph, st);
     ph = prof_begin(LOOMHIP_KT_ATTN_PV, st);
     if (n <= 4) {
-        const dim3 pg(((HD + 63) / 64) * D.n_heads, 1, n);
+        const dim3 pg(((HD + PVS_COLS - 1) / PVS_COLS) * D.n_heads, 1, n);
         hipLaunchKernelGGL((attn_pv_split_kernel<HD>), pg, dim3(64 * (1 + PVS_NP)), 0, st, D, vc, pos, li, S,
                            s_stride, att);
     } else if (n < 8) {
