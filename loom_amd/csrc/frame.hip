@@ -1296,9 +1296,10 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         if (l.is_moe) {
             const int combine = n == 1 ? LOOMHIP_COMBINE_SELECTION_ADD : LOOMHIP_COMBINE_EXPERT_ASC;
             uint32_t *ids = m->ids_out ? m->ids_out + li * n * l.moe.n_used : nullptr;
-            if (!parity && moe_decode_fusable(&l.moe, n)) {
-                // FAST: the router launch applies the rmsnorm itself
-                if (int rc = moe_layer_fused_norm(&l.moe, w.x, l.ffn_norm, D.eps, n, combine, w.x, ids, st))
+            if (moe_decode_fusable(&l.moe, n, parity)) {
+                // the router launch applies the rmsnorm itself (PARITY: one
+                // lane, the squares summed in order in every work group)
+                if (int rc = moe_layer_fused_norm(&l.moe, w.x, l.ffn_norm, D.eps, n, combine, w.x, ids, parity, st))
                     return rc;
                 continue;
             }

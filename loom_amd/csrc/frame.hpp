@@ -149,25 +149,41 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
     if (j0 < n64 && j0 % L == 0)
         s.fst[j0 / L] = __float_as_uint((float)ex);
     __syncthreads();
-    // 2. every chunk's chain from 64 starts around its estimate; the values
-    //    are read four float4 ahead of the adds
+    // 2. every chunk's chain from 64 starts around its estimate: blocks of 64
+    //    values (16 float4 groups, unrolled), read eight groups ahead at
+    //    immediate offsets from the block's base, one wait per two groups.
+    //    Past the chunk's last block the ring re-reads that block (in range,
+    //    never added).
     auto chain = [&](float r, int c) {
-        const int ng = min(L, n64 - c * L) / 4; // a multiple of 16
+        constexpr int AH = NW >= 16 ? 4 : 8; // 1024-thread callers keep rows in registers across the sum
+        static_assert(16 % AH == 0 && AH % 2 == 0, "the ring wraps at block boundaries, two groups a wait");
+        const int nb = min(L, n64 - c * L) / 64;
         const float4 *src = (const float4 *)(v + c * L);
-        float4 ring[4];
+        float4 ring[AH];
 #pragma unroll
-        for (int a = 0; a < 4; a++)
+        for (int a = 0; a < AH; a++)
             ring[a] = src[a];
-        for (int g = 0; g < ng; g += 4) {
+        for (int bk = 0; bk < nb; bk++) {
+            const float4 *cur = src + 16 * bk, *nxt = bk + 1 < nb ? cur + 16 : cur;
 #pragma unroll
-            for (int a = 0; a < 4; a++) {
-                const float4 x = ring[a];
-                ring[a] = src[min(g + a + 4, ng - 1)];
+            for (int g = 0; g < 16; g += 2) {
+                const int a = g % AH;
+                __builtin_amdgcn_s_waitcnt(0xC07F & ~(0xF << 8) | ((AH - 2) << 8)); // the two oldest reads
+                const float4 x0 = ring[a], x1 = ring[a + 1];
                 __builtin_amdgcn_sched_barrier(0);
-                r = r + x.x;
-                r = r + x.y;
-                r = r + x.z;
-                r = r + x.w;
+                ring[a] = g + AH < 16 ? cur[g + AH] : nxt[g + AH - 16];
+                __builtin_amdgcn_sched_barrier(0);
+                r = r + x0.x;
+                r = r + x0.y;
+                r = r + x0.z;
+                r = r + x0.w;
+                __builtin_amdgcn_sched_barrier(0);
+                ring[a + 1] = g + 1 + AH < 16 ? cur[g + 1 + AH] : nxt[g + 1 + AH - 16];
+                __builtin_amdgcn_sched_barrier(0);
+                r = r + x1.x;
+                r = r + x1.y;
+                r = r + x1.z;
+                r = r + x1.w;
                 __builtin_amdgcn_sched_barrier(0);
             }
         }

@@ -126,6 +126,7 @@ struct GateParams {
     // rmsnorm (weights norm_w, tree-summed squares) itself; null: x is normed
     const float *norm_w;
     float norm_eps;
+    int norm_exact; // with norm_w, one token: the squares summed in the reference's order
     // set by launch_gate
     int n_chunks, wgs_per_chunk, gemv_wgs, quant_wgs;
 };
@@ -133,6 +134,9 @@ bool gate_supported(int n, int n_expert, int k);
 void launch_gate(GateParams p, hipStream_t st);
 // Decode path: router GEMV (router != null) + quantization of x, no routing.
 void launch_router_small(GateParams p, hipStream_t st);
+// the exact-norm form of the fused-norm router (norm_exact): one token, dim a
+// multiple of 32 that fits its LDS row
+bool router_exact_supported(int n, int dim);
 
 // Decode path (few tokens): gate/up with an in-kernel routing prologue per
 // (token, slot) pair, then down + gated combine per token.  No bucketing and

@@ -11,6 +11,7 @@
 // by expert.  "Last" is decided by self-resetting completion counters with
 // agent-scope fences on both sides; nothing ever waits on another workgroup.
 #include "device.hpp"
+#include "frame.hpp"
 
 namespace lh {
 
@@ -412,6 +413,70 @@ __device__ inline void wave_rmsnorm(const float *__restrict__ x, const float *__
 
 constexpr int RS_MAX_DIM = 8192; // fused-norm router: LDS row
 
+// logits[t][e] of half-wave hw's expert e (lanes 32 hw + P) from the normed
+// input xt: the dotF32 order of the reference (columns 32 i + P added in order
+// of i, then the lanes' sums as below, then the tail).
+// FULL: dim is exactly 32 RS_STEPS (one pass, every step live, no tail).
+template <bool FULL = false>
+__device__ __forceinline__ void router_row_dot(const GateParams &p, int e, bool valid, const float *row,
+                                               const float *xt, int t, bool one_pass,
+                                               const float (&wpre)[RS_STEPS]) {
+    const int lane = threadIdx.x & 63, hw = lane >> 5, P = lane & 31, dim = FULL ? 32 * RS_STEPS : p.dim;
+    const int n32 = dim / 32;
+    float acc = 0.0f;
+    if (FULL) {
+#pragma unroll
+        for (int u = 0; u < RS_STEPS; u++) {
+            const float pr = wpre[u] * xt[32 * u + P];
+            acc = acc + pr;
+        }
+    } else
+    for (int i0 = 0; i0 < n32; i0 += RS_STEPS) {
+        const int cnt = min(RS_STEPS, n32 - i0);
+        float wv[RS_STEPS], xv[RS_STEPS];
+#pragma unroll
+        for (int u = 0; u < RS_STEPS; u++) { // unconditional: steps past cnt re-read the last
+            const int c = 32 * (i0 + min(u, cnt - 1)) + P;
+            wv[u] = one_pass ? wpre[u] : row[c];
+            xv[u] = xt[c];
+        }
+        // steps past cnt add +0: acc starts at +0 and a sum of products
+        // is never -0, so they change nothing
+#pragma unroll
+        for (int u = 0; u < RS_STEPS; u++) {
+            const float pr = u < cnt ? wv[u] * xv[u] : 0.0f;
+            acc = acc + pr;
+        }
+    }
+    // leftover whole 8-chunks go to accumulator 0 (lanes 0..7)
+    for (int i = n32 * 32; i + 8 <= dim; i += 8)
+        if (P < 8) {
+            const float pr = row[i + P] * xt[i + P];
+            acc = acc + pr;
+        }
+    const int src = 32 * hw + (P & 7);
+    const float c1 = __int_as_float(__builtin_amdgcn_ds_bpermute((src + 8) << 2, __float_as_int(acc)));
+    const float c2 = __int_as_float(__builtin_amdgcn_ds_bpermute((src + 16) << 2, __float_as_int(acc)));
+    const float c3 = __int_as_float(__builtin_amdgcn_ds_bpermute((src + 24) << 2, __float_as_int(acc)));
+    const float v = ((acc + c1) + c2) + c3; // v_l in lanes 32hw + l, l < 8
+    float s0 = -0.0f, s1 = -0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; l++) {
+        s0 = s0 + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+        s1 = s1 + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32 + l));
+    }
+    if (P == 0 && valid) {
+        float s = hw ? s1 : s0;
+        for (int j = dim / 8 * 8; j < dim; j++) {
+            const float pr = row[j] * xt[j];
+            s = s + pr;
+        }
+        if (p.router_bias)
+            s = s + p.router_bias[e];
+        p.logits[(size_t)t * p.n_expert + e] = s;
+    }
+}
+
 __global__ __launch_bounds__(64) void router_small_kernel(GateParams p) {
     __shared__ __align__(16) float xn[RS_MAX_DIM];
     const int lane = threadIdx.x, hw = lane >> 5, P = lane & 31;
@@ -453,55 +518,121 @@ __global__ __launch_bounds__(64) void router_small_kernel(GateParams p) {
             __syncthreads();
             xt = xn;
         }
-        float acc = 0.0f;
-        for (int i0 = 0; i0 < n32; i0 += RS_STEPS) {
-            const int cnt = min(RS_STEPS, n32 - i0);
-            float wv[RS_STEPS], xv[RS_STEPS];
+        if (dim == 32 * RS_STEPS)
+            router_row_dot<true>(p, e, valid, row, xt, t, one_pass, wpre);
+        else
+            router_row_dot(p, e, valid, row, xt, t, one_pass, wpre);
+    }
+}
+
+// PARITY numerics, one token: the fused-norm router with the rmsnorm's sum of
+// squares in the reference's order (tensor.zig:9-15; the speculative
+// composition of seq_sum_nonneg, which returns that sequential sum itself).
+// Every work group (RX_WAVES waves) computes the norm of the token itself --
+// there is no norm launch, and the router rows' loads go out before it.
+// Gemv groups: two experts per wave; quant groups: one item per wave.
+constexpr int RX_WAVES = 8;
+constexpr int RX_MAX_DIM = 7936; // the squares, then the normed row, in LDS
+
+// x and the norm weights in registers: float4 k of thread tid holds values
+// 4 tid + 4 NT k (RX_XV of them cover RX_MAX_DIM)
+constexpr int RX_XV = (RX_MAX_DIM + 4 * 64 * RX_WAVES - 1) / (4 * 64 * RX_WAVES);
+
+template <int NW>
+__device__ __forceinline__ void norm_exact_load(const float *__restrict__ x, const float *__restrict__ w, int dim,
+                                                float4 (&xv)[RX_XV], float4 (&wv)[RX_XV]) {
+    const int tid = threadIdx.x;
 #pragma unroll
-            for (int u = 0; u < RS_STEPS; u++) { // unconditional: steps past cnt re-read the last
-                const int c = 32 * (i0 + min(u, cnt - 1)) + P;
-                wv[u] = one_pass ? wpre[u] : row[c];
-                xv[u] = xt[c];
-            }
-            // steps past cnt add +0: acc starts at +0 and a sum of products
-            // is never -0, so they change nothing
-#pragma unroll
-            for (int u = 0; u < RS_STEPS; u++) {
-                const float pr = u < cnt ? wv[u] * xv[u] : 0.0f;
-                acc = acc + pr;
-            }
-        }
-        // leftover whole 8-chunks go to accumulator 0 (lanes 0..7)
-        for (int i = n32 * 32; i + 8 <= dim; i += 8)
-            if (P < 8) {
-                const float pr = row[i + P] * xt[i + P];
-                acc = acc + pr;
-            }
-        const int src = 32 * hw + (P & 7);
-        const float c1 = __int_as_float(__builtin_amdgcn_ds_bpermute((src + 8) << 2, __float_as_int(acc)));
-        const float c2 = __int_as_float(__builtin_amdgcn_ds_bpermute((src + 16) << 2, __float_as_int(acc)));
-        const float c3 = __int_as_float(__builtin_amdgcn_ds_bpermute((src + 24) << 2, __float_as_int(acc)));
-        const float v = ((acc + c1) + c2) + c3; // v_l in lanes 32hw + l, l < 8
-        float s0 = -0.0f, s1 = -0.0f;
-#pragma unroll
-        for (int l = 0; l < 8; l++) {
-            s0 = s0 + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-            s1 = s1 + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32 + l));
-        }
-        if (P == 0 && valid) {
-            float s = hw ? s1 : s0;
-            for (int j = dim / 8 * 8; j < dim; j++) {
-                const float pr = row[j] * xt[j];
-                s = s + pr;
-            }
-            if (p.router_bias)
-                s = s + p.router_bias[e];
-            p.logits[(size_t)t * p.n_expert + e] = s;
+    for (int k = 0; k < RX_XV; k++) {
+        const int i = 4 * tid + 4 * 64 * NW * k;
+        xv[k] = wv[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < dim) { // dim is a multiple of 32
+            xv[k] = *(const float4 *)(x + i);
+            wv[k] = *(const float4 *)(w + i);
         }
     }
 }
 
+// xn = rmsnorm(x) (tensor.zig:9-15): the squares in order, zero-padded to
+// whole 64s, summed sequentially, then (x * scale) * w.
+template <int NW>
+__device__ __forceinline__ void norm_exact_block(const float4 (&xv)[RX_XV], const float4 (&wv)[RX_XV], int dim,
+                                                 float eps, float *xn, SeqSumLds &seq) {
+    const int tid = threadIdx.x, n64 = (dim + 63) & ~63;
+#pragma unroll
+    for (int k = 0; k < RX_XV; k++) {
+        const int i = 4 * tid + 4 * 64 * NW * k;
+        if (i < n64) {
+            float4 q;
+            q.x = xv[k].x * xv[k].x;
+            q.y = xv[k].y * xv[k].y;
+            q.z = xv[k].z * xv[k].z;
+            q.w = xv[k].w * xv[k].w;
+            *(float4 *)(xn + i) = q;
+        }
+    }
+    __syncthreads();
+    const float total = seq_sum_nonneg<NW>(xn, dim, seq); // ends with a barrier: xn is free again
+    const float scale = 1.0f / sqrtf(total / (float)dim + eps);
+#pragma unroll
+    for (int k = 0; k < RX_XV; k++) {
+        const int i = 4 * tid + 4 * 64 * NW * k;
+        if (i < dim) {
+            float4 o;
+            o.x = (xv[k].x * scale) * wv[k].x;
+            o.y = (xv[k].y * scale) * wv[k].y;
+            o.z = (xv[k].z * scale) * wv[k].z;
+            o.w = (xv[k].w * scale) * wv[k].w;
+            *(float4 *)(xn + i) = o;
+        }
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(64 * RX_WAVES) void router_exact_kernel(GateParams p) {
+    __shared__ __align__(16) float xn[RX_MAX_DIM];
+    __shared__ SeqSumLds seq;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hw = lane >> 5, P = lane & 31;
+    const int dim = p.dim, n32 = dim / 32;
+    const bool gemv = (int)blockIdx.x < p.gemv_wgs;
+    const int e = ((int)blockIdx.x * RX_WAVES + wave) * 2 + hw;
+    const bool valid = gemv && e < p.n_expert;
+    const float *row = gemv ? p.router + (size_t)(valid ? e : 0) * dim : nullptr;
+    const bool one_pass = n32 <= RS_STEPS;
+    // x and the norm weights first: the router rows' loads queue behind them
+    float4 xv[RX_XV], wv[RX_XV];
+    norm_exact_load<RX_WAVES>(p.x, p.norm_w, dim, xv, wv);
+    float wpre[RS_STEPS];
+    if (gemv && one_pass) {
+#pragma unroll
+        for (int u = 0; u < RS_STEPS; u++)
+            wpre[u] = row[32 * min(u, n32 - 1) + P];
+    }
+    norm_exact_block<RX_WAVES>(xv, wv, dim, p.norm_eps, xn, seq);
+    if (gemv) {
+        if (dim == 32 * RS_STEPS)
+            router_row_dot<true>(p, e, valid, row, xn, 0, one_pass, wpre);
+        else
+            router_row_dot(p, e, valid, row, xn, 0, one_pass, wpre);
+    } else {
+        const int item = ((int)blockIdx.x - p.gemv_wgs) * RX_WAVES + wave;
+        if (item < quant_items(p.qt, dim))
+            quant_item_wave(p.qt, xn, dim, 0, item, p.qx);
+    }
+}
+
+bool router_exact_supported(int n, int dim) { return n == 1 && dim % 32 == 0 && dim <= RX_MAX_DIM; }
+
 void launch_router_small(GateParams p, hipStream_t st) {
+    if (p.norm_exact) { // callers check router_exact_supported
+        p.gemv_wgs = p.router ? (p.n_expert + 2 * RX_WAVES - 1) / (2 * RX_WAVES) : 0;
+        p.quant_wgs = p.qt ? (quant_items(p.qt, p.dim) + RX_WAVES - 1) / RX_WAVES : 0;
+        if (p.gemv_wgs + p.quant_wgs == 0)
+            return;
+        hipLaunchKernelGGL(router_exact_kernel, dim3(p.gemv_wgs + p.quant_wgs), dim3(64 * RX_WAVES), 0, st, p);
+        note_launch();
+        return;
+    }
     p.gemv_wgs = p.router ? (p.n_expert + 1) / 2 : 0; // no router: logits come from the caller
     p.quant_wgs = p.qt ? quant_items(p.qt, p.dim) * p.n : 0;
     if (p.gemv_wgs + p.quant_wgs == 0)

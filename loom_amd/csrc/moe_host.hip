@@ -49,6 +49,7 @@ struct MoeRun {
     const void *gate, *up, *down;
     const float *norm_w = nullptr; // decode path: rmsnorm the input first (normed = residual x)
     float norm_eps = 0.0f;
+    bool norm_exact = false;       // ... with the squares summed in the reference's order (one token)
     DenseFfn sh{}; // the shared expert (sh.gate null: none)
 };
 
@@ -294,6 +295,9 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
         gp.chain = 0;
         gp.norm_w = m.norm_w;
         gp.norm_eps = m.norm_eps;
+        gp.norm_exact = m.norm_w && m.norm_exact;
+        if (gp.norm_exact && !router_exact_supported((int)n, (int)m.dim))
+            return fail(LOOMHIP_ERR_ARG, "moe: the exact fused norm takes one token of dim <= 7936");
         launch_router_small(gp, st);
         if (!launch_moe_decode(m.gate_t, m.down_t, dp, (int)n, st, LOOMHIP_KT_GATE_UP, LOOMHIP_KT_DOWN))
             return fail(LOOMHIP_ERR_ARG, "moe: decode kernels declined the shape");
@@ -390,18 +394,19 @@ int moe_layer_check(const loomhip_moe_layer *L, size_t n, bool shexp_ok) {
 int moe_frame_check(const loomhip_moe_layer *L, size_t n) { return moe_layer_check(L, n, false); }
 
 int moe_layer_fused_norm(const loomhip_moe_layer *L, const float *x, const float *norm_w, float eps, size_t n_tok,
-                         int combine, float *out, uint32_t *ids_out, hipStream_t st) {
+                         int combine, float *out, uint32_t *ids_out, bool exact, hipStream_t st) {
     MoeRun m{L->dim, L->ffn, L->n_expert, L->n_used, L->gating, L->weights_norm, L->weights_scale,
              L->router, L->router_bias, L->sel_bias, L->gate_t, L->up_t, L->down_t, L->gate,
              L->up, L->down};
     m.norm_w = norm_w;
     m.norm_eps = eps;
+    m.norm_exact = exact;
     return moe_run(m, x, nullptr, n_tok, combine, out, ids_out, nullptr, st);
 }
 
-bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok) {
+bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok, bool exact) {
     return n_tok <= DECODE_MAX_TOK && decode_supported(L->gate_t, L->down_t, (int)L->ffn) && L->router &&
-           L->dim <= 8192 && L->dim % 32 == 0;
+           L->dim <= 8192 && L->dim % 32 == 0 && (!exact || router_exact_supported((int)n_tok, (int)L->dim));
 }
 
 } // namespace lh

@@ -71,9 +71,10 @@ int dense_ffn_add(const DenseFfn &f, const float *x, size_t n, size_t dim, float
 int moe_noalloc_setup(int device);
 // The decode MoE path with its rmsnorm fused into the router launch (x = the
 // residual stream); moe_decode_fusable says whether the layer takes it.
+// exact: the squares summed in the reference's order (one token), else a tree.
 int moe_layer_fused_norm(const loomhip_moe_layer *L, const float *x, const float *norm_w, float eps, size_t n_tok,
-                         int combine, float *out, uint32_t *ids_out, hipStream_t st);
-bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok);
+                         int combine, float *out, uint32_t *ids_out, bool exact, hipStream_t st);
+bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok, bool exact);
 // What the MoE layer would decline at n tokens, checked before any launch.
 int moe_frame_check(const loomhip_moe_layer *L, size_t n);
 // The same checks for a caller that forms acc = routed + shared itself
