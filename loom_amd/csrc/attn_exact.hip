@@ -346,10 +346,16 @@ static_assert((PVS_TJ / 4) % PVS_AHEAD == 0, "the read ring must wrap at tile bo
 // groups.
 
 template <int HD>
+// qwt >= 0: the output is also quantized for a weight of type qwt (the wo
+// matvec's input, 256-column items): the last of an item's eight groups to
+// store its columns quantizes the item (its data handed over through
+// agent-scope stores and loads, counters in the sync buffer), in place of a
+// quantizer launch.
 __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameDims D, const uint16_t *__restrict__ vc,
                                                                          const int32_t *__restrict__ pos, int li,
                                                                          const float *__restrict__ Pm, int s_stride,
-                                                                         float *__restrict__ att) {
+                                                                         float *__restrict__ att, int qwt, QAct qa,
+                                                                         int *__restrict__ sync) {
     constexpr int PP = PVS_TJ / PVS_NP; // positions per producer per tile
     __shared__ __align__(16) float prod[PVS_NBUF][PVS_COLS * PVS_STR];
     const int ncb = (HD + PVS_COLS - 1) / PVS_COLS;
@@ -412,8 +418,17 @@ __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameD
             __asm__ volatile("s_barrier" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (ln < ncol)
-            att[(size_t)t * D.qd + (size_t)h * HD + c0 + ln] = o;
+        float *dst = att + (size_t)t * D.qd + (size_t)h * HD + c0 + ln;
+        if (qwt < 0) {
+            if (ln < ncol)
+                *dst = o;
+        } else {
+            if (ln < ncol)
+                st_dev(dst, o);
+            const int it = (h * HD + c0) / 256;
+            if (last_arrival_wave(sync + SYNC_PV_QUANT + t * 64 + it, 256 / PVS_COLS))
+                quant_item_wave<true>(qwt, att + (size_t)t * D.qd, D.qd, t, it, qa);
+        }
     } else { // producer wave - 1: positions [PP (wave - 1), PP wave) of each tile
         // lane (row group rg, column octet cq): eight columns of four
         // positions, 4 rg + [0, 4) of the producer's 64; a dwordx4 load per
@@ -494,7 +509,8 @@ size_t exact_softmax_lds(int s_stride) { return (size_t)s_stride * 4; }
 template <int HD>
 static void launch_hd(const FrameDims &D, const float *q, const float *k, const float *v, const float *q_norm,
                       const float *k_norm, const float *rope_cs, uint16_t *kc, uint16_t *vc, const int32_t *pos,
-                      int li, bool fuse, float *S, int s_stride, float *att, size_t n, hipStream_t st) {
+                      int li, bool fuse, float *S, int s_stride, float *att, size_t n, int qwt, QAct qa,
+                      hipStream_t st) {
     const int n_chunks = (D.ctx + ATT_TC - 1) / ATT_TC;
     const int G = D.n_heads / D.n_kv;
     int ph = prof_begin(LOOMHIP_KT_ATTN_SCORES, st);
@@ -513,7 +529,7 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
     if (n <= 4) {
         const dim3 pg(((HD + PVS_COLS - 1) / PVS_COLS) * D.n_heads, 1, n);
         hipLaunchKernelGGL((attn_pv_split_kernel<HD>), pg, dim3(64 * (1 + PVS_NP)), 0, st, D, vc, pos, li, S,
-                           s_stride, att);
+                           s_stride, att, qwt, qa, g_ctx.sync);
     } else if (n < 8) {
         const dim3 pg((HD + 63) / 64, D.n_kv * ((G + 1) / 2), n);
         hipLaunchKernelGGL((attn_pv_kernel<HD, 2>), pg, dim3(128), 0, st, D, vc, pos, li, S, s_stride, att);
@@ -527,20 +543,27 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
     note_launch();
 }
 
+bool attn_exact_quant_fusable(const FrameDims &D, size_t n) {
+    return n <= 4 && (D.hd == 64 || D.hd == 128) && D.qd % 256 == 0 && D.qd / 256 <= 64;
+}
+
 bool launch_attn_exact(const FrameDims &D, const float *q, const float *k, const float *v, const float *q_norm,
                        const float *k_norm, const float *rope_cs, uint16_t *kc, uint16_t *vc, const int32_t *pos,
-                       int li, bool fuse, float *S, int s_stride, float *att, size_t n, hipStream_t st) {
+                       int li, bool fuse, float *S, int s_stride, float *att, size_t n, int qwt, const QAct &qa,
+                       hipStream_t st) {
     if (D.ctx > EXACT_MAX_CTX || s_stride % 64 || s_stride < D.ctx)
+        return false;
+    if (qwt >= 0 && !attn_exact_quant_fusable(D, n))
         return false;
     switch (D.hd) {
     case 128:
-        launch_hd<128>(D, q, k, v, q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse, S, s_stride, att, n, st);
+        launch_hd<128>(D, q, k, v, q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse, S, s_stride, att, n, qwt, qa, st);
         return true;
     case 64:
-        launch_hd<64>(D, q, k, v, q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse, S, s_stride, att, n, st);
+        launch_hd<64>(D, q, k, v, q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse, S, s_stride, att, n, qwt, qa, st);
         return true;
     case 48:
-        launch_hd<48>(D, q, k, v, q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse, S, s_stride, att, n, st);
+        launch_hd<48>(D, q, k, v, q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse, S, s_stride, att, n, qwt, qa, st);
         return true;
     default:
         return false;

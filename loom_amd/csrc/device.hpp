@@ -284,6 +284,7 @@ __device__ inline void lds_barrier() {
 // is all zeros between launches.
 constexpr int SYNC_GATE_CHUNK = 0;   // [MAX_TOK / GT_TOK]
 constexpr int SYNC_GATE_FINAL = 128; // [1]
+constexpr int SYNC_PV_QUANT = 256;   // [4 lanes][64 items]: P.V groups of one 256-column item
 //
 // Data handed from one workgroup to another inside a launch travels through
 // relaxed agent-scope atomic stores and loads (st_dev / ld_dev), which are
@@ -320,6 +321,22 @@ __device__ inline bool last_arrival(int *counter, int target) {
     }
     __syncthreads();
     return s_last;
+}
+
+// The same for one wave: the calling wave alone has stored the data (all its
+// lanes active); lane 0 counts, and every lane gets the verdict.
+__device__ inline bool last_arrival_wave(int *counter, int target) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0); // this wave's stores are acknowledged
+    int last = 0;
+    if ((threadIdx.x & 63) == 0) {
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old == target - 1;
+        if (last)
+            __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return __builtin_amdgcn_readfirstlane(last) != 0;
 }
 
 // ---- routing ------------------------------------------------------------------------

@@ -1247,10 +1247,13 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
         const float *qin = fuse_rope ? w.q : w.qrot;
         if (parity) {
             // the reference's own order over the whole context: scores, softmax, P.V
+            // few lanes: P.V quantizes wo's input itself
+            const bool qfuse = attn_exact_quant_fusable(D, n);
             if (!launch_attn_exact(D, qin, w.k, w.v, l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li,
-                                   fuse_rope, w.S, w.s_stride, w.att, n, st))
+                                   fuse_rope, w.S, w.s_stride, w.att, n, qfuse ? l.wo_t : -1, w.qa_att, st))
                 return fail(LOOMHIP_ERR_ARG, "token_frame: exact attention declined");
-            launch_quant_act(l.wo_t, w.att, D.qd, D.qd, (int)n, w.qa_att, st);
+            if (!qfuse)
+                launch_quant_act(l.wo_t, w.att, D.qd, D.qd, (int)n, w.qa_att, st);
             if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_WO, true, 16))
                 return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
         } else {

@@ -290,8 +290,12 @@ __device__ __forceinline__ void softmax_row_exact(float *row, int P, float *e, f
 
 constexpr int EXACT_MAX_CTX = 7936; // the softmax's e[] and the sequential sum's LDS in 64 KB
 size_t exact_softmax_lds(int s_stride);
+// qwt >= 0 (attn_exact_quant_fusable): P.V also quantizes att into qa for a
+// weight of type qwt, in place of a quantizer launch.
+bool attn_exact_quant_fusable(const FrameDims &D, size_t n);
 bool launch_attn_exact(const FrameDims &D, const float *q, const float *k, const float *v, const float *q_norm,
                        const float *k_norm, const float *rope_cs, uint16_t *kc, uint16_t *vc, const int32_t *pos,
-                       int li, bool fuse, float *S, int s_stride, float *att, size_t n, hipStream_t st);
+                       int li, bool fuse, float *S, int s_stride, float *att, size_t n, int qwt, const QAct &qa,
+                       hipStream_t st);
 
 } // namespace lh
