@@ -345,19 +345,33 @@ static_assert((PVS_TJ / 4) % PVS_AHEAD == 0, "the read ring must wrap at tile bo
 // every 8 and every 16 consecutive lanes of either access hit distinct bank
 // groups.
 
-template <int HD>
 // qwt >= 0: the output is also quantized for a weight of type qwt (the wo
 // matvec's input, 256-column items): the last of an item's eight groups to
 // store its columns quantizes the item (its data handed over through
 // agent-scope stores and loads, counters in the sync buffer), in place of a
 // quantizer launch.
-__global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameDims D, const uint16_t *__restrict__ vc,
-                                                                         const int32_t *__restrict__ pos, int li,
-                                                                         const float *__restrict__ Pm, int s_stride,
-                                                                         float *__restrict__ att, int qwt, QAct qa,
-                                                                         int *__restrict__ sync) {
+//
+// SM: the group computes its head's softmax itself (the scores in Pm,
+// tensor.zig:18-28 in the reference's order, as attn_softmax_kernel) into
+// LDS, and the producers form p_t = e_t * inv from there -- the same
+// rounding as the softmax launch's p, with no launch, and the first value
+// tiles' loads in flight while the softmax runs.  512 threads: waves 4..7
+// help with the softmax, then only pass the tiles' barriers.
+constexpr int PVS_SM_WAVES = 8;
+constexpr int PVS_SM_VALS = (EXACT_MAX_CTX + 64 * PVS_SM_WAVES - 1) / (64 * PVS_SM_WAVES); // scores per thread
+size_t pv_softmax_lds(int s_stride) { return (size_t)s_stride * 4; }
+
+template <int HD, bool SM>
+__global__ __launch_bounds__(SM ? 64 * PVS_SM_WAVES : 64 * (1 + PVS_NP)) void attn_pv_split_kernel(
+    FrameDims D, const uint16_t *__restrict__ vc, const int32_t *__restrict__ pos, int li,
+    const float *__restrict__ Pm, int s_stride, float *__restrict__ att, int qwt, QAct qa,
+    int *__restrict__ sync) {
     constexpr int PP = PVS_TJ / PVS_NP; // positions per producer per tile
+    constexpr int NW = SM ? PVS_SM_WAVES : 1 + PVS_NP;
     __shared__ __align__(16) float prod[PVS_NBUF][PVS_COLS * PVS_STR];
+    extern __shared__ __align__(16) float e[]; // SM: e_t of the head, 64 * ceil(P / 64) values
+    __shared__ float redf[NW];
+    __shared__ SeqSumLds seq;
     const int ncb = (HD + PVS_COLS - 1) / PVS_COLS;
     // XCD-aware order: consecutive work items share an XCD (work groups are
     // dealt to the 8 XCDs round robin), so one KV head's values stay in few L2s
@@ -370,6 +384,85 @@ __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameD
     const int ntile = (P + PVS_TJ - 1) / PVS_TJ;
     const int ntp = (ntile + PVS_SETS - 1) / PVS_SETS * PVS_SETS; // tiles the loops run (padded)
     const int c0 = sl * PVS_COLS, ncol = min(PVS_COLS, HD - c0);
+    const float *prow = Pm + ((size_t)t * D.n_heads + h) * s_stride; // p (SM: the scores)
+
+    // ---- the producers' value tiles (declared here: SM issues the first
+    // loads before the softmax) ----
+    // lane (row group rg, column octet cq): eight columns of four positions,
+    // 4 rg + [0, 4) of the producer's 64; a dwordx4 load per position brings
+    // the eight values, so each load instruction reads 64 contiguous bytes
+    // of 16 rows.  Offsets are 32-bit byte offsets from the layer's
+    // (uniform) base, clamped to row P - 1.  p of the lane's four positions
+    // is one float4, clamped to the last whole quad holding position P - 1
+    // (inside the row: s_stride is a multiple of 64 and at least P).
+    static_assert(PP == 64 && PVS_COLS == 32, "lane = (16 row groups of 4 positions, 4 column octets)");
+    const bool producer = wave >= 1 && wave <= PVS_NP;
+    const int pw = wave - 1, rg = ln & 15, cq = ln >> 4;
+    const int cqc = min(cq, ncol / 8 - 1);
+    const char *vb0 = (const char *)(vc + (((size_t)t * D.n_layers + li) * D.ctx) * D.kvd + (size_t)kvh * HD);
+    const uint32_t rowb = (uint32_t)D.kvd * 2, colb = (uint32_t)(c0 + 8 * cqc) * 2;
+    const uint32_t lim = (uint32_t)(P - 1) * rowb + colb;
+    const int p4 = (P - 1) & ~3;
+    const int r0 = PP * pw + 4 * rg; // first position of this lane within a tile
+    uint4 hv[PVS_SETS][4];
+    float4 pp[PVS_SETS];
+    auto load_v = [&](int tile, uint4 (&v)[4]) {
+        const uint32_t o = (uint32_t)(tile * PVS_TJ + r0) * rowb + colb;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            v[j] = *(const uint4 *)(vb0 + min(o + (uint32_t)j * rowb, lim));
+    };
+    float inv = 0.0f;
+    if constexpr (SM) {
+        // the scores first, then the value loads: the in-order load counter
+        // lets the softmax wait for its scores alone
+        float sv[PVS_SM_VALS];
+#pragma unroll
+        for (int k = 0; k < PVS_SM_VALS; k++) {
+            const int j = threadIdx.x + 64 * NW * k;
+            sv[k] = j < P ? prow[j] : -INFINITY;
+        }
+        if (producer) {
+#pragma unroll
+            for (int d = 0; d < PVS_SETS; d++)
+                load_v(d, hv[d]);
+        }
+        // softmax_row_exact's steps: the max (order-free), e_t = exp(s_t - m)
+        // zero-filled to whole 64s, 1 / the position-ordered sum
+        float m = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < PVS_SM_VALS; k++)
+            m = fmaxf(m, sv[k]);
+        m = wave_max(m);
+        if (ln == 0)
+            redf[wave] = m;
+        __syncthreads();
+        m = redf[0];
+        for (int w = 1; w < NW; w++)
+            m = fmaxf(m, redf[w]);
+        const int n64 = (P + 63) & ~63;
+#pragma unroll
+        for (int k = 0; k < PVS_SM_VALS; k++) {
+            const int j = threadIdx.x + 64 * NW * k;
+            if (j < n64)
+                e[j] = j < P ? exp_f32_poly(sv[k] - m) : 0.0f;
+        }
+        __syncthreads();
+        inv = 1.0f / seq_sum_nonneg<NW>(e, P, seq);
+    }
+    auto load = [&](int tile, uint4 (&v)[4], float4 &p) {
+        load_v(tile, v);
+        if constexpr (!SM)
+            p = *(const float4 *)(prow + min(tile * PVS_TJ + r0, p4));
+    };
+    auto pget = [&](int tile, const float4 &p) {
+        if constexpr (SM) { // p_t = e_t * inv, the softmax's own expression
+            const float4 ev = *(const float4 *)&e[min(tile * PVS_TJ + r0, p4)];
+            return make_float4(ev.x * inv, ev.y * inv, ev.z * inv, ev.w * inv);
+        } else {
+            return p;
+        }
+    };
     if (wave == 0) { // consumer
         float o = 0.0f;
         lds_barrier(); // tiles 0 and 1 are in
@@ -429,39 +522,14 @@ __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameD
             if (last_arrival_wave(sync + SYNC_PV_QUANT + t * 64 + it, 256 / PVS_COLS))
                 quant_item_wave<true>(qwt, att + (size_t)t * D.qd, D.qd, t, it, qa);
         }
-    } else { // producer wave - 1: positions [PP (wave - 1), PP wave) of each tile
-        // lane (row group rg, column octet cq): eight columns of four
-        // positions, 4 rg + [0, 4) of the producer's 64; a dwordx4 load per
-        // position brings the eight values, so each load instruction reads
-        // 64 contiguous bytes of 16 rows.  Offsets are 32-bit byte offsets
-        // from the layer's (uniform) base, clamped to row P - 1.
-        static_assert(PP == 64 && PVS_COLS == 32, "lane = (16 row groups of 4 positions, 4 column octets)");
-        const int pw = wave - 1, rg = ln & 15, cq = ln >> 4;
-        const int cqc = min(cq, ncol / 8 - 1);
-        const char *vb0 = (const char *)(vc + (((size_t)t * D.n_layers + li) * D.ctx) * D.kvd + (size_t)kvh * HD);
-        const uint32_t rowb = (uint32_t)D.kvd * 2, colb = (uint32_t)(c0 + 8 * cqc) * 2;
-        const uint32_t lim = (uint32_t)(P - 1) * rowb + colb;
-        // p of the lane's four positions as one float4, clamped to the last
-        // whole quad holding position P - 1 (inside the row: s_stride is a
-        // multiple of 64 and at least P)
-        const float *pb = Pm + ((size_t)t * D.n_heads + h) * s_stride;
-        const int p4 = (P - 1) & ~3;
-        const int r0 = PP * pw + 4 * rg; // first position of this lane within a tile
+    } else if (producer) { // producer wave - 1: positions [PP (wave - 1), PP wave) of each tile
         int rw[8];
 #pragma unroll
         for (int k = 0; k < 8; k++)
             rw[k] = (8 * cq + k) * PVS_STR + r0;
-        uint4 hv[PVS_SETS][4];
-        float4 pp[PVS_SETS];
-        auto load = [&](int tile, uint4 (&v)[4], float4 &p) {
-            const uint32_t o = (uint32_t)(tile * PVS_TJ + r0) * rowb + colb;
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                v[j] = *(const uint4 *)(vb0 + min(o + (uint32_t)j * rowb, lim));
-            p = *(const float4 *)(pb + min(tile * PVS_TJ + r0, p4));
-        };
-        auto produce = [&](int tile, const uint4 (&v)[4], const float4 &q) {
+        auto produce = [&](int tile, const uint4 (&v)[4], const float4 &pv) {
             float *dst = prod[tile % PVS_NBUF];
+            const float4 q = pget(tile, pv);
             const uint32_t w[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w},
                                       {v[1].x, v[1].y, v[1].z, v[1].w},
                                       {v[2].x, v[2].y, v[2].z, v[2].w},
@@ -477,9 +545,11 @@ __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameD
                 *(float4 *)&dst[rw[k]] = a;
             }
         };
+        if constexpr (!SM) { // SM: the value loads went out before the softmax
 #pragma unroll
-        for (int d = 0; d < PVS_SETS; d++)
-            load(d, hv[d], pp[d]);
+            for (int d = 0; d < PVS_SETS; d++)
+                load(d, hv[d], pp[d]);
+        }
         produce(0, hv[0], pp[0]);
         load(PVS_SETS, hv[0], pp[0]);
         produce(1, hv[1], pp[1]);
@@ -501,6 +571,13 @@ __global__ __launch_bounds__(64 * (1 + PVS_NP)) void attn_pv_split_kernel(FrameD
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+    } else { // SM's helper waves: the same barriers as the consumer, nothing else
+        lds_barrier();
+        for (int k = 0; k < ntp; k++) {
+            __builtin_amdgcn_sched_barrier(0);
+            __asm__ volatile("s_barrier" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 }
 
@@ -517,19 +594,18 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
     hipLaunchKernelGGL(attn_scores_kernel<HD>, dim3(n_chunks, D.n_kv, n), dim3(SC_THREADS), 0, st, D, q, k, v,
                        q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse ? 1 : 0, S, s_stride);
     prof_end(ph, st);
-    ph = prof_begin(LOOMHIP_KT_ATTN_SOFTMAX, st);
-    if (n <= 4)
-        hipLaunchKernelGGL((attn_softmax_kernel<SM_THREADS>), dim3(D.n_heads, 1, n), dim3(SM_THREADS),
-                           exact_softmax_lds(s_stride), st, D, pos, S, s_stride);
-    else
+    if (n > 4) {
+        ph = prof_begin(LOOMHIP_KT_ATTN_SOFTMAX, st);
         hipLaunchKernelGGL((attn_softmax_kernel<256>), dim3(D.n_heads, 1, n), dim3(256), exact_softmax_lds(s_stride),
                            st, D, pos, S, s_stride);
-    prof_end(ph, st);
+        prof_end(ph, st);
+        note_launch();
+    }
     ph = prof_begin(LOOMHIP_KT_ATTN_PV, st);
-    if (n <= 4) {
+    if (n <= 4) { // the softmax inside the P.V groups
         const dim3 pg(((HD + PVS_COLS - 1) / PVS_COLS) * D.n_heads, 1, n);
-        hipLaunchKernelGGL((attn_pv_split_kernel<HD>), pg, dim3(64 * (1 + PVS_NP)), 0, st, D, vc, pos, li, S,
-                           s_stride, att, qwt, qa, g_ctx.sync);
+        hipLaunchKernelGGL((attn_pv_split_kernel<HD, true>), pg, dim3(64 * PVS_SM_WAVES), pv_softmax_lds(s_stride),
+                           st, D, vc, pos, li, S, s_stride, att, qwt, qa, g_ctx.sync);
     } else if (n < 8) {
         const dim3 pg((HD + 63) / 64, D.n_kv * ((G + 1) / 2), n);
         hipLaunchKernelGGL((attn_pv_kernel<HD, 2>), pg, dim3(128), 0, st, D, vc, pos, li, S, s_stride, att);
@@ -538,7 +614,6 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
         hipLaunchKernelGGL((attn_pv_kernel<HD, 4>), pg, dim3(256), 0, st, D, vc, pos, li, S, s_stride, att);
     }
     prof_end(ph, st);
-    note_launch();
     note_launch();
     note_launch();
 }
