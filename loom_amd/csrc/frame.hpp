@@ -134,18 +134,34 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
     int K = 1; // values per thread in the estimates: a power of two, so it divides L
     while (K * NT < n64)
         K *= 2;
-    // 1. the estimates: an exclusive prefix sum in double at every chunk start
+    // 1. the estimates: an exclusive prefix sum in double at every chunk
+    //    start (each thread's K values summed in f32 first: their error is
+    //    far below one ulp of the running sum at any chunk start)
     const int j0 = tid * K;
-    double own = 0.0;
-    for (int j = j0; j < min(j0 + K, n64); j++)
-        own = own + (double)v[j];
+    float ownf = 0.0f;
+    if (K >= 4) { // K divides n64: whole float4s, read several at a time
+        const int je = min(j0 + K, n64);
+#pragma unroll 8
+        for (int j = j0; j < je; j += 4) {
+            const float4 x = *(const float4 *)(v + j);
+            ownf = ownf + x.x;
+            ownf = ownf + x.y;
+            ownf = ownf + x.z;
+            ownf = ownf + x.w;
+        }
+    } else {
+        for (int j = j0; j < min(j0 + K, n64); j++)
+            ownf = ownf + v[j];
+    }
+    const double own = (double)ownf;
     const double inc = wave_scan_d(own);
     if (ln == 63)
         s.wtot[wave] = inc;
     __syncthreads();
     double ex = inc - own;
-    for (int w = 0; w < wave; w++)
-        ex = ex + s.wtot[w];
+#pragma unroll
+    for (int w = 0; w < NW - 1; w++) // the earlier waves' totals (+0 from the rest: ex >= 0)
+        ex = ex + (w < wave ? s.wtot[w] : 0.0);
     if (j0 < n64 && j0 % L == 0)
         s.fst[j0 / L] = __float_as_uint((float)ex);
     __syncthreads();
@@ -205,34 +221,20 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
     //    followed serially from the start (rare).
     if (wave == 0) {
         const int fa = ln < C ? (int)s.fst[ln] : 0;
-        int idx = 0;
-        int flags = 0;
-        int ea[8], eb[8]; // eight chunks a batch, the next batch in flight
-        auto load = [&](int (&e)[8], int cb) { // past the last chunk, its row: the identity
+        // the path's maps composed as a tree (five levels of lane permutes):
+        // (g after f)(l) = g[f(l) & 63], flagged if either step is
+        int e[SEQ_MAX_CHUNKS]; // past the last chunk, its row: the identity
 #pragma unroll
-            for (int a = 0; a < 8; a++)
-                e[a] = s.nx[min(cb + a, C - 1) * 64 + ln];
-        };
-        auto follow = [&](const int (&e)[8]) {
+        for (int c = 0; c < SEQ_MAX_CHUNKS; c++)
+            e[c] = s.nx[min(c, C - 1) * 64 + ln];
 #pragma unroll
-            for (int a = 0; a < 8; a++) {
-                idx = __builtin_amdgcn_readlane(e[a], idx);
-                flags |= idx;
-            }
-        };
-        load(ea, 0);
+        for (int w = 1; w < SEQ_MAX_CHUNKS; w *= 2) {
 #pragma unroll
-        for (int cb = 0; cb < SEQ_MAX_CHUNKS; cb += 16) {
-            load(eb, cb + 8);
-            __builtin_amdgcn_sched_barrier(0);
-            follow(ea);
-            __builtin_amdgcn_sched_barrier(0);
-            if (cb + 16 < SEQ_MAX_CHUNKS)
-                load(ea, cb + 16);
-            __builtin_amdgcn_sched_barrier(0);
-            follow(eb);
-            __builtin_amdgcn_sched_barrier(0);
+            for (int c = 0; c < SEQ_MAX_CHUNKS; c += 2 * w)
+                e[c] = __builtin_amdgcn_ds_bpermute((e[c] & 63) << 2, e[c + w]) | (e[c] & 0x100);
         }
+        const int idx = __builtin_amdgcn_readfirstlane(e[0]); // the path from lane 0 of chunk 0
+        const int flags = idx;
         int run;
         if (!(flags & 0x100)) {
             run = __builtin_amdgcn_readfirstlane(__float_as_int(s.ends[(C - 1) * 64 + (idx & 63)]));
