@@ -51,8 +51,12 @@ ROUTER_BYTES = N_EXPERT * DIM * 4
 ATTN_W_BYTES = 4_718_592 + 589_824 + 860_160 + 4_718_592  # wq, wk (Q4_K), wv (Q6_K), wo (Q4_K)
 HEAD_BYTES = 151936 * 8 * 210  # Q6_K [151936][2048]
 # Latency of a dependent f32 add on gfx950 (in-kernel clock64 over a chain of
-# adds, the split P.V kernel's probe) and the engine clock it was measured at.
-ADD_LATENCY_CYCLES = 5.75
+# register adds; clock64 against wall_clock64 gave the 2.4 GHz engine clock),
+# and the cycles per position measured for the same chain when each addend
+# arrives from LDS (a ds_read_b128 per four adds: the read's return into the
+# wave's registers costs as much issue time as the adds).
+ADD_LATENCY_CYCLES = 4.7
+LDS_FED_CYCLES = 8.4
 CLOCK_HZ = 2.4e9
 # Largest per-step logit max-rel of FAST numerics against the CPU path at the
 # 4096-token context (32 lanes), measured by the GPU parity test named in the
@@ -179,7 +183,7 @@ def per_launch_bytes(name, b, ctx, distinct):
         return b * P * KVD * 2 + b * N_HEADS * P * 4
     if name == "attn_softmax":  # scores in, p out
         return b * N_HEADS * P * 4 * 2
-    if name == "attn_pv":  # values (fp16) and p in
+    if name == "attn_pv":  # values (fp16) and p in (up to 4 lanes: the scores in, the softmax inside)
         return b * P * KVD * 2 + b * N_HEADS * P * 4
     if name == "head":
         return HEAD_BYTES
@@ -212,9 +216,9 @@ def rocprof_us(tag, b):
     rocprofv3 trace summary of this same benchmark (profiles/
     kernel_durations.json), for the per-lane kernels whose grid z is the lane
     count; None where the table has no entry."""
-    names = {"attn_pv": ("lh::attn_pv_split_kernel<128>" if b <= 4 else
+    names = {"attn_pv": ("lh::attn_pv_split_kernel<128, true>" if b <= 4 else
                          "lh::attn_pv_kernel<128, 2>" if b < 8 else "lh::attn_pv_kernel<128, 4>"),
-             "attn_softmax": "lh::attn_softmax_kernel<1024>" if b <= 4 else "lh::attn_softmax_kernel<256>",
+             "attn_softmax": "lh::attn_softmax_kernel<256>",
              "attn_scores": "lh::attn_scores_kernel<128>",
              "attn": "lh::attn_partial_kernel<128>" if b <= 4 else "lh::attn_direct_kernel<128, 128>"}
     try:
@@ -257,9 +261,12 @@ def roofline(r, b, ctx, layers):
             roof["valu"]["frac_rocprof"] = round(ops / (prof / 1e6) / VALU_LANE_OPS, 4)
         # every output column is one chain of ctx + 1 dependent f32 adds in
         # position order: its latency floors the launch whatever the bytes
+        # (lds_fed_floor_us: the same chain at the cycles per position
+        # measured when the addends come through LDS, as they do here)
         floor_s = (ctx + 1) * ADD_LATENCY_CYCLES / CLOCK_HZ
         roof["chain"] = {"adds_in_order": ctx + 1, "add_latency_cycles": ADD_LATENCY_CYCLES,
                          "clock_GHz": CLOCK_HZ / 1e9, "floor_us": round(floor_s * 1e6, 2),
+                         "lds_fed_floor_us": round((ctx + 1) * LDS_FED_CYCLES / CLOCK_HZ * 1e6, 2),
                          "frac": round(floor_s / avg_s, 4)}
         if prof:
             roof["chain"]["frac_rocprof"] = round(floor_s / (prof / 1e6), 4)
