@@ -8,17 +8,24 @@
 //
 // so the attention output -- and with it the int8 input of wo -- is bit-
 // identical to Loom's CPU path at every context length, which a
-// split-context (flash-decoding) merge is not.  Three launches:
+// split-context (flash-decoding) merge is not.  Up to 4 lanes, two launches:
 //
-//   attn_scores_kernel   per (64 positions, KV head, lane): the group's query
-//                        heads against 64 keys, dotF32 order on the VALU
-//                        (up to 4 lanes it also applies the per-head Q/K
-//                        RMSNorm and RoPE and appends the new K/V row)
-//   attn_softmax_kernel  per (query head, lane): the max, e_t, the position-
-//                        ordered sum, p_t (in place of the scores)
-//   attn_pv_kernel       per (64 value columns, KV head, lane): one lane per
-//                        (head, column) runs o = o + p_t * v_t over the whole
-//                        context from value tiles staged in LDS as f32
+//   attn_scores_kernel    per (64 positions, KV head, lane): the group's query
+//                         heads against 64 keys, dotF32 order on the VALU, with
+//                         the per-head Q/K RMSNorm and RoPE and the K/V append
+//   attn_pv_split_kernel  per (32 value columns, head, lane): the head's
+//                         softmax, then o = o + p_t * v_t position by position
+//                         (a consumer wave fed products by producer waves)
+//
+// and from 5 lanes (after qk_rope_kernel has rotated the queries and appended
+// the rows), three:
+//
+//   attn_scores_many_kernel  per (256 positions, KV head, lane): a thread per
+//                            position, the query elements as scalar operands
+//   attn_softmax_kernel      per (query head, lane): the max, e_t, the
+//                            position-ordered sum, p_t (in place of the scores)
+//   attn_pv_many_kernel      per (64 value columns, KV head, lane): a wave per
+//                            head, lane = column, over value tiles staged in LDS
 //
 // The sequential sum of e_t is a dependent chain of P adds (~5.7 cycles each
 // on gfx950).  It is evaluated by speculative composition instead: the
@@ -37,9 +44,6 @@ namespace lh {
 
 constexpr int SC_THREADS = 512;   // scores: 8 waves
 constexpr int SM_THREADS = 1024;  // softmax: 16 waves
-constexpr int PV_TJ = 64;         // positions per staged value tile
-constexpr int PV_VST = PV_TJ + 4; // f32 row stride of the transposed tile
-constexpr int PV_DEPTH = 2;       // value tiles per register set (two sets; even)
 
 // ---- scores -------------------------------------------------------------------------
 // Work group (chunk of 64 positions, KV head, lane).  All 512 threads load the
@@ -157,6 +161,71 @@ __global__ __launch_bounds__(SC_THREADS) void attn_scores_kernel(
     }
 }
 
+// ---- scores for many lanes ------------------------------------------------------------
+// Work group (256 positions, KV head, lane), one thread per position: the
+// thread loads its key row, converts it to f32 once, and scores it against
+// each query head of the group in turn.  The query elements are wave-uniform
+// and arrive as scalar operands (scalar loads of the rotated queries, which
+// an earlier launch wrote), so the dot's only vector work is dotF32's own
+// multiply and add per element, then its fixed tree.  The first product of
+// each of the 32 accumulators is taken as the accumulator itself instead of
+// 0 + x: the two differ only when x = -0 (0 + -0 = +0), and an accumulator
+// that holds -0 where the reference holds +0 can only change the sign of a
+// zero score -- s = +-0, which softmax reads only through s - m and max,
+// where both zeros give the same e and p.  The new K/V rows were appended by
+// qk_rope_kernel before this launch.
+constexpr int SCM_THREADS = 256;
+
+template <int HD>
+__global__ __launch_bounds__(SCM_THREADS) void attn_scores_many_kernel(FrameDims D, const float *__restrict__ qrot,
+                                                                     const uint16_t *__restrict__ kc,
+                                                                     const int32_t *__restrict__ pos, int li,
+                                                                     float *__restrict__ S, int s_stride) {
+    static_assert(HD % 8 == 0 && HD <= 256, "whole 8-element chunks");
+    constexpr int W32 = HD / 32 * 32; // elements in whole 32-steps; the rest go to accumulators 0..7
+    const int kvh = blockIdx.y, t = blockIdx.z;
+    const int G = D.n_heads / D.n_kv;
+    const int P = min(pos[t], D.ctx - 1) + 1;
+    const int j = blockIdx.x * SCM_THREADS + threadIdx.x;
+    if (blockIdx.x * SCM_THREADS >= P)
+        return;
+    const uint16_t *krow =
+        kc + (((size_t)t * D.n_layers + li) * D.ctx + min(j, P - 1)) * D.kvd + (size_t)kvh * HD;
+    float k[HD];
+#pragma unroll
+    for (int i = 0; i < HD; i += 8) {
+        const uint4 w = *(const uint4 *)(krow + i);
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            k[i + e] = half_bits_to_float(ww[e >> 1] >> (16 * (e & 1)));
+    }
+    const float *qg = qrot + (size_t)t * D.qd + (size_t)kvh * G * HD;
+    float *srow = S + ((size_t)t * D.n_heads + (size_t)kvh * G) * s_stride + j;
+    for (int g = 0; g < G; g++) {
+        const float *q = qg + (size_t)g * HD; // uniform: scalar loads
+        float acc[32];
+#pragma unroll
+        for (int i = 0; i < HD; i++) {
+            const int u = i < W32 ? i % 32 : (i - W32) % 8;
+            const float pr = q[i] * k[i];
+            if (i < 32)
+                acc[u] = pr;
+            else
+                acc[u] = acc[u] + pr;
+        }
+#pragma unroll
+        for (int u = HD < 32 ? HD : 32; u < 32; u++)
+            acc[u] = 0.0f;
+        float s = -0.0f;
+#pragma unroll
+        for (int l = 0; l < 8; l++)
+            s = s + (((acc[l] + acc[8 + l]) + acc[16 + l]) + acc[24 + l]);
+        if (j < P)
+            srow[(size_t)g * s_stride] = s * D.scale;
+    }
+}
+
 // ---- softmax ------------------------------------------------------------------------
 // Work group (query head, lane): the max, e_t, the position-ordered sum of e
 // (the speculative composition), p_t.  NT = 1024 for few lanes (the launch
@@ -174,135 +243,183 @@ __global__ __launch_bounds__(NT) void attn_softmax_kernel(FrameDims D, const int
     softmax_row_exact<NT>(S + ((size_t)t * D.n_heads + h) * s_stride, P, e, redf, seq);
 }
 
-// ---- P.V ----------------------------------------------------------------------------
-// Work group (64 value columns, group of W query heads of one KV head, lane),
-// W waves: wave w runs the chain of head w of the group, lane = column.
-// Value tiles of 64 positions are staged transposed in LDS as f32
-// ([column][position], converted once for the group's heads) with p beside
-// them, double-buffered; the tiles' global loads are requested a group of
-// PV_DEPTH tiles ahead (two register sets), and inside a tile each wave reads
-// its values and p PV_AHEAD 4-position groups ahead of the chain, so the
-// chain (one multiply and one dependent add per position) waits on neither.
-// Positions past the context enter as p = 0, v = 0: o + (+0) = o, as no
-// position at all.  W = 2 puts one wave on each of two SIMDs (few lanes:
-// latency); W = 4 stages each value tile for four heads (many lanes: issue).
-constexpr int PV_AHEAD = 4;
+// ---- P.V for many lanes ----------------------------------------------------------------
+// Work group (64 value columns, up to NW query heads of one KV head, lane),
+// one wave per head, lane = column.  A tile of PVM_TJ positions x 64 columns
+// is staged in LDS once for the group's heads, as position quads: the two
+// dwords of (quad q, column c) hold v[4q..4q+3][c] as f16 pairs, so one
+// 8-byte read per lane brings four positions of its column (consecutive
+// lanes: consecutive 8 bytes, conflict-free).  p of each wave's head is
+// staged beside it and read four positions at a time by a broadcast read.
+// Per position the wave issues the product (fma(p, v, +0) on the f16 value:
+// v_fma_mix) and the dependent add, from a software pipeline whose order the
+// fences keep: at step j the chain adds its product of position j and forms
+// the product of position j + 4, and every fourth step reads the quad three
+// ahead.  The tiles' global loads run PVM_SETS tiles ahead, and every
+// iteration issues the same loads (tiles past the last are staged from
+// clamped addresses and run no chain), so the in-order load counter waits
+// for each set's own loads alone.  The chain stops at position P - 1 exactly
+// (the last tile runs a bounded loop): nothing past the context enters a sum.
+//
+// Measured at 32 lanes x 4096 positions (Qwen3 shapes): 57 us.  The bound is
+// the LDS (per CU and position: 8 waves x (128 B of values + 256 B of p))
+// with the VALU close behind (v_fma_mix issues at about half the rate of an
+// f32 multiply); p by v_readlane, p broadcast by the matrix cores
+// (v_mfma_f32_32x32x1f32 against 1.0), two heads per lane, and the values as
+// f32 with v_mul all measured slower.
+constexpr int PVM_TJ = 128;        // positions per tile
+constexpr int PVM_Q = PVM_TJ / 4;  // position quads per tile
+constexpr int PVM_RS = 2 * 64 + 4; // dwords per quad row (64 columns x 2, padded)
+constexpr int PVM_SETS = 3;        // tiles of loads in flight (register sets)
+constexpr int PVM_AH = 3;          // quads read ahead of the chain
 
-template <int HD, int W>
-__global__ __launch_bounds__(64 * W) void attn_pv_kernel(FrameDims D, const uint16_t *__restrict__ vc,
-                                                         const int32_t *__restrict__ pos, int li,
-                                                         const float *__restrict__ Pm, int s_stride,
-                                                         float *__restrict__ att) {
-    constexpr int NT = 64 * W;
-    constexpr int VPT = 512 / NT;                // 16-byte value pieces per thread per tile
-    constexpr int PPT = (16 * W + NT - 1) / NT;  // p float4 pieces per thread per tile
-    __shared__ __align__(16) float vt[2][64 * PV_VST];
-    __shared__ __align__(16) float pt[2][W * PV_TJ];
-    const int G = D.n_heads / D.n_kv, n_hg = (G + W - 1) / W;
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_pv_many_kernel(FrameDims D, const uint16_t *__restrict__ vc,
+                                                               const int32_t *__restrict__ pos, int li,
+                                                               const float *__restrict__ Pm, int s_stride,
+                                                               float *__restrict__ att) {
+    constexpr int NT = 64 * NW;
+    constexpr int ITEMS = PVM_Q * 8;           // (quad, column octet) items per tile
+    constexpr int IPT = (ITEMS + NT - 1) / NT; // items per thread
+    __shared__ __align__(16) uint32_t vt[2][PVM_Q * PVM_RS];
+    __shared__ __align__(16) float pt[2][NW][PVM_TJ];
+    const int G = D.n_heads / D.n_kv;
+    const int n_hg = (G + NW - 1) / NW;
     const int sl = blockIdx.x, kvh = blockIdx.y / n_hg, hg = blockIdx.y % n_hg, t = blockIdx.z;
-    const int tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
+    const int tid = threadIdx.x, ln = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int P = min(pos[t], D.ctx - 1) + 1;
-    const int ntile = (P + PV_TJ - 1) / PV_TJ;
+    const int ntile = (P + PVM_TJ - 1) / PVM_TJ;
     const int c0 = sl * 64, ncol = min(64, HD - c0);
-    const int g = hg * W + wave; // this wave's query head within the KV group
-    const uint16_t *vbase = vc + (((size_t)t * D.n_layers + li) * D.ctx) * D.kvd + (size_t)kvh * HD + c0;
-    const float *pbase = Pm + ((size_t)t * D.n_heads + (size_t)kvh * G) * s_stride;
-    // Every load is unconditional, from an address clamped into range (the
-    // context, the value columns, the group's heads), so the compiler counts
-    // them and waits for each tile's own loads only; what lies past the
-    // context is zeroed when the tile is staged.
-    auto load = [&](int tile, uint4 (&vr)[VPT], float4 (&pr)[PPT]) {
-#pragma unroll
-        for (int u = 0; u < VPT; u++) {
-            const int i = tid + NT * u, r = i & 63, cg = i >> 6;
-            const int j = min(tile * PV_TJ + r, P - 1);
-            vr[u] = *(const uint4 *)(vbase + (size_t)j * D.kvd + (8 * cg < ncol ? 8 * cg : 0));
-        }
-#pragma unroll
-        for (int u = 0; u < PPT; u++) {
-            const int i = min(tid + NT * u, 16 * W - 1), ph = min(hg * W + (i >> 4), G - 1), q4 = i & 15;
-            pr[u] = *(const float4 *)(pbase + (size_t)ph * s_stride + (size_t)min(tile, ntile - 1) * PV_TJ + 4 * q4);
-        }
+    const int g = hg * NW + wave; // the wave's head within the KV group
+    const char *vb = (const char *)(vc + (((size_t)t * D.n_layers + li) * D.ctx) * D.kvd + (size_t)kvh * HD + c0);
+    const uint32_t rowb = (uint32_t)D.kvd * 2;
+    // a wave past the group's last head runs on a clamped p row and stores nothing
+    const float *prow = Pm + ((size_t)t * D.n_heads + (size_t)kvh * G + min(g, G - 1)) * s_stride;
+
+    struct Set {
+        uint4 v[IPT][4];
+        float p[2];
     };
-    auto stage = [&](int buf, int tile, const uint4 (&vr)[VPT], const float4 (&pr)[PPT]) {
+    // Every load is unconditional from a clamped address (rows to P - 1,
+    // column octets to the head's last, p to the row's end).
+    auto load = [&](int tile, Set &s) {
 #pragma unroll
-        for (int u = 0; u < VPT; u++) {
-            const int i = tid + NT * u, r = i & 63, cg = i >> 6;
-            const bool in = tile * PV_TJ + r < P;
-            const uint32_t w4[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
+        for (int u = 0; u < IPT; u++) {
+            const int i = min(tid + NT * u, ITEMS - 1), q = i >> 3, cg = min(i & 7, ncol / 8 - 1);
 #pragma unroll
-            for (int k = 0; k < 8; k++)
-                vt[buf][(8 * cg + k) * PV_VST + r] = half_bits_to_float((uint16_t)(w4[k >> 1] >> (16 * (k & 1))));
+            for (int r = 0; r < 4; r++) {
+                const int row = min(tile * PVM_TJ + 4 * q + r, P - 1);
+                s.v[u][r] = *(const uint4 *)(vb + (size_t)row * rowb + 16 * cg);
+            }
         }
 #pragma unroll
-        for (int u = 0; u < PPT; u++) {
+        for (int k = 0; k < 2; k++)
+            s.p[k] = prow[min(tile * PVM_TJ + 64 * k + ln, s_stride - 1)];
+    };
+    auto stage = [&](int buf, const Set &s) {
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+            pt[buf][wave][64 * k + ln] = s.p[k];
+#pragma unroll
+        for (int u = 0; u < IPT; u++) {
             const int i = tid + NT * u;
-            if (i < 16 * W) {
-                const int ph = i >> 4, q4 = i & 15, jp = tile * PV_TJ + 4 * q4;
-                float4 q = pr[u];
-                q.x = jp < P ? q.x : 0.0f;
-                q.y = jp + 1 < P ? q.y : 0.0f;
-                q.z = jp + 2 < P ? q.z : 0.0f;
-                q.w = jp + 3 < P ? q.w : 0.0f;
-                *(float4 *)(&pt[buf][ph * PV_TJ + 4 * q4]) = q;
+            if (ITEMS % NT == 0 || i < ITEMS) {
+                const int q = i >> 3, cg = i & 7;
+                const uint32_t r0[4] = {s.v[u][0].x, s.v[u][0].y, s.v[u][0].z, s.v[u][0].w};
+                const uint32_t r1[4] = {s.v[u][1].x, s.v[u][1].y, s.v[u][1].z, s.v[u][1].w};
+                const uint32_t r2[4] = {s.v[u][2].x, s.v[u][2].y, s.v[u][2].z, s.v[u][2].w};
+                const uint32_t r3[4] = {s.v[u][3].x, s.v[u][3].y, s.v[u][3].z, s.v[u][3].w};
+#pragma unroll
+                for (int m = 0; m < 4; m++) { // columns 8 cg + 2m (low halves) and + 1 (high halves)
+                    uint4 w;
+                    w.x = __builtin_amdgcn_perm(r1[m], r0[m], 0x05040100u);
+                    w.y = __builtin_amdgcn_perm(r3[m], r2[m], 0x05040100u);
+                    w.z = __builtin_amdgcn_perm(r1[m], r0[m], 0x07060302u);
+                    w.w = __builtin_amdgcn_perm(r3[m], r2[m], 0x07060302u);
+                    *(uint4 *)&vt[buf][q * PVM_RS + 16 * cg + 4 * m] = w;
+                }
             }
         }
     };
     float o = 0.0f;
-    auto group = [&](int tb, uint4 (&vr)[PV_DEPTH][VPT], float4 (&pr)[PV_DEPTH][PPT]) {
+    auto compute = [&](int buf, int tile) {
+        const uint32_t *src = &vt[buf][2 * ln];
+        const float *pw = pt[buf][wave];
+        const int nk = min(PVM_TJ, P - tile * PVM_TJ);
+        if (nk == PVM_TJ) {
+            uint2 w[PVM_AH + 1];
+            float4 pq[PVM_AH + 1];
 #pragma unroll
-        for (int d = 0; d < PV_DEPTH; d++) {
-            const int tile = tb + d, buf = d & 1; // tb is a multiple of PV_DEPTH (even)
-            stage(buf, tile, vr[d], pr[d]);
-            __syncthreads();
-            if (g < G && tile < ntile) { // tiles past the context skip their chain
-                const float *vv = &vt[buf][ln * PV_VST];
-                const float *pv = &pt[buf][wave * PV_TJ];
-                float4 xr[PV_AHEAD], prr[PV_AHEAD];
+            for (int q = 0; q < PVM_AH; q++) {
+                w[q] = *(const uint2 *)(src + q * PVM_RS);
+                pq[q] = *(const float4 *)(pw + 4 * q);
+            }
+            auto vval = [&](int j) {
+                const uint2 &x = w[(j >> 2) % (PVM_AH + 1)];
+                return half_bits_to_float(((j & 2) ? x.y : x.x) >> (16 * (j & 1)));
+            };
+            auto pval = [&](int j) {
+                const float4 &x = pq[(j >> 2) % (PVM_AH + 1)];
+                return (j & 3) == 0 ? x.x : (j & 3) == 1 ? x.y : (j & 3) == 2 ? x.z : x.w;
+            };
+            float xp[4];
 #pragma unroll
-                for (int a = 0; a < PV_AHEAD; a++) {
-                    xr[a] = *(const float4 *)(vv + 4 * a);
-                    prr[a] = *(const float4 *)(pv + 4 * a);
+            for (int j = 0; j < 4; j++)
+                xp[j] = __builtin_fmaf(pval(j), vval(j), 0.0f);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < PVM_TJ; j++) {
+                if ((j & 3) == 0 && j / 4 + PVM_AH < PVM_Q) {
+                    const int q = j / 4 + PVM_AH;
+                    w[q % (PVM_AH + 1)] = *(const uint2 *)(src + q * PVM_RS);
+                    pq[q % (PVM_AH + 1)] = *(const float4 *)(pw + 4 * q);
                 }
-#pragma unroll
-                for (int gj = 0; gj < PV_TJ / 4; gj++) {
-                    const int a = gj % PV_AHEAD;
-                    const float4 x = xr[a], pp = prr[a];
-                    if (gj + PV_AHEAD < PV_TJ / 4) {
-                        xr[a] = *(const float4 *)(vv + 4 * (gj + PV_AHEAD));
-                        prr[a] = *(const float4 *)(pv + 4 * (gj + PV_AHEAD));
-                    }
-                    float q;
-                    q = pp.x * x.x;
-                    o = o + q;
-                    q = pp.y * x.y;
-                    o = o + q;
-                    q = pp.z * x.z;
-                    o = o + q;
-                    q = pp.w * x.w;
-                    o = o + q;
-                }
+                o = o + xp[j & 3];
+                if (j + 4 < PVM_TJ)
+                    xp[j & 3] = __builtin_fmaf(pval(j + 4), vval(j + 4), 0.0f);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            for (int j = 0; j < nk; j++) {
+                const uint32_t w = src[(j >> 2) * PVM_RS + ((j >> 1) & 1)];
+                const float x = __builtin_fmaf(pw[j], half_bits_to_float(w >> (16 * (j & 1))), 0.0f);
+                o = o + x;
             }
         }
     };
-    uint4 va[PV_DEPTH][VPT], vb[PV_DEPTH][VPT];
-    float4 pa[PV_DEPTH][PPT], pb[PV_DEPTH][PPT];
+    Set s[PVM_SETS];
+    // the sets' loads are issued in set order (the fences keep them there),
+    // so that each set's wait leaves the later sets' loads in flight
 #pragma unroll
-    for (int d = 0; d < PV_DEPTH; d++)
-        load(d, va[d], pa[d]);
-    for (int tb = 0; tb < ntile; tb += 2 * PV_DEPTH) {
-#pragma unroll
-        for (int d = 0; d < PV_DEPTH; d++)
-            load(tb + PV_DEPTH + d, vb[d], pb[d]);
-        group(tb, va, pa);
-        if (tb + PV_DEPTH >= ntile)
-            break;
-#pragma unroll
-        for (int d = 0; d < PV_DEPTH; d++)
-            load(tb + 2 * PV_DEPTH + d, va[d], pa[d]);
-        group(tb + PV_DEPTH, vb, pb);
+    for (int d = 0; d < PVM_SETS; d++) {
+        load(d, s[d]);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    if (g < G && ln < ncol)
+    stage(0, s[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    load(PVM_SETS, s[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    // iteration k: tile k + 1 is staged from set (k + 1) % SETS into buffer
+    // (k + 1) & 1 and that set reloaded with tile k + 1 + SETS; tile k's
+    // chains run from buffer k & 1; one barrier per tile.  The loop runs
+    // whole register sets.
+    const int ntp = (ntile + PVM_SETS - 1) / PVM_SETS * PVM_SETS;
+    for (int kb = 0; kb < ntp; kb += PVM_SETS) {
+#pragma unroll
+        for (int d = 0; d < PVM_SETS; d++) {
+            const int k = kb + d, nxt = (d + 1) % PVM_SETS;
+            stage((k + 1) & 1, s[nxt]);
+            __builtin_amdgcn_sched_barrier(0);
+            load(k + 1 + PVM_SETS, s[nxt]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k < ntile)
+                compute(k & 1, k);
+            lds_barrier();
+        }
+    }
+    if (ln < ncol && g < G)
         att[(size_t)t * D.qd + ((size_t)kvh * G + g) * HD + c0 + ln] = o;
 }
 
@@ -591,8 +708,12 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
     const int n_chunks = (D.ctx + ATT_TC - 1) / ATT_TC;
     const int G = D.n_heads / D.n_kv;
     int ph = prof_begin(LOOMHIP_KT_ATTN_SCORES, st);
-    hipLaunchKernelGGL(attn_scores_kernel<HD>, dim3(n_chunks, D.n_kv, n), dim3(SC_THREADS), 0, st, D, q, k, v,
-                       q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse ? 1 : 0, S, s_stride);
+    if (!fuse) // the rotated queries and the appended rows come from qk_rope_kernel
+        hipLaunchKernelGGL(attn_scores_many_kernel<HD>, dim3((D.ctx + SCM_THREADS - 1) / SCM_THREADS, D.n_kv, n),
+                           dim3(SCM_THREADS), 0, st, D, q, kc, pos, li, S, s_stride);
+    else
+        hipLaunchKernelGGL(attn_scores_kernel<HD>, dim3(n_chunks, D.n_kv, n), dim3(SC_THREADS), 0, st, D, q, k, v,
+                           q_norm, k_norm, rope_cs, kc, vc, pos, li, fuse ? 1 : 0, S, s_stride);
     prof_end(ph, st);
     if (n > 4) {
         ph = prof_begin(LOOMHIP_KT_ATTN_SOFTMAX, st);
@@ -606,12 +727,18 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
         const dim3 pg(((HD + PVS_COLS - 1) / PVS_COLS) * D.n_heads, 1, n);
         hipLaunchKernelGGL((attn_pv_split_kernel<HD, true>), pg, dim3(64 * PVS_SM_WAVES), pv_softmax_lds(s_stride),
                            st, D, vc, pos, li, S, s_stride, att, qwt, qa, g_ctx.sync);
-    } else if (n < 8) {
-        const dim3 pg((HD + 63) / 64, D.n_kv * ((G + 1) / 2), n);
-        hipLaunchKernelGGL((attn_pv_kernel<HD, 2>), pg, dim3(128), 0, st, D, vc, pos, li, S, s_stride, att);
     } else {
-        const dim3 pg((HD + 63) / 64, D.n_kv * ((G + 3) / 4), n);
-        hipLaunchKernelGGL((attn_pv_kernel<HD, 4>), pg, dim3(256), 0, st, D, vc, pos, li, S, s_stride, att);
+        // one wave per head of the KV group (up to 8 per group)
+        const int nw = G >= 8 ? 8 : G >= 4 ? 4 : G >= 2 ? 2 : 1;
+        const dim3 pg((HD + 63) / 64, D.n_kv * ((G + nw - 1) / nw), n);
+        if (nw == 8)
+            hipLaunchKernelGGL((attn_pv_many_kernel<HD, 8>), pg, dim3(512), 0, st, D, vc, pos, li, S, s_stride, att);
+        else if (nw == 4)
+            hipLaunchKernelGGL((attn_pv_many_kernel<HD, 4>), pg, dim3(256), 0, st, D, vc, pos, li, S, s_stride, att);
+        else if (nw == 2)
+            hipLaunchKernelGGL((attn_pv_many_kernel<HD, 2>), pg, dim3(128), 0, st, D, vc, pos, li, S, s_stride, att);
+        else
+            hipLaunchKernelGGL((attn_pv_many_kernel<HD, 1>), pg, dim3(64), 0, st, D, vc, pos, li, S, s_stride, att);
     }
     prof_end(ph, st);
     note_launch();

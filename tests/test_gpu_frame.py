@@ -222,6 +222,27 @@ def test_qwen3moe_frame_batch(lh, oracle, n, numerics):
         assert same
 
 
+@pytest.mark.parametrize("heads", [(6, 6, 48), (8, 4, 64), (16, 4, 64)])
+def test_llama_frame_batch_head_layouts(lh, oracle, heads):
+    """PARITY at 5 lanes over a 200-position prefilled context (a whole
+    128-position value tile and a partial one) for head layouts the Qwen3
+    tests do not reach: 1, 2 and 4 query heads per KV head, head sizes 48
+    and 64 -- the many-lane scores and P.V kernels at each work-group shape
+    they take.  Per-lane logits against lo_decode_batch on identical state,
+    identical greedy tokens."""
+    import dataclasses
+
+    n_heads, n_kv, hd = heads
+    spec = dataclasses.replace(lh.stories15m(ctx_len=224), n_layers=2, vocab=4096, n_heads=n_heads,
+                               n_kv_heads=n_kv, head_dim=hd, rope_dim=hd)
+    dm = lh.DeviceModel.synth(spec, seed=21, keep_ggml=True)
+    om = OracleModel(oracle, dm)
+    rels, same = _batch_steps(lh, om, dm, 5, 3, 200, seed=hd + n_heads)
+    print(f"heads {heads}: max-rel {rels.max():.2e}")
+    _check(rels, "parity")
+    assert same
+
+
 @pytest.mark.parametrize("numerics", ["parity", "fast"])
 @pytest.mark.parametrize("n", [1, 32])
 def test_qwen3moe_frame_4096_context(lh, oracle, n, numerics):
