@@ -216,10 +216,9 @@ def rocprof_us(tag, b):
     rocprofv3 trace summary of this same benchmark (profiles/
     kernel_durations.json), for the per-lane kernels whose grid z is the lane
     count; None where the table has no entry."""
-    names = {"attn_pv": ("lh::attn_pv_split_kernel<128, true>" if b <= 4 else
-                         "lh::attn_pv_kernel<128, 2>" if b < 8 else "lh::attn_pv_kernel<128, 4>"),
+    names = {"attn_pv": "lh::attn_pv_split_kernel<128, true>" if b <= 4 else "lh::attn_pv_many_kernel<128, 8>",
              "attn_softmax": "lh::attn_softmax_kernel<256>",
-             "attn_scores": "lh::attn_scores_kernel<128>",
+             "attn_scores": "lh::attn_scores_kernel<128>" if b <= 4 else "lh::attn_scores_many_kernel<128>",
              "attn": "lh::attn_partial_kernel<128>" if b <= 4 else "lh::attn_direct_kernel<128, 128>"}
     try:
         with open(os.path.join(ROOT, "profiles", "kernel_durations.json")) as f:

@@ -203,10 +203,13 @@ _KERNEL_SYMBOLS = {
     "head": "dmmv_kernel<T, NT, false> / from 16 lanes mmq_stream_kernel<T, MT, false> (output head)",
     "qkv": "dmmv_seg_kernel<NT> / from 16 lanes mmq_seg_kernel<1, SBW> (q, k, v in one launch)",
     "wo": "dmmv_kernel<T, NT, false> / from 16 lanes mmq_kernel<T, 1, false, SBW> (wo + residual)",
-    "attn_scores": "attn_scores_kernel<HD> (PARITY: dotF32-order scores)",
+    "attn_scores": "attn_scores_kernel<HD> (PARITY, up to 4 lanes: dotF32-order scores with the q/k norm, rope and "
+                   "K/V append) / attn_scores_many_kernel<HD> (more lanes: a thread per position, query elements "
+                   "as scalar operands)",
     "attn_softmax": "attn_softmax_kernel<256> (PARITY, more than 4 lanes: max, exp, position-ordered sum, p)",
     "attn_pv": "attn_pv_split_kernel<HD, true> (PARITY, up to 4 lanes: the head's softmax, then position-ordered "
-               "P.V, and wo's input quantized) / attn_pv_kernel<HD, W> (more lanes: position-ordered P.V)",
+               "P.V, and wo's input quantized) / attn_pv_many_kernel<HD, NW> (more lanes: position-ordered P.V, a "
+               "wave per head over position-quad value tiles)",
     "mla_absorb": "mla_absorb_kernel (MLA: qa = W_k^T q_nope in axpy order)",
     "mla_scores": "mla_scores_kernel (MLA: dotF32-order scores over the compressed cache)",
     "mla_softmax": "mla_softmax_kernel<1024> (MLA: max, exp, position-ordered sum, p)",

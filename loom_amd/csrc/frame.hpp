@@ -165,11 +165,12 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
     if (j0 < n64 && j0 % L == 0)
         s.fst[j0 / L] = __float_as_uint((float)ex);
     __syncthreads();
-    // 2. every chunk's chain from 64 starts around its estimate: blocks of 64
-    //    values (16 float4 groups, unrolled), read eight groups ahead at
-    //    immediate offsets from the block's base, one wait per two groups.
-    //    Past the chunk's last block the ring re-reads that block (in range,
-    //    never added).
+    // 2. every chunk's chain from 64 starts around its estimate (below).
+    //    chain(r, c) is chunk c's chain from the one start r, for the serial
+    //    fallback of step 3: blocks of 64 values (16 float4 groups, unrolled),
+    //    read eight groups ahead at immediate offsets from the block's base,
+    //    one wait per two groups.  Past the chunk's last block the ring
+    //    re-reads that block (in range, never added).
     auto chain = [&](float r, int c) {
         constexpr int AH = NW >= 16 ? 4 : 8; // 1024-thread callers keep rows in registers across the sum
         static_assert(16 % AH == 0 && AH % 2 == 0, "the ring wraps at block boundaries, two groups a wait");
@@ -205,12 +206,49 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
         }
         return r;
     };
-    for (int c = wave; c < C; c += NW) {
-        const int b = c == 0 ? 0 : max((int)s.fst[c] + ln - 32, 0);
-        const float r = chain(__uint_as_float((uint32_t)b), c);
-        s.ends[c * 64 + ln] = r;
-        const int n = c + 1 < C ? __float_as_int(r) - (int)s.fst[c + 1] + 32 : ln; // the last: itself
-        s.nx[c * 64 + ln] = (unsigned)n < 64u ? n : 0x100 | (n & 63);
+    // Lane (quarter qc, slot sl) of a wave runs the four starts 4 sl .. 4 sl + 3
+    // of chunk 4 k + qc, so one LDS read (the same address across its
+    // quarter) feeds four chains: a quarter of the LDS traffic of one start
+    // per lane, and four independent adds per value.
+    {
+        const int qc = ln >> 4, sl = ln & 15;
+        for (int cb = 4 * wave; cb < C; cb += 4 * NW) {
+            const int c = min(cb + qc, C - 1); // quarters past the last chunk repeat it and store nothing
+            const int nb = min(L, n64 - c * L) / 64;
+            const float4 *src = (const float4 *)(v + c * L);
+            float r[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                r[k] = c == 0 ? 0.0f : __uint_as_float((uint32_t)max((int)s.fst[c] + 4 * sl + k - 32, 0));
+            for (int bk = 0; bk < nb; bk++) {
+                const float4 *blk = src + 16 * bk;
+#pragma unroll
+                for (int g = 0; g < 16; g++) {
+                    const float4 x = blk[g];
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+                        r[k] = r[k] + x.x;
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+                        r[k] = r[k] + x.y;
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+                        r[k] = r[k] + x.z;
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+                        r[k] = r[k] + x.w;
+                }
+            }
+            if (cb + qc < C) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int i = 4 * sl + k;
+                    s.ends[c * 64 + i] = r[k];
+                    const int n = c + 1 < C ? __float_as_int(r[k]) - (int)s.fst[c + 1] + 32 : i; // the last: itself
+                    s.nx[c * 64 + i] = (unsigned)n < 64u ? n : 0x100 | (n & 63);
+                }
+            }
+        }
     }
     __syncthreads();
     // 3. the exact running sum through the chunks: lane i of chunk c has
@@ -262,19 +300,32 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
 // one softmax launch per (head, lane), one P.V launch per (64 columns, KV
 // head, lane).  S is [n][n_heads][s_stride] f32 (scores, then p in place),
 // att the f32 attention output [n][n_heads * head_dim].
+constexpr int EXACT_MAX_CTX = 7936; // the softmax's e[] and the sequential sum's LDS in 64 KB
+
 // softmax (tensor.zig:18-28) of one row of P scores in place, in the
 // reference's order: m = max (order-free), e_t = exp(s_t - m) rounded once
 // from a double exponential (the polynomial form: this loop is exp's heaviest
 // user), the position-ordered sum of e (speculative composition, exact),
 // p_t = e_t * (1 / sum).  e holds 64 * ceil(P / 64) floats of LDS (positions
 // past P read +0); all NT threads of the work group call it.
+
 template <int NT>
 __device__ __forceinline__ void softmax_row_exact(float *row, int P, float *e, float *redf, SeqSumLds &seq) {
+    // the row is read once, every load issued before the first use (a loop
+    // over P would wait out one memory round trip per iteration)
+    constexpr int NV = (EXACT_MAX_CTX + NT - 1) / NT;
     const int tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
     const int C = (P + 63) / 64;
+    float sv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int j = tid + NT * k;
+        sv[k] = j < P ? row[j] : -INFINITY;
+    }
     float m = -INFINITY;
-    for (int j = tid; j < P; j += NT)
-        m = fmaxf(m, row[j]);
+#pragma unroll
+    for (int k = 0; k < NV; k++)
+        m = fmaxf(m, sv[k]);
     m = wave_max(m);
     if (ln == 0)
         redf[wave] = m;
@@ -282,15 +333,18 @@ __device__ __forceinline__ void softmax_row_exact(float *row, int P, float *e, f
     m = redf[0];
     for (int w = 1; w < NT / 64; w++)
         m = fmaxf(m, redf[w]);
-    for (int j = tid; j < 64 * C; j += NT)
-        e[j] = j < P ? exp_f32_poly(row[j] - m) : 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int j = tid + NT * k;
+        if (j < 64 * C)
+            e[j] = j < P ? exp_f32_poly(sv[k] - m) : 0.0f;
+    }
     __syncthreads();
     const float inv = 1.0f / seq_sum_nonneg<NT / 64>(e, P, seq);
     for (int j = tid; j < P; j += NT)
         row[j] = e[j] * inv;
 }
 
-constexpr int EXACT_MAX_CTX = 7936; // the softmax's e[] and the sequential sum's LDS in 64 KB
 size_t exact_softmax_lds(int s_stride);
 // qwt >= 0 (attn_exact_quant_fusable): P.V also quantizes att into qa for a
 // weight of type qwt, in place of a quantizer launch.
