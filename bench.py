@@ -92,6 +92,7 @@ def parse():
     ap.add_argument("--mla", action="store_true",
                     help="config 5's MLA attention alone: 61 layers at contexts 1024, 2048, 4096")
     ap.add_argument("--mla-ctx", default="1024,2048,4096", help="contexts of the --mla run")
+    ap.add_argument("--sweep-rounds", type=int, default=5, help="rounds over each weight ring in --sweep")
     ap.add_argument("--no-mla", action="store_true", help="skip the MLA attention run of the default bench")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="first copy MB megabytes device to device three times: the known-size kernel that "
@@ -392,7 +393,7 @@ def bench_sweep(args):
                     be.matvec_dev(t, out, pl, x, n, rows, cols)
                 torch.cuda.synchronize()
                 rounds = []
-                for _ in range(5):
+                for _ in range(max(1, args.sweep_rounds)):
                     be.profileKernels(True)
                     for pl in planes:
                         be.matvec_dev(t, out, pl, x, n, rows, cols)
@@ -922,10 +923,6 @@ def main():
                 "data": "synthetic", "dtype": "f32", **bench_mla(args, tuple(int(v) for v in args.mla_ctx.split(",") if v), cpu=not args.no_cpu)}
         print(json.dumps(line), flush=True)
         return
-    if args.sweep or args.moe_layer:
-        line = bench_sweep(args) if args.sweep else bench_moe_layer(args)
-        print(json.dumps(line), flush=True)
-        return
     if args.copy_probe:
         src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device="cuda").fill_(1)
         dst = torch.empty_like(src)
@@ -934,6 +931,10 @@ def main():
         torch.cuda.synchronize()
         log(f"copy probe: 3 x {args.copy_probe} MB device to device")
         del src, dst
+    if args.sweep or args.moe_layer:
+        line = bench_sweep(args) if args.sweep else bench_moe_layer(args)
+        print(json.dumps(line), flush=True)
+        return
     batches = [int(v) for v in args.batch.split(",") if v]
     spec = qwen3_30b_a3b(ctx_len=args.ctx + 2 * args.warmup + args.steps + 64, n_layers=args.layers)
     t0 = time.perf_counter()
