@@ -218,7 +218,7 @@ def rocprof_us(tag, b):
     kernel_durations.json), for the per-lane kernels whose grid z is the lane
     count; None where the table has no entry."""
     names = {"attn_pv": "lh::attn_pv_split_kernel<128, true>" if b <= 4 else "lh::attn_pv_many_kernel<128, 8>",
-             "attn_softmax": "lh::attn_softmax_kernel<256>",
+             "attn_softmax": "lh::attn_softmax_kernel<512>",
              "attn_scores": "lh::attn_scores_kernel<128>" if b <= 4 else "lh::attn_scores_many_kernel<128>",
              "attn": "lh::attn_partial_kernel<128>" if b <= 4 else "lh::attn_direct_kernel<128, 128>"}
     try:

@@ -206,7 +206,7 @@ _KERNEL_SYMBOLS = {
     "attn_scores": "attn_scores_kernel<HD> (PARITY, up to 4 lanes: dotF32-order scores with the q/k norm, rope and "
                    "K/V append) / attn_scores_many_kernel<HD> (more lanes: a thread per position, query elements "
                    "as scalar operands)",
-    "attn_softmax": "attn_softmax_kernel<256> (PARITY, more than 4 lanes: max, exp, position-ordered sum, p)",
+    "attn_softmax": "attn_softmax_kernel<512> (PARITY, more than 4 lanes: max, exp, position-ordered sum, p)",
     "attn_pv": "attn_pv_split_kernel<HD, true> (PARITY, up to 4 lanes: the head's softmax, then position-ordered "
                "P.V, and wo's input quantized) / attn_pv_many_kernel<HD, NW> (more lanes: position-ordered P.V, a "
                "wave per head over position-quad value tiles)",

@@ -228,12 +228,13 @@ __global__ __launch_bounds__(SCM_THREADS) void attn_scores_many_kernel(FrameDims
 
 // ---- softmax ------------------------------------------------------------------------
 // Work group (query head, lane): the max, e_t, the position-ordered sum of e
-// (the speculative composition), p_t.  NT = 1024 for few lanes (the launch
-// has few groups, and each group's latency is the step's); 256 for many, so
-// that four groups share a CU and the whole launch runs in one round.
+// (the speculative composition), p_t.  The many-lane launch runs NT = 512:
+// at 64 registers (eight waves per SIMD) four groups share a CU, so 32 lanes
+// x 32 heads run in one round, and eight waves take the sum's chunk chains
+// in one pass.
 
 template <int NT>
-__global__ __launch_bounds__(NT) void attn_softmax_kernel(FrameDims D, const int32_t *__restrict__ pos,
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void attn_softmax_kernel(FrameDims D, const int32_t *__restrict__ pos,
                                                           float *__restrict__ S, int s_stride) {
     extern __shared__ __align__(16) float e[]; // e[s_stride]
     __shared__ float redf[NT / 64];
@@ -717,7 +718,7 @@ static void launch_hd(const FrameDims &D, const float *q, const float *k, const 
     prof_end(ph, st);
     if (n > 4) {
         ph = prof_begin(LOOMHIP_KT_ATTN_SOFTMAX, st);
-        hipLaunchKernelGGL((attn_softmax_kernel<256>), dim3(D.n_heads, 1, n), dim3(256), exact_softmax_lds(s_stride),
+        hipLaunchKernelGGL((attn_softmax_kernel<512>), dim3(D.n_heads, 1, n), dim3(512), exact_softmax_lds(s_stride),
                            st, D, pos, S, s_stride);
         prof_end(ph, st);
         note_launch();
