@@ -241,6 +241,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void at
     __shared__ SeqSumLds seq;
     const int h = blockIdx.x, t = blockIdx.z;
     const int P = min(pos[t], D.ctx - 1) + 1;
+    if (P <= 0) // a lane at a negative position has no scores (the whole group leaves)
+        return;
     softmax_row_exact<NT>(S + ((size_t)t * D.n_heads + h) * s_stride, P, e, redf, seq);
 }
 
@@ -293,6 +295,11 @@ __global__ __launch_bounds__(64 * NW) void attn_pv_many_kernel(FrameDims D, cons
     const int ntile = (P + PVM_TJ - 1) / PVM_TJ;
     const int c0 = sl * 64, ncol = min(64, HD - c0);
     const int g = hg * NW + wave; // the wave's head within the KV group
+    if (P <= 0) { // a lane at a negative position has no context: +0 out, no loads
+        if (ln < ncol && g < G)
+            att[(size_t)t * D.qd + ((size_t)kvh * G + g) * HD + c0 + ln] = 0.0f;
+        return;
+    }
     const char *vb = (const char *)(vc + (((size_t)t * D.n_layers + li) * D.ctx) * D.kvd + (size_t)kvh * HD + c0);
     const uint32_t rowb = (uint32_t)D.kvd * 2;
     // a wave past the group's last head runs on a clamped p row and stores nothing
