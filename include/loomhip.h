@@ -436,8 +436,10 @@ typedef struct {
 int loomhip_gguf_get_info(const loomhip_gguf *g, loomhip_gguf_info *info);
 /* Tensor i (gguf.zig:36-47 TensorInfo): dims[0] is the row length (unused
  * dims read 1); nbytes is its GGML size for F32/F16/Q4_0/Q8_0/Q4_K/Q6_K (0
- * for other types), data its bytes in the mapping (NULL when unknown or
- * outside the file). */
+ * for other types and for a size that overflows 64 bits, every product
+ * checked as ggml.zig:143-153 tensorBytesChecked does), data its bytes in
+ * the mapping (NULL when unknown or outside the file, the offset sum
+ * checked too). */
 typedef struct {
     const char *name;
     uint32_t n_dims;

@@ -510,6 +510,26 @@ __global__ __launch_bounds__(SM ? 64 * PVS_SM_WAVES : 64 * (1 + PVS_NP)) void at
     const int ntp = (ntile + PVS_SETS - 1) / PVS_SETS * PVS_SETS; // tiles the loops run (padded)
     const int c0 = sl * PVS_COLS, ncol = min(PVS_COLS, HD - c0);
     const float *prow = Pm + ((size_t)t * D.n_heads + h) * s_stride; // p (SM: the scores)
+    // the consumer's end: its column's o out, and with a fused quantization
+    // the item's arrival (the last of its eight groups quantizes it)
+    auto finish = [&](float o) {
+        float *dst = att + (size_t)t * D.qd + (size_t)h * HD + c0 + ln;
+        if (qwt < 0) {
+            if (ln < ncol)
+                *dst = o;
+        } else {
+            if (ln < ncol)
+                st_dev(dst, o);
+            const int it = (h * HD + c0) / 256;
+            if (last_arrival_wave(sync + SYNC_PV_QUANT + t * 64 + it, 256 / PVS_COLS))
+                quant_item_wave<true>(qwt, att + (size_t)t * D.qd, D.qd, t, it, qa);
+        }
+    };
+    if (P <= 0) { // a lane at a negative position has no context: +0 out, no
+        if (wave == 0) // loads, no softmax; the arrival still counts
+            finish(0.0f);
+        return;      // (P is uniform over the group: every wave leaves here)
+    }
 
     // ---- the producers' value tiles (declared here: SM issues the first
     // loads before the softmax) ----
@@ -636,17 +656,7 @@ __global__ __launch_bounds__(SM ? 64 * PVS_SM_WAVES : 64 * (1 + PVS_NP)) void at
             __asm__ volatile("s_barrier" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
         }
-        float *dst = att + (size_t)t * D.qd + (size_t)h * HD + c0 + ln;
-        if (qwt < 0) {
-            if (ln < ncol)
-                *dst = o;
-        } else {
-            if (ln < ncol)
-                st_dev(dst, o);
-            const int it = (h * HD + c0) / 256;
-            if (last_arrival_wave(sync + SYNC_PV_QUANT + t * 64 + it, 256 / PVS_COLS))
-                quant_item_wave<true>(qwt, att + (size_t)t * D.qd, D.qd, t, it, qa);
-        }
+        finish(o);
     } else if (producer) { // producer wave - 1: positions [PP (wave - 1), PP wave) of each tile
         int rw[8];
 #pragma unroll

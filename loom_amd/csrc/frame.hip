@@ -793,11 +793,13 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) void 
     const int nh = (min(blockIdx.x * 256 + 255, D.qd - 1)) / hd - h_lo + 1;
     const int kvh = h / G, g = h % G;
     const int p = min(pos[t], D.ctx - 1);
-    const int nc = p / span + 1; // records that hold positions
+    const int nc = p < 0 ? 0 : p / span + 1; // records that hold positions (none at a negative position)
     const size_t rs = (size_t)G * (hd + 2);
     const float *rec0 = part + ((size_t)t * D.n_kv + kvh) * n_chunks * rs;
     float val;
-    if (nc == 1 && !merge_one) { // one chunk: its record is already the softmax-weighted sum
+    if (nc == 0) { // no context: +0, as the exact path (nc is uniform over the group)
+        val = 0.0f;
+    } else if (nc == 1 && !merge_one) { // one chunk: its record is already the softmax-weighted sum
         val = rec0[2 * G + (size_t)g * hd + d];
     } else {
         float *wt = cmb + 4 * 256;

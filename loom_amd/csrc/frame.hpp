@@ -127,6 +127,8 @@ __device__ inline double wave_scan_d(double x) {
 template <int NW>
 __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds &s) {
     constexpr int NT = 64 * NW;
+    if (n <= 0) // the empty sum (n is uniform over the work group)
+        return 0.0f;
     const int tid = threadIdx.x, wave = tid >> 6, ln = tid & 63;
     const int n64 = (n + 63) & ~63;
     const int L = 64 * ((n64 / 64 + SEQ_MAX_CHUNKS - 1) / SEQ_MAX_CHUNKS);

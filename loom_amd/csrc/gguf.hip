@@ -57,18 +57,25 @@ struct Tensor {
 };
 
 // GGML bytes of a tensor: dims[0] values per row, the other dims' product
-// rows; 0 for a type without a known block geometry.
+// rows; 0 for a type without a known block geometry, a row length that is
+// not a whole number of blocks, or a size that overflows 64 bits (every
+// product checked, as ggml.zig:143-153 tensorBytesChecked checks them: a
+// wrapped size would pass the in-file test and let a reader walk past the
+// mapping).
 static uint64_t tensor_bytes(const Tensor &t) {
-    uint64_t rows = 1;
-    for (uint32_t d = 1; d < t.n_dims; d++)
-        rows *= t.dims[d];
     const int T = (int)t.type;
     if (T != LH_F32 && T != LH_F16 && T != LH_Q4_0 && T != LH_Q8_0 && T != LH_Q4_K && T != LH_Q6_K)
         return 0;
     const uint64_t be = (uint64_t)block_elems(T), bb = (uint64_t)block_bytes(T);
-    if (t.dims[0] % be)
+    if (t.n_dims == 0 || t.dims[0] % be)
         return 0;
-    return rows * (t.dims[0] / be) * bb;
+    uint64_t n = 0;
+    if (__builtin_mul_overflow(t.dims[0] / be, bb, &n))
+        return 0;
+    for (uint32_t d = 1; d < t.n_dims; d++)
+        if (__builtin_mul_overflow(n, t.dims[d], &n))
+            return 0;
+    return n;
 }
 
 struct Cursor {
@@ -337,9 +344,11 @@ int loomhip_gguf_get_tensor(const loomhip_gguf *g, size_t i, loomhip_gguf_tensor
     t->ggml_type = s.type;
     t->offset = s.offset;
     t->nbytes = tensor_bytes(s);
-    const uint64_t at = g->data_offset + s.offset;
-    // the data pointer only when the bytes lie inside the file
-    t->data = (t->nbytes && at <= g->file_size && t->nbytes <= g->file_size - at) ? g->map + at : nullptr;
+    // the data pointer only when the bytes lie inside the file (the offset sum
+    // checked for overflow, llama.zig:262-266 resolve)
+    uint64_t at = 0;
+    const bool sum_ok = !__builtin_add_overflow(g->data_offset, s.offset, &at);
+    t->data = (t->nbytes && sum_ok && at <= g->file_size && t->nbytes <= g->file_size - at) ? g->map + at : nullptr;
     return LOOMHIP_OK;
 }
 

@@ -19,7 +19,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import (GATING_SIGMOID, GATING_SOFTMAX, NUMERICS_PARITY, Q4_0, Q4_K, Q6_K, Q8_0, LayerDesc,
-               ModelDesc, MoeLayerDesc, check, lib, OK)
+               ModelDesc, MoeLayerDesc, check, ggml_bytes, lib, OK)
 from .backend import _ptr, _stream, repack_dev, synth_ggml_dev
 
 
@@ -208,12 +208,23 @@ class DeviceModel:
                 raise ValueError(f"missing tensor {name}")
             return t
 
+        # llama.zig:316-334 validateConfig: metadata that would divide by zero
+        # or break an index bound is rejected before any tensor is read
+        n_kv = u("attention.head_count_kv", n_heads)
+        ctx = ctx_len or u("context_length", 2048)
+        rope_dim = u("rope.dimension_count", head_dim)
+        if (not head_dim or not n_layers or n_layers < 0 or not ctx or not n_kv or n_heads % n_kv
+                or rope_dim > head_dim or n_used > 16 or n_expert > 256 or (n_expert and n_used > n_expert)
+                or (n_expert and (not n_used or not moe_ffn)) or (not n_expert and not ffn)):
+            raise ValueError("BadConfig: the model's metadata is inconsistent")
+
         embd = tensor("token_embd.weight")
+        if len(embd.dims) < 2:
+            raise ValueError(f"BadTensorShape: tensor {embd.name} has shape {list(embd.dims)}")
         out = g.find_tensor("output.weight") or embd  # tied embeddings
         first_moe = tensor("blk.0.ffn_gate_exps.weight") if n_expert else None
         spec = ModelSpec(dim=dim, head_dim=head_dim, n_layers=n_layers, n_heads=n_heads,
-                         n_kv_heads=u("attention.head_count_kv", n_heads), vocab=embd.dims[1],
-                         ctx_len=ctx_len or u("context_length", 2048), rope_dim=u("rope.dimension_count", head_dim),
+                         n_kv_heads=n_kv, vocab=embd.dims[1], ctx_len=ctx, rope_dim=rope_dim,
                          rope_base=fl("rope.freq_base", 10000.0), eps=fl("attention.layer_norm_rms_epsilon", 1e-5),
                          rope_neox=arch == "qwen3moe", qk_norm=g.find_tensor("blk.0.attn_q_norm.weight") is not None,
                          embed_t=embd.ggml_type, output_t=out.ggml_type,
@@ -228,20 +239,42 @@ class DeviceModel:
                          weights_scale=fl("expert_weights_scale", 1.0))
         m = cls(spec)
 
+        def expect_shape(t, want):
+            # llama.zig:293-309 expectShape / expectExpertShape: the file's dims
+            # must be exactly what the configuration implies (trailing unit
+            # dims read as absent, as resolve reads a missing ne1/ne2 as 1)
+            dims = tuple(int(d) for d in t.dims)
+            while len(dims) > len(want) and dims[-1] == 1:
+                dims = dims[:-1]
+            if dims != tuple(want):
+                raise ValueError(f"BadTensorShape: tensor {t.name} has shape {list(dims)}, "
+                                 f"config implies {list(want)}")
+
+        # every tensor is resolved and checked first; nothing reaches the
+        # device before all of them pass
+        plan = []
+
         def quant(key, t, rows, cols, planes=1):
-            if t.ggml_type not in (Q4_0, Q8_0, Q4_K, Q6_K) or t.data is None:
-                raise ValueError(f"{t.name}: GGML type {t.ggml_type} is not served")
-            gb = torch.from_numpy(np.array(t.data, copy=True)).cuda()
-            m.tensors[key] = _Tensor(t.ggml_type, rows, cols, planes, repack_dev(t.ggml_type, gb, rows, cols, planes),
-                                     gb if keep_ggml else None)
+            if t.ggml_type not in (Q4_0, Q8_0, Q4_K, Q6_K):
+                raise ValueError(f"UnsupportedTensorType: {t.name}: GGML type {t.ggml_type} is not served")
+            expect_shape(t, (cols, rows) if planes == 1 else (cols, rows, planes))
+            # llama.zig:258-272 resolve: the bytes the shape implies, inside the file
+            want = ggml_bytes(t.ggml_type, rows, cols) * planes
+            if t.nbytes != want:
+                raise ValueError(f"BadTensorShape: tensor {t.name} holds {t.nbytes} bytes, its shape {want}")
+            if t.data is None or t.data.size != want:
+                raise ValueError(f"TruncatedGguf: tensor {t.name} lies outside the file")
+            plan.append((key, t, (rows, cols, planes)))
 
-        def f32(key, t, n):
-            if t.ggml_type != 0 or t.nbytes != 4 * n:
-                raise ValueError(f"{t.name}: expected {n} f32 values")
-            m.f32[key] = torch.from_numpy(np.array(t.data.view(np.float32), copy=True)).cuda()
+        def f32(key, t, n, shape=None):
+            # llama.zig:281-291 expectF32, then the configured shape
+            if t.ggml_type != 0:
+                raise ValueError(f"BadTensorType: tensor {t.name} must be f32, got type {t.ggml_type}")
+            expect_shape(t, shape or (n,))
+            if t.nbytes != 4 * n or t.data is None or t.data.size != 4 * n:
+                raise ValueError(f"TruncatedGguf: tensor {t.name}: expected {n} f32 values inside the file")
+            plan.append((key, t, None))
 
-        m.f32["ones_dim"] = torch.ones(dim, dtype=torch.float32, device="cuda")
-        m.f32["ones_hd"] = torch.ones(head_dim, dtype=torch.float32, device="cuda")
         quant("embed", embd, spec.vocab, dim)
         quant("output", out, spec.vocab, dim)
         f32("out_norm", tensor("output_norm.weight"), dim)
@@ -257,7 +290,7 @@ class DeviceModel:
             quant(p + "wv", tensor(b + "attn_v.weight"), spec.kvd, dim)
             quant(p + "wo", tensor(b + "attn_output.weight"), dim, spec.qd)
             if n_expert:
-                f32(p + "router", tensor(b + "ffn_gate_inp.weight"), n_expert * dim)
+                f32(p + "router", tensor(b + "ffn_gate_inp.weight"), n_expert * dim, (dim, n_expert))
                 if spec.router_bias:
                     f32(p + "router_bias", tensor(b + "exp_probs_b.bias"), n_expert)
                 quant(p + "gate", tensor(b + "ffn_gate_exps.weight"), moe_ffn, dim, n_expert)
@@ -267,6 +300,17 @@ class DeviceModel:
                 quant(p + "ffn_gate", tensor(b + "ffn_gate.weight"), ffn, dim)
                 quant(p + "ffn_up", tensor(b + "ffn_up.weight"), ffn, dim)
                 quant(p + "ffn_down", tensor(b + "ffn_down.weight"), dim, ffn)
+
+        m.f32["ones_dim"] = torch.ones(dim, dtype=torch.float32, device="cuda")
+        m.f32["ones_hd"] = torch.ones(head_dim, dtype=torch.float32, device="cuda")
+        for key, t, shp in plan:
+            if shp is None:
+                m.f32[key] = torch.from_numpy(np.array(t.data.view(np.float32), copy=True)).cuda()
+            else:
+                rows, cols, planes = shp
+                gb = torch.from_numpy(np.array(t.data, copy=True)).cuda()
+                m.tensors[key] = _Tensor(t.ggml_type, rows, cols, planes,
+                                         repack_dev(t.ggml_type, gb, rows, cols, planes), gb if keep_ggml else None)
         m._build_desc()
         return m
 

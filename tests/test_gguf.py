@@ -181,3 +181,74 @@ def test_every_truncation_fails_cleanly(tmp_path):
             gguf_ref.parse(raw[:cut])
         with pytest.raises(loom_amd.LoomHipError):
             gguf.GgufFile(str(cut_path))
+
+
+# A qwen3moe file at frame-served shapes, every matrix Q8_0 (any served type
+# exercises the same checks; Q8_0 quantizes fastest).
+_SHAPE = gguf.FixtureShape(dim=64, n_heads=2, n_kv_heads=1, head_dim=32, ffn=128, n_expert=4, n_used=2,
+                           moe_ffn=64, n_layers=2, vocab_bytes=False, vocab=64, context_length=32)
+
+
+def _q8_file(oracle, path, reshape=None):
+    """writeMoeFixture's qwen3moe layout with Q8_0 matrices; ``reshape``
+    maps a tensor name to the dims it is written with instead."""
+    kvs, table = gguf.moe_fixture_layout("qwen3moe", _SHAPE)
+    rng = np.random.default_rng(5)
+    tensors = []
+    for name, dims in table:
+        dims = (reshape or {}).get(name, dims)
+        n = int(np.prod(dims))
+        if len(dims) == 1 or name.endswith("ffn_gate_inp.weight"):
+            tensors.append((name, dims, 0, rng.standard_normal(n).astype(np.float32)))
+        else:
+            w = (0.02 * rng.standard_normal((n // dims[0], dims[0]))).astype(np.float32)
+            tensors.append((name, dims, 8, oracle.quantize(8, w)))
+    gguf.write_gguf(str(path), kvs, tensors, alignment=32)
+
+
+def test_from_gguf_rejects_a_mis_shaped_tensor_before_any_upload(oracle, tmp_path):
+    """llama.zig:293-309 expectShape: layer 1's attn_q written as
+    [dim, 2*q_dim] (its bytes consistent with those dims) against the q_dim
+    rows the metadata implies raises BadTensorShape.  Every tensor is checked
+    before the first upload: layer 0's tensors come first in the file, and
+    on this GPU-less host an upload would raise a torch error, not this
+    ValueError."""
+    from loom_amd.frame import DeviceModel
+
+    qd = _SHAPE.n_heads * _SHAPE.head_dim
+    path = tmp_path / "bad_q.gguf"
+    _q8_file(oracle, path, {"blk.1.attn_q.weight": (_SHAPE.dim, 2 * qd)})
+    with gguf.GgufFile(str(path)) as g:
+        with pytest.raises(ValueError, match=r"BadTensorShape: tensor blk\.1\.attn_q\.weight"):
+            DeviceModel.from_gguf(g)
+
+
+def test_from_gguf_rejects_a_truncated_tensor_before_any_upload(oracle, tmp_path):
+    """llama.zig:258-272 resolve: a file cut inside its last tensor still
+    parses (the data section starts inside the file), but that tensor's bytes
+    do not lie inside it: TruncatedGguf, before anything is uploaded."""
+    from loom_amd.frame import DeviceModel
+
+    path = tmp_path / "cut.gguf"
+    _q8_file(oracle, path)
+    raw = path.read_bytes()
+    path.write_bytes(raw[:-7])
+    with gguf.GgufFile(str(path)) as g:
+        last = max(g.tensors, key=lambda t: t.offset)
+        assert last.data is None and last.nbytes > 0
+        with pytest.raises(ValueError, match=f"TruncatedGguf: tensor {last.name}"):
+            DeviceModel.from_gguf(g)
+
+
+def test_tensor_bytes_overflow_reads_as_unknown(tmp_path):
+    """ggml.zig:143-153 tensorBytesChecked: an F32 tensor of 2^62 + 1 values
+    has a representable element count but 2^64 + 4 bytes.  Unchecked, the
+    size wraps to 4 and those 4 bytes pass the in-file test; checked, the
+    size reads as unknown (0) and no data pointer is handed out."""
+    raw = (_header(1, 0) + _s("t") + struct.pack("<IQ", 1, (1 << 62) + 1) + struct.pack("<IQ", 0, 0))
+    raw += b"\0" * ((-len(raw)) % 32) + b"\0" * 64
+    path = tmp_path / "wrap.gguf"
+    path.write_bytes(raw)
+    with gguf.GgufFile(str(path)) as g:
+        assert g.tensors[0].dims == ((1 << 62) + 1,)
+        assert g.tensors[0].nbytes == 0 and g.tensors[0].data is None

@@ -258,3 +258,88 @@ def test_hit_on_a_prefetched_slot_waits_for_its_fill(ec_mod):
     st = ec.stats
     assert st.warmup_reads == 6 and st.lru_hits == 6
     ec.close()
+
+
+@pytest.mark.parametrize("n_tok,steps", [(1, 6), (64, 2)])
+def test_cached_layer_config5_matches_oracle(ec_mod, oracle, n_tok, steps):
+    """Config 5's routed block as the benchmark drives it: loomhip_moe_layer_
+    cached at hidden 7168, expert ffn 2048, Q4_K, sigmoid gating with renorm,
+    the Zipf(1.1) popularity as a logit bias, and the resident shared expert
+    (its arm of the cached layer), over 32 experts streamed from pinned host
+    memory through an 8-slot LRU, so misses and evictions occur and 64 tokens
+    need several rounds of gets.  Against the oracle on the same GGML bytes:
+    moeRun + shared expert at one token (src/gguf/deepseek.zig:1485-1502),
+    moeBatchUnion + shared expert at 64 (src/gguf/llama.zig:1828-1924).  Ids
+    exact, gates within 1e-6, outputs bit-identical (north_star asks for
+    2e-3), and the hit and miss counts equal to the oracle's replay of the
+    call's own access trace (src/engine/expert_cache.zig:230-249)."""
+    import torch
+
+    import npref
+    from loom_amd import GATING_SIGMOID, MoeLayerEcDesc, plane_bytes
+    from loom_amd import backend as be
+
+    E, k, dim, ffn, sffn, cap = 32, 8, 7168, 2048, 2048, 8
+    rng = np.random.default_rng(77)
+    gate = npref.pinned_scale_blocks(Q4_K, ffn, dim, rng, planes=E)
+    up = npref.pinned_scale_blocks(Q4_K, ffn, dim, rng, planes=E)
+    down = npref.pinned_scale_blocks(Q4_K, dim, ffn, rng, planes=E)
+    sg = npref.pinned_scale_blocks(Q4_K, sffn, dim, rng)
+    su = npref.pinned_scale_blocks(Q4_K, sffn, dim, rng)
+    sd = npref.pinned_scale_blocks(Q4_K, dim, sffn, rng)
+    router = oracle.normal(E * dim, 78, 0.0, 1.0 / np.sqrt(dim)).reshape(E, dim)
+    ranks = rng.permutation(E) + 1
+    zipf = np.log(1.0 / ranks ** 1.1)
+    rb = (zipf - zipf.mean()).astype(np.float32)
+    w = oracle.MoeWeights(dim, ffn, E, k, router, gate, up, down, Q4_K, Q4_K, Q4_K, router_bias=rb,
+                          gating=oracle.GATING_SIGMOID, weights_norm=True,
+                          shexp=(sg, su, sd, Q4_K, Q4_K, Q4_K, sffn))
+
+    def dev(raw, rows, cols, planes=1):
+        return be.repack_dev(Q4_K, torch.from_numpy(raw).cuda(), rows, cols, planes)
+
+    gb, db = plane_bytes(Q4_K, ffn, dim), plane_bytes(Q4_K, dim, ffn)
+    slot = 2 * gb + db
+    host = ec_mod.HostBuffer(E * slot)
+    hv = torch.from_numpy(host.array)
+    for part, (raw, rows, cols, off, pb) in enumerate(((gate, ffn, dim, 0, gb), (up, ffn, dim, gb, gb),
+                                                       (down, dim, ffn, 2 * gb, db))):
+        d = dev(raw, rows, cols, E).view(E, pb).cpu()
+        for e in range(E):
+            hv[e * slot + off:e * slot + off + pb].copy_(d[e])
+        del d
+    sh = (dev(sg, sffn, dim), dev(su, sffn, dim), dev(sd, dim, sffn))
+    router_d, rb_d = torch.from_numpy(router).cuda(), torch.from_numpy(rb).cuda()
+    desc = MoeLayerEcDesc(dim, ffn, E, k, GATING_SIGMOID, 1, 1.0, router_d.data_ptr(), rb_d.data_ptr(), None,
+                          Q4_K, Q4_K, 0, 0, gb, 2 * gb, Q4_K, Q4_K, Q4_K, sh[0].data_ptr(), sh[1].data_ptr(),
+                          sh[2].data_ptr(), sffn)
+    ec = ec_mod.ExpertCache(cap, slot, E)
+    for e in range(E):
+        ec.set_source(e, host, e * slot, slot)
+    trace = []
+    try:
+        for step in range(steps):
+            xs = np.stack([oracle.normal(dim, 700 + 100 * step + i, 0.0, 1.0) for i in range(n_tok)])
+            got = torch.full((n_tok, dim), float("nan"), device="cuda")
+            print(f"n_tok={n_tok} step {step}", flush=True)
+            ids, gates = ec.moe_layer(desc, torch.from_numpy(xs).cuda(), got, n_tok, want_ids=True)
+            torch.cuda.synchronize()
+            got = got.cpu().numpy()
+            if n_tok == 1:
+                want, wids, wgates = oracle.moe_layer_token(w, xs[0])
+                want, wids, wgates = want[None], wids[None], wgates[None]
+            else:
+                want, wids, wgates = oracle.moe_batch_union(w, xs, np.zeros_like(xs))
+            assert np.array_equal(ids, wids), step
+            assert np.abs(gates - wgates).max() <= 1e-6, step
+            rel = max(float(np.abs(got[i] - want[i]).max() / np.abs(want[i]).max()) for i in range(n_tok))
+            print(f"  max-rel {rel:.2e}, distinct experts {len(set(ids.ravel().tolist()))}", flush=True)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (step, rel)
+            trace += list(ids[0]) if n_tok == 1 else sorted(set(ids.ravel().tolist()))
+        counts, _ = oracle.cache_replay(cap, np.array(trace, np.uint32))
+        st = ec.stats
+        assert st.disk_misses > 0 and (st.pin_hits, st.lru_hits, st.disk_misses) == tuple(int(c) for c in counts)
+        assert st.bytes_read == st.disk_misses * slot
+    finally:
+        ec.close()
+        host.free()

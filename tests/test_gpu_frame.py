@@ -4,9 +4,10 @@ llama.step / decodeBatch (src/gguf/llama.zig:1111-1227, 1939-2043).
 Two kinds of check:
   * per step, with the oracle's K/V cache and position reset to the device's
     before the step, so that each step compares one token's arithmetic on
-    identical state: logits within max-relative 2e-3 (north_star), and in
-    PARITY numerics within 1e-5 (bit-identical but for rare exp last-bit
-    differences);
+    identical state: in PARITY numerics the logits are bit-identical
+    (max-relative 0.0: every reduction runs in the reference's order, and
+    exp is the once-rounded double exponential on both sides); FAST is
+    bounded, not held to north_star's 2e-3;
   * free-running greedy decode on both sides: identical tokens (north_star:
     64 tokens at config 1).
 """
@@ -108,8 +109,7 @@ def test_stories15m_steps_parity(lh, oracle):
     dm = lh.DeviceModel.synth(spec, seed=4, keep_ggml=True)
     om = OracleModel(oracle, dm)
     rels = _synced_steps(lh, om, dm, np.random.default_rng(2).integers(0, spec.vocab, 40))
-    assert rels.max() <= 2e-3, rels.max()
-    assert (rels <= 1e-5).mean() >= 0.95, rels
+    _check(rels, "parity")
 
 
 def _qwen_small(lh, n_layers=2, vocab=4096, n_expert=16, ctx_len=80):
@@ -125,8 +125,7 @@ def test_qwen3moe_frame_steps_parity(lh, oracle):
     dm = lh.DeviceModel.synth(spec, seed=5, keep_ggml=True)
     om = OracleModel(oracle, dm)
     rels = _synced_steps(lh, om, dm, np.random.default_rng(4).integers(0, spec.vocab, 40))
-    assert rels.max() <= 2e-3, rels.max()
-    assert (rels <= 1e-5).mean() >= 0.95, rels
+    _check(rels, "parity")
 
 
 def test_qwen3moe_frame_greedy(lh, oracle):
@@ -153,10 +152,10 @@ FAST_BOUND = 5e-2
 
 
 def _check(rels, numerics):
+    """PARITY: every lane-step bit-identical to the oracle.  FAST: bounded."""
     rels = np.asarray(rels)
     if numerics == "parity":
-        assert rels.max() <= 2e-3, rels
-        assert (rels <= 1e-5).mean() >= 0.95, rels
+        assert rels.max() == 0.0, rels
     else:
         assert rels.max() <= FAST_BOUND, rels
 
@@ -165,7 +164,7 @@ def _check(rels, numerics):
 def test_qwen3moe_frame_prefilled_context(lh, oracle, numerics):
     """A prefilled fp16 context (random K/V rows 0..99), then 12 steps on
     identical state: PARITY runs the reference-order attention over the whole
-    context (bit-identical but for exp's last bit), FAST the split-context
+    context (bit-identical), FAST the split-context
     merge.  Every step's greedy token matches."""
     spec = _qwen_small(lh, ctx_len=128)
     dm = lh.DeviceModel.synth(spec, seed=6, keep_ggml=True)
@@ -249,8 +248,8 @@ def test_qwen3moe_frame_4096_context(lh, oracle, n, numerics):
     """The benchmark's shape: two layers at the full Qwen3-30B-A3B layer
     shapes (128 experts top-8, vocab 4096) over a 4096-token prefilled fp16
     context, 1 lane (llama.step) and 32 lanes (decodeBatch), 3 steps on
-    identical state.  PARITY: every logit within north_star's 2e-3 (in fact
-    bit-identical) and identical greedy tokens -- the reference's sequential
+    identical state.  PARITY: every logit bit-identical (north_star asks for
+    2e-3) and identical greedy tokens -- the reference's sequential
     softmax sum and position-ordered P.V over all 4096 positions, the merge
     tail of long contexts included."""
     spec = lh.qwen3_30b_a3b(ctx_len=4096 + 16, n_layers=2, vocab=4096, n_expert=128)
@@ -306,3 +305,52 @@ def test_frame_declines_unserved_moe_layer(lh, bad):
         assert dec.step() == loom_amd.DECLINED
     assert loom_amd.take_launch_count() == 0
     assert int(dec.k_cache.abs().sum().item()) == 0
+
+
+@pytest.mark.parametrize("numerics", ["parity", "fast"])
+@pytest.mark.parametrize("n", [1, 3, 4, 6])
+def test_frame_lane_at_negative_position(lh, oracle, n, numerics):
+    """A lane at position -1 (no context) among n lanes over a 200-position
+    prefilled context.  Its attention is +0: no K/V row read or written, no
+    softmax over an empty row, and with wo's quantization fused into the
+    few-lane P.V (n <= 4) its arrival still counts, so its neighbours'
+    quantized inputs complete.  The other lanes' logits are those
+    lo_decode_batch gives them on their own (PARITY: bit-identical); the
+    empty lane's are finite and it leaves at position 0.  n = 6 runs the
+    many-lane kernels."""
+    import torch
+
+    spec = _qwen_small(lh, ctx_len=224)
+    dm = lh.DeviceModel.synth(spec, seed=13, keep_ggml=True)
+    _set_numerics(dm, numerics)
+    om = OracleModel(oracle, dm)
+    dec = lh.Decoder(dm, n)
+    dec.prefill_random(200, seed=5, scale=0.5)
+    neg = n // 2
+    pos0 = [200 - (i % 7) for i in range(n)]
+    pos0[neg] = -1
+    dec.pos.copy_(torch.tensor(pos0, dtype=torch.int32))
+    toks = np.random.default_rng(n).integers(0, spec.vocab, n).astype(np.int32)
+    dec.tokens.copy_(torch.from_numpy(toks))
+    others = [i for i in range(n) if i != neg]
+    seqs, bufs = om.new_seqs(max(1, len(others)))
+    torch.cuda.synchronize()
+    for j, i in enumerate(others):
+        bufs[2 * j][:] = dec.k_cache[i].cpu().numpy().view(np.uint8).ravel()
+        bufs[2 * j + 1][:] = dec.v_cache[i].cpu().numpy().view(np.uint8).ravel()
+        seqs[j].pos = pos0[i]
+    k_before, v_before = dec.k_cache[neg].clone(), dec.v_cache[neg].clone()
+    print(f"n={n} {numerics}: lane {neg} at position -1", flush=True)
+    dec.step()
+    torch.cuda.synchronize()
+    got = dec.logits.cpu().numpy()
+    assert torch.equal(dec.k_cache[neg], k_before) and torch.equal(dec.v_cache[neg], v_before)
+    assert np.isfinite(got[neg]).all()
+    assert int(dec.pos[neg].item()) == 0
+    if others:
+        want = om.decode_batch(seqs, toks[others])
+        rels = [maxrel(got[i], want[j]) for j, i in enumerate(others)]
+        if numerics == "parity":
+            assert max(rels) == 0.0, rels
+        else:
+            assert max(rels) <= FAST_BOUND, rels

@@ -36,6 +36,15 @@ def _maxrel(got, want):
     return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
 
 
+def _same_bits(got, want, what=""):
+    """Bit-identical layer outputs (north_star asks for 2e-3; every matvec is
+    exact and each combine runs in the reference's order, so the device
+    gives the CPU path's own bits)."""
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    print(f"{what} max-rel {_maxrel(got, want):.2e}", flush=True)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (what, _maxrel(got, want))
+
+
 @pytest.mark.parametrize("gating,norm,scale,bias", [
     ("softmax", True, 1.0, False), ("sigmoid", True, 1.0, True), ("sigmoid", True, 1.0, False),
     ("softmax", False, 2.5, False), ("sigmoid", False, 1.0, True),
@@ -109,7 +118,7 @@ def test_moe_ffn_routed_single_token(be, oracle, dim, ffn, E, k):
     assert ok
     assert be.takeCmdBufCount() >= 3  # gate, gate/up, down ran on the device
     want, ids, gates = oracle.moe_layer_token(w, normed)
-    assert _maxrel(out, want) <= 2e-3, _maxrel(out, want)
+    _same_bits(out, want, f"dim {dim}")
 
 
 def _dev_layer(be, w):
@@ -153,9 +162,7 @@ def test_moe_layer_dev_matches_oracle(be, oracle, n):
     torch.cuda.synchronize()
     assert np.array_equal(ids.cpu().numpy().astype(np.uint32), wid)
     assert np.all(np.abs(gates.cpu().numpy() - wg) <= 1e-6)
-    got = out.cpu().numpy()
-    for i in range(n):
-        assert _maxrel(got[i], want[i]) <= 2e-3, (i, _maxrel(got[i], want[i]))
+    _same_bits(out.cpu().numpy(), want, f"n={n}")
 
 
 @pytest.mark.parametrize("n", [1, 2, 6])
@@ -177,9 +184,7 @@ def test_moe_layer_dev_wide_hidden(be, oracle, n):
     torch.cuda.synchronize()
     assert np.array_equal(ids.cpu().numpy().astype(np.uint32), wid)
     assert np.all(np.abs(gates.cpu().numpy() - wg) <= 1e-6)
-    got = out.cpu().numpy()
-    for i in range(n):
-        assert _maxrel(got[i] - resid[i], want[i] - resid[i]) <= 2e-3, i
+    _same_bits(out.cpu().numpy(), want, f"n={n}")
 
 
 @pytest.mark.parametrize("n", [5, 7, 9, 16, 17, 31, 33, 47, 64, 65, 100, 127, 128, 129, 200, 256])
@@ -188,8 +193,8 @@ def test_moe_gate_handoff_at_many_lane_counts(be, oracle, n):
     to work group inside the launch (agent-scope stores, a completion
     counter whose last arrival reads them back).  Every lane count from the
     batched path's smallest to the largest served, partial last chunks
-    included, three launches each with fresh inputs: ids bit-exact and
-    outputs within 2e-3 of moeBatchUnion every time."""
+    included, three launches each with fresh inputs: ids and outputs
+    bit-identical to moeBatchUnion every time."""
     import torch
 
     dim, ffn, E, k = 512, 256, 32, 4
@@ -206,8 +211,7 @@ def test_moe_gate_handoff_at_many_lane_counts(be, oracle, n):
         torch.cuda.synchronize()
         assert np.array_equal(ids.cpu().numpy().astype(np.uint32), wid), (n, rep)
         assert np.all(np.abs(gates.cpu().numpy() - wg) <= 1e-6), (n, rep)
-        got = out.cpu().numpy()
-        assert max(_maxrel(got[i], want[i]) for i in range(n)) <= 2e-3, (n, rep)
+        _same_bits(out.cpu().numpy(), want, f"n={n} launch {rep}")
 
 
 Q8_0, Q4_0 = 8, 2
@@ -251,9 +255,7 @@ def test_moe_layer_dev_gatings_and_down_types(be, oracle, down_t, ffn, gi, n):
     torch.cuda.synchronize()
     assert np.array_equal(ids.cpu().numpy().astype(np.uint32), wid)
     assert np.all(np.abs(gates.cpu().numpy() - wg) <= 1e-5 * max(1.0, scale))
-    got = out.cpu().numpy()
-    for i in range(n):
-        assert _maxrel(got[i] - resid[i], want[i] - resid[i]) <= 2e-3, i
+    _same_bits(out.cpu().numpy(), want, f"gating {gating} down {down_t} n={n}")
 
 
 # ---- config 5's block: the shared expert, and moeFfnBlock -------------------------
@@ -277,7 +279,9 @@ def test_moe_ffn_routed_with_shared_expert(be, oracle):
     """backend.moeFfnBlockRouted with `shexp` (src/compute/cpu.zig:68;
     src/vulkan/backend.zig:527-548): the shared expert's FFN added after the
     routed sum in one submission, at config 5's shapes; against the oracle's
-    moeRun + shared expert (deepseek.zig:1485-1502) within 2e-3, ids exact."""
+    moeRun + shared expert (deepseek.zig:1485-1502): bit-identical (every
+    matvec is exact, the combine runs in selection order, then the shared
+    expert; north_star asks for 2e-3)."""
     from loom_amd.backend import RoutedCfg, WeightRef
 
     w = _c5_layer(oracle, E=16, k=8, seed=51)
@@ -294,7 +298,8 @@ def test_moe_ffn_routed_with_shared_expert(be, oracle):
         assert ok
         assert be.takeCmdBufCount() >= 6  # the routed chain and the shared expert's launches
         want, _, _ = oracle.moe_layer_token(w, normed)
-        assert _maxrel(out, want) <= 2e-3, _maxrel(out, want)
+        print(f"routed + shared, token {s}: max-rel {_maxrel(out, want):.2e}", flush=True)
+        assert np.array_equal(out.view(np.uint32), want.view(np.uint32)), _maxrel(out, want)
         # the same block without the shared expert differs by that expert's output
         w2 = oracle.MoeWeights(w.dim, w.ffn, w.n_expert, w.n_used, w.router, w.gate, w.up, w.down, Q4_K, Q4_K,
                                Q4_K, gating=oracle.GATING_SIGMOID)
@@ -306,7 +311,8 @@ def test_moe_ffn_routed_with_shared_expert(be, oracle):
 def test_moe_layer_dev_shared_expert(be, oracle, n):
     """loomhip_moe_layer_dev with the layer's shared expert: n = 1 in
     selection order (moeRun), n > 1 ascending-expert (moeBatchUnion), the
-    shared expert of every token after its routed experts."""
+    shared expert of every token after its routed experts: bit-identical to
+    the oracle."""
     import torch
 
     from loom_amd import COMBINE_EXPERT_ASC, COMBINE_SELECTION
@@ -329,11 +335,12 @@ def test_moe_layer_dev_shared_expert(be, oracle, n):
     got = out.cpu().numpy()
     if n == 1:
         want, _, _ = oracle.moe_layer_token(w, xs[0])
-        assert _maxrel(got[0], want) <= 2e-3
+        want = want[None]
     else:
         want, _, _ = oracle.moe_batch_union(w, xs, resid)
-        for i in range(n):
-            assert _maxrel(got[i], want[i]) <= 2e-3, (i, _maxrel(got[i], want[i]))
+    print(f"n={n}: max-rel {max(_maxrel(got[i], want[i]) for i in range(n)):.2e}", flush=True)
+    for i in range(n):
+        assert np.array_equal(got[i].view(np.uint32), want[i].view(np.uint32)), (i, _maxrel(got[i], want[i]))
 
 
 def test_moe_ffn_block_matches_oracle_and_caches(be, oracle):
