@@ -332,6 +332,120 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
  * a frame must never decline halfway through a token. */
 int loomhip_frame_check(const loomhip_model *m, size_t n);
 
+/* ---- the seam's frame calls over host buffers ------------------------------
+ * A model held by the engine (host GGML bytes, mapped from the GGUF file),
+ * one sequence.  Weights are uploaded and repacked on first use, keyed by
+ * host pointer like every seam call.  The device K/V cache is fp16
+ * [n_layers][ctx_len][kvd] (config 4's fp16 cache; the engine's own cache is
+ * f32): attention over it is the PARITY frame's, in the reference's order.
+ * The engine's host cache stays authoritative -- kvAppend mirrors the rows
+ * the host path writes (rounded to fp16, as the frame's own append rounds),
+ * and after a frame the rows it wrote are read back with loomhip_read_kv (the
+ * fp16 values widened), so a later decline falls back to a cache holding
+ * exactly what the device attended over.  Calls are synchronous except
+ * inside a begin_frame / end_frame bracket. */
+
+/* A tensor as the engine hands it over (cpu.zig WeightRef: type and the
+ * GGML bytes as a slice); a call declines when len is not the size its shape
+ * implies. */
+typedef struct {
+    int type;
+    const void *data;
+    size_t len;
+} loomhip_weight_ref;
+
+/* attnInit (src/compute/backend.zig:121-123; cpu.zig:104-107): allocate the
+ * device cache (zeroed).  DECLINED past 7,936 positions (the PARITY
+ * attention's limit) or for kvd 0. */
+int loomhip_attn_init(size_t layers, size_t ctx_len, size_t kvd);
+/* hasKvCache / releaseKvCache (backend.zig:130-133): 1 when a cache exists;
+ * free it. */
+int loomhip_has_kv_cache(void);
+void loomhip_release_kv_cache(void);
+/* kvAppend (backend.zig:125-127; cpu.zig:153-156): mirror one host row of
+ * layer li at pos (kvd f32 each) into the device cache. */
+int loomhip_kv_append(size_t li, size_t pos, const float *k_new, const float *v_new, size_t kvd);
+/* The read-back that keeps the host cache authoritative (the GQA form of
+ * mlaReadCache, backend.zig:191): the device rows of layer li at pos as f32.
+ * After a frame, the rows of its position come from a host mirror copied
+ * with the frame's results. */
+int loomhip_read_kv(size_t li, size_t pos, float *k_out, float *v_out, size_t kvd);
+/* attnHeads (backend.zig:151-160; cpu.zig:157-170): every query head of
+ * layer li over cache rows [0, pos] (row pos already appended), q
+ * [n_heads*hd] normalised and rotated, out [n_heads*hd]: dotF32 scores
+ * times scale, the sequential softmax, P.V in position order
+ * (llama.zig:1162-1192), bit-identical to the host loop over the same
+ * cache. */
+int loomhip_attn_heads(size_t li, size_t pos, const float *q, float *out, size_t n_heads, size_t n_kv_heads,
+                       size_t hd, float scale);
+
+/* beginFrame / frameOpen / frameLoadX / layerBlock / endFrame / frameStoreX
+ * (backend.zig:141-149; llama.zig:1067-1108 stepRecorded): layers of one
+ * token recorded on the library's stream with the residual in device memory,
+ * submitted and waited for by end_frame.  LayerSpec is cpu.zig:116-138 (a
+ * dense SwiGLU layer, as gpuLayersSupported admits).  layer_block checks
+ * and uploads everything before it records anything, and DECLINES (nothing
+ * recorded for that layer) for an unserved shape or type, a missing device
+ * cache or a position other than the frame's.  Every layer appends its K/V
+ * row at pos on the device; loomhip_read_kv returns them. */
+typedef struct {
+    size_t li, pos;
+    const float *attn_norm, *ffn_norm; /* [dim] */
+    float eps;
+    loomhip_weight_ref wq, wk, wv, wo, gate, up, down;
+    size_t dim, ffn, n_heads, n_kv_heads, hd, rope_dim;
+    float rope_base;
+    int rope_neox;
+    float attn_scale;
+} loomhip_layer_spec;
+int loomhip_begin_frame(void);
+int loomhip_frame_open(void); /* 1 while a frame is open */
+int loomhip_frame_load_x(const float *x, size_t dim);
+int loomhip_layer_block(const loomhip_layer_spec *s);
+int loomhip_end_frame(void);
+int loomhip_frame_store_x(float *x, size_t dim);
+
+/* The GQA+MoE whole token as one submission, the qwen3moe form of
+ * mlaTokenFrame (backend.zig:186-191; cpu.zig:73-79; the Vulkan arm
+ * src/vulkan/backend.zig:905-916), one descriptor per layer as MlaLayerDesc:
+ * in, the residual stream after embedding (x [dim], host); every layer --
+ * attention norm, q/k/v, per-head Q/K norm (q_norm NULL: none), RoPE, the
+ * K/V append at pos, attention, wo and residual, then the routed MoE layer
+ * (router f32 [n_expert][dim] with an optional logit bias and selection-
+ * only bias, gate/up/down stacked [n_expert] planes, the shared expert when
+ * shexp_gate.data is set) or the dense FFN -- then the output norm and head.
+ * Out: x after the last layer and logits [vocab].  PARITY numerics: the
+ * engine's own llama.step arithmetic, bit for bit (moeRun's selection
+ * order).  DECLINED, with nothing launched, for anything the frame does not
+ * serve (loomhip_frame_check's rules), a weight whose length does not match
+ * its shape, or a device cache of other dims. */
+typedef struct {
+    const float *attn_norm, *ffn_norm; /* [dim] */
+    const float *q_norm, *k_norm;      /* [head_dim] or NULL */
+    loomhip_weight_ref wq, wk, wv, wo;
+    int is_moe;
+    loomhip_weight_ref router;                     /* f32 [n_expert][dim] */
+    const float *router_bias;                      /* [n_expert] logit bias (ffn_gate_inp.bias) or NULL */
+    const float *sel_bias;                         /* [n_expert] selection-only bias (exp_probs_b) or NULL */
+    loomhip_weight_ref gate, up, down;             /* [n_expert][ffn][dim] x2, [n_expert][dim][ffn] */
+    loomhip_weight_ref shexp_gate, shexp_up, shexp_down; /* [shexp_ffn][dim] x2, [dim][shexp_ffn] */
+    size_t ffn, shexp_ffn;
+    loomhip_weight_ref dgate, dup, ddown; /* dense FFN (is_moe == 0): [dffn][dim] x2, [dim][dffn] */
+    size_t dffn;
+} loomhip_gqa_layer_desc;
+typedef struct {
+    size_t dim, n_heads, n_kv_heads, head_dim, rope_dim;
+    float eps, scale, rope_base;
+    int rope_neox;
+    /* RoutedCfg (cpu.zig) */
+    size_t n_expert, n_used;
+    int gating, weights_norm; /* LOOMHIP_GATING_* */
+    float weights_scale;
+} loomhip_gqa_frame_cfg;
+int loomhip_gqa_token_frame(const loomhip_gqa_layer_desc *descs, size_t n_layers, const loomhip_gqa_frame_cfg *fc,
+                            float *x, size_t pos, const float *out_norm, loomhip_weight_ref lm_head, float *logits,
+                            size_t vocab);
+
 /* ---- MLA attention over the compressed cache (src/gguf/deepseek.zig) ------
  * The seam's mlaInit / mlaAppend / hasMlaCache / mlaReadCache / mlaSetWk /
  * mlaAttnHeads (src/compute/backend.zig:162-169,193-197; the CPU arm

@@ -121,6 +121,41 @@ class ModelDesc(C.Structure):
     ]
 
 
+class WeightRefDesc(C.Structure):
+    """Mirror of ``loomhip_weight_ref`` in include/loomhip.h."""
+
+    _fields_ = [("type", C.c_int), ("data", C.c_void_p), ("len", C.c_size_t)]
+
+
+class LayerSpecDesc(C.Structure):
+    """Mirror of ``loomhip_layer_spec`` (src/compute/cpu.zig:116-138 LayerSpec)."""
+
+    _fields_ = ([("li", C.c_size_t), ("pos", C.c_size_t), ("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p),
+                 ("eps", C.c_float)] + [(n, WeightRefDesc) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")] +
+                [(n, C.c_size_t) for n in ("dim", "ffn", "n_heads", "n_kv_heads", "hd", "rope_dim")] +
+                [("rope_base", C.c_float), ("rope_neox", C.c_int), ("attn_scale", C.c_float)])
+
+
+class GqaLayerDescC(C.Structure):
+    """Mirror of ``loomhip_gqa_layer_desc`` (the qwen3moe form of MlaLayerDesc)."""
+
+    _fields_ = ([(n, C.c_void_p) for n in ("attn_norm", "ffn_norm", "q_norm", "k_norm")] +
+                [(n, WeightRefDesc) for n in ("wq", "wk", "wv", "wo")] + [("is_moe", C.c_int),
+                ("router", WeightRefDesc), ("router_bias", C.c_void_p), ("sel_bias", C.c_void_p)] +
+                [(n, WeightRefDesc) for n in ("gate", "up", "down", "shexp_gate", "shexp_up", "shexp_down")] +
+                [("ffn", C.c_size_t), ("shexp_ffn", C.c_size_t)] +
+                [(n, WeightRefDesc) for n in ("dgate", "dup", "ddown")] + [("dffn", C.c_size_t)])
+
+
+class GqaFrameCfg(C.Structure):
+    """Mirror of ``loomhip_gqa_frame_cfg`` (MlaFrameCfg's GQA counterpart)."""
+
+    _fields_ = ([(n, C.c_size_t) for n in ("dim", "n_heads", "n_kv_heads", "head_dim", "rope_dim")] +
+                [(n, C.c_float) for n in ("eps", "scale", "rope_base")] + [("rope_neox", C.c_int),
+                ("n_expert", C.c_size_t), ("n_used", C.c_size_t), ("gating", C.c_int), ("weights_norm", C.c_int),
+                ("weights_scale", C.c_float)])
+
+
 class EcStats(C.Structure):
     """Mirror of ``loomhip_ec_stats`` in include/loomhip.h."""
 
@@ -245,6 +280,20 @@ def lib() -> C.CDLL:
         "loomhip_moe_layer_dev_noalloc": (i, [C.POINTER(MoeLayerDesc), vp, sz, i, vp, vp, vp, vp]),
         "loomhip_token_frame_dev": (i, [C.POINTER(ModelDesc), vp, vp, sz, vp, vp, vp, vp, vp]),
         "loomhip_frame_check": (i, [C.POINTER(ModelDesc), sz]),
+        "loomhip_attn_init": (i, [sz, sz, sz]),
+        "loomhip_has_kv_cache": (i, []),
+        "loomhip_release_kv_cache": (None, []),
+        "loomhip_kv_append": (i, [sz, sz, vp, vp, sz]),
+        "loomhip_read_kv": (i, [sz, sz, vp, vp, sz]),
+        "loomhip_attn_heads": (i, [sz, sz, vp, vp, sz, sz, sz, C.c_float]),
+        "loomhip_begin_frame": (i, []),
+        "loomhip_frame_open": (i, []),
+        "loomhip_frame_load_x": (i, [vp, sz]),
+        "loomhip_layer_block": (i, [C.POINTER(LayerSpecDesc)]),
+        "loomhip_end_frame": (i, []),
+        "loomhip_frame_store_x": (i, [vp, sz]),
+        "loomhip_gqa_token_frame": (i, [C.POINTER(GqaLayerDescC), sz, C.POINTER(GqaFrameCfg), vp, sz, vp,
+                                        WeightRefDesc, vp, sz]),
         "loomhip_host_alloc": (vp, [sz]),
         "loomhip_host_free": (None, [vp]),
         "loomhip_ec_create": (i, [sz, sz, sz, sz, C.POINTER(vp)]),

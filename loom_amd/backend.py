@@ -298,6 +298,195 @@ def dequant_dev(t: int, out, w, rows: int, cols: int) -> int:
                  "dequant_dev")
 
 
+# ---- the GQA device cache and frames (src/compute/backend.zig:121-160,
+# 186-191; src/gguf/llama.zig:1067-1108 stepRecorded) ---------------------------
+
+
+def _wref(w):
+    """A WeightRef (or None) as the C ABI's loomhip_weight_ref."""
+    from . import WeightRefDesc
+
+    if w is None:
+        return WeightRefDesc(0, None, 0)
+    return WeightRefDesc(w.ty, _p(w.data), w.data.nbytes)
+
+
+def attnInit(layers: int, ctx_len: int, kvd: int) -> bool:
+    """backend.attnInit: allocate the device K/V cache (fp16); False declines."""
+    return _served(lib().loomhip_attn_init(layers, ctx_len, kvd), "attnInit")
+
+
+def hasKvCache() -> bool:
+    return bool(lib().loomhip_has_kv_cache())
+
+
+def releaseKvCache() -> None:
+    lib().loomhip_release_kv_cache()
+
+
+def kvAppend(li: int, pos: int, k_new: np.ndarray, v_new: np.ndarray) -> bool:
+    """backend.kvAppend: mirror one host cache row into the device cache."""
+    k_new = np.ascontiguousarray(k_new, np.float32)
+    v_new = np.ascontiguousarray(v_new, np.float32)
+    assert k_new.size == v_new.size
+    return _served(lib().loomhip_kv_append(li, pos, _p(k_new), _p(v_new), k_new.size), "kvAppend")
+
+
+def readKvCache(li: int, pos: int, k_out: np.ndarray, v_out: np.ndarray) -> bool:
+    """The read-back that keeps the host cache authoritative: the device rows
+    of layer li at pos (fp16 widened to f32) into k_out / v_out."""
+    assert k_out.dtype == np.float32 and v_out.dtype == np.float32 and k_out.size == v_out.size
+    return _served(lib().loomhip_read_kv(li, pos, _p(k_out), _p(v_out), k_out.size), "readKvCache")
+
+
+def attnHeads(li: int, pos: int, q: np.ndarray, out: np.ndarray, n_heads: int, n_kv_heads: int, hd: int,
+              scale: float) -> bool:
+    """backend.attnHeads: one layer's GQA attention over the device cache
+    (row pos already appended) into out [n_heads * hd]; False declines."""
+    q = np.ascontiguousarray(q, np.float32)
+    assert out.dtype == np.float32 and out.size == n_heads * hd
+    return _served(lib().loomhip_attn_heads(li, pos, _p(q), _p(out), n_heads, n_kv_heads, hd, scale), "attnHeads")
+
+
+@dataclass
+class LayerSpec:
+    """src/compute/cpu.zig:116-138 LayerSpec (a dense GQA layer)."""
+
+    li: int
+    pos: int
+    attn_norm: np.ndarray
+    ffn_norm: np.ndarray
+    eps: float
+    wq: WeightRef
+    wk: WeightRef
+    wv: WeightRef
+    wo: WeightRef
+    gate: WeightRef
+    up: WeightRef
+    down: WeightRef
+    dim: int
+    ffn: int
+    n_heads: int
+    n_kv_heads: int
+    hd: int
+    rope_dim: int
+    rope_base: float
+    rope_neox: bool
+    attn_scale: float
+
+
+def beginFrame() -> bool:
+    return _served(lib().loomhip_begin_frame(), "beginFrame")
+
+
+def frameOpen() -> bool:
+    return bool(lib().loomhip_frame_open())
+
+
+def frameLoadX(x: np.ndarray) -> bool:
+    x = np.ascontiguousarray(x, np.float32)
+    return _served(lib().loomhip_frame_load_x(_p(x), x.size), "frameLoadX")
+
+
+def layerBlock(s: LayerSpec) -> bool:
+    """backend.layerBlock: one whole dense layer recorded into the open
+    frame; False declines before anything of the layer is recorded."""
+    from . import LayerSpecDesc
+
+    d = LayerSpecDesc(s.li, s.pos, _p(s.attn_norm), _p(s.ffn_norm), s.eps, *(_wref(w) for w in (
+        s.wq, s.wk, s.wv, s.wo, s.gate, s.up, s.down)), s.dim, s.ffn, s.n_heads, s.n_kv_heads, s.hd, s.rope_dim,
+        s.rope_base, int(s.rope_neox), s.attn_scale)
+    return _served(lib().loomhip_layer_block(C.byref(d)), "layerBlock")
+
+
+def endFrame() -> None:
+    check(lib().loomhip_end_frame(), "endFrame")
+
+
+def frameStoreX(x: np.ndarray) -> bool:
+    assert x.dtype == np.float32
+    return _served(lib().loomhip_frame_store_x(_p(x), x.size), "frameStoreX")
+
+
+@dataclass
+class GqaLayerDesc:
+    """The qwen3moe counterpart of src/compute/cpu.zig:73 MlaLayerDesc: norms as
+    f32 arrays, weights as WeightRefs (3D expert tensors whole), q_norm /
+    k_norm / router_bias / sel_bias / shexp optional."""
+
+    attn_norm: np.ndarray
+    ffn_norm: np.ndarray
+    wq: WeightRef
+    wk: WeightRef
+    wv: WeightRef
+    wo: WeightRef
+    is_moe: bool
+    q_norm: np.ndarray | None = None
+    k_norm: np.ndarray | None = None
+    router: WeightRef | None = None
+    router_bias: np.ndarray | None = None
+    sel_bias: np.ndarray | None = None
+    gate: WeightRef | None = None
+    up: WeightRef | None = None
+    down: WeightRef | None = None
+    shexp: tuple | None = None  # (gate, up, down) WeightRefs
+    ffn: int = 0
+    shexp_ffn: int = 0
+    dgate: WeightRef | None = None
+    dup: WeightRef | None = None
+    ddown: WeightRef | None = None
+    dffn: int = 0
+
+
+@dataclass
+class GqaFrameCfg:
+    """MlaFrameCfg's GQA counterpart, with its RoutedCfg."""
+
+    dim: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    rope_dim: int
+    eps: float
+    scale: float
+    rope_base: float
+    rope_neox: bool
+    routed: RoutedCfg | None = None
+    gating: int = GATING_SOFTMAX
+
+
+def gqaTokenFrame(descs: list, fc: GqaFrameCfg, x: np.ndarray, pos: int, out_norm: np.ndarray, lm_head: WeightRef,
+                  logits: np.ndarray) -> bool:
+    """The whole token as one submission (mlaTokenFrame's form): x [dim] in
+    (after embedding) and out (after the last layer), logits [vocab] out;
+    the device cache holds this position's rows afterwards (readKvCache).
+    False declines before anything is launched."""
+    from . import GqaFrameCfg as CCfg, GqaLayerDescC
+
+    arr = (GqaLayerDescC * len(descs))()
+    for d, c in zip(descs, arr):
+        sh = d.shexp or (None, None, None)
+        c.attn_norm, c.ffn_norm, c.q_norm, c.k_norm = (_p(a) for a in (d.attn_norm, d.ffn_norm, d.q_norm, d.k_norm))
+        c.wq, c.wk, c.wv, c.wo = (_wref(w) for w in (d.wq, d.wk, d.wv, d.wo))
+        c.is_moe = int(d.is_moe)
+        c.router = _wref(d.router)
+        c.router_bias, c.sel_bias = _p(d.router_bias), _p(d.sel_bias)
+        c.gate, c.up, c.down = (_wref(w) for w in (d.gate, d.up, d.down))
+        c.shexp_gate, c.shexp_up, c.shexp_down = (_wref(w) for w in sh)
+        c.ffn, c.shexp_ffn = d.ffn, d.shexp_ffn
+        c.dgate, c.dup, c.ddown = (_wref(w) for w in (d.dgate, d.dup, d.ddown))
+        c.dffn = d.dffn
+    r = fc.routed
+    cfg = CCfg(fc.dim, fc.n_heads, fc.n_kv_heads, fc.head_dim, fc.rope_dim, fc.eps, fc.scale, fc.rope_base,
+               int(fc.rope_neox), r.n_expert if r else 0, r.n_used if r else 0,
+               (GATING_SIGMOID if r.gating_sigmoid else fc.gating) if r else fc.gating,
+               int(r.weights_norm) if r else 1, r.weights_scale if r else 1.0)
+    assert x.dtype == np.float32 and logits.dtype == np.float32 and x.flags.c_contiguous
+    rc = lib().loomhip_gqa_token_frame(arr, len(descs), C.byref(cfg), _p(x), pos, _p(out_norm), _wref(lm_head),
+                                       _p(logits), logits.size)
+    return _served(rc, "gqaTokenFrame")
+
+
 # ---- MLA attention over the compressed cache (src/compute/backend.zig:162-169,
 # 193-197; src/gguf/deepseek.zig:851-1048) ----------------------------------
 

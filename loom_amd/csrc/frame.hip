@@ -32,8 +32,7 @@
 // positions softmax's sum and P.V are a split-context merge.  Last-bit
 // differences from these can move one int8 step of a quantized matvec
 // input (the 2e-3 layer/logit tolerance).
-#include "frame.hpp"
-#include "runtime.hpp"
+#include "frame_host.hpp"
 
 #include <cmath>
 #include <string>
@@ -933,6 +932,7 @@ __global__ __launch_bounds__(64) void argmax_merge_kernel(const float *__restric
 
 // ---- host -------------------------------------------------------------------------
 
+
 static Scratch g_frame; // per-call workspace
 
 // RoPE tables computed on the host in ropeTheta's expressions
@@ -966,18 +966,6 @@ static const float *rope_table(int ctx, int rope_dim, float base) {
     tables[key] = d;
     return d;
 }
-
-struct FrameWs {
-    float *x, *normed, *q, *k, *v, *qrot, *part, *act, *amax_v;
-    float *S, *att; // PARITY attention: scores / p [n][n_heads][s_stride], output [n][qd]
-    int s_stride;
-    uint16_t *qsplit; // the rotated queries as (f16 hi, f16 lo) planes, [2][n][qd]
-    int *amax_i;
-    QAct qa_dim, qa_att, qa_ffn;
-    const DmmvGroup *groups; // lanes in groups of nt against plane 0
-    int n_groups, nt;
-    size_t bytes;
-};
 
 static FrameWs frame_layout(char *base, size_t n, const loomhip_model *m, size_t ffn_max,
                             int n_chunks, bool parity) {
@@ -1116,46 +1104,224 @@ int rmsnorm_exact_dev(const float *x, int dim, const float *w, float eps, float 
     return LOOMHIP_OK;
 }
 
-static int frame_check(const loomhip_model *m, size_t n, size_t *ffn_max) {
-    if (!m || !m->layers || n == 0 || n > 256)
+int frame_dims_check(const loomhip_model *m, size_t n) {
+    if (!m || n == 0 || n > 256)
         return fail(LOOMHIP_ERR_ARG, "token_frame: bad model or lane count %zu (1..256)", n);
     const size_t dim = m->dim, hd = m->head_dim, qd = m->n_heads * hd;
     if (dim == 0 || dim % 32 || dim > (size_t)EXACT_NORM_MAX_DIM || qd % 32 || (hd != 48 && hd != 64 && hd != 128) ||
         m->n_kv_heads == 0 || m->n_heads % m->n_kv_heads || m->n_heads / m->n_kv_heads > MAX_G ||
-        m->rope_dim > hd || m->rope_dim % 2 || m->ctx_len == 0 || m->vocab == 0)
+        m->rope_dim > hd || m->rope_dim % 2 || m->ctx_len == 0)
         return fail(LOOMHIP_DECLINED, "token_frame: dims not served (dim %zu, head_dim %zu, heads %zu/%zu)",
                     dim, hd, m->n_heads, m->n_kv_heads);
-    const int qb_out = act_block(m->output_t);
-    if (!dmmv_supported(m->output_t, (int)dim) || (qb_out == 256 && dim % 256))
-        return fail(LOOMHIP_DECLINED, "token_frame: output type %d not served", m->output_t);
-    *ffn_max = 0;
-    for (size_t li = 0; li < m->n_layers; li++) {
-        const loomhip_layer &l = m->layers[li];
-        const int qb = act_block(l.wq_t);
-        if (act_block(l.wk_t) != qb || act_block(l.wv_t) != qb || !dmmv_supported(l.wq_t, (int)dim) ||
-            !dmmv_supported(l.wk_t, (int)dim) || !dmmv_supported(l.wv_t, (int)dim) ||
-            !dmmv_supported(l.wo_t, (int)qd) || (qb == 256 && dim % 256) ||
-            (act_block(l.wo_t) == 256 && qd % 256))
-            return fail(LOOMHIP_DECLINED, "token_frame: layer %zu attention types not served", li);
-        if (l.is_moe) {
-            if (l.moe.dim != dim)
-                return fail(LOOMHIP_ERR_ARG, "token_frame: layer %zu MoE dim %zu != %zu", li, l.moe.dim, dim);
-            if (int rc = moe_frame_check(&l.moe, n))
-                return rc;
-        } else {
-            const int gq = act_block(l.ffn_gate_t);
-            if (l.ffn_gate_t != l.ffn_up_t || !dmmv_supported(l.ffn_gate_t, (int)dim) ||
-                !dmmv_supported(l.ffn_down_t, (int)l.ffn) || (gq == 256 && dim % 256) ||
-                (act_block(l.ffn_down_t) == 256 && l.ffn % 256) || l.ffn % 32)
-                return fail(LOOMHIP_DECLINED, "token_frame: layer %zu dense FFN types not served", li);
-            *ffn_max = l.ffn > *ffn_max ? l.ffn : *ffn_max;
-        }
-    }
     if (m->numerics != LOOMHIP_NUMERICS_PARITY && m->numerics != LOOMHIP_NUMERICS_FAST)
         return fail(LOOMHIP_ERR_ARG, "token_frame: unknown numerics mode %d", m->numerics);
     if (m->numerics == LOOMHIP_NUMERICS_PARITY && m->ctx_len > (size_t)EXACT_MAX_CTX)
         return fail(LOOMHIP_DECLINED, "token_frame: PARITY attention serves contexts up to %d (ctx_len %zu)",
                     EXACT_MAX_CTX, m->ctx_len);
+    return LOOMHIP_OK;
+}
+
+int frame_layer_check(const loomhip_model *m, const loomhip_layer &l, size_t li, size_t n, size_t *ffn_max) {
+    const size_t dim = m->dim, qd = m->n_heads * m->head_dim;
+    const int qb = act_block(l.wq_t);
+    if (act_block(l.wk_t) != qb || act_block(l.wv_t) != qb || !dmmv_supported(l.wq_t, (int)dim) ||
+        !dmmv_supported(l.wk_t, (int)dim) || !dmmv_supported(l.wv_t, (int)dim) ||
+        !dmmv_supported(l.wo_t, (int)qd) || (qb == 256 && dim % 256) || (act_block(l.wo_t) == 256 && qd % 256))
+        return fail(LOOMHIP_DECLINED, "token_frame: layer %zu attention types not served", li);
+    if (!l.attn_norm || !l.ffn_norm || !l.wq || !l.wk || !l.wv || !l.wo)
+        return fail(LOOMHIP_ERR_ARG, "token_frame: layer %zu misses a norm or an attention weight", li);
+    if (l.is_moe) {
+        if (l.moe.dim != dim)
+            return fail(LOOMHIP_ERR_ARG, "token_frame: layer %zu MoE dim %zu != %zu", li, l.moe.dim, dim);
+        return moe_frame_check(&l.moe, n);
+    }
+    const int gq = act_block(l.ffn_gate_t);
+    if (l.ffn_gate_t != l.ffn_up_t || !dmmv_supported(l.ffn_gate_t, (int)dim) ||
+        !dmmv_supported(l.ffn_down_t, (int)l.ffn) || (gq == 256 && dim % 256) ||
+        (act_block(l.ffn_down_t) == 256 && l.ffn % 256) || l.ffn % 32 || l.ffn == 0)
+        return fail(LOOMHIP_DECLINED, "token_frame: layer %zu dense FFN types not served", li);
+    if (!l.ffn_gate || !l.ffn_up || !l.ffn_down)
+        return fail(LOOMHIP_ERR_ARG, "token_frame: layer %zu misses a dense FFN weight", li);
+    *ffn_max = l.ffn > *ffn_max ? l.ffn : *ffn_max;
+    return LOOMHIP_OK;
+}
+
+int frame_check(const loomhip_model *m, size_t n, size_t *ffn_max) {
+    if (int rc = frame_dims_check(m, n))
+        return rc;
+    if (!m->layers || m->vocab == 0)
+        return fail(LOOMHIP_ERR_ARG, "token_frame: no layers or no vocabulary");
+    const int qb_out = act_block(m->output_t);
+    if (!dmmv_supported(m->output_t, (int)m->dim) || (qb_out == 256 && m->dim % 256))
+        return fail(LOOMHIP_DECLINED, "token_frame: output type %d not served", m->output_t);
+    *ffn_max = 0;
+    for (size_t li = 0; li < m->n_layers; li++)
+        if (int rc = frame_layer_check(m, m->layers[li], li, n, ffn_max))
+            return rc;
+    return LOOMHIP_OK;
+}
+
+int frame_setup(const loomhip_model *m, size_t n, size_t ffn_max, float scale, int32_t *pos, uint16_t *kc,
+                uint16_t *vc, hipStream_t st, FrameCall &c) {
+    c.n = n;
+    c.st = st;
+    c.pos = pos;
+    c.kc = kc;
+    c.vc = vc;
+    c.n_chunks = (int)((m->ctx_len + ATT_TC - 1) / ATT_TC);
+    c.parity = m->numerics == LOOMHIP_NUMERICS_PARITY;
+    const FrameWs probe = frame_layout(nullptr, n, m, ffn_max, c.n_chunks, c.parity);
+    if (int rc = g_frame.reserve(probe.bytes))
+        return rc;
+    c.w = frame_layout((char *)g_frame.ptr, n, m, ffn_max, c.n_chunks, c.parity);
+    c.w.nt = pick_nt((int)n);
+    c.w.groups = dense_groups((int)n, c.w.nt, &c.w.n_groups); // built once per lane count, before any capture
+    if (!c.w.groups)
+        return fail(LOOMHIP_ERR_HIP, "token_frame: group table");
+    FrameDims &D = c.D;
+    D.dim = (int)m->dim;
+    D.hd = (int)m->head_dim;
+    D.n_heads = (int)m->n_heads;
+    D.n_kv = (int)m->n_kv_heads;
+    D.qd = D.n_heads * D.hd;
+    D.kvd = D.n_kv * D.hd;
+    D.ctx = (int)m->ctx_len;
+    D.rope_dim = (int)m->rope_dim;
+    D.rope_neox = m->rope_neox;
+    D.n_layers = (int)m->n_layers;
+    D.vocab = (int)m->vocab;
+    D.rope_base = m->rope_base;
+    D.eps = m->eps;
+    D.scale = scale;
+    const int G = D.n_heads / D.n_kv;
+    c.att_lds = (size_t)G * D.hd * 4 + (size_t)16 * ATT_TC * 4 + (size_t)ATT_TC * (D.hd + 8) * 2 +
+                (size_t)ATT_TC * (D.hd + 2) * 2;
+    if (c.att_lds > 64 * 1024)
+        return fail(LOOMHIP_DECLINED, "token_frame: attention tile exceeds LDS (%zu B)", c.att_lds);
+    // the direct form keeps p and the values only
+    c.att_lds_direct = (size_t)16 * ATT_TC_DIRECT * 4 + (size_t)ATT_TC_DIRECT * (D.hd + 2) * 2;
+    c.cmb_lds = (4 * 256 + (size_t)CMB_NH * c.n_chunks) * 4;
+    if (c.cmb_lds > 64 * 1024)
+        return fail(LOOMHIP_DECLINED, "token_frame: context %zu exceeds the merge's LDS", m->ctx_len);
+    c.rope_cs = m->rope_cs ? m->rope_cs : rope_table(D.ctx, D.rope_dim, D.rope_base);
+    if (!c.rope_cs)
+        return fail(LOOMHIP_ERR_HIP, "token_frame: rope table");
+    return LOOMHIP_OK;
+}
+
+int frame_layer(const FrameCall &c, const loomhip_layer &l, size_t li, uint32_t *ids) {
+    const FrameDims &D = c.D;
+    const FrameWs &w = c.w;
+    const size_t n = c.n;
+    const bool parity = c.parity;
+    hipStream_t st = c.st;
+    // attention block (llama.zig:1127-1201)
+    // layer 0 normalises the embedding row: exact sum in either mode
+    launch_norm(act_block(l.wq_t), w.x, D.dim, l.attn_norm, D.eps, w.qa_dim, nullptr, n, st, parity || li == 0);
+    if (!frame_qkv(l, D, w, n, st))
+        return fail(LOOMHIP_ERR_ARG, "token_frame: q/k/v matvec declined");
+    // few lanes: norm/rope/append inside the attention launch; more lanes:
+    // once per head in their own launch (the attention is then
+    // throughput-bound and the fused prologue would repeat per chunk)
+    const bool fuse_rope = n <= ATT_FUSE_MAX_LANES;
+    // FAST with rope done apart and an MFMA head size: the attention takes
+    // its query operands pre-split and its keys straight from HBM
+    const bool direct = !parity && !fuse_rope && D.hd % 32 == 0;
+    uint16_t *qsplit = direct ? w.qsplit : nullptr;
+    if (!fuse_rope) {
+        hipLaunchKernelGGL(qk_rope_kernel, dim3(D.n_heads + D.n_kv, n), dim3(64), 0, st, D, w.q, w.k, w.v,
+                           l.q_norm, l.k_norm, c.pos, (int)li, c.rope_cs, w.qrot, qsplit, c.kc, c.vc);
+        note_launch();
+    }
+    const float *qin = fuse_rope ? w.q : w.qrot;
+    if (parity) {
+        // the reference's own order over the whole context: scores, softmax, P.V
+        // few lanes: P.V quantizes wo's input itself
+        const bool qfuse = attn_exact_quant_fusable(D, n);
+        if (!launch_attn_exact(D, qin, w.k, w.v, l.q_norm, l.k_norm, c.rope_cs, c.kc, c.vc, c.pos, (int)li,
+                               fuse_rope, w.S, w.s_stride, w.att, n, qfuse ? l.wo_t : -1, w.qa_att, st))
+            return fail(LOOMHIP_ERR_ARG, "token_frame: exact attention declined");
+        if (!qfuse)
+            launch_quant_act(l.wo_t, w.att, D.qd, D.qd, (int)n, w.qa_att, st);
+    } else {
+        const int ph = prof_begin(LOOMHIP_KT_ATTN, st);
+        const dim3 agrid(c.n_chunks, D.n_kv, n);
+        // records of the merge: chunks of ATT_TC positions, ATT_TC_DIRECT direct
+        const int span = direct ? ATT_TC_DIRECT : ATT_TC;
+        const int n_rec = (D.ctx + span - 1) / span;
+        if (direct) {
+            const dim3 dgrid(n_rec, D.n_kv, n);
+            if (D.hd == 128)
+                hipLaunchKernelGGL((attn_direct_kernel<128, ATT_TC_DIRECT>), dgrid, dim3(64 * ATT_WAVES),
+                                   c.att_lds_direct, st, D, c.kc, c.vc, c.pos, (int)li, n_rec, qsplit, w.part);
+            else
+                hipLaunchKernelGGL((attn_direct_kernel<64, ATT_TC_DIRECT>), dgrid, dim3(64 * ATT_WAVES),
+                                   c.att_lds_direct, st, D, c.kc, c.vc, c.pos, (int)li, n_rec, qsplit, w.part);
+        } else if (D.hd == 128)
+            hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(64 * ATT_WAVES), c.att_lds, st, D, qin, w.k,
+                               w.v, l.q_norm, l.k_norm, c.rope_cs, c.kc, c.vc, c.pos, (int)li, c.n_chunks, 1,
+                               fuse_rope ? 1 : 0, w.part);
+        else if (D.hd == 64)
+            hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(64 * ATT_WAVES), c.att_lds, st, D, qin, w.k,
+                               w.v, l.q_norm, l.k_norm, c.rope_cs, c.kc, c.vc, c.pos, (int)li, c.n_chunks, 1,
+                               fuse_rope ? 1 : 0, w.part);
+        else
+            hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(64 * ATT_WAVES), c.att_lds, st, D, qin, w.k,
+                               w.v, l.q_norm, l.k_norm, c.rope_cs, c.kc, c.vc, c.pos, (int)li, c.n_chunks, 1,
+                               fuse_rope ? 1 : 0, w.part);
+        prof_end(ph, st);
+        note_launch();
+        if (act_block(l.wo_t) == 256)
+            hipLaunchKernelGGL(attn_combine_kernel<256>, dim3((D.qd + 255) / 256, n), dim3(1024), c.cmb_lds, st,
+                               D, w.part, c.pos, n_rec, span, direct ? 1 : 0, w.qa_att);
+        else
+            hipLaunchKernelGGL(attn_combine_kernel<32>, dim3((D.qd + 255) / 256, n), dim3(1024), c.cmb_lds, st,
+                               D, w.part, c.pos, n_rec, span, direct ? 1 : 0, w.qa_att);
+        note_launch();
+    }
+    if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_WO, true, 16))
+        return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
+    // FFN block (llama.zig:1203-1224)
+    if (l.is_moe) {
+        const int combine = n == 1 ? LOOMHIP_COMBINE_SELECTION_ADD : LOOMHIP_COMBINE_EXPERT_ASC;
+        if (moe_decode_fusable(&l.moe, n, parity))
+            // the router launch applies the rmsnorm itself (PARITY: one
+            // lane, the squares summed in order in every work group)
+            return moe_layer_fused_norm(&l.moe, w.x, l.ffn_norm, D.eps, n, combine, w.x, ids, parity, st);
+        launch_norm(0, w.x, D.dim, l.ffn_norm, D.eps, QAct{}, w.normed, n, st, parity);
+        return loomhip_moe_layer_dev(&l.moe, w.normed, n, combine, w.x, ids, nullptr, st);
+    }
+    launch_norm(act_block(l.ffn_gate_t), w.x, D.dim, l.ffn_norm, D.eps, w.qa_dim, nullptr, n, st, parity);
+    DmmvParams p{};
+    p.w = (const uint8_t *)l.ffn_gate;
+    p.w2 = (const uint8_t *)l.ffn_up;
+    p.rows = (int)l.ffn;
+    p.cols = D.dim;
+    p.xq = w.qa_dim.q;
+    p.xd = w.qa_dim.d;
+    p.xs = w.qa_dim.s;
+    p.pair_src = g_ctx.iota;
+    p.pair_dst = g_ctx.iota;
+    p.groups = w.groups;
+    p.n_groups = w.n_groups;
+    p.out = w.act;
+    p.out_stride = (int)l.ffn;
+    p.rpw = dmmv_pick_rpw(l.ffn_gate_t, D.dim, (int)l.ffn, w.n_groups, w.nt, true);
+    if (!launch_dmmv(l.ffn_gate_t, w.nt, true, p, st))
+        return fail(LOOMHIP_ERR_ARG, "token_frame: gate/up matvec declined");
+    launch_quant_act(l.ffn_down_t, w.act, (int)l.ffn, (int)l.ffn, (int)n, w.qa_ffn, st);
+    if (!frame_matvec(l.ffn_down_t, l.ffn_down, D.dim, (int)l.ffn, w, n, w.qa_ffn, w.x, 1, st))
+        return fail(LOOMHIP_ERR_ARG, "token_frame: down matvec declined");
+    return LOOMHIP_OK;
+}
+
+int frame_head(const FrameCall &c, const loomhip_model *m, float *logits) {
+    const FrameDims &D = c.D;
+    launch_norm(act_block(m->output_t), c.w.x, D.dim, m->out_norm, D.eps, c.w.qa_dim, nullptr, c.n, c.st,
+                c.parity);
+    if (!frame_matvec(m->output_t, m->output, D.vocab, D.dim, c.w, c.n, c.w.qa_dim, logits, 0, c.st,
+                      LOOMHIP_KT_HEAD, true))
+        return fail(LOOMHIP_ERR_ARG, "token_frame: output matvec declined");
     return LOOMHIP_OK;
 }
 
@@ -1182,168 +1348,25 @@ int loomhip_token_frame_dev(const loomhip_model *m, const uint32_t *tokens, int3
     size_t ffn_max = 0;
     if (int rc = frame_check(m, n, &ffn_max))
         return rc;
-    hipStream_t st = stream_of(stream);
-    const int n_chunks = (int)((m->ctx_len + ATT_TC - 1) / ATT_TC);
-    const bool parity = m->numerics == LOOMHIP_NUMERICS_PARITY;
-    const FrameWs probe = frame_layout(nullptr, n, m, ffn_max, n_chunks, parity);
-    if (int rc = g_frame.reserve(probe.bytes))
+    FrameCall c;
+    if (int rc = frame_setup(m, n, ffn_max, 1.0f / sqrtf((float)m->head_dim), pos, k_cache, v_cache,
+                             stream_of(stream), c)) // llama.zig attn scale
         return rc;
-    FrameWs w = frame_layout((char *)g_frame.ptr, n, m, ffn_max, n_chunks, parity);
-    w.nt = pick_nt((int)n);
-    w.groups = dense_groups((int)n, w.nt, &w.n_groups); // built once per lane count, before any capture
-    if (!w.groups)
-        return fail(LOOMHIP_ERR_HIP, "token_frame: group table");
-    FrameDims D;
-    D.dim = (int)m->dim;
-    D.hd = (int)m->head_dim;
-    D.n_heads = (int)m->n_heads;
-    D.n_kv = (int)m->n_kv_heads;
-    D.qd = D.n_heads * D.hd;
-    D.kvd = D.n_kv * D.hd;
-    D.ctx = (int)m->ctx_len;
-    D.rope_dim = (int)m->rope_dim;
-    D.rope_neox = m->rope_neox;
-    D.n_layers = (int)m->n_layers;
-    D.vocab = (int)m->vocab;
-    D.rope_base = m->rope_base;
-    D.eps = m->eps;
-    D.scale = 1.0f / sqrtf((float)m->head_dim); // llama.zig attn scale
-    const int G = D.n_heads / D.n_kv;
-    const size_t att_lds = (size_t)G * D.hd * 4 + (size_t)16 * ATT_TC * 4 + (size_t)ATT_TC * (D.hd + 8) * 2 +
-                           (size_t)ATT_TC * (D.hd + 2) * 2;
-    if (att_lds > 64 * 1024)
-        return fail(LOOMHIP_DECLINED, "token_frame: attention tile exceeds LDS (%zu B)", att_lds);
-    // the direct form keeps p and the values only
-    const size_t att_lds_direct = (size_t)16 * ATT_TC_DIRECT * 4 + (size_t)ATT_TC_DIRECT * (D.hd + 2) * 2;
-    const size_t cmb_lds = (4 * 256 + (size_t)CMB_NH * n_chunks) * 4;
-    if (cmb_lds > 64 * 1024)
-        return fail(LOOMHIP_DECLINED, "token_frame: context %zu exceeds the merge's LDS", m->ctx_len);
-
-    const float *rope_cs = m->rope_cs ? m->rope_cs : rope_table(D.ctx, D.rope_dim, D.rope_base);
-    if (!rope_cs)
-        return fail(LOOMHIP_ERR_HIP, "token_frame: rope table");
-    hipLaunchKernelGGL(embed_kernel, dim3((D.dim + 255) / 256, n), dim3(256), 0, st, m->embed_t,
-                       (const uint8_t *)m->embed, D.vocab, D.dim, tokens, w.x);
+    hipLaunchKernelGGL(embed_kernel, dim3((c.D.dim + 255) / 256, n), dim3(256), 0, c.st, m->embed_t,
+                       (const uint8_t *)m->embed, c.D.vocab, c.D.dim, tokens, c.w.x);
     note_launch();
     for (size_t li = 0; li < m->n_layers; li++) {
         const loomhip_layer &l = m->layers[li];
-        // attention block (llama.zig:1127-1201)
-        // layer 0 normalises the embedding row: exact sum in either mode
-        launch_norm(act_block(l.wq_t), w.x, D.dim, l.attn_norm, D.eps, w.qa_dim, nullptr, n, st,
-                    parity || li == 0);
-        if (!frame_qkv(l, D, w, n, st))
-            return fail(LOOMHIP_ERR_ARG, "token_frame: q/k/v matvec declined");
-        // few lanes: norm/rope/append inside the attention launch; more lanes:
-        // once per head in their own launch (the attention is then
-        // throughput-bound and the fused prologue would repeat per chunk)
-        const bool fuse_rope = n <= ATT_FUSE_MAX_LANES;
-        // FAST with rope done apart and an MFMA head size: the attention takes
-        // its query operands pre-split and its keys straight from HBM
-        const bool direct = !parity && !fuse_rope && D.hd % 32 == 0;
-        uint16_t *qsplit = direct ? w.qsplit : nullptr;
-        if (!fuse_rope) {
-            hipLaunchKernelGGL(qk_rope_kernel, dim3(D.n_heads + D.n_kv, n), dim3(64), 0, st, D, w.q, w.k, w.v,
-                               l.q_norm, l.k_norm, pos, (int)li, rope_cs, w.qrot, qsplit, k_cache, v_cache);
-            note_launch();
-        }
-        const float *qin = fuse_rope ? w.q : w.qrot;
-        if (parity) {
-            // the reference's own order over the whole context: scores, softmax, P.V
-            // few lanes: P.V quantizes wo's input itself
-            const bool qfuse = attn_exact_quant_fusable(D, n);
-            if (!launch_attn_exact(D, qin, w.k, w.v, l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li,
-                                   fuse_rope, w.S, w.s_stride, w.att, n, qfuse ? l.wo_t : -1, w.qa_att, st))
-                return fail(LOOMHIP_ERR_ARG, "token_frame: exact attention declined");
-            if (!qfuse)
-                launch_quant_act(l.wo_t, w.att, D.qd, D.qd, (int)n, w.qa_att, st);
-            if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_WO, true, 16))
-                return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
-        } else {
-        const int ph = prof_begin(LOOMHIP_KT_ATTN, st);
-        const dim3 agrid(n_chunks, D.n_kv, n);
-        // records of the merge: chunks of ATT_TC positions, ATT_TC_DIRECT direct
-        const int span = direct ? ATT_TC_DIRECT : ATT_TC;
-        const int n_rec = (int)((m->ctx_len + span - 1) / span);
-        if (direct) {
-            const dim3 dgrid(n_rec, D.n_kv, n);
-            if (D.hd == 128)
-                hipLaunchKernelGGL((attn_direct_kernel<128, ATT_TC_DIRECT>), dgrid, dim3(64 * ATT_WAVES),
-                                   att_lds_direct, st, D, k_cache, v_cache, pos, (int)li, n_rec, qsplit, w.part);
-            else
-                hipLaunchKernelGGL((attn_direct_kernel<64, ATT_TC_DIRECT>), dgrid, dim3(64 * ATT_WAVES),
-                                   att_lds_direct, st, D, k_cache, v_cache, pos, (int)li, n_rec, qsplit, w.part);
-        } else if (D.hd == 128)
-            hipLaunchKernelGGL(attn_partial_kernel<128>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
-                               l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
-                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
-        else if (D.hd == 64)
-            hipLaunchKernelGGL(attn_partial_kernel<64>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
-                               l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
-                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
-        else
-            hipLaunchKernelGGL(attn_partial_kernel<48>, agrid, dim3(64 * ATT_WAVES), att_lds, st, D, qin, w.k, w.v,
-                               l.q_norm, l.k_norm, rope_cs, k_cache, v_cache, pos, (int)li, n_chunks,
-                               parity ? 0 : 1, fuse_rope ? 1 : 0, w.part);
-        prof_end(ph, st);
-        note_launch();
-        const int qb_o = act_block(l.wo_t);
-        if (qb_o == 256)
-            hipLaunchKernelGGL(attn_combine_kernel<256>, dim3((D.qd + 255) / 256, n), dim3(1024), cmb_lds, st,
-                               D, w.part, pos, n_rec, span, direct ? 1 : 0, w.qa_att);
-        else
-            hipLaunchKernelGGL(attn_combine_kernel<32>, dim3((D.qd + 255) / 256, n), dim3(1024), cmb_lds, st,
-                               D, w.part, pos, n_rec, span, direct ? 1 : 0, w.qa_att);
-        note_launch();
-        if (!frame_matvec(l.wo_t, l.wo, D.dim, D.qd, w, n, w.qa_att, w.x, 1, st, LOOMHIP_KT_WO, true, 16))
-            return fail(LOOMHIP_ERR_ARG, "token_frame: wo matvec declined");
-        }
-        // FFN block (llama.zig:1203-1224)
-        if (l.is_moe) {
-            const int combine = n == 1 ? LOOMHIP_COMBINE_SELECTION_ADD : LOOMHIP_COMBINE_EXPERT_ASC;
-            uint32_t *ids = m->ids_out ? m->ids_out + li * n * l.moe.n_used : nullptr;
-            if (moe_decode_fusable(&l.moe, n, parity)) {
-                // the router launch applies the rmsnorm itself (PARITY: one
-                // lane, the squares summed in order in every work group)
-                if (int rc = moe_layer_fused_norm(&l.moe, w.x, l.ffn_norm, D.eps, n, combine, w.x, ids, parity, st))
-                    return rc;
-                continue;
-            }
-            launch_norm(0, w.x, D.dim, l.ffn_norm, D.eps, QAct{}, w.normed, n, st, parity);
-            if (int rc = loomhip_moe_layer_dev(&l.moe, w.normed, n, combine, w.x, ids, nullptr, st))
-                return rc;
-        } else {
-            launch_norm(act_block(l.ffn_gate_t), w.x, D.dim, l.ffn_norm, D.eps, w.qa_dim, nullptr, n, st,
-                        parity);
-            DmmvParams p{};
-            p.w = (const uint8_t *)l.ffn_gate;
-            p.w2 = (const uint8_t *)l.ffn_up;
-            p.rows = (int)l.ffn;
-            p.cols = D.dim;
-            p.xq = w.qa_dim.q;
-            p.xd = w.qa_dim.d;
-            p.xs = w.qa_dim.s;
-            p.pair_src = g_ctx.iota;
-            p.pair_dst = g_ctx.iota;
-            p.groups = w.groups;
-            p.n_groups = w.n_groups;
-            p.out = w.act;
-            p.out_stride = (int)l.ffn;
-            p.rpw = dmmv_pick_rpw(l.ffn_gate_t, D.dim, (int)l.ffn, w.n_groups, w.nt, true);
-            if (!launch_dmmv(l.ffn_gate_t, w.nt, true, p, st))
-                return fail(LOOMHIP_ERR_ARG, "token_frame: gate/up matvec declined");
-            launch_quant_act(l.ffn_down_t, w.act, (int)l.ffn, (int)l.ffn, (int)n, w.qa_ffn, st);
-            if (!frame_matvec(l.ffn_down_t, l.ffn_down, D.dim, (int)l.ffn, w, n, w.qa_ffn, w.x, 1, st))
-                return fail(LOOMHIP_ERR_ARG, "token_frame: down matvec declined");
-        }
+        uint32_t *ids = m->ids_out && l.is_moe ? m->ids_out + li * n * l.moe.n_used : nullptr;
+        if (int rc = frame_layer(c, l, li, ids))
+            return rc;
     }
     // head (llama.zig:1225-1227) and the greedy pick
-    launch_norm(act_block(m->output_t), w.x, D.dim, m->out_norm, D.eps, w.qa_dim, nullptr, n, st, parity);
-    if (!frame_matvec(m->output_t, m->output, D.vocab, D.dim, w, n, w.qa_dim, logits, 0, st,
-                      LOOMHIP_KT_HEAD, true))
-        return fail(LOOMHIP_ERR_ARG, "token_frame: output matvec declined");
-    hipLaunchKernelGGL(argmax_part_kernel, dim3(ARGMAX_SLICES, n), dim3(256), 0, st, logits, D.vocab, w.amax_v,
-                       w.amax_i);
-    hipLaunchKernelGGL(argmax_merge_kernel, dim3(n), dim3(64), 0, st, w.amax_v, w.amax_i, next, pos);
+    if (int rc = frame_head(c, m, logits))
+        return rc;
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(ARGMAX_SLICES, n), dim3(256), 0, c.st, logits, c.D.vocab,
+                       c.w.amax_v, c.w.amax_i);
+    hipLaunchKernelGGL(argmax_merge_kernel, dim3(n), dim3(64), 0, c.st, c.w.amax_v, c.w.amax_i, next, pos);
     note_launch();
     note_launch();
     const hipError_t e = hipGetLastError();

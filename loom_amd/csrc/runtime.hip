@@ -329,6 +329,7 @@ void loomhip_shutdown(void) {
     ec_release_scratch();
     block_release_cache();
     mla_release();
+    seam_release();
     prof_drain();
     for (hipEvent_t e : g_prof_pool)
         (void)hipEventDestroy(e);

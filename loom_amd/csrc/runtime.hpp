@@ -83,6 +83,7 @@ int moe_layer_check(const loomhip_moe_layer *L, size_t n, bool shexp_ok);
 void ec_release_scratch();
 void block_release_cache();
 void mla_release();
+void seam_release(); // the seam's device K/V cache, frame residual and staging
 // The exact rmsnorm (squares summed in order) of n rows into normed.
 int rmsnorm_exact_dev(const float *x, int dim, const float *w, float eps, float *normed, size_t n, hipStream_t st);
 

@@ -175,6 +175,7 @@ def lib() -> C.CDLL:
             "lo_seq_cache_bytes": (sz, [C.POINTER(Model)]),
             "lo_step": (i, [C.POINTER(Model), C.POINTER(Seq), C.c_uint32, vp]),
             "lo_decode_batch": (i, [C.POINTER(Model), vp, vp, sz, vp]),
+            "lo_attn_heads": (None, [C.POINTER(Model), vp, vp, sz, sz, vp, vp, C.c_float]),
             "lo_set_batch_slip": (None, [i]),
             "lo_lru_create": (vp, [sz]),
             "lo_lru_destroy": (None, [vp]),

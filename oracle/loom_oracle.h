@@ -189,6 +189,10 @@ size_t lo_seq_cache_bytes(const lo_model *m);
 int lo_step(const lo_model *m, lo_seq *seq, uint32_t token, float *logits);
 /* Continuous batching (llama.decodeBatch): n lanes, out [n][vocab]. */
 int lo_decode_batch(const lo_model *m, lo_seq *seqs, const uint32_t *tokens, size_t n, float *out);
+/* backend.attnHeads (llama.zig:1162-1192): every query head over cache rows
+ * [0, pos] of layer li (a lo_seq cache layout), into attn_out [n_heads][hd]. */
+void lo_attn_heads(const lo_model *m, const void *k_cache, const void *v_cache, size_t li, size_t pos,
+                   const float *q, float *attn_out, float scale);
 /* Test-only planted mistakes in lo_decode_batch (0 = none): 1 cross-lane cache
  * read, 2 K/V row written at the batch index, 3 rope at lane 0's position. */
 void lo_set_batch_slip(int slip);

@@ -102,5 +102,16 @@ class OracleModel:
         return out
 
 
+def attn_heads(om: OracleModel, k_cache: np.ndarray, v_cache: np.ndarray, li: int, pos: int, q: np.ndarray,
+               scale: float) -> np.ndarray:
+    """backend.attnHeads on the oracle: every query head over cache rows
+    [0, pos] of layer li (a lo_seq cache: fp16 bytes as the device keeps)."""
+    q = np.ascontiguousarray(q, np.float32)
+    out = np.empty(om.spec.n_heads * om.spec.head_dim, np.float32)
+    om.o.lib().lo_attn_heads(C.byref(om.model), k_cache.ctypes.data, v_cache.ctypes.data, li, pos,
+                             q.ctypes.data, out.ctypes.data, scale)
+    return out
+
+
 def maxrel(got: np.ndarray, want: np.ndarray) -> float:
     return float(np.abs(got - want).max() / max(float(np.abs(want).max()), 1e-30))

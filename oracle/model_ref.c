@@ -394,6 +394,33 @@ static void rope_vec(const lo_model *m, float *v, size_t pos) {
 static int batch_slip;
 void lo_set_batch_slip(int slip) { batch_slip = slip; }
 
+/* llama.zig:1162-1192, the per-head attention loop (backend.attnHeads'
+ * contract, src/compute/cpu.zig:163-176): for each query head h of KV head
+ * kvh, s_t = dotF32(q_h, k_t) * scale over cache rows [0, pos] of layer li,
+ * softmax, then o_h = sum_t p_t v_t by axpy in position order from +0.
+ * kf/vf hold one KV head's rows widened to f32 (pos + 1 rows of head_dim),
+ * scores pos + 1 floats. */
+static void attn_heads_impl(const lo_model *m, const void *k_cache, const void *v_cache, size_t li, size_t pos,
+                            const float *q, float *attn_out, float scale, float *scores, float *kf, float *vf) {
+    size_t hd = m->head_dim, kvd = kv_dim(m);
+    size_t q_per_kv = m->n_heads / m->n_kv_heads;
+    for (size_t kvh = 0; kvh < m->n_kv_heads; kvh++) {
+        size_t row0 = (li * m->ctx_len) * kvd + kvh * hd;
+        kv_rows(m, k_cache, row0, pos + 1, kvd, kf);
+        kv_rows(m, v_cache, row0, pos + 1, kvd, vf);
+        for (size_t h = kvh * q_per_kv; h < (kvh + 1) * q_per_kv; h++) {
+            const float *qh = q + h * hd;
+            for (size_t t = 0; t <= pos; t++)
+                scores[t] = lo_dot_f32(qh, kf + t * hd, hd) * scale;
+            lo_softmax(scores, pos + 1);
+            float *oh = attn_out + h * hd;
+            memset(oh, 0, hd * sizeof(float));
+            for (size_t t = 0; t <= pos; t++)
+                lo_axpy(oh, vf + t * hd, scores[t], hd);
+        }
+    }
+}
+
 /* llama.zig:1127-1192: q/k/v for one lane, Q/K norm, rope, KV append and the
  * per-head attention loop, into attn_out.  The lane writes its own cache at
  * write_pos and reads rows [0, pos] of read_seq's cache (both its own outside
@@ -414,23 +441,19 @@ static void attention_lane(const lo_model *m, const lo_layer *l, size_t li, lo_s
     size_t base = (li * m->ctx_len + write_pos) * kvd;
     kv_store(m, seq->k_cache, base, k, kvd);
     kv_store(m, seq->v_cache, base, v, kvd);
-    float scale = 1.0f / sqrtf((float)hd);
-    size_t q_per_kv = m->n_heads / m->n_kv_heads;
-    for (size_t kvh = 0; kvh < m->n_kv_heads; kvh++) {
-        size_t row0 = (li * m->ctx_len) * kvd + kvh * hd;
-        kv_rows(m, read_seq->k_cache, row0, pos + 1, kvd, kf);
-        kv_rows(m, read_seq->v_cache, row0, pos + 1, kvd, vf);
-        for (size_t h = kvh * q_per_kv; h < (kvh + 1) * q_per_kv; h++) {
-            const float *qh = q + h * hd;
-            for (size_t t = 0; t <= pos; t++)
-                scores[t] = lo_dot_f32(qh, kf + t * hd, hd) * scale;
-            lo_softmax(scores, pos + 1);
-            float *oh = attn_out + h * hd;
-            memset(oh, 0, hd * sizeof(float));
-            for (size_t t = 0; t <= pos; t++)
-                lo_axpy(oh, vf + t * hd, scores[t], hd);
-        }
-    }
+    attn_heads_impl(m, read_seq->k_cache, read_seq->v_cache, li, pos, q, attn_out, 1.0f / sqrtf((float)hd),
+                    scores, kf, vf);
+}
+
+void lo_attn_heads(const lo_model *m, const void *k_cache, const void *v_cache, size_t li, size_t pos,
+                   const float *q, float *attn_out, float scale) {
+    float *scores = (float *)malloc((pos + 1) * 4);
+    float *kf = (float *)malloc((pos + 1) * m->head_dim * 4), *vf = (float *)malloc((pos + 1) * m->head_dim * 4);
+    f16_table_init();
+    attn_heads_impl(m, k_cache, v_cache, li, pos, q, attn_out, scale, scores, kf, vf);
+    free(scores);
+    free(kf);
+    free(vf);
 }
 
 static void mv(const lo_tensor *t, float *out, const float *x) {

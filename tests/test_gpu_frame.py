@@ -354,3 +354,27 @@ def test_frame_lane_at_negative_position(lh, oracle, n, numerics):
             assert max(rels) == 0.0, rels
         else:
             assert max(rels) <= FAST_BOUND, rels
+
+
+def test_parity_frame_declines_past_its_context_limit(lh):
+    """PARITY attention serves contexts up to 7,936 positions (its softmax
+    row and sequential sum live in LDS): a model with a longer context is
+    refused at load (frame_check, gpuLayersSupported's question) and on the
+    step itself before anything is launched -- no K/V row written, the
+    position unchanged.  FAST numerics serve the same model."""
+    import dataclasses
+
+    import loom_amd
+
+    spec = dataclasses.replace(lh.stories15m(ctx_len=7937), n_layers=1, vocab=512)
+    dm = lh.DeviceModel.synth(spec, seed=2)
+    dec = lh.Decoder(dm, 1)
+    loom_amd.take_launch_count()
+    assert not dm.frame_check(1)
+    assert dec.step() == loom_amd.DECLINED
+    assert loom_amd.take_launch_count() == 0
+    assert int(dec.k_cache.abs().sum().item()) == 0 and int(dec.pos[0].item()) == 0
+    _set_numerics(dm, "fast")
+    assert dm.frame_check(1)
+    assert dec.step() == loom_amd.OK
+    assert int(dec.pos[0].item()) == 1

@@ -321,3 +321,45 @@ def test_decode_batch_planted_mistakes_break_the_invariant(oracle, slip, name):
     finally:
         oracle.lib().lo_set_batch_slip(0)
     assert worst > 10.0, (name, worst)
+
+
+@pytest.mark.parametrize("heads", [(4, 1, 64), (8, 4, 48), (6, 6, 32)])
+def test_attn_heads_against_float64(oracle, heads):
+    """lo_attn_heads (backend.attnHeads' contract, llama.zig:1162-1192; the
+    loop lo_step itself runs) against float64 attention over the same fp16
+    cache: softmax(scale * q_h . K^T) V with head h reading KV head h / G,
+    within 1e-5 of the output's scale.  Planted in the oracle's inputs: the
+    scale off by 2x, or the query heads permuted (another KV head mapping),
+    each miss by far more than the bound."""
+    n_heads, n_kv, hd = heads
+    layers, ctx, li, pos = 3, 40, 1, 33
+    kvd = n_kv * hd
+    rng = np.random.default_rng(n_heads * 100 + hd)
+    kc = rng.standard_normal((layers, ctx, kvd)).astype(np.float16)
+    vc = rng.standard_normal((layers, ctx, kvd)).astype(np.float16)
+    q = rng.standard_normal(n_heads * hd).astype(np.float32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    m = oracle.Model()
+    m.head_dim, m.n_layers, m.n_heads, m.n_kv_heads, m.ctx_len, m.kv_f16 = hd, layers, n_heads, n_kv, ctx, 1
+
+    def run(qv, sc):
+        out = np.empty(n_heads * hd, np.float32)
+        oracle.lib().lo_attn_heads(C.byref(m), kc.ctypes.data, vc.ctypes.data, li, pos, qv.ctypes.data,
+                                   out.ctypes.data, sc)
+        return out
+
+    G = n_heads // n_kv
+    K = kc[li, :pos + 1].astype(np.float64).reshape(pos + 1, n_kv, hd)
+    V = vc[li, :pos + 1].astype(np.float64).reshape(pos + 1, n_kv, hd)
+    want = np.empty((n_heads, hd))
+    for h in range(n_heads):
+        s = K[:, h // G] @ q[h * hd:(h + 1) * hd].astype(np.float64) * scale
+        p = np.exp(s - s.max())
+        want[h] = (p / p.sum()) @ V[:, h // G]
+    want = want.ravel()
+    bound = 1e-5 * np.abs(want).max()
+    assert np.abs(run(q, scale) - want).max() <= bound
+    assert np.abs(run(q, 2 * scale) - want).max() > 100 * bound
+    perm = np.roll(q.reshape(n_heads, hd), G, axis=0).ravel().copy()
+    if n_kv > 1:
+        assert np.abs(run(perm, scale) - want).max() > 100 * bound
