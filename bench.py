@@ -780,10 +780,9 @@ def bench_cache(args):
     """Config 5: the routed block (and its resident shared expert) decoding
     with its experts streamed from pinned host memory through a 64-slot HBM
     LRU (loomhip_moe_layer_cached); tok/s, hit rate and bytes over each link
-    at batch 1 and 64 over args.cache_steps steps each.  The access trace of
-    each run is kept for the oracle's replay (cpu leg).  A second batch-1 run
-    prefetches, after each step, the most-accessed experts not resident
-    (up to 4; loomhip_ec_prefetch), so their fills overlap the next step."""
+    at batch 1 and 64 over args.cache_steps steps each, then the whole block
+    with its MLA attention in front (bench_c5_block).  The access trace of
+    each run is kept for the oracle's replay (cpu leg)."""
     import torch
 
     from loom_amd.expert_cache import ExpertCache
@@ -807,8 +806,8 @@ def bench_cache(args):
     res = {"fill_GBs": round(fill_gbs, 2)}
     traces = {}
     g = torch.Generator(device="cuda").manual_seed(77)
-    for b, steps, prefetch in ((1, args.cache_steps, False), (64, args.cache_steps, False),
-                               (1, args.cache_steps, True)):
+    for b in (1, 64):
+        steps = args.cache_steps
         ec.clear()
         warm = 16
         x = torch.randn(warm + steps, b, C5_DIM, generator=g, device="cuda")
@@ -820,22 +819,16 @@ def bench_cache(args):
         torch.cuda.synchronize()
         s0 = ec.stats
         trace = []
-        resident = None
         t0 = time.perf_counter()
         for i in range(warm, warm + steps):
             ids, _ = ec.moe_layer(desc, x[i], out, b, want_ids=True)
             trace += _c5_gets(ids, b)
-            if prefetch:  # the hottest experts (access counts) not resident, ahead of the next step
-                acc = ec.access_counts()
-                hot = [int(e) for e in np.argsort(-acc, kind="stable")[:C5_SLOTS - 8]]
-                resident = set(trace[-C5_SLOTS:]) if resident is None else resident | set(trace[-8:])
-                ec.prefetch([e for e in hot if e not in resident][:4])
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
         s1 = ec.stats
         hits = (s1.pin_hits - s0.pin_hits) + (s1.lru_hits - s0.lru_hits)
         miss = s1.disk_misses - s0.disk_misses
-        key = f"b{b}" + ("_prefetch" if prefetch else "")
+        key = f"b{b}"
         res[key] = {
             "steps": steps, "tok_s": round(b * steps / dt, 2), "ms_per_step": round(dt / steps * 1e3, 3),
             "hit_rate": round(hits / max(1, hits + miss), 4), "gets_per_step": round((hits + miss) / steps, 2),
@@ -843,15 +836,108 @@ def bench_cache(args):
             "host_link_GBs": round((s1.bytes_read - s0.bytes_read) / dt / 1e9, 2),
             "hbm_hit_bytes_per_step": int(hits * slot / steps),
         }
-        if prefetch:
-            res[key]["prefetched_per_step"] = round((s1.warmup_reads - s0.warmup_reads) / steps, 2)
-        else:
-            # the state the trace starts from is the warm-up's: replayed with it
-            traces[key] = {"warm": warm_trace, "trace": trace,
-                           "counts": (s1.pin_hits - s0.pin_hits, s1.lru_hits - s0.lru_hits, miss)}
+        # the state the trace starts from is the warm-up's: replayed with it
+        traces[key] = {"warm": warm_trace, "trace": trace,
+                       "counts": (s1.pin_hits - s0.pin_hits, s1.lru_hits - s0.lru_hits, miss)}
         log(f"config 5 {key}: {res[key]}")
+        del x
+    res["block"] = bench_c5_block(args, ec, desc, traces, fill_gbs)
     ec.close()
     return res, host, gb, keep, traces
+
+
+C5_LINK_PEAK_GBS = 64.0  # PCIe Gen5 x16, one direction: the host link's ceiling
+
+
+def bench_c5_block(args, ec, desc, traces, fill_gbs):
+    """Config 5 as one block (loomhip_mla_layer_cached_dev): deepseek.step's
+    MLA layer with its experts streamed -- the MLA attention of each sequence
+    over its own compressed cache (128 heads, kv_lora 512, rope 64, Q4_K
+    kv_b), x += wo . heads (Q4_K [7168][16384]), the exact FFN rmsnorm, the
+    256 routed experts through the 64-slot HBM LRU plus the resident shared
+    expert, x += that -- for args.cache_steps sequential decode steps at batch
+    1 and 64.  Each sequence's context grows by one position per step from a
+    prefill of args.ctx seeded latent rows (the projections that would write
+    the new rows are outside the block).  Per-step roofline: the step's HBM
+    bytes at 8 TB/s plus its miss bytes over the host link (at the PCIe Gen5
+    x16 peak, and at the measured fill rate)."""
+    import torch
+
+    from loom_amd import Q4_K
+    from loom_amd import backend as be
+
+    H, nope, rope, kvr, vd = MLA_H, MLA_NOPE, MLA_ROPE, MLA_KVR, MLA_VD
+    scale = float(1.0 / np.sqrt(nope + rope))
+    steps, warm, ctx0 = args.cache_steps, 16, args.ctx
+    g = torch.Generator(device="cuda").manual_seed(83)
+    kvb = be.synth_ggml_dev(Q4_K, H * (nope + vd), kvr, 1, 800, float(1 / np.sqrt(kvr)))
+    attn = be.MlaAttn(Q4_K, kvb, H, nope, vd, kvr, rope, scale)
+    wo = be.repack_dev(Q4_K, be.synth_ggml_dev(Q4_K, C5_DIM, H * vd, 1, 801, 0.02), C5_DIM, H * vd, 1)
+    norm = (1.0 + 0.05 * torch.randn(C5_DIM, generator=g, device="cuda")).contiguous()
+    ring = 16  # distinct queries, cycled (x, fresh every step, drives the routing)
+    res = {}
+    for b in (1, 64):
+        cap = ctx0 + warm + steps
+        caches = [(torch.randn(cap, kvr, generator=g, device="cuda"), torch.randn(cap, rope, generator=g, device="cuda"))
+                  for _ in range(b)]
+        cl, rl = [c for c, _ in caches], [r for _, r in caches]
+        qn = torch.randn(ring, b, H * nope, generator=g, device="cuda")
+        qr = torch.randn(ring, b, H * rope, generator=g, device="cuda")
+        xs = torch.randn(warm + steps, b, C5_DIM, generator=g, device="cuda")
+        ec.clear()
+        warm_trace, trace = [], []
+        for i in range(warm):
+            ids = attn.cached_block(cl, rl, ctx0 + i + 1, qn[i % ring], qr[i % ring], Q4_K, wo, norm, 1e-6, desc, ec,
+                                    xs[i], want_ids=True)
+            warm_trace += _c5_gets(ids, b)
+        torch.cuda.synchronize()
+        s0 = ec.stats
+        t0 = time.perf_counter()
+        for i in range(warm, warm + steps):
+            ids = attn.cached_block(cl, rl, ctx0 + i + 1, qn[i % ring], qr[i % ring], Q4_K, wo, norm, 1e-6, desc, ec,
+                                    xs[i], want_ids=True)
+            trace += _c5_gets(ids, b)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        s1 = ec.stats
+        hits = (s1.pin_hits - s0.pin_hits) + (s1.lru_hits - s0.lru_hits)
+        miss = s1.disk_misses - s0.disk_misses
+        # the step's bytes: attention at the mean context (per sequence), wo,
+        # the router, the hit experts and the shared expert from HBM; the
+        # misses over the host link
+        S = ctx0 + warm + (steps + 1) / 2
+        attn_b = b * sum(mla_launch_bytes(k, S) for k in ("mla_scores", "mla_softmax", "mla_wsum")) + \
+            mla_launch_bytes("mla_absorb", S) + mla_launch_bytes("mla_wv", S)
+        hbm = attn_b + plane_bytes_q4k(C5_DIM, H * vd) + C5_E * C5_DIM * 4 + \
+            hits / steps * C5_EXPERT_BYTES + 3 * plane_bytes_q4k(C5_SFFN, C5_DIM)
+        link = miss / steps * C5_EXPERT_BYTES
+        t_step = dt / steps
+        floor_pcie = hbm / (HBM_PEAK_GBS * 1e9) + link / (C5_LINK_PEAK_GBS * 1e9)
+        floor_fill = hbm / (HBM_PEAK_GBS * 1e9) + link / (fill_gbs * 1e9)
+        key = f"block_b{b}"
+        res[f"b{b}"] = {
+            "steps": steps, "tok_s": round(b * steps / dt, 2), "ms_per_step": round(t_step * 1e3, 3),
+            "hit_rate": round(hits / max(1, hits + miss), 4), "misses_per_step": round(miss / steps, 2),
+            "ctx": [ctx0 + warm + 1, ctx0 + warm + steps],
+            "hbm_bytes_per_step": int(hbm), "host_link_bytes_per_step": int(link),
+            "roofline": {"bound": "hbm + host link", "floor_ms": round(floor_pcie * 1e3, 4),
+                         "frac": round(floor_pcie / t_step, 4), "link_peak_GBs": C5_LINK_PEAK_GBS,
+                         "floor_ms_at_fill_rate": round(floor_fill * 1e3, 4),
+                         "frac_at_fill_rate": round(floor_fill / t_step, 4), "fill_GBs": round(fill_gbs, 2)},
+        }
+        traces[key] = {"warm": warm_trace, "trace": trace,
+                       "counts": (s1.pin_hits - s0.pin_hits, s1.lru_hits - s0.lru_hits, miss)}
+        log(f"config 5 block b{b}: {res[f'b{b}']}")
+        del caches, cl, rl, qn, qr, xs
+        torch.cuda.empty_cache()
+    res["workload"] = (f"config 5 block (loomhip_mla_layer_cached_dev): MLA attention ({H} heads, kv_lora {kvr}, "
+                       f"rope {rope}, Q4_K kv_b) over each sequence's own f32 latent cache, context growing from "
+                       f"{ctx0 + warm + 1} by one per step, Q4_K wo [7168][16384] + residual, exact rmsnorm, "
+                       f"{C5_E} streamed Q4_K experts top-{C5_K} through the {C5_SLOTS}-slot HBM LRU + the "
+                       "resident shared expert + residual")
+    del attn, wo, norm
+    torch.cuda.empty_cache()
+    return res
 
 
 def cache_replay_check(traces):
@@ -1006,8 +1092,8 @@ def main():
             "workload": f"config 5: DeepSeek-V3-class routed block, hidden {C5_DIM}, {C5_E} experts top-{C5_K} "
                         "(sigmoid, renorm, Zipf(1.1) logit bias) plus 1 shared expert (ffn 2048, resident), "
                         "expert ffn 2048, Q4_K gate/up/down (24,772,608 B per expert), 6.34 GB pinned host "
-                        f"backing store, {C5_SLOTS}-slot HBM LRU (1.59 GB); synthetic hidden states; the MLA "
-                        "attention of the block is not included",
+                        f"backing store, {C5_SLOTS}-slot HBM LRU (1.59 GB); synthetic hidden states; b1/b64: the "
+                        "routed block alone; block: the whole block with its MLA attention",
             **c5}
         if not args.no_cpu:
             line["expert_cache"]["cpu_baseline"] = cpu_baseline_c5(host, gb, keep, cores, args.cpu_seconds / 3)

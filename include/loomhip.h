@@ -705,6 +705,25 @@ int loomhip_moe_layer_cached(const loomhip_moe_layer_ec *L, loomhip_ec *ec, cons
                              size_t n_tok, float *out, uint32_t *ids_out, float *gates_out,
                              void *stream);
 
+/* Config 5's block with its routed experts streamed: deepseek.step's MLA
+ * layer with an expert Source behind it (src/gguf/deepseek.zig:1275-1440;
+ * the experts' bytes through the HBM LRU of src/engine/expert_cache.zig).
+ * For n sequences at one position each: the MLA attention of sequence i over
+ * its own cache rows (c_kv[i], k_rope[i]: host arrays of n device pointers,
+ * seq positions each), x_i += attn_output . heads_i, normed_i = rmsnorm(x_i)
+ * * ffn_norm (the squares summed in order), acc = the routed experts read
+ * through the cache plus the resident shared expert (loomhip_moe_layer_
+ * cached: moeRun's selection order at one sequence, moeBatchUnion's
+ * ascending order for more), x_i += acc_i.  x [n][dim], q_nope [n][n_heads *
+ * nope], q_rope [n][n_heads * rope] (device); ids_out (host, [n][n_used],
+ * optional) receives the routed ids.  Synchronises the stream once per call
+ * (the routed ids, as the cached layer does). */
+int loomhip_mla_layer_cached_dev(const loomhip_mla_attn *a, const float *const *c_kv, const float *const *k_rope,
+                                 size_t seq, size_t n, const float *q_nope, const float *q_rope, int attn_out_type,
+                                 const void *attn_out, const float *ffn_norm, float eps,
+                                 const loomhip_moe_layer_ec *moe, loomhip_ec *ec, float *x, uint32_t *ids_out,
+                                 void *stream);
+
 #ifdef __cplusplus
 }
 #endif

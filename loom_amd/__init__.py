@@ -340,6 +340,8 @@ def lib() -> C.CDLL:
                                        vp, i, vp, i, vp, i, vp, i, vp, sz, sz, sz, sz, i, i, f, sz, sz, sz, f]),
         "loomhip_mla_layer_tail_dev": (i, [C.POINTER(MlaAttnDesc), vp, vp, sz, vp, vp, i, vp, vp, f,
                                            C.POINTER(MoeLayerDesc), vp, vp]),
+        "loomhip_mla_layer_cached_dev": (i, [C.POINTER(MlaAttnDesc), C.POINTER(vp), C.POINTER(vp), sz, sz, vp, vp, i,
+                                             vp, vp, f, C.POINTER(MoeLayerEcDesc), vp, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -584,6 +584,22 @@ class MlaAttn:
                                                       _ptr(ffn_norm), eps, C.byref(moe.desc), _ptr(x), _stream()),
                      "mla_layer_tail_dev")
 
+    def cached_block(self, c_kvs, k_ropes, seq: int, q_nope, q_rope, attn_out_t: int, attn_out, ffn_norm,
+                     eps: float, moe_desc, ec, x, want_ids: bool = False):
+        """Config 5's block with its routed experts streamed through the
+        expert cache `ec` (loom_amd.expert_cache.ExpertCache), for n =
+        len(c_kvs) sequences: x [n][dim] in place; returns the routed ids
+        [n][n_used] when want_ids."""
+        n = len(c_kvs)
+        cp = (C.c_void_p * n)(*[_ptr(c) for c in c_kvs])
+        rp = (C.c_void_p * n)(*[_ptr(r) for r in k_ropes])
+        ids = np.zeros((n, moe_desc.n_used), np.uint32) if want_ids else None
+        check(lib().loomhip_mla_layer_cached_dev(C.byref(self.desc), cp, rp, seq, n, _ptr(q_nope), _ptr(q_rope),
+                                                 attn_out_t, _ptr(attn_out), _ptr(ffn_norm), eps,
+                                                 C.byref(moe_desc), ec.h, _ptr(x), _p(ids), _stream()),
+              "mla_layer_cached_dev")
+        return ids
+
 
 class MoeLayer:
     """Device-resident MoE layer (weights are torch uint8 tensors in the

@@ -865,6 +865,61 @@ int loomhip_mla_layer_tail_dev(const loomhip_mla_attn *a, const float *c_kv, con
                          stream_of(stream));
 }
 
+int loomhip_mla_layer_cached_dev(const loomhip_mla_attn *a, const float *const *c_kv, const float *const *k_rope,
+                                 size_t seq, size_t n, const float *q_nope, const float *q_rope, int attn_out_type,
+                                 const void *attn_out, const float *ffn_norm, float eps,
+                                 const loomhip_moe_layer_ec *moe, loomhip_ec *ec, float *x, uint32_t *ids_out,
+                                 void *stream) {
+    if (int rc = require_ready())
+        return rc;
+    std::lock_guard<std::mutex> lk(g_mla.mu);
+    if (!a || !c_kv || !k_rope || !q_nope || !q_rope || !attn_out || !ffn_norm || !moe || !ec || !x || n == 0 ||
+        n > 256)
+        return fail(LOOMHIP_ERR_ARG, "mla_layer_cached_dev: null pointer or %zu sequences (1..256)", n);
+    for (size_t i = 0; i < n; i++)
+        if (!c_kv[i] || !k_rope[i])
+            return fail(LOOMHIP_ERR_ARG, "mla_layer_cached_dev: sequence %zu has no cache", i);
+    if (int rc = mla_check(a, seq))
+        return rc;
+    const size_t hv = a->n_heads * a->vd, dim = moe->dim;
+    if (attn_out_type == LH_F32 || attn_out_type == LH_F16 || !dmmv_supported(attn_out_type, (int)hv))
+        return fail(LOOMHIP_DECLINED, "mla_layer_cached_dev: attn_output type %d with %zu columns not served",
+                    attn_out_type, hv);
+    if (dim == 0 || dim % 32 || dim > 7936)
+        return fail(LOOMHIP_DECLINED, "mla_layer_cached_dev: dim %zu not served", dim);
+    hipStream_t st = stream_of(stream);
+    // heads [n][hv] | proj [n][dim] (then acc) | normed [n][dim]
+    const size_t o_proj = align16(n * hv * 4), o_norm = o_proj + align16(n * dim * 4);
+    if (int rc = reserve_on(g_mla.tail, o_norm + align16(n * dim * 4), st))
+        return rc;
+    float *heads = (float *)g_mla.tail.ptr;
+    float *proj = (float *)((char *)g_mla.tail.ptr + o_proj);
+    float *normed = (float *)((char *)g_mla.tail.ptr + o_norm);
+    const size_t qn = a->n_heads * a->nope, qr = a->n_heads * a->rope;
+    int rc;
+    for (size_t i = 0; i < n; i++) // each sequence's attention over its own cache (deepseek.zig:977-1047)
+        if ((rc = mla_attn_impl(a, c_kv[i], k_rope[i], seq, q_nope + i * qn, q_rope + i * qr, heads + i * hv,
+                                nullptr, st)))
+            return rc;
+    const int nd = (int)(n * dim);
+    // x += attn_output . heads (deepseek.zig:1044-1046): n matvecs in one
+    // launch (bit-identical to one per sequence), then the residual add
+    if ((rc = matvec_dev_impl(attn_out_type, proj, attn_out, heads, n, dim, hv, st)))
+        return rc;
+    hipLaunchKernelGGL(mla_add_kernel, dim3((unsigned)((nd + 255) / 256)), dim3(256), 0, st, x, proj, nd);
+    note_launch();
+    if ((rc = rmsnorm_exact_dev(x, (int)dim, ffn_norm, eps, normed, n, st)))
+        return rc;
+    // the routed experts through the cache plus the resident shared expert,
+    // from +0 into proj's space; then x += acc (deepseek.zig:1325-1440)
+    if ((rc = loomhip_moe_layer_cached(moe, ec, normed, n, proj, ids_out, nullptr, stream)))
+        return rc;
+    hipLaunchKernelGGL(mla_add_kernel, dim3((unsigned)((nd + 255) / 256)), dim3(256), 0, st, x, proj, nd);
+    note_launch();
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? LOOMHIP_OK : hip_fail(e, "mla_layer_cached_dev");
+}
+
 int loomhip_mla_layer_tail(size_t li, size_t pos, float *x, size_t dim, const float *q_nope, size_t qn_len,
                            const float *q_rope, size_t qr_len, int kvb_type, const uint8_t *kv_b, size_t kvb_len,
                            int attn_out_type, const uint8_t *attn_out, const float *ffn_norm, float eps,

@@ -260,6 +260,57 @@ def test_hit_on_a_prefetched_slot_waits_for_its_fill(ec_mod):
     ec.close()
 
 
+def _c5_cached_layer(ec_mod, oracle, E, cap, seed, dim=7168, ffn=2048, sffn=2048, k=8):
+    """Config 5's routed block as the benchmark builds it -- Q4_K experts of
+    hidden `dim` and ffn `ffn`, sigmoid gating with renorm, the Zipf(1.1)
+    popularity as a logit bias, a resident shared expert -- with its E
+    experts in pinned host memory behind a `cap`-slot cache.  Returns the
+    oracle's MoeWeights over the same GGML bytes, the cached layer's
+    descriptor, the cache, and what must stay alive."""
+    import torch
+
+    import npref
+    from loom_amd import GATING_SIGMOID, MoeLayerEcDesc, plane_bytes
+    from loom_amd import backend as be
+
+    rng = np.random.default_rng(seed)
+    gate = npref.pinned_scale_blocks(Q4_K, ffn, dim, rng, planes=E)
+    up = npref.pinned_scale_blocks(Q4_K, ffn, dim, rng, planes=E)
+    down = npref.pinned_scale_blocks(Q4_K, dim, ffn, rng, planes=E)
+    sg = npref.pinned_scale_blocks(Q4_K, sffn, dim, rng)
+    su = npref.pinned_scale_blocks(Q4_K, sffn, dim, rng)
+    sd = npref.pinned_scale_blocks(Q4_K, dim, sffn, rng)
+    router = oracle.normal(E * dim, seed + 1, 0.0, 1.0 / np.sqrt(dim)).reshape(E, dim)
+    ranks = rng.permutation(E) + 1
+    zipf = np.log(1.0 / ranks ** 1.1)
+    rb = (zipf - zipf.mean()).astype(np.float32)
+    w = oracle.MoeWeights(dim, ffn, E, k, router, gate, up, down, Q4_K, Q4_K, Q4_K, router_bias=rb,
+                          gating=oracle.GATING_SIGMOID, weights_norm=True,
+                          shexp=(sg, su, sd, Q4_K, Q4_K, Q4_K, sffn))
+
+    def dev(raw, rows, cols, planes=1):
+        return be.repack_dev(Q4_K, torch.from_numpy(raw).cuda(), rows, cols, planes)
+
+    gb, db = plane_bytes(Q4_K, ffn, dim), plane_bytes(Q4_K, dim, ffn)
+    slot = 2 * gb + db
+    host = ec_mod.HostBuffer(E * slot)
+    hv = torch.from_numpy(host.array)
+    for raw, rows, cols, off, pb in ((gate, ffn, dim, 0, gb), (up, ffn, dim, gb, gb), (down, dim, ffn, 2 * gb, db)):
+        d = dev(raw, rows, cols, E).view(E, pb).cpu()
+        for e in range(E):
+            hv[e * slot + off:e * slot + off + pb].copy_(d[e])
+        del d
+    sh = (dev(sg, sffn, dim), dev(su, sffn, dim), dev(sd, dim, sffn))
+    router_d, rb_d = torch.from_numpy(router).cuda(), torch.from_numpy(rb).cuda()
+    desc = MoeLayerEcDesc(dim, ffn, E, k, GATING_SIGMOID, 1, 1.0, router_d.data_ptr(), rb_d.data_ptr(), None,
+                          Q4_K, Q4_K, 0, 0, gb, 2 * gb, Q4_K, Q4_K, Q4_K, sh[0].data_ptr(), sh[1].data_ptr(),
+                          sh[2].data_ptr(), sffn)
+    ec = ec_mod.ExpertCache(cap, slot, E)
+    for e in range(E):
+        ec.set_source(e, host, e * slot, slot)
+    return w, desc, ec, (host, sh, router_d, rb_d), slot
+
+
 @pytest.mark.parametrize("n_tok,steps", [(1, 6), (64, 2)])
 def test_cached_layer_config5_matches_oracle(ec_mod, oracle, n_tok, steps):
     """Config 5's routed block as the benchmark drives it: loomhip_moe_layer_
@@ -275,47 +326,8 @@ def test_cached_layer_config5_matches_oracle(ec_mod, oracle, n_tok, steps):
     call's own access trace (src/engine/expert_cache.zig:230-249)."""
     import torch
 
-    import npref
-    from loom_amd import GATING_SIGMOID, MoeLayerEcDesc, plane_bytes
-    from loom_amd import backend as be
-
-    E, k, dim, ffn, sffn, cap = 32, 8, 7168, 2048, 2048, 8
-    rng = np.random.default_rng(77)
-    gate = npref.pinned_scale_blocks(Q4_K, ffn, dim, rng, planes=E)
-    up = npref.pinned_scale_blocks(Q4_K, ffn, dim, rng, planes=E)
-    down = npref.pinned_scale_blocks(Q4_K, dim, ffn, rng, planes=E)
-    sg = npref.pinned_scale_blocks(Q4_K, sffn, dim, rng)
-    su = npref.pinned_scale_blocks(Q4_K, sffn, dim, rng)
-    sd = npref.pinned_scale_blocks(Q4_K, dim, sffn, rng)
-    router = oracle.normal(E * dim, 78, 0.0, 1.0 / np.sqrt(dim)).reshape(E, dim)
-    ranks = rng.permutation(E) + 1
-    zipf = np.log(1.0 / ranks ** 1.1)
-    rb = (zipf - zipf.mean()).astype(np.float32)
-    w = oracle.MoeWeights(dim, ffn, E, k, router, gate, up, down, Q4_K, Q4_K, Q4_K, router_bias=rb,
-                          gating=oracle.GATING_SIGMOID, weights_norm=True,
-                          shexp=(sg, su, sd, Q4_K, Q4_K, Q4_K, sffn))
-
-    def dev(raw, rows, cols, planes=1):
-        return be.repack_dev(Q4_K, torch.from_numpy(raw).cuda(), rows, cols, planes)
-
-    gb, db = plane_bytes(Q4_K, ffn, dim), plane_bytes(Q4_K, dim, ffn)
-    slot = 2 * gb + db
-    host = ec_mod.HostBuffer(E * slot)
-    hv = torch.from_numpy(host.array)
-    for part, (raw, rows, cols, off, pb) in enumerate(((gate, ffn, dim, 0, gb), (up, ffn, dim, gb, gb),
-                                                       (down, dim, ffn, 2 * gb, db))):
-        d = dev(raw, rows, cols, E).view(E, pb).cpu()
-        for e in range(E):
-            hv[e * slot + off:e * slot + off + pb].copy_(d[e])
-        del d
-    sh = (dev(sg, sffn, dim), dev(su, sffn, dim), dev(sd, dim, sffn))
-    router_d, rb_d = torch.from_numpy(router).cuda(), torch.from_numpy(rb).cuda()
-    desc = MoeLayerEcDesc(dim, ffn, E, k, GATING_SIGMOID, 1, 1.0, router_d.data_ptr(), rb_d.data_ptr(), None,
-                          Q4_K, Q4_K, 0, 0, gb, 2 * gb, Q4_K, Q4_K, Q4_K, sh[0].data_ptr(), sh[1].data_ptr(),
-                          sh[2].data_ptr(), sffn)
-    ec = ec_mod.ExpertCache(cap, slot, E)
-    for e in range(E):
-        ec.set_source(e, host, e * slot, slot)
+    E, cap, dim = 32, 8, 7168
+    w, desc, ec, keep, slot = _c5_cached_layer(ec_mod, oracle, E, cap, 77)
     trace = []
     try:
         for step in range(steps):
@@ -342,4 +354,70 @@ def test_cached_layer_config5_matches_oracle(ec_mod, oracle, n_tok, steps):
         assert st.bytes_read == st.disk_misses * slot
     finally:
         ec.close()
-        host.free()
+        keep[0].free()
+
+
+@pytest.mark.parametrize("n", [1, 4])
+def test_mla_block_with_streamed_experts_matches_the_engine_sequence(ec_mod, oracle, n):
+    """Config 5 as one block (loomhip_mla_layer_cached_dev): for n sequences
+    each over its own 37-position compressed cache, the MLA attention (16
+    heads of nope 128 / rope 64 / v 128, kv_lora 512, Q4_K kv_b), x += wo .
+    heads (Q4_K [7168][2048]), the exact FFN rmsnorm, the routed experts
+    through an 8-slot cache over 32 streamed experts plus the resident shared
+    expert, x += that -- against the engine's own sequence on the oracle (the
+    host head loop, matvec, residual add, rmsnorm, moeRun + shared expert at
+    one sequence, moeBatchUnion + shared expert for more; deepseek.zig:
+    1044-1046, 1275-1440): x bit-identical over three calls, ids exact, the
+    LRU counts equal to the oracle's replay."""
+    import torch
+
+    from loom_amd import backend as be
+    from mla_case import make_case
+    from recipes import planes
+
+    E, cap, dim, H, nope, vd, kvr, rope, ctx, seq, eps = 32, 8, 7168, 16, 128, 128, 512, 64, 48, 37, 1e-6
+    w, desc, ec, keep, slot = _c5_cached_layer(ec_mod, oracle, E, cap, 91)
+    cases = [make_case(oracle, Q4_K, H, nope, vd, kvr, rope, ctx, seed=200 + i) for i in range(n)]
+    kvb = cases[0].kv_b  # one layer: one kv_b for every sequence
+    attn = be.MlaAttn(Q4_K, torch.from_numpy(kvb).cuda(), H, nope, vd, kvr, rope, cases[0].scale)
+    wo = planes(Q4_K, dim, H * vd, 1, 93)
+    wo_d = be.repack_dev(Q4_K, torch.from_numpy(wo).cuda(), dim, H * vd, 1)
+    rng = np.random.default_rng(94)
+    ffn_norm = (1.0 + 0.05 * rng.standard_normal(dim)).astype(np.float32)
+    caches = [(torch.from_numpy(c.c_kv).cuda(), torch.from_numpy(c.k_rope).cuda()) for c in cases]
+    x = rng.standard_normal((n, dim)).astype(np.float32)
+    xd = torch.from_numpy(x.copy()).cuda()
+    norm_d = torch.from_numpy(ffn_norm).cuda()
+    trace = []
+    try:
+        for call in range(3):
+            qn = rng.standard_normal((n, H * nope)).astype(np.float32)
+            qr = rng.standard_normal((n, H * rope)).astype(np.float32)
+            ids = attn.cached_block([c for c, _ in caches], [r for _, r in caches], seq, torch.from_numpy(qn).cuda(),
+                                    torch.from_numpy(qr).cuda(), Q4_K, wo_d, norm_d, eps, desc, ec, xd,
+                                    want_ids=True)
+            torch.cuda.synchronize()
+            # the engine's sequence on the oracle
+            x1 = np.empty_like(x)
+            for i, c in enumerate(cases):
+                heads, _ = oracle.mla_attn_heads(c.c_kv, c.k_rope, seq, qn[i], qr[i], Q4_K, kvb, H, nope, vd,
+                                                 c.scale)
+                x1[i] = x[i] + oracle.matvec(Q4_K, wo, heads, dim, H * vd)
+            normed = np.stack([oracle.rmsnorm(x1[i], ffn_norm, eps) for i in range(n)])
+            if n == 1:
+                acc, wids, _ = oracle.moe_layer_token(w, normed[0])
+                acc, wids = acc[None], wids[None]
+            else:
+                acc, wids, _ = oracle.moe_batch_union(w, normed, np.zeros_like(normed))
+            x = x1 + acc
+            got = xd.cpu().numpy()
+            print(f"n={n} call {call}: max |diff| {float(np.abs(got - x).max()):.2e}", flush=True)
+            assert np.array_equal(ids, wids), call
+            assert np.array_equal(got.view(np.uint32), x.view(np.uint32)), call
+            trace += list(ids[0]) if n == 1 else sorted(set(ids.ravel().tolist()))
+        counts, _ = oracle.cache_replay(cap, np.array(trace, np.uint32))
+        st = ec.stats
+        assert (st.pin_hits, st.lru_hits, st.disk_misses) == tuple(int(c) for c in counts)
+    finally:
+        ec.close()
+        keep[0].free()
