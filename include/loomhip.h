@@ -531,6 +531,53 @@ int loomhip_mla_layer_tail_dev(const loomhip_mla_attn *a, const float *c_kv, con
                                const float *ffn_norm, float eps, const loomhip_moe_layer *moe, float *x,
                                void *stream);
 
+/* mlaTokenFrame (src/compute/backend.zig:186-191; cpu.zig:73-79; the Vulkan
+ * arm src/vulkan/backend.zig:905-1000): the whole MLA token as one
+ * submission over the device cache of mlaInit, one MlaLayerDesc per layer.
+ * In: the residual stream after embedding (x [dim], host).  Per layer, the
+ * engine's own sequence (deepseek.zig:851-1048 attnLayer, 1275-1440 step):
+ * normed = rmsnorm(x) * attn_norm; q = wq . normed (the direct-q path);
+ * kv_a = kv_a_mqa . normed; the cache row c_kv = rmsnorm(kv_a[0, kvr)) *
+ * kv_a_norm and k_rope = rope(kv_a[kvr, kvr + rope), pos); q's rope slice of
+ * every head rotated; the attention (loomhip_mla_attn_dev's order);
+ * x += attn_output . heads; normed = rmsnorm(x) * ffn_norm; then the routed
+ * MoE (f32 router, RoutedCfg; moeRun's selection order; the shared expert
+ * when shexp_gate.data is set) or the dense SwiGLU FFN, and x += that.  Then
+ * logits = lm_head . (rmsnorm(x) * out_norm).  Out: x after the last layer
+ * and logits [vocab]; the cache holds this position's rows (mlaReadCache).
+ * rope is deepseek.zig:581-629's ropeApply: NORM pairs, with YaRN when
+ * yarn_factor > 1, its cos/sin computed on the host with the C library's
+ * logf/powf/cosf/sinf in ropeApply's expressions.  Bit-identical to the
+ * engine's host path on the oracle.  DECLINED, with nothing launched, for a
+ * shape or type the kernels do not serve, a weight whose length does not
+ * match its shape, or more layers / another position than the cache has. */
+typedef struct {
+    const float *attn_norm;                 /* [dim] */
+    loomhip_weight_ref wq;                  /* [n_heads * (nope + rope)][dim] */
+    loomhip_weight_ref kv_a;                /* [kvr + rope][dim] */
+    const float *kv_a_norm;                 /* [kvr] */
+    loomhip_weight_ref kv_b;                /* [n_heads * (nope + v_head_dim)][kvr] */
+    loomhip_weight_ref attn_out;            /* [dim][n_heads * v_head_dim] */
+    const float *ffn_norm;                  /* [dim] */
+    int is_moe;
+    loomhip_weight_ref router, gate, up, down; /* f32 [n_expert][dim]; [n_expert] planes */
+    loomhip_weight_ref shexp_gate, shexp_up, shexp_down;
+    size_t ffn, shexp_ffn;
+    loomhip_weight_ref dgate, dup, ddown; /* dense FFN (is_moe == 0) */
+    size_t dffn;
+} loomhip_mla_layer_desc;
+typedef struct {
+    size_t dim, n_heads, nope, rope, kvr, v_head_dim;
+    float eps, scale, rope_base, yarn_factor, yarn_orig_ctx;
+    /* RoutedCfg (cpu.zig) */
+    size_t n_expert, n_used;
+    int gating, weights_norm; /* LOOMHIP_GATING_* */
+    float weights_scale;
+} loomhip_mla_frame_cfg;
+int loomhip_mla_token_frame(const loomhip_mla_layer_desc *descs, size_t n_layers, const loomhip_mla_frame_cfg *fc,
+                            float *x, size_t pos, const float *out_norm, loomhip_weight_ref lm_head, float *logits,
+                            size_t vocab);
+
 /* ---- GGUF v3 files (src/gguf/gguf.zig) ------------------------------------
  * gguf.zig:251-332 parse: the header, the metadata key/values and the tensor
  * table, with the whole file mapped read-only so a tensor's bytes are a

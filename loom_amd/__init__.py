@@ -156,6 +156,25 @@ class GqaFrameCfg(C.Structure):
                 ("weights_scale", C.c_float)])
 
 
+class MlaLayerDescC(C.Structure):
+    """Mirror of ``loomhip_mla_layer_desc`` (src/compute/cpu.zig:73 MlaLayerDesc)."""
+
+    _fields_ = ([("attn_norm", C.c_void_p), ("wq", WeightRefDesc), ("kv_a", WeightRefDesc), ("kv_a_norm", C.c_void_p),
+                 ("kv_b", WeightRefDesc), ("attn_out", WeightRefDesc), ("ffn_norm", C.c_void_p), ("is_moe", C.c_int)] +
+                [(n, WeightRefDesc) for n in ("router", "gate", "up", "down", "shexp_gate", "shexp_up", "shexp_down")] +
+                [("ffn", C.c_size_t), ("shexp_ffn", C.c_size_t)] +
+                [(n, WeightRefDesc) for n in ("dgate", "dup", "ddown")] + [("dffn", C.c_size_t)])
+
+
+class MlaFrameCfgC(C.Structure):
+    """Mirror of ``loomhip_mla_frame_cfg`` (src/compute/cpu.zig:74 MlaFrameCfg)."""
+
+    _fields_ = ([(n, C.c_size_t) for n in ("dim", "n_heads", "nope", "rope", "kvr", "v_head_dim")] +
+                [(n, C.c_float) for n in ("eps", "scale", "rope_base", "yarn_factor", "yarn_orig_ctx")] +
+                [("n_expert", C.c_size_t), ("n_used", C.c_size_t), ("gating", C.c_int), ("weights_norm", C.c_int),
+                 ("weights_scale", C.c_float)])
+
+
 class EcStats(C.Structure):
     """Mirror of ``loomhip_ec_stats`` in include/loomhip.h."""
 
@@ -340,6 +359,8 @@ def lib() -> C.CDLL:
                                        vp, i, vp, i, vp, i, vp, i, vp, sz, sz, sz, sz, i, i, f, sz, sz, sz, f]),
         "loomhip_mla_layer_tail_dev": (i, [C.POINTER(MlaAttnDesc), vp, vp, sz, vp, vp, i, vp, vp, f,
                                            C.POINTER(MoeLayerDesc), vp, vp]),
+        "loomhip_mla_token_frame": (i, [C.POINTER(MlaLayerDescC), sz, C.POINTER(MlaFrameCfgC), vp, sz, vp,
+                                        WeightRefDesc, vp, sz]),
         "loomhip_mla_layer_cached_dev": (i, [C.POINTER(MlaAttnDesc), C.POINTER(vp), C.POINTER(vp), sz, sz, vp, vp, i,
                                              vp, vp, f, C.POINTER(MoeLayerEcDesc), vp, vp, vp, vp]),
     }

@@ -555,6 +555,79 @@ def mlaLayerTail(li: int, pos: int, x: np.ndarray, q_nope: np.ndarray, q_rope: n
     return _served(rc, "mlaLayerTail")
 
 
+@dataclass
+class MlaLayerDesc:
+    """src/compute/cpu.zig:73 MlaLayerDesc: norms as f32 arrays, weights as
+    WeightRefs (3D expert tensors whole); shexp (gate, up, down) optional."""
+
+    attn_norm: np.ndarray
+    wq: WeightRef
+    kv_a: WeightRef
+    kv_a_norm: np.ndarray
+    kv_b: WeightRef
+    attn_out: WeightRef
+    ffn_norm: np.ndarray
+    is_moe: bool
+    router: WeightRef | None = None
+    gate: WeightRef | None = None
+    up: WeightRef | None = None
+    down: WeightRef | None = None
+    shexp: tuple | None = None
+    ffn: int = 0
+    shexp_ffn: int = 0
+    dgate: WeightRef | None = None
+    dup: WeightRef | None = None
+    ddown: WeightRef | None = None
+    dffn: int = 0
+
+
+@dataclass
+class MlaFrameCfg:
+    """src/compute/cpu.zig:74 MlaFrameCfg."""
+
+    dim: int
+    n_heads: int
+    nope: int
+    rope: int
+    kvr: int
+    v_head_dim: int
+    eps: float
+    scale: float
+    rope_base: float
+    yarn_factor: float
+    yarn_orig_ctx: float
+    routed: RoutedCfg | None = None
+
+
+def mlaTokenFrame(descs: list, fc: MlaFrameCfg, x: np.ndarray, pos: int, out_norm: np.ndarray, lm_head: WeightRef,
+                  logits: np.ndarray) -> bool:
+    """backend.mlaTokenFrame: the whole MLA token as one submission over the
+    device cache of mlaInit; x [dim] in (after embedding) and out (after the
+    last layer), logits [vocab] out; False declines before anything runs."""
+    from . import MlaFrameCfgC, MlaLayerDescC
+
+    arr = (MlaLayerDescC * len(descs))()
+    for d, c in zip(descs, arr):
+        sh = d.shexp or (None, None, None)
+        c.attn_norm, c.kv_a_norm, c.ffn_norm = _p(d.attn_norm), _p(d.kv_a_norm), _p(d.ffn_norm)
+        c.wq, c.kv_a, c.kv_b, c.attn_out = (_wref(w) for w in (d.wq, d.kv_a, d.kv_b, d.attn_out))
+        c.is_moe = int(d.is_moe)
+        c.router, c.gate, c.up, c.down = (_wref(w) for w in (d.router, d.gate, d.up, d.down))
+        c.shexp_gate, c.shexp_up, c.shexp_down = (_wref(w) for w in sh)
+        c.ffn, c.shexp_ffn = d.ffn, d.shexp_ffn
+        c.dgate, c.dup, c.ddown = (_wref(w) for w in (d.dgate, d.dup, d.ddown))
+        c.dffn = d.dffn
+    r = fc.routed
+    cfg = MlaFrameCfgC(fc.dim, fc.n_heads, fc.nope, fc.rope, fc.kvr, fc.v_head_dim, fc.eps, fc.scale, fc.rope_base,
+                       fc.yarn_factor, fc.yarn_orig_ctx, r.n_expert if r else 0, r.n_used if r else 0,
+                       (GATING_SIGMOID if r.gating_sigmoid else GATING_SOFTMAX) if r else GATING_SOFTMAX,
+                       int(r.weights_norm) if r else 1, r.weights_scale if r else 1.0)
+    assert x.dtype == np.float32 and logits.dtype == np.float32 and x.flags.c_contiguous
+    rc = lib().loomhip_mla_token_frame(arr, len(descs), C.byref(cfg), _p(x), pos, _p(out_norm), _wref(lm_head),
+                                       _p(logits), logits.size)
+    return _served(rc, "mlaTokenFrame")
+
+
 class MlaAttn:
     """Device-resident MLA attention of one layer: kv_b (GGML bytes, a torch
     uint8 device tensor) split per head into W_k / W_v planes once."""

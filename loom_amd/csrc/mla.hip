@@ -28,6 +28,8 @@
 #include "runtime.hpp"
 
 #include <mutex>
+#include <string>
+#include <vector>
 
 namespace lh {
 
@@ -394,7 +396,8 @@ struct Mla {
     size_t layers = 0, ctx = 0, kvr = 0, rope = 0;
     bool want = false;
     size_t wk_layers = 0;
-    Scratch qa, S, olat, act, kvb_stage, tail, act2;
+    Scratch qa, S, olat, act, kvb_stage, tail, act2, frame;
+    std::unordered_map<std::string, float *> yarn; // rope (cos, sin) tables per shape
     std::unordered_map<size_t, void *> vgroups; // per head count: groups {h, h, 1}
     std::unordered_map<const void *, KvbSplit> kvb;
 };
@@ -709,6 +712,83 @@ void mla_release() {
     g_mla.kvb_stage.release();
     g_mla.tail.release();
     g_mla.act2.release();
+    g_mla.frame.release();
+    for (auto &kv : g_mla.yarn)
+        (void)hipFree(kv.second);
+    g_mla.yarn.clear();
+}
+
+// ---- the whole MLA token (mlaTokenFrame) ------------------------------------------
+
+// deepseek.zig:581-629 ropeApply's angles for vectors of `rope` values, as
+// (cos, sin) per (position, pair) [ctx][rope / 2][2]: the YaRN ramp between
+// the interpolated (theta / factor) and extrapolated angle over the
+// corrected dimension range (beta_fast 32, beta_slow 1) when factor > 1,
+// else the plain NORM angle; f32 throughout with the C library's logf,
+// powf, cosf and sinf, in the reference's expressions.  Kept per shape.
+static const float *yarn_table(size_t ctx, size_t rope, float base, float factor, float orig) {
+    char key[128];
+    snprintf(key, sizeof key, "%zu/%zu/%a/%a/%a", ctx, rope, base, factor, orig);
+    auto it = g_mla.yarn.find(key);
+    if (it != g_mla.yarn.end())
+        return it->second;
+    const size_t half = rope / 2;
+    const float d = (float)rope;
+    const bool yarn = factor > 1.0f;
+    float low = 0.0f, high = 0.0f;
+    if (yarn) {
+        const float two_pi = (float)(2.0 * 3.14159265358979323846); // comptime 2*pi as f32
+        auto corr = [&](float beta) { return d * logf(orig / (beta * two_pi)) / (2.0f * logf(base)); };
+        low = fmaxf(0.0f, floorf(corr(32.0f)));
+        high = fminf(d - 1.0f, ceilf(corr(1.0f)));
+    }
+    std::vector<float> h(ctx * half * 2);
+    for (size_t p = 0; p < ctx; p++)
+        for (size_t i = 0; i < half; i++) {
+            const float exponent = (float)(2 * i) / d;
+            const float freq = powf(base, -exponent);
+            const float theta_extrap = (float)p * freq;
+            float theta = theta_extrap;
+            if (yarn) {
+                const float theta_interp = theta_extrap / factor;
+                const float y = ((float)i - low) / fmaxf(0.001f, high - low);
+                const float ramp_mix = 1.0f - fminf(fmaxf(y, 0.0f), 1.0f); // 1 = extrapolate
+                theta = theta_interp * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
+            }
+            h[(p * half + i) * 2] = cosf(theta);
+            h[(p * half + i) * 2 + 1] = sinf(theta);
+        }
+    float *dev = nullptr;
+    if (hipMalloc(&dev, h.size() * 4) != hipSuccess)
+        return nullptr;
+    if (hipMemcpy(dev, h.data(), h.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(dev);
+        return nullptr;
+    }
+    g_mla.yarn[key] = dev;
+    return dev;
+}
+
+// Work group h < H: head h's nope slice of q copied out and its rope slice
+// rotated at this position; work group H: the new k_rope row (kv_a's tail)
+// rotated into the cache.  NORM pairs: (a, b) -> (a c - b s, a s + b c),
+// each product rounded before its add (deepseek.zig:606-611).
+__global__ __launch_bounds__(64) void mla_rope_kernel(const float *__restrict__ q, int H, int nope, int rope,
+                                                      const float *__restrict__ kr_src, const float *__restrict__ cs,
+                                                      float *__restrict__ q_nope, float *__restrict__ q_rope,
+                                                      float *__restrict__ kr_row) {
+    const int h = blockIdx.x, kd = nope + rope;
+    const float *src = h < H ? q + (size_t)h * kd + nope : kr_src;
+    float *dst = h < H ? q_rope + (size_t)h * rope : kr_row;
+    if (h < H)
+        for (int i = threadIdx.x; i < nope; i += 64)
+            q_nope[(size_t)h * nope + i] = q[(size_t)h * kd + i];
+    for (int i = threadIdx.x; 2 * i + 1 < rope; i += 64) {
+        const float c = cs[2 * i], sn = cs[2 * i + 1];
+        const float a = src[2 * i], b = src[2 * i + 1];
+        dst[2 * i] = a * c - b * sn;
+        dst[2 * i + 1] = a * sn + b * c;
+    }
 }
 
 } // namespace lh
@@ -863,6 +943,194 @@ int loomhip_mla_layer_tail_dev(const loomhip_mla_attn *a, const float *c_kv, con
         return fail(LOOMHIP_ERR_ARG, "mla_layer_tail_dev: null pointer");
     return mla_tail_impl(a, c_kv, k_rope, seq, q_nope, q_rope, attn_out_type, attn_out, ffn_norm, eps, moe, x,
                          stream_of(stream));
+}
+
+int loomhip_mla_token_frame(const loomhip_mla_layer_desc *descs, size_t n_layers, const loomhip_mla_frame_cfg *fc,
+                            float *x, size_t pos, const float *out_norm, loomhip_weight_ref lm_head, float *logits,
+                            size_t vocab) {
+    if (int rc = require_ready())
+        return rc;
+    std::lock_guard<std::mutex> lk(g_mla.mu);
+    if (!descs || !fc || !x || !out_norm || !logits || n_layers == 0 || vocab == 0)
+        return fail(LOOMHIP_ERR_ARG, "mla_token_frame: null argument");
+    if (int rc = ensure_cache())
+        return rc;
+    const size_t dim = fc->dim, H = fc->n_heads, nope = fc->nope, rope = fc->rope, kvr = fc->kvr, vd = fc->v_head_dim;
+    const size_t kd = nope + rope, hv = H * vd;
+    if (n_layers > g_mla.layers || pos >= g_mla.ctx || kvr != g_mla.kvr || rope != g_mla.rope)
+        return fail(LOOMHIP_DECLINED, "mla_token_frame: %zu layers / position %zu / kvr %zu / rope %zu outside the cache",
+                    n_layers, pos, kvr, rope);
+    if (dim == 0 || dim % 32 || dim > 7936 || kvr % 32 || kvr > 7936 || rope % 2 || H == 0)
+        return fail(LOOMHIP_DECLINED, "mla_token_frame: dim %zu / kvr %zu / rope %zu not served", dim, kvr, rope);
+    auto ref_ok = [](const loomhip_weight_ref &r, size_t rows, size_t cols, size_t planes = 1) {
+        return r.data && r.len == ggml_bytes(r.type, rows, cols) * planes;
+    };
+    auto quant_ok = [](int t, size_t cols) { return t != LH_F32 && t != LH_F16 && dmmv_supported(t, (int)cols); };
+    if (!ref_ok(lm_head, vocab, dim) || !quant_ok(lm_head.type, dim))
+        return fail(LOOMHIP_DECLINED, "mla_token_frame: lm_head type %d / %zu bytes not served", lm_head.type,
+                    lm_head.len);
+    // every layer checked (host pointers stand in for the device copies)
+    // before anything is uploaded or launched
+    std::vector<loomhip_moe_layer> moes(n_layers);
+    for (size_t li = 0; li < n_layers; li++) {
+        const loomhip_mla_layer_desc &d = descs[li];
+        const int kt = d.kv_b.type;
+        const loomhip_mla_attn probe{kt, d.kv_b.data, d.kv_b.data, H, nope, vd, kvr, rope, fc->scale};
+        if (!d.attn_norm || !d.kv_a_norm || !d.ffn_norm || !ref_ok(d.wq, H * kd, dim) || !quant_ok(d.wq.type, dim) ||
+            !ref_ok(d.kv_a, kvr + rope, dim) || !quant_ok(d.kv_a.type, dim) || !ref_ok(d.attn_out, dim, hv) ||
+            !quant_ok(d.attn_out.type, hv) || !ref_ok(d.kv_b, H * (nope + vd), kvr))
+            return fail(LOOMHIP_DECLINED, "mla_token_frame: layer %zu attention tensors do not match their shapes",
+                        li);
+        if (int rc = mla_check(&probe, pos + 1))
+            return rc;
+        if (d.is_moe) {
+            const size_t E = fc->n_expert;
+            const bool sh = d.shexp_gate.data != nullptr;
+            if (d.router.type != LH_F32 || !ref_ok(d.router, E, dim) || !ref_ok(d.gate, d.ffn, dim, E) ||
+                !ref_ok(d.up, d.ffn, dim, E) || !ref_ok(d.down, dim, d.ffn, E) ||
+                (sh && (!ref_ok(d.shexp_gate, d.shexp_ffn, dim) || !ref_ok(d.shexp_up, d.shexp_ffn, dim) ||
+                        !ref_ok(d.shexp_down, dim, d.shexp_ffn))))
+                return fail(LOOMHIP_DECLINED, "mla_token_frame: layer %zu MoE tensors do not match their shapes", li);
+            loomhip_moe_layer &m = moes[li];
+            m.dim = dim;
+            m.ffn = d.ffn;
+            m.n_expert = E;
+            m.n_used = fc->n_used;
+            m.gating = fc->gating;
+            m.weights_norm = fc->weights_norm;
+            m.weights_scale = fc->weights_scale;
+            m.router = (const float *)d.router.data;
+            m.gate_t = d.gate.type;
+            m.up_t = d.up.type;
+            m.down_t = d.down.type;
+            m.gate = d.gate.data;
+            m.up = d.up.data;
+            m.down = d.down.data;
+            if (sh) {
+                m.shexp_gate_t = d.shexp_gate.type;
+                m.shexp_up_t = d.shexp_up.type;
+                m.shexp_down_t = d.shexp_down.type;
+                m.shexp_gate = d.shexp_gate.data;
+                m.shexp_up = d.shexp_up.data;
+                m.shexp_down = d.shexp_down.data;
+                m.shexp_ffn = d.shexp_ffn;
+            }
+            if (int rc = moe_layer_check(&m, 1, true))
+                return rc;
+        } else {
+            if (!ref_ok(d.dgate, d.dffn, dim) || !ref_ok(d.dup, d.dffn, dim) || !ref_ok(d.ddown, dim, d.dffn))
+                return fail(LOOMHIP_DECLINED, "mla_token_frame: layer %zu FFN tensors do not match their shapes", li);
+            const DenseFfn f{d.dgate.type, d.dup.type, d.ddown.type, d.dgate.data, d.dup.data, d.ddown.data, d.dffn};
+            if (int rc = dense_ffn_check(f, dim))
+                return rc;
+        }
+    }
+    hipStream_t st = g_ctx.compute;
+    const float *cs = yarn_table(g_mla.ctx, rope, fc->rope_base, fc->yarn_factor, fc->yarn_orig_ctx);
+    if (!cs)
+        return fail(LOOMHIP_ERR_HIP, "mla_token_frame: rope table");
+    cs += pos * rope; // rope / 2 (cos, sin) pairs per position
+    // the device copies (uploaded once per host tensor)
+    struct Dev {
+        const void *wq, *kv_a, *attn_out, *gate, *up, *down, *sg, *su, *sd, *dg, *du, *dd;
+        const float *attn_norm, *kv_a_norm, *ffn_norm, *router;
+        KvbSplit *kvb;
+    };
+    std::vector<Dev> dv(n_layers);
+    int rc;
+    auto up_ref = [&](const loomhip_weight_ref &r, size_t rows, size_t cols, size_t planes, const void **out) {
+        void *p = nullptr;
+        const int c = upload_weights(r.type, r.data, rows, cols, planes, &p);
+        *out = p;
+        return c;
+    };
+    auto up_f32 = [&](const float *h, size_t n, const float **out) {
+        void *p = nullptr;
+        const int c = upload_weights(LH_F32, h, 1, n, 1, &p);
+        *out = (const float *)p;
+        return c;
+    };
+    for (size_t li = 0; li < n_layers; li++) {
+        const loomhip_mla_layer_desc &d = descs[li];
+        Dev &v = dv[li];
+        if ((rc = up_f32(d.attn_norm, dim, &v.attn_norm)) || (rc = up_f32(d.kv_a_norm, kvr, &v.kv_a_norm)) ||
+            (rc = up_f32(d.ffn_norm, dim, &v.ffn_norm)) || (rc = up_ref(d.wq, H * kd, dim, 1, &v.wq)) ||
+            (rc = up_ref(d.kv_a, kvr + rope, dim, 1, &v.kv_a)) || (rc = up_ref(d.attn_out, dim, hv, 1, &v.attn_out)) ||
+            (rc = kvb_cached(d.kv_b.type, (const uint8_t *)d.kv_b.data, d.kv_b.len, H, nope, vd, kvr, st, &v.kvb)))
+            return rc;
+        if (d.is_moe) {
+            const size_t E = fc->n_expert;
+            loomhip_moe_layer &m = moes[li];
+            if ((rc = up_f32(m.router, E * dim, &m.router)) || (rc = up_ref(d.gate, d.ffn, dim, E, &m.gate)) ||
+                (rc = up_ref(d.up, d.ffn, dim, E, &m.up)) || (rc = up_ref(d.down, dim, d.ffn, E, &m.down)))
+                return rc;
+            if (m.shexp_gate &&
+                ((rc = up_ref(d.shexp_gate, d.shexp_ffn, dim, 1, &m.shexp_gate)) ||
+                 (rc = up_ref(d.shexp_up, d.shexp_ffn, dim, 1, &m.shexp_up)) ||
+                 (rc = up_ref(d.shexp_down, dim, d.shexp_ffn, 1, &m.shexp_down))))
+                return rc;
+        } else if ((rc = up_ref(d.dgate, d.dffn, dim, 1, &v.dg)) || (rc = up_ref(d.dup, d.dffn, dim, 1, &v.du)) ||
+                   (rc = up_ref(d.ddown, dim, d.dffn, 1, &v.dd))) {
+            return rc;
+        }
+    }
+    const float *d_out_norm;
+    const void *d_lm;
+    if ((rc = up_f32(out_norm, dim, &d_out_norm)) || (rc = up_ref(lm_head, vocab, dim, 1, &d_lm)))
+        return rc;
+    // workspace: x | normed | q | kv_a | q_nope | q_rope | heads | logits
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        const size_t o = off;
+        off += align16(n * 4);
+        return o;
+    };
+    const size_t o_x = take(dim), o_n = take(dim), o_q = take(H * kd), o_kv = take(kvr + rope), o_qn = take(H * nope),
+                 o_qr = take(H * rope), o_h = take(hv), o_l = take(vocab);
+    if ((rc = reserve_on(g_mla.frame, off, st)))
+        return rc;
+    char *base = (char *)g_mla.frame.ptr;
+    float *dx = (float *)(base + o_x), *normed = (float *)(base + o_n), *q = (float *)(base + o_q);
+    float *kv = (float *)(base + o_kv), *qn = (float *)(base + o_qn), *qr = (float *)(base + o_qr);
+    float *heads = (float *)(base + o_h), *dlog = (float *)(base + o_l);
+    hipError_t e = hipMemcpyAsync(dx, x, dim * 4, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess)
+        return hip_fail(e, "mla_token_frame upload");
+    for (size_t li = 0; li < n_layers; li++) {
+        const loomhip_mla_layer_desc &d = descs[li];
+        const Dev &v = dv[li];
+        // the attention head (deepseek.zig:860-886)
+        if ((rc = rmsnorm_exact_dev(dx, (int)dim, v.attn_norm, fc->eps, normed, 1, st)) ||
+            (rc = matvec_dev_impl(d.wq.type, q, v.wq, normed, 1, H * kd, dim, st)) ||
+            (rc = matvec_dev_impl(d.kv_a.type, kv, v.kv_a, normed, 1, kvr + rope, dim, st)) ||
+            (rc = rmsnorm_exact_dev(kv, (int)kvr, v.kv_a_norm, fc->eps, cache_c(li, pos), 1, st)))
+            return rc;
+        hipLaunchKernelGGL(mla_rope_kernel, dim3((unsigned)(H + 1)), dim3(64), 0, st, q, (int)H, (int)nope, (int)rope,
+                           kv + kvr, cs, qn, qr, cache_r(li, pos));
+        note_launch();
+        const loomhip_mla_attn a{d.kv_b.type, v.kvb->wk, v.kvb->wv, H, nope, vd, kvr, rope, fc->scale};
+        if (d.is_moe) { // attention through the FFN residual (deepseek.zig:1044-1046, 1325-1387)
+            if ((rc = mla_tail_impl(&a, cache_c(li, 0), cache_r(li, 0), pos + 1, qn, qr, d.attn_out.type, v.attn_out,
+                                    v.ffn_norm, fc->eps, &moes[li], dx, st)))
+                return rc;
+        } else { // dense: attention, x += wo . heads, x += denseFFN(rmsnorm(x))
+            const DenseFfn f{d.dgate.type, d.dup.type, d.ddown.type, v.dg, v.du, v.dd, d.dffn};
+            if ((rc = mla_attn_impl(&a, cache_c(li, 0), cache_r(li, 0), pos + 1, qn, qr, heads, nullptr, st)) ||
+                (rc = matvec_add(d.attn_out.type, v.attn_out, heads, (int)dim, (int)hv, dx, st)) ||
+                (rc = rmsnorm_exact_dev(dx, (int)dim, v.ffn_norm, fc->eps, normed, 1, st)) ||
+                (rc = dense_ffn_add(f, normed, 1, dim, dx, st, true)))
+                return rc;
+        }
+    }
+    if ((rc = rmsnorm_exact_dev(dx, (int)dim, d_out_norm, fc->eps, normed, 1, st)) ||
+        (rc = matvec_dev_impl(lm_head.type, dlog, d_lm, normed, 1, vocab, dim, st)))
+        return rc;
+    e = hipMemcpyAsync(logits, dlog, vocab * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(x, dx, dim * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(st);
+    return e == hipSuccess ? LOOMHIP_OK : hip_fail(e, "mla_token_frame");
 }
 
 int loomhip_mla_layer_cached_dev(const loomhip_mla_attn *a, const float *const *c_kv, const float *const *k_rope,

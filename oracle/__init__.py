@@ -125,6 +125,19 @@ class Model(C.Structure):
     ]
 
 
+class MlaLayer(C.Structure):
+    _fields_ = [("attn_norm", C.c_void_p), ("wq", Tensor), ("kv_a", Tensor), ("kv_a_norm", C.c_void_p),
+                ("kv_b", Tensor), ("attn_out", Tensor), ("ffn_norm", C.c_void_p), ("is_moe", C.c_int),
+                ("moe", MoeLayer), ("dgate", Tensor), ("dup", Tensor), ("ddown", Tensor)]
+
+
+class MlaModel(C.Structure):
+    _fields_ = ([(n, C.c_size_t) for n in ("dim", "n_heads", "nope", "rope", "kvr", "vd", "n_layers", "ctx_len",
+                                           "vocab")] +
+                [(n, C.c_float) for n in ("eps", "scale", "rope_base", "yarn_factor", "yarn_orig_ctx")] +
+                [("layers", C.c_void_p), ("out_norm", C.c_void_p), ("output", Tensor)])
+
+
 class Seq(C.Structure):
     _fields_ = [("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("pos", C.c_size_t)]
 
@@ -176,6 +189,8 @@ def lib() -> C.CDLL:
             "lo_step": (i, [C.POINTER(Model), C.POINTER(Seq), C.c_uint32, vp]),
             "lo_decode_batch": (i, [C.POINTER(Model), vp, vp, sz, vp]),
             "lo_attn_heads": (None, [C.POINTER(Model), vp, vp, sz, sz, vp, vp, C.c_float]),
+            "lo_mla_step": (i, [C.POINTER(MlaModel), vp, vp, sz, vp, vp]),
+            "lo_set_mla_slip": (None, [i]),
             "lo_set_batch_slip": (None, [i]),
             "lo_lru_create": (vp, [sz]),
             "lo_lru_destroy": (None, [vp]),

@@ -227,6 +227,36 @@ void lo_mla_attn_heads(const float *c_kv, const float *k_rope, size_t seq, size_
                        const float *q_nope, const float *q_rope, int kvb_type, const uint8_t *kv_b,
                        size_t n_heads, size_t nope, size_t vd, float scale, float *out, float *o_lat);
 
+/* The MLA token (deepseek.zig:851-1048 attnLayer, 1275-1440 step) in the
+ * shape mlaTokenFrame records: direct q, fused kv_b, MoE layers as
+ * moeRun + shared expert, or dense SwiGLU layers. */
+typedef struct {
+    const float *attn_norm; /* [dim] */
+    lo_tensor wq;           /* [n_heads * (nope + rope)][dim] */
+    lo_tensor kv_a;         /* [kvr + rope][dim] */
+    const float *kv_a_norm; /* [kvr] */
+    lo_tensor kv_b;         /* [n_heads * (nope + vd)][kvr] */
+    lo_tensor attn_out;     /* [dim][n_heads * vd] */
+    const float *ffn_norm;  /* [dim] */
+    int is_moe;
+    lo_moe_layer moe;
+    lo_tensor dgate, dup, ddown; /* dense FFN */
+} lo_mla_layer;
+typedef struct {
+    size_t dim, n_heads, nope, rope, kvr, vd, n_layers, ctx_len, vocab;
+    float eps, scale, rope_base, yarn_factor, yarn_orig_ctx;
+    const lo_mla_layer *layers;
+    const float *out_norm;
+    lo_tensor output;
+} lo_mla_model;
+/* One token at pos: x [dim] is the embedding row in and the residual stream
+ * after the last layer out; the caches ([n_layers][ctx_len][kvr] and
+ * [n_layers][ctx_len][rope]) receive this position's rows; logits [vocab]. */
+int lo_mla_step(const lo_mla_model *m, float *c_kv_cache, float *k_rope_cache, size_t pos, float *x, float *logits);
+/* Test-only planted mistakes in lo_mla_step (0 = none): 1 k_rope cached
+ * unrotated, 2 q's rope on the nope slice, 3 kv_a's norm skipped. */
+void lo_set_mla_slip(int slip);
+
 #ifdef __cplusplus
 }
 #endif

@@ -90,3 +90,85 @@ void lo_mla_attn_heads(const float *c_kv, const float *k_rope, size_t seq, size_
     free(sc);
     free(acc);
 }
+
+/* Planted-mistake switch for the step's pin test (test infrastructure only;
+ * 0 in every other use): 1 = k_rope cached before its rope, 2 = q's rope
+ * applied to the nope slice, 3 = kv_a's norm skipped. */
+static int mla_slip;
+void lo_set_mla_slip(int slip) { mla_slip = slip; }
+
+/* deepseek.zig:851-1048 attnLayer and 1275-1440 step, in the shape
+ * mlaTokenFrame records (compute/cpu.zig:73-79): per layer
+ *   normed = rmsnorm(x) * attn_norm;  q = wq . normed;  kv_a = kv_a_mqa . normed
+ *   c_kv row = rmsnorm(kv_a[0, kvr)) * kv_a_norm;  k_rope row = rope(kv_a[kvr, kvr + rope), pos)
+ *   q's rope slice of every head = rope(., pos);  heads = the host head loop
+ *   x += attn_output . heads;  normed = rmsnorm(x) * ffn_norm
+ *   MoE: acc = moeRun + shared expert (moeFfnBlockRouted's sum), x += acc
+ *   dense: x += down . swiglu(gate . normed, up . normed)
+ * then logits = output . (rmsnorm(x) * out_norm). */
+int lo_mla_step(const lo_mla_model *m, float *c_kv_cache, float *k_rope_cache, size_t pos, float *x, float *logits) {
+    if (pos >= m->ctx_len)
+        return -1;
+    const size_t dim = m->dim, H = m->n_heads, nope = m->nope, rope = m->rope, kvr = m->kvr, vd = m->vd;
+    const size_t kd = nope + rope;
+    size_t fmax = 1;
+    for (size_t li = 0; li < m->n_layers; li++) {
+        const lo_mla_layer *L = &m->layers[li];
+        const size_t f = L->is_moe ? 0 : L->dgate.ne1;
+        fmax = f > fmax ? f : fmax;
+    }
+    float *normed = (float *)malloc(dim * 4), *q = (float *)malloc(H * kd * 4);
+    float *kv_a = (float *)malloc((kvr + rope) * 4), *qn = (float *)malloc(H * nope * 4);
+    float *qr = (float *)malloc(H * rope * 4), *heads = (float *)malloc(H * vd * 4), *tmp = (float *)malloc(dim * 4);
+    float *g = (float *)malloc(fmax * 4), *u = (float *)malloc(fmax * 4), *act = (float *)malloc(fmax * 4);
+    for (size_t li = 0; li < m->n_layers; li++) {
+        const lo_mla_layer *L = &m->layers[li];
+        lo_rmsnorm(normed, x, L->attn_norm, dim, m->eps);
+        lo_matvec(L->wq.ty, q, L->wq.data, normed, L->wq.ne1, L->wq.ne0);
+        lo_matvec(L->kv_a.ty, kv_a, L->kv_a.data, normed, L->kv_a.ne1, L->kv_a.ne0);
+        float *c_row = c_kv_cache + (li * m->ctx_len + pos) * kvr;
+        float *r_row = k_rope_cache + (li * m->ctx_len + pos) * rope;
+        if (mla_slip == 3)
+            memcpy(c_row, kv_a, kvr * 4);
+        else
+            lo_rmsnorm(c_row, kv_a, L->kv_a_norm, kvr, m->eps);
+        memcpy(r_row, kv_a + kvr, rope * 4);
+        if (mla_slip != 1)
+            lo_rope_yarn(r_row, rope, pos, m->rope_base, m->yarn_factor, m->yarn_orig_ctx);
+        for (size_t h = 0; h < H; h++)
+            lo_rope_yarn(q + h * kd + (mla_slip == 2 ? 0 : nope), rope, pos, m->rope_base, m->yarn_factor,
+                         m->yarn_orig_ctx);
+        for (size_t h = 0; h < H; h++) {
+            memcpy(qn + h * nope, q + h * kd, nope * 4);
+            memcpy(qr + h * rope, q + h * kd + nope, rope * 4);
+        }
+        lo_mla_attn_heads(c_kv_cache + li * m->ctx_len * kvr, k_rope_cache + li * m->ctx_len * rope, pos + 1, kvr,
+                          rope, qn, qr, L->kv_b.ty, L->kv_b.data, H, nope, vd, m->scale, heads, NULL);
+        lo_matvec(L->attn_out.ty, tmp, L->attn_out.data, heads, dim, H * vd);
+        lo_add(x, tmp, dim);
+        lo_rmsnorm(normed, x, L->ffn_norm, dim, m->eps);
+        if (L->is_moe) {
+            lo_moe_layer_token(&L->moe, normed, tmp, NULL, NULL);
+        } else {
+            const size_t f = L->dgate.ne1;
+            lo_matvec(L->dgate.ty, g, L->dgate.data, normed, f, dim);
+            lo_matvec(L->dup.ty, u, L->dup.data, normed, f, dim);
+            lo_swiglu(act, g, u, f);
+            lo_matvec(L->ddown.ty, tmp, L->ddown.data, act, dim, f);
+        }
+        lo_add(x, tmp, dim);
+    }
+    lo_rmsnorm(normed, x, m->out_norm, dim, m->eps);
+    lo_matvec(m->output.ty, logits, m->output.data, normed, m->vocab, dim);
+    free(normed);
+    free(q);
+    free(kv_a);
+    free(qn);
+    free(qr);
+    free(heads);
+    free(tmp);
+    free(g);
+    free(u);
+    free(act);
+    return 0;
+}

@@ -168,3 +168,75 @@ def test_seam_mla_layer_tail_matches_the_engine_sequence(lh, oracle):
     assert not lh.mlaLayerTail(0, seq - 1, x, *bad)
     assert not lh.mlaLayerTail(0, ctx, x, *args)
     assert np.array_equal(x, x0)
+
+
+def _mla_descs(lh, mc):
+    """MlaLayerDesc per layer over the model case's host arrays."""
+    WR = lh.WeightRef
+    ty = lambda k: mc.types.get(k, Q4_K)  # noqa: E731
+    descs = []
+    for L in mc.layers:
+        d = lh.MlaLayerDesc(L["attn_norm"], WR(Q4_K, L["wq"]), WR(Q4_K, L["kv_a"]), L["kv_a_norm"], WR(Q4_K, L["kv_b"]),
+                            WR(Q4_K, L["attn_out"]), L["ffn_norm"], bool(L["is_moe"]))
+        if L["is_moe"]:
+            d.router = WR(F32, L["router"].view(np.uint8).ravel())
+            d.gate, d.up, d.down = WR(Q4_K, L["gate"]), WR(Q4_K, L["up"]), WR(ty("down"), L["down"])
+            d.shexp = (WR(Q4_K, L["sg"]), WR(Q4_K, L["su"]), WR(ty("sd"), L["sd"]))
+            d.ffn, d.shexp_ffn = mc.ffn, mc.sffn
+        else:
+            d.dgate, d.dup, d.ddown = WR(Q4_K, L["dgate"]), WR(Q4_K, L["dup"]), WR(ty("ddown"), L["ddown"])
+            d.dffn = mc.dffn
+        descs.append(d)
+    cfg = lh.MlaFrameCfg(mc.dim, mc.n_heads, mc.nope, mc.rope, mc.kvr, mc.vd, mc.eps, mc.scale, mc.rope_base,
+                         mc.yarn_factor, mc.yarn_orig_ctx, lh.RoutedCfg(mc.n_expert, mc.n_used, True, True, mc.wscale))
+    return descs, cfg
+
+
+def test_mla_token_frame_matches_the_engine_step(lh, oracle):
+    """mlaTokenFrame (src/compute/backend.zig:186-191) on a DeepSeek-V3-style
+    model at reduced width (dim 1024, 8 heads of nope 128 / rope 64 / v 128,
+    kv_lora 512, YaRN factor 40 over an original 4096 context; a dense layer,
+    then a MoE layer of 8 experts top-2 with sigmoid gating, renorm, scale
+    2.5 and a shared expert; Q4_K with Q6_K downs and head): over 10 tokens,
+    the 5th and 6th through the engine's host path (the oracle's step, its
+    cache rows mirrored in by mlaAppend), every frame's logits and residual
+    stream bit-identical to the engine's own step (lo_mla_step, pinned by a
+    float64 forward), and mlaReadCache's rows equal to the rows the step
+    wrote -- the device YaRN rope and head projections included."""
+    import loom_amd
+    from mla_case import MlaOracleStepper, make_mla_model
+
+    mc = make_mla_model(oracle, 21, moe=(False, True), ctx=32)
+    st = MlaOracleStepper(oracle, mc)
+    descs, cfg = _mla_descs(lh, mc)
+    lh.clearWeightCache()
+    assert lh.mlaInit(len(mc.layers), mc.ctx, mc.kvr, mc.rope)
+    logits = np.empty(mc.vocab, np.float32)
+    c_row, r_row = np.empty(mc.kvr, np.float32), np.empty(mc.rope, np.float32)
+    head = lh.WeightRef(Q6_K, mc.output)
+    for pos, tok in enumerate(np.random.default_rng(5).integers(0, mc.vocab, 10)):
+        x_ref = st.embed(tok)
+        x = x_ref.copy()
+        want = st.step(x_ref, pos)
+        if pos in (4, 5):  # the engine's host path, its rows mirrored onto the device
+            for li in range(len(mc.layers)):
+                assert lh.mlaAppend(li, pos, st.c_kv[li, pos], st.k_rope[li, pos])
+            continue
+        loom_amd.take_launch_count()
+        assert lh.mlaTokenFrame(descs, cfg, x, pos, mc.out_norm, head, logits), loom_amd.last_error()
+        assert loom_amd.take_launch_count() > 0
+        print(f"pos {pos}: max |diff| logits {float(np.abs(logits - want).max()):.2e}, "
+              f"x {float(np.abs(x - x_ref).max()):.2e}", flush=True)
+        assert np.array_equal(logits.view(np.uint32), want.view(np.uint32)), pos
+        assert np.array_equal(x.view(np.uint32), x_ref.view(np.uint32)), pos
+        for li in range(len(mc.layers)):
+            assert lh.mlaReadCache(li, pos, c_row, r_row)
+            assert np.array_equal(c_row, st.c_kv[li, pos]) and np.array_equal(r_row, st.k_rope[li, pos]), (li, pos)
+    # declines before anything runs: a weight of the wrong length, a position past the cache
+    import dataclasses
+    bad = [dataclasses.replace(descs[0], wq=lh.WeightRef(Q4_K, mc.layers[0]["wq"][:-144]))] + descs[1:]
+    loom_amd.take_launch_count()
+    assert not lh.mlaTokenFrame(bad, cfg, st.embed(1), 10, mc.out_norm, head, logits)
+    assert not lh.mlaTokenFrame(descs, cfg, st.embed(1), mc.ctx, mc.out_norm, head, logits)
+    assert loom_amd.take_launch_count() == 0
+    lh.clearWeightCache()

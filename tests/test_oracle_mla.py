@@ -123,3 +123,134 @@ def test_rope_yarn_regimes(oracle):
                 continue
             want = (a * np.cos(ang) - b * np.sin(ang), a * np.sin(ang) + b * np.cos(ang))
             assert abs(got[2 * i] - want[0]) < 2e-3 and abs(got[2 * i + 1] - want[1]) < 2e-3, (pos, i)
+
+
+def _q(t, v):
+    """The reference's int8 activation for weight type t, dequantized."""
+    import oracle as o
+
+    v = np.ascontiguousarray(v, np.float32)
+    if t in (Q4_K, Q6_K):
+        d, q, _ = o.quantize_x256(v)
+    else:
+        d, _, q = o.quantize_x(v)
+    return (q.astype(np.float64) * d.astype(np.float64)[:, None]).ravel()
+
+
+def _yarn64(v, pos, base, factor, orig):
+    """deepseek.zig:581-613 in float64."""
+    d = len(v)
+    corr = lambda beta: d * np.log(orig / (beta * 2 * np.pi)) / (2 * np.log(base))  # noqa: E731
+    low, high = max(0.0, np.floor(corr(32.0))), min(d - 1.0, np.ceil(corr(1.0)))
+    out = v.copy()
+    for i in range(d // 2):
+        te = pos * base ** (-2 * i / d)
+        ramp = 1.0 - min(max((i - low) / max(0.001, high - low), 0.0), 1.0)
+        th = te / factor * (1.0 - ramp) + te * ramp
+        a, b = v[2 * i], v[2 * i + 1]
+        out[2 * i], out[2 * i + 1] = a * np.cos(th) - b * np.sin(th), a * np.sin(th) + b * np.cos(th)
+    return out
+
+
+class _Step64:
+    """The MLA token in float64 from the independent decoder's weights: norms,
+    projections (int8 activations as the reference's matvecs quantize them),
+    YaRN, attention with the keys decompressed (K = W_k c per position and
+    head) and W_v applied to the softmax-weighted latent sum, residuals; the routed MoE layer through the oracle's moeRun +
+    shared expert (pinned in test_oracle_moe) on the float64 stream rounded
+    to f32."""
+
+    def __init__(self, oracle, mc, stepper):
+        self.o, self.mc, self.st = oracle, mc, stepper
+        self.c = [[] for _ in mc.layers]
+        self.r = [[] for _ in mc.layers]
+        deq = lambda t, a, rows, cols: npref.dequant(t, a, rows, cols).astype(np.float64)  # noqa: E731
+        H, kd = mc.n_heads, mc.nope + mc.rope
+        self.W = []
+        for L in mc.layers:
+            w = {"wq": deq(Q4_K, L["wq"], H * kd, mc.dim), "kv_a": deq(Q4_K, L["kv_a"], mc.kvr + mc.rope, mc.dim),
+                 "kv_b": deq(Q4_K, L["kv_b"], H * (mc.nope + mc.vd), mc.kvr),
+                 "attn_out": deq(Q4_K, L["attn_out"], mc.dim, H * mc.vd)}
+            if not L["is_moe"]:
+                w["dgate"] = deq(Q4_K, L["dgate"], mc.dffn, mc.dim)
+                w["dup"] = deq(Q4_K, L["dup"], mc.dffn, mc.dim)
+                w["ddown"] = deq(Q6_K, L["ddown"], mc.dim, mc.dffn)
+            self.W.append(w)
+        self.out = deq(Q6_K, mc.output, mc.vocab, mc.dim)
+
+    def norm(self, x, w):
+        x = np.asarray(x, np.float64)
+        return x / np.sqrt(np.mean(x * x) + self.mc.eps) * w.astype(np.float64)
+
+    def step(self, x, pos):
+        mc, H, nope, rope, kvr, vd = self.mc, self.mc.n_heads, self.mc.nope, self.mc.rope, self.mc.kvr, self.mc.vd
+        kd = nope + rope
+        x = np.asarray(x, np.float64).copy()
+        for li, (L, W) in enumerate(zip(mc.layers, self.W)):
+            n = self.norm(x, L["attn_norm"])
+            q = W["wq"] @ _q(Q4_K, n)
+            kv = W["kv_a"] @ _q(Q4_K, n)
+            self.c[li].append(self.norm(kv[:kvr], L["kv_a_norm"]))
+            self.r[li].append(_yarn64(kv[kvr:], pos, mc.rope_base, mc.yarn_factor, mc.yarn_orig_ctx))
+            C_, R_ = np.array(self.c[li]), np.array(self.r[li])
+            heads = []
+            for h in range(H):
+                qn = q[h * kd:h * kd + nope]
+                qr = _yarn64(q[h * kd + nope:(h + 1) * kd], pos, mc.rope_base, mc.yarn_factor, mc.yarn_orig_ctx)
+                Wk = W["kv_b"][h * (nope + vd):h * (nope + vd) + nope]
+                Wv = W["kv_b"][h * (nope + vd) + nope:(h + 1) * (nope + vd)]
+                s = ((C_ @ Wk.T) @ qn + R_ @ qr) * mc.scale
+                p = np.exp(s - s.max())
+                p /= p.sum()
+                # o = W_v (sum_t p_t c_t): W_v is a matvec, whose input the
+                # reference quantizes to int8 like every matvec's
+                heads.append(Wv @ _q(Q4_K, p @ C_))
+            x = x + W["attn_out"] @ _q(Q4_K, np.concatenate(heads))
+            n = self.norm(x, L["ffn_norm"])
+            if L["is_moe"]:
+                acc, _, _ = self.o.moe_layer_token(self.st.keep[0], n.astype(np.float32))
+                x = x + acc
+            else:
+                g, u = W["dgate"] @ _q(Q4_K, n), W["dup"] @ _q(Q4_K, n)
+                x = x + W["ddown"] @ _q(Q6_K, g / (1.0 + np.exp(-g)) * u)
+        return self.out @ _q(Q6_K, self.norm(x, mc.out_norm)), x
+
+
+# observed without a slip: 3.9e-7 relative; the slips miss by 3.4e-2, 0.18 and 0.55.  The float64
+# forward quantizes its own values at every matvec input, so a value on an int8 rounding boundary
+# could round the other way than the oracle's f32 value (a ~1e-2 miss); the seed is fixed and
+# shows none (seed 11 does, at position 2's W_v input of head 1)
+STEP_BOUND = 1e-4
+
+
+@pytest.mark.parametrize("slip", [0, 1, 2, 3], ids=["none", "k_rope_unrotated", "rope_on_nope", "no_kv_a_norm"])
+def test_mla_step_against_float64(oracle, slip):
+    """lo_mla_step (the MLA token mlaTokenFrame records: deepseek.zig:
+    851-1048, 1275-1440) over 5 positions of a dense layer then a MoE layer
+    with a shared expert, DeepSeek-V3's per-head shape and YaRN (factor 40,
+    original context 4096) at position offsets where the ramp matters,
+    against the float64 forward: logits and the residual stream within
+    1e-4.  Each planted slip (k_rope cached before its rope, q's rope on the
+    nope slice, kv_a's norm skipped) misses by far more."""
+    from mla_case import MlaOracleStepper, make_mla_model
+
+    mc = make_mla_model(oracle, 12, moe=(False, True), dim=512, n_heads=4, ctx=16, vocab=256, n_expert=8,
+                        n_used=2, ffn=256, sffn=256, dffn=256)
+    st = MlaOracleStepper(oracle, mc)
+    ref = _Step64(oracle, mc, st)
+    oracle.lib().lo_set_mla_slip(slip)
+    try:
+        worst = 0.0
+        for pos, tok in enumerate(np.random.default_rng(4).integers(0, mc.vocab, 5)):
+            x = st.embed(tok)
+            x0 = x.astype(np.float64)
+            logits = st.step(x, pos)
+            want, x64 = ref.step(x0, pos)
+            worst = max(worst, np.abs(logits - want).max() / np.abs(want).max(),
+                        np.abs(x - x64).max() / np.abs(x64).max())
+        if slip == 0:
+            assert worst < STEP_BOUND, worst
+        else:
+            assert worst > 100 * STEP_BOUND, (slip, worst)
+    finally:
+        oracle.lib().lo_set_mla_slip(0)
