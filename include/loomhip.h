@@ -412,8 +412,9 @@ int loomhip_frame_store_x(float *x, size_t dim);
  * attention norm, q/k/v, per-head Q/K norm (q_norm NULL: none), RoPE, the
  * K/V append at pos, attention, wo and residual, then the routed MoE layer
  * (router f32 [n_expert][dim] with an optional logit bias and selection-
- * only bias, gate/up/down stacked [n_expert] planes, the shared expert when
- * shexp_gate.data is set) or the dense FFN -- then the output norm and head.
+ * only bias, gate/up/down stacked [n_expert] planes; a layer with a shared
+ * expert, shexp_gate.data set, is DECLINED: the frame adds the routed output
+ * to the residual directly) or the dense FFN -- then the output norm and head.
  * Out: x after the last layer and logits [vocab].  PARITY numerics: the
  * engine's own llama.step arithmetic, bit for bit (moeRun's selection
  * order).  DECLINED, with nothing launched, for anything the frame does not

@@ -40,6 +40,10 @@ struct DmmvParams {
     int accumulate; // 1: out = out + value (a residual add, tensor.zig:50-52)
     int ident_n;    // launch_mmq only: > 0 means ident_n vectors in groups of consecutive
                     // vectors, identity pair maps, plane 0 -- no group or pair table is read
+    // the streamed gate/up of launch_mmq (mmqs_kernel) only:
+    const int *group_src; // [n_groups][group_stride]: the vector of each group's t-th pair (past n: the
+    int group_stride;     // last one's), read in place of pair_src at the group's index; null: pair_src
+    int pos_ident;        // pair_dst (and, without group_src, pair_src) is the identity over pair positions
 };
 
 // Up to DMMV_MAX_SEG matrices of any supported types against one activation
@@ -103,6 +107,8 @@ struct MoeBuckets {
     int *iota;        // [n*k] identity
     DmmvGroup *groups; // [max_groups]
     int *n_groups;    // [1]; null = route only, no bucketing
+    int max_groups;   // with group_src: its rows ([max_groups][nt]) receive each group's
+    int *group_src;   // pairs' tokens (the last repeated to nt), or null
 };
 int moe_max_groups(int n, int k, int n_expert, int nt);
 

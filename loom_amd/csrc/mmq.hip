@@ -16,6 +16,7 @@
 // the result lane l holds tokens 4*(l/16) .. +3 of that row.
 #include <type_traits>
 
+#include "device.hpp"
 #include "fmt.hpp"
 #include "kernels.hpp"
 
@@ -184,6 +185,109 @@ __device__ __forceinline__ void q6k_tile(const Q6kTile &w, int q4, const mmq_i4 
             r[mt][i] = s * (float)isum[mt][i];
         }
 }
+
+// ---- Q4_K with (token, group) rows: up to 16 tokens against unmasked weights -------
+// A 64-deep MFMA span holds two Q4_K groups, each with its own scale.
+// q4k_tile zeroes the weights outside one group and runs one MFMA per group:
+// a masked copy of every weight tile, and a quarter-rate integer multiply
+// per scale.  Here the A rows of an MFMA are (token, group) pairs instead:
+// row m = (t, g) carries token t's activations on the k slots of group part g
+// and zeros elsewhere -- arranged once per token as it loads -- so one MFMA
+// over the unmasked weights returns both groups' integer dots for 8 tokens,
+// and the scales multiply those dots with full-rate 24-bit multiply-adds
+// (|dot| < 2^16, scale <= 63).  The mins are one chained MFMA per span
+// against the part's group min replicated over its k slots: sum_g mn_g *
+// sum(x_g).  Integer dots are exact in any order, so every block's integers
+// -- and the f32 tail after them -- are the reference's.
+//
+// k slots.  MFMA (P, half) covers quant spans 2P and 2P + 1: lane
+// quarter q4 holds the 16 bytes 64P + 16*q4 of the block's 128 (span
+// 2P + q4/2, bytes 16*(q4&1) + [0, 16)), their low nibbles for half 0 and
+// high nibbles for half 1 -- group 4P + 2*(q4/2) + half.  A lane loads each
+// weight byte once.  A row r16 = (token r16/2, part r16&1) is nonzero on the
+// quarters with q4/2 == r16&1.
+struct Q4kTileV {
+    uint4 hdr;
+    uint4 qs[2]; // quant bytes 64P + 16*q4, P = 0, 1
+};
+
+__device__ __forceinline__ Q4kTileV q4kv_load(const uint8_t *blk, int q4) {
+    Q4kTileV w;
+    w.hdr = *(const uint4 *)blk;
+    w.qs[0] = *(const uint4 *)(blk + 16 + 16 * q4);
+    w.qs[1] = *(const uint4 *)(blk + 80 + 16 * q4);
+    return w;
+}
+
+// Offset in the block's 256 activations of lane quarter q4's 16 k slots in
+// MFMA j = 2P + half.
+__device__ __forceinline__ int q4kv_xoff(int j, int q4) {
+    return 128 * (j >> 1) + 64 * (q4 >> 1) + 32 * (j & 1) + 16 * (q4 & 1);
+}
+
+// Result lane (row r16, quarter q4) holds A rows 4*q4 + i: tokens 2*q4 + i/2
+// of the set (part i&1), whose two values r[s][0..1] it returns.
+template <int NS>
+__device__ __forceinline__ void q4kv_tile(const Q4kTileV &w, int q4, int ns, const mmq_i4 (&xa)[NS][4],
+                                          const float (&xd)[NS][2], float (&r)[NS][2]) {
+    const uint32_t a = w.hdr.y, b = w.hdr.z, c = w.hdr.w;
+    // Fmt<LH_Q4_K>::scales four groups at a time: bytes 0-3 are groups 0-3 (P = 0), 4-7 (P = 1)
+    const uint32_t scv[2] = {a & 0x3F3F3F3Fu, (c & 0x0F0F0F0Fu) | ((a >> 2) & 0x30303030u)};
+    const uint32_t mnv[2] = {b & 0x3F3F3F3Fu, ((c >> 4) & 0x0F0F0F0Fu) | ((b >> 2) & 0x30303030u)};
+    const float d = half_bits_to_float(w.hdr.x & 0xffff);
+    const float dmin = half_bits_to_float(w.hdr.x >> 16);
+    const mmq_i4 z = {0, 0, 0, 0};
+    // MFMA j = 2P + half: the nibbles (they replace the packed bytes), this
+    // lane's group min replicated (its k slots are group 4P + 2*(q4/2) +
+    // half), and the scales of parts 0 and 1 (groups 4P + half, 4P + 2 + half)
+    mmq_i4 wv[4];
+    int mr[4], s0[4], s1[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int P = j >> 1, half = j & 1;
+        const uint4 v = w.qs[P];
+        const uint32_t sh = 4 * half;
+        wv[j] = mmq_i4{(int)((v.x >> sh) & 0x0F0F0F0Fu), (int)((v.y >> sh) & 0x0F0F0F0Fu),
+                       (int)((v.z >> sh) & 0x0F0F0F0Fu), (int)((v.w >> sh) & 0x0F0F0F0Fu)};
+        mr[j] = (int)__builtin_amdgcn_perm(mnv[P], mnv[P], (uint32_t)(2 * (q4 >> 1) + half) * 0x01010101u);
+        s0[j] = (int)((scv[P] >> (8 * half)) & 0xFF);
+        s1[j] = (int)((scv[P] >> (8 * (2 + half))) & 0xFF);
+    }
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        if (s >= ns)
+            break;
+        mmq_i4 dq[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            dq[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[s][j], wv[j], z, 0, 0, 0);
+        mmq_i4 msum = z;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const mmq_i4 mrep = {mr[j], mr[j], mr[j], mr[j]};
+            msum = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[s][j], mrep, msum, 0, 0, 0);
+        }
+        int isum[2] = {0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            isum[0] += __mul24(s0[j], dq[j][0]) + __mul24(s1[j], dq[j][1]);
+            isum[1] += __mul24(s0[j], dq[j][2]) + __mul24(s1[j], dq[j][3]);
+        }
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) {
+            // xb.d * (d * f32(isum) - dmin * f32(min_isum))  (ggml.zig:1016-1017)
+            const int ms = msum[2 * jj] + msum[2 * jj + 1];
+            const float aa = d * (float)isum[jj];
+            const float bb = dmin * (float)ms;
+            r[s][jj] = xd[s][jj] * (aa - bb);
+        }
+    }
+}
+
+// LDS row stride of the (token, group) values: a result lane stores tokens
+// 2*q4 + jj of row r16, so the quarters' stores land 2*RS floats apart --
+// 16 or 48 mod 64 (RS = R + 8, R a multiple of 16) puts them in distinct banks.
+__host__ __device__ constexpr int q4kv_rs(int R) { return R + 8; }
 
 // LDS of one work group: the per-block values [FUSED + 1][nb][16*MT][16*RG + 1]
 // (the +1 staggers the four token quarters a wave writes across banks).
@@ -483,6 +587,281 @@ __global__ __launch_bounds__(64 * MMQ_WAVES) void mmq_stream_kernel(DmmvParams p
     }
 }
 
+// ---- grouped Q4_K expert matmuls streamed through LDS ------------------------------
+// The one-shot work groups of mmq_kernel hold their weights in registers from
+// the first load to the last MFMA: two of them fit a CU, each waits ~2.5 us
+// on its loads, and a grouped launch also queues a work group per group the
+// routing could make (at 32 tokens x top-8 over 128 experts: 144 possible,
+// ~45 made).  Here one work group per CU walks (group, run of row tiles)
+// items, sized on the device from the groups actually made, and streams each
+// tile's weights through a ring of three LDS stages with direct
+// global->LDS loads (16 bytes per lane, 1 KB of LDS per wave instruction):
+// the next tiles load while one computes, and the registers hold only the
+// group's activations.
+//
+// Geometry: a tile is TR = 16*RG rows x all NB super-blocks of one matrix
+// (both for the fused gate/up); wave (rg, b) computes block b of rows
+// 16*rg .. +16, RG = 8 / NB.  LDS slot j of a matrix is (block, 16-byte chunk
+// c, row r), r fastest, so a wave's operand read is 1 KB of consecutive
+// slots and a row header a broadcast; chunk 0 of a (row, block) is its
+// header, 1..8 its quants.
+template <bool FUSED, int NB>
+struct Mmqs {
+    static constexpr int RG = 8 / NB, W = RG * NB, TR = 16 * RG;
+    static constexpr int MAT = TR * NB * 9; // 16-byte chunks per matrix
+    static constexpr int MATS = FUSED ? 2 : 1;
+    static constexpr int CH = MATS * MAT;
+    static constexpr int INS = (CH + 63) / 64; // 1 KB wave loads per tile, dealt round robin:
+    static constexpr int K = (INS + W - 1) / W; // waves below KW issue K, the rest K - 1
+    static constexpr int KW = INS % W == 0 ? W : INS % W;
+    static constexpr int STAGE = INS * 1024;    // bytes per stage
+    static constexpr int RS = q4kv_rs(TR);
+    static constexpr int PART = MATS * NB * 16 * RS; // floats
+    static constexpr size_t LDS = 3 * (size_t)STAGE + 2 * 4 * (size_t)PART;
+    static_assert(LDS <= 160 * 1024, "three stages and two sums buffers fit a CU's LDS");
+};
+
+// Global address of chunk j of a tile (rows row0 .. +TR, clamped to the
+// matrix) of the Q4_K matrix at mb.
+template <int NB, int TR>
+__device__ __forceinline__ const uint8_t *mmqs_chunk(const uint8_t *mb, int rows, int row0, int j) {
+    const int bb = j / (9 * TR), c = (j / TR) % 9, r = j % TR;
+    const int row = min(row0 + r, rows - 1);
+    return mb + ((size_t)row * NB + bb) * 144 + c * 16;
+}
+
+// A work-group barrier that waits for this wave's LDS stores only: the
+// workgroup fence of lds_barrier also waits for the direct-to-LDS loads in
+// flight (they are LDS stores), which would drain the ring at every tile.
+// The loads a barrier must cover are waited for explicitly (wait_vm) before
+// it; the asm's memory clobber keeps the compiler from moving LDS accesses
+// across it.
+__device__ __forceinline__ void ring_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0); vmcnt and expcnt left open
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// Reads of a stage.  The compiler cannot tell the three stages apart, so
+// before any LDS read it would wait for every direct-to-LDS load in flight;
+// the reads are issued as one asm block instead, ending in its own lgkmcnt
+// wait, after the explicit vmcnt wait and barrier that order them behind
+// their own tile's loads.
+typedef unsigned mmqs_u4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t lds_off(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+__device__ __forceinline__ void lds_read3(uint32_t a0, uint32_t a1, uint32_t a2, uint4 &r0, uint4 &r1, uint4 &r2) {
+    mmqs_u4 x0, x1, x2;
+    asm volatile("ds_read_b128 %0, %3\n\tds_read_b128 %1, %4\n\tds_read_b128 %2, %5\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(x0), "=&v"(x1), "=&v"(x2)
+                 : "v"(a0), "v"(a1), "v"(a2)
+                 : "memory");
+    r0 = make_uint4(x0.x, x0.y, x0.z, x0.w);
+    r1 = make_uint4(x1.x, x1.y, x1.z, x1.w);
+    r2 = make_uint4(x2.x, x2.y, x2.z, x2.w);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() { // s_waitcnt vmcnt(N) alone
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+template <bool FUSED, int NB>
+__global__ __launch_bounds__(64 * MMQ_WAVES) void mmqs_kernel(DmmvParams p) {
+    using G = Mmqs<FUSED, NB>;
+    constexpr int TOK = 16, TR = G::TR, RS = G::RS, K = G::K;
+    constexpr int TPS = 8, NS = TOK / TPS; // tokens per MFMA set (x 2 groups = 16 A rows), sets
+    __shared__ __align__(16) uint8_t st0[G::STAGE], st1[G::STAGE], st2[G::STAGE];
+    __shared__ __align__(16) float part0[G::PART], part1[G::PART];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ln = threadIdx.x & 63;
+    const int r16 = ln & 15, q4 = ln >> 4;
+    const int rg = wave % G::RG, b = wave / G::RG;
+    const int rl = 16 * rg + r16;
+    const int tiles = (p.rows + TR - 1) / TR;
+    const size_t mat = (size_t)NB * TOK * RS;
+    const mmq_i4 z = {0, 0, 0, 0};
+    const bool live = (q4 >> 1) == (r16 & 1); // A row r16 = (token r16/2, group part r16&1)
+    // items: each group's tiles in cpg runs, so that the items about fill the grid
+    const int ng = p.n_groups_dev ? *p.n_groups_dev : p.n_groups;
+    const int nwg = gridDim.x;
+    const int cpg = ng > 0 ? max(1, min(tiles, nwg / ng)) : 1;
+    const int run = (tiles + cpg - 1) / cpg;
+    const int items = ng * cpg;
+    for (int item = blockIdx.x; item < items; item += nwg) {
+        const int gi = item / cpg, t0 = (item % cpg) * run;
+        const int nt = min(run, tiles - t0);
+        if (nt <= 0)
+            continue;
+        const DmmvGroup grp = p.groups[gi];
+        const int n = grp.n, ns = (n + TPS - 1) / TPS;
+        const uint8_t *pb = p.w + (size_t)grp.plane * p.plane_bytes;
+        const uint8_t *pb2 = FUSED ? p.w2 + (size_t)grp.plane * p.plane_bytes : pb;
+        // the group's activations as A rows, and the block scales of this
+        // lane's result tokens 2*q4 + jj of each set
+        auto vec_of = [&](int t) {
+            if (p.group_src)
+                return p.group_src[(size_t)gi * p.group_stride + t];
+            t = min(t, n - 1);
+            return p.pos_ident ? grp.first + t : p.pair_src[grp.first + t];
+        };
+        mmq_i4 xa[NS][4];
+        float xd[NS][2];
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const int8_t *xr = p.xq + (size_t)vec_of(TPS * s + r16 / 2) * p.cols + 256 * b;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                xa[s][j] = live && s < ns ? *(const mmq_i4 *)(xr + q4kv_xoff(j, q4)) : z;
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++)
+                xd[s][jj] = s < ns ? p.xd[(size_t)vec_of(TPS * s + 2 * q4 + jj) * NB + b] : 0.0f;
+        }
+        // one tile's weights into a stage: this wave's 1 KB pieces I = wave + W*i
+        auto issue = [&](int tile, uint8_t *stg) {
+            const int row0 = tile * TR;
+#pragma unroll
+            for (int i = 0; i < K; i++) {
+                const int I = wave + G::W * i;
+                if (I >= G::INS)
+                    break; // (uniform)
+                int j = I * 64 + ln;
+                const uint8_t *src = pb; // past the tile's chunks: a valid address, never read back
+                if (j < G::CH) {
+                    const uint8_t *mb = pb;
+                    if (FUSED && j >= G::MAT) {
+                        mb = pb2;
+                        j -= G::MAT;
+                    }
+                    src = mmqs_chunk<NB, TR>(mb, p.rows, row0, j);
+                }
+                __builtin_amdgcn_global_load_lds((const void *)src,
+                                                 (__attribute__((address_space(3))) void *)(stg + I * 1024), 16, 0, 0);
+            }
+        };
+        // tile k's loads have landed once only the next tile's (this wave's
+        // K or K - 1 pieces, issued after it) may be outstanding
+        auto wait_tile = [&](int k) {
+            if (k + 1 >= nt)
+                wait_vm<0>();
+            else if (wave < G::KW)
+                wait_vm<K>();
+            else
+                wait_vm<K - 1>();
+        };
+        // a tile's MFMAs from its stage, its per-block values into pbuf
+        auto compute = [&](const uint8_t *stg, float *pbuf) {
+            auto frag = [&](int m) {
+                const uint32_t mbase = lds_off(stg) + (uint32_t)m * G::MAT * 16;
+                Q4kTileV w;
+                lds_read3(mbase + ((b * 9 + 0) * TR + rl) * 16, mbase + ((b * 9 + 1 + q4) * TR + rl) * 16,
+                          mbase + ((b * 9 + 5 + q4) * TR + rl) * 16, w.hdr, w.qs[0], w.qs[1]);
+                return w;
+            };
+            float r[NS][2], r2[NS][2];
+            q4kv_tile<NS>(frag(0), q4, ns, xa, xd, r);
+            if constexpr (FUSED)
+                q4kv_tile<NS>(frag(1), q4, ns, xa, xd, r2);
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+                if (s < ns)
+#pragma unroll
+                    for (int jj = 0; jj < 2; jj++) {
+                        const size_t o = ((size_t)b * TOK + TPS * s + 2 * q4 + jj) * RS + rl;
+                        pbuf[o] = r[s][jj];
+                        if constexpr (FUSED)
+                            pbuf[mat + o] = r2[s][jj];
+                    }
+        };
+        // tile k's outputs: every (token, row) summed over its blocks in block
+        // order from pbuf (all the block values read first), SwiGLU(gate, up)
+        // when fused, stored -- pos_ident, no residual add (launch_mmqs), so
+        // no global load here, which would wait (vmcnt counts in order) for
+        // the tiles in flight
+        auto reduce = [&](int k, const float *pbuf) {
+            const int row0 = (t0 + k) * TR;
+            for (int idx = threadIdx.x; idx < n * TR; idx += blockDim.x) {
+                const int tk = idx / TR, rr = idx % TR;
+                if (row0 + rr >= p.rows)
+                    continue;
+                const float *pv = pbuf + (size_t)tk * RS + rr;
+                float v1[NB], v2[NB];
+#pragma unroll
+                for (int bb = 0; bb < NB; bb++) {
+                    v1[bb] = pv[(size_t)bb * TOK * RS];
+                    if constexpr (FUSED)
+                        v2[bb] = pv[mat + (size_t)bb * TOK * RS];
+                }
+                float acc = 0.0f;
+#pragma unroll
+                for (int bb = 0; bb < NB; bb++)
+                    acc = acc + v1[bb];
+                float v = acc;
+                if constexpr (FUSED) {
+                    float acc2 = 0.0f;
+#pragma unroll
+                    for (int bb = 0; bb < NB; bb++)
+                        acc2 = acc2 + v2[bb];
+                    v = swiglu1(acc, acc2);
+                }
+                p.out[(size_t)(grp.first + tk) * p.out_stride + row0 + rr] = v;
+            }
+        };
+        // Step k: wait for tile k, one barrier, then tile k - 1's sums out (its
+        // values were written before this barrier), tile k + 2's loads into
+        // the stage tile k - 1 computed from (every wave has passed its reads),
+        // and tile k's MFMAs.  The sums buffers alternate, so tile k's values
+        // are written while tile k - 1's are read.  The stores precede the next
+        // loads, so the next wait (vmcnt counts in order) covers them too.
+        auto step = [&](int k, const uint8_t *cur, uint8_t *refill) {
+            wait_tile(k);
+            ring_barrier();
+            if (k > 0)
+                reduce(k - 1, (k - 1) & 1 ? part1 : part0);
+            if (k + 2 < nt)
+                issue(t0 + k + 2, refill);
+            compute(cur, k & 1 ? part1 : part0);
+        };
+        issue(t0, st0);
+        if (nt > 1)
+            issue(t0 + 1, st1);
+        for (int k = 0; k < nt; k += 3) {
+            step(k, st0, st2);
+            if (k + 1 >= nt)
+                break;
+            step(k + 1, st1, st0);
+            if (k + 2 >= nt)
+                break;
+            step(k + 2, st2, st1);
+        }
+        ring_barrier();
+        reduce(nt - 1, (nt - 1) & 1 ? part1 : part0);
+        ring_barrier(); // the next item's stages and sums reuse this one's LDS
+    }
+}
+
+// The streamed launch: the fused gate/up of grouped experts (not lane
+// groups), Q4_K over 2048 columns, up to 16 tokens per group, outputs at the
+// pair positions with no residual add; false = not served.
+static bool launch_mmqs(int t, bool fused, const DmmvParams &p, hipStream_t st) {
+    if (t != LH_Q4_K || !fused || p.ident_n > 0 || !p.groups || !p.pos_ident || p.accumulate || p.rows < 1 ||
+        p.cols != 8 * 256)
+        return false;
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
+            cus = c;
+        else
+            cus = 256;
+    }
+    // one work group per CU (its LDS fills one)
+    hipLaunchKernelGGL((mmqs_kernel<true, 8>), dim3(cus), dim3(64 * Mmqs<true, 8>::W), 0, st, p);
+    return true;
+}
+
+
 // Shape of a launch: KS = min(nb, MMQ_WAVES) slices of SBW super-blocks per
 // wave, as many row tiles beside them as fit the wave count and 64 KB of LDS,
 // but no more than the matrix has.
@@ -590,6 +969,10 @@ bool launch_mmq(int t, int max_tok, bool fused, const DmmvParams &p, hipStream_t
     int rg, ks, sbw;
     if (!mmq_shape(p.rows, p.cols, mt, fused, rg, ks, sbw))
         return false;
+    if (mt == 1 && launch_mmqs(t, fused, p, st)) {
+        note_launch();
+        return true;
+    }
     if (t == LH_Q4_K) {
         if (mt == 1)
             fused ? mmq_launch_t<LH_Q4_K, 1, true>(p, rg, ks, sbw, st)

@@ -243,6 +243,20 @@ __device__ void bucket_block(const GateParams &p) {
             g.n = (c - gi * nt) < nt ? (c - gi * nt) : nt;
             p.b.groups[go + gi] = g;
         }
+    if (!p.b.group_src)
+        return;
+    // each group's tokens in pair order (the last one repeated to nt; 0 past
+    // the groups made), read by the expert kernels at the group's index
+    __syncthreads(); // this work group's groups and pair_tok stores are visible to it
+    for (int i = tid; i < p.b.max_groups * nt; i += GT_THREADS) {
+        const int g = i / nt, t = i % nt;
+        int src = 0;
+        if (g < gtot) {
+            const DmmvGroup gr = p.b.groups[g];
+            src = p.b.pair_tok[gr.first + min(t, gr.n - 1)];
+        }
+        p.b.group_src[i] = src;
+    }
 }
 
 __global__ __launch_bounds__(GT_THREADS) void moe_gate_kernel(GateParams p) {

@@ -215,6 +215,7 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     const size_t o_ids = take(P * 4), o_gates = take(P * 4);
     const size_t o_ptok = take(P * 4), o_pof = take(P * 4), o_iota = take(P * 4);
     const size_t o_groups = take(maxg * sizeof(DmmvGroup)), o_ng = take(16);
+    const size_t o_gsrc = take(mq ? (size_t)maxg * nt * 4 : 0);
     const size_t o_act = take(P * m.ffn * 4);
     const size_t o_qa = take(qbytes(P, m.ffn));
     const size_t o_y = take(decode ? 0 : P * m.dim * 4);
@@ -313,6 +314,8 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     b.iota = (int *)(base + o_iota);
     b.groups = (DmmvGroup *)(base + o_groups);
     b.n_groups = (int *)(base + o_ng);
+    b.max_groups = mq ? maxg : 0;
+    b.group_src = mq ? (int *)(base + o_gsrc) : nullptr;
     float *y = (float *)(base + o_y);
     gp.b = b;
     gp.chain = 1;
@@ -335,6 +338,9 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     gu.n_groups = maxg;
     gu.out = act;
     gu.out_stride = (int)m.ffn;
+    gu.group_src = b.group_src;
+    gu.group_stride = nt;
+    gu.pos_ident = 1;
     gu.rpw = mq ? 0 : dmmv_pick_rpw(m.gate_t, (int)m.dim, (int)m.ffn, exp_groups, nt, true);
     int ph = prof_begin(LOOMHIP_KT_GATE_UP, st);
     bool launched = mq ? launch_mmq(m.gate_t, nt, true, gu, st) : launch_dmmv(m.gate_t, nt, true, gu, st);
