@@ -559,18 +559,15 @@ __global__ __launch_bounds__(SM ? 64 * PVS_SM_WAVES : 64 * (1 + PVS_NP)) void at
     };
     float inv = 0.0f;
     if constexpr (SM) {
-        // the scores first, then the value loads: the in-order load counter
-        // lets the softmax wait for its scores alone
+        // the scores, their max, then the value loads: issued before the max,
+        // the loads would be waited for with the scores (the compiler's wait
+        // covers every load in flight), and the producers would reach the
+        // softmax's first barrier only when their values had landed
         float sv[PVS_SM_VALS];
 #pragma unroll
         for (int k = 0; k < PVS_SM_VALS; k++) {
             const int j = threadIdx.x + 64 * NW * k;
             sv[k] = j < P ? prow[j] : -INFINITY;
-        }
-        if (producer) {
-#pragma unroll
-            for (int d = 0; d < PVS_SETS; d++)
-                load_v(d, hv[d]);
         }
         // softmax_row_exact's steps: the max (order-free), e_t = exp(s_t - m)
         // zero-filled to whole 64s, 1 / the position-ordered sum
@@ -579,20 +576,19 @@ __global__ __launch_bounds__(SM ? 64 * PVS_SM_WAVES : 64 * (1 + PVS_NP)) void at
         for (int k = 0; k < PVS_SM_VALS; k++)
             m = fmaxf(m, sv[k]);
         m = wave_max(m);
+        if (producer) {
+#pragma unroll
+            for (int d = 0; d < PVS_SETS; d++)
+                load_v(d, hv[d]);
+        }
         if (ln == 0)
             redf[wave] = m;
-        __syncthreads();
+        lds_barrier();
         m = redf[0];
         for (int w = 1; w < NW; w++)
             m = fmaxf(m, redf[w]);
-        const int n64 = (P + 63) & ~63;
-#pragma unroll
-        for (int k = 0; k < PVS_SM_VALS; k++) {
-            const int j = threadIdx.x + 64 * NW * k;
-            if (j < n64)
-                e[j] = j < P ? exp_f32_poly(sv[k] - m) : 0.0f;
-        }
-        __syncthreads();
+        softmax_exps<64 * NW>(sv, m, P, (P + 63) & ~63, e);
+        lds_barrier();
         inv = 1.0f / seq_sum_nonneg<NW>(e, P, seq);
     }
     auto load = [&](int tile, uint4 (&v)[4], float4 &p) {

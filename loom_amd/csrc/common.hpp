@@ -95,13 +95,12 @@ __device__ inline float exp_f32(float x) { return (float)exp((double)x); }
 // (float)exp((double)x) on every f32 input checked (every seventh bit pattern
 // in [-110, 90]).  Inputs at or below -104 round to +0, above 88.8 to +inf.
 // Its constants take 26 VGPRs where the compiler hoists them, so kernels
-// short of registers keep exp_f32.
-__device__ inline float exp_f32_poly(float xf) {
-    if (!(xf > -104.0f))
-        return xf != xf ? xf : 0.0f;
-    if (xf > 88.8f)
-        return __builtin_inff();
-    const double x = (double)xf;
+// short of registers keep exp_f32.  exp_f32_core evaluates the input clamped
+// into [-104, 88.8] with no branch (NaN becomes -104), exp_f32_fix selects
+// the special values; a caller with several independent exponentials
+// computes their cores together so the dependent FMA chains interleave.
+__device__ inline float exp_f32_core(float xf) {
+    const double x = (double)__builtin_fminf(__builtin_fmaxf(xf, -104.0f), 88.8f);
     const double kd = __builtin_rint(x * 0x1.71547652b82fep+0); // x / ln 2
     const double r = __builtin_fma(kd, -0x1.abc9e3b39803fp-56, __builtin_fma(kd, -0x1.62e42fefa39efp-1, x));
     double p = 0x1.6124613a86d09p-33; // 1/13!
@@ -120,6 +119,10 @@ __device__ inline float exp_f32_poly(float xf) {
     p = __builtin_fma(p, r, 1.0);
     return (float)__builtin_ldexp(p, (int)kd);
 }
+__device__ inline float exp_f32_fix(float xf, float y) {
+    return xf > 88.8f ? __builtin_inff() : xf > -104.0f ? y : xf != xf ? xf : 0.0f;
+}
+__device__ inline float exp_f32_poly(float xf) { return exp_f32_fix(xf, exp_f32_core(xf)); }
 
 // Round half away from zero, saturate at +-127, non-finite -> 0
 // (src/gguf/ggml.zig:1067-1073 toI8Saturating).

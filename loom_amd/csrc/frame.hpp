@@ -159,14 +159,14 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
     const double inc = wave_scan_d(own);
     if (ln == 63)
         s.wtot[wave] = inc;
-    __syncthreads();
+    lds_barrier();
     double ex = inc - own;
 #pragma unroll
     for (int w = 0; w < NW - 1; w++) // the earlier waves' totals (+0 from the rest: ex >= 0)
         ex = ex + (w < wave ? s.wtot[w] : 0.0);
     if (j0 < n64 && j0 % L == 0)
         s.fst[j0 / L] = __float_as_uint((float)ex);
-    __syncthreads();
+    lds_barrier();
     // 2. every chunk's chain from 64 starts around its estimate (below).
     //    chain(r, c) is chunk c's chain from the one start r, for the serial
     //    fallback of step 3: blocks of 64 values (16 float4 groups, unrolled),
@@ -252,7 +252,7 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
     // 3. the exact running sum through the chunks: lane i of chunk c has
     //    stored n_c(i), the lane of chunk c + 1's window that holds its end
     //    (flag 0x100: outside the window), so the exact path is a chain of
@@ -292,8 +292,36 @@ __device__ __forceinline__ float seq_sum_nonneg(const float *v, int n, SeqSumLds
         if (ln == 0)
             s.out = __int_as_float(run);
     }
-    __syncthreads();
+    lds_barrier();
     return s.out;
+}
+
+// e[j] = exp(sv[k] - m) (j = threadIdx.x + NT*k) for j < P, +0 up to n64:
+// the exponentials four at a time, unconditionally inside a group (sv is
+// -inf past P), so their dependent FMA chains interleave; groups wholly past
+// n64 are skipped (uniform).
+template <int NT, int NV>
+__device__ __forceinline__ void softmax_exps(const float (&sv)[NV], float m, int P, int n64, float *e) {
+#pragma unroll
+    for (int kb = 0; kb < NV; kb += 4) {
+        if (NT * kb >= n64)
+            break;
+        float a[4], y[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            a[i] = kb + i < NV ? sv[kb + i] - m : -INFINITY;
+            y[i] = exp_f32_core(a[i]);
+        }
+        // all four cores before any select: left to itself the compiler sinks
+        // each into the branch of its range test, one chain at a time
+        asm volatile("" : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int j = (int)threadIdx.x + NT * (kb + i);
+            if (kb + i < NV && j < n64)
+                e[j] = j < P ? exp_f32_fix(a[i], y[i]) : 0.0f;
+        }
+    }
 }
 
 // ---- the reference-order attention (attn_exact.hip), PARITY numerics --------
@@ -331,17 +359,12 @@ __device__ __forceinline__ void softmax_row_exact(float *row, int P, float *e, f
     m = wave_max(m);
     if (ln == 0)
         redf[wave] = m;
-    __syncthreads();
+    lds_barrier();
     m = redf[0];
     for (int w = 1; w < NT / 64; w++)
         m = fmaxf(m, redf[w]);
-#pragma unroll
-    for (int k = 0; k < NV; k++) {
-        const int j = tid + NT * k;
-        if (j < 64 * C)
-            e[j] = j < P ? exp_f32_poly(sv[k] - m) : 0.0f;
-    }
-    __syncthreads();
+    softmax_exps<NT>(sv, m, P, 64 * C, e);
+    lds_barrier();
     const float inv = 1.0f / seq_sum_nonneg<NT / 64>(e, P, seq);
     for (int j = tid; j < P; j += NT)
         row[j] = e[j] * inv;
