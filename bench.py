@@ -58,6 +58,14 @@ HEAD_BYTES = 151936 * 8 * 210  # Q6_K [151936][2048]
 ADD_LATENCY_CYCLES = 4.7
 LDS_FED_CYCLES = 8.4
 CLOCK_HZ = 2.4e9
+# MI355X dense matrix-core peaks (no sparsity) and one v_mfma_i32_16x16x64_i8
+# (16 x 16 outputs, 64 deep, a multiply and an add each)
+PEAK_BF16_OPS, PEAK_INT8_OPS = 2.5e15, 5.0e15
+MFMA_I8_OPS = 2 * 16 * 16 * 64
+FFN = 768
+# The grouped expert launches at 16+ tokens and the kernels that serve them
+# (config 4: Q4_K gate/up over 2048 columns, Q6_K down over 768)
+MOE_GEMM_KERNELS = {"gate_up": "lh::mmqs_kernel<true, 8>", "down": "lh::mmq_kernel<14, 1, false, 1>"}
 # Largest per-step logit max-rel of FAST numerics against the CPU path at the
 # 4096-token context (32 lanes), measured by the GPU parity test named in the
 # output line.
@@ -148,7 +156,7 @@ def bench_batch(dm, b, args):
     dm.desc.ids_out = ids.data_ptr()
     dec.pos.fill_(args.ctx)
     be.profileKernels(True)
-    distinct = []
+    distinct, groups, sets8 = [], [], []
     prof_steps = min(args.steps, 6)
     for _ in range(prof_steps):
         torch.cuda._sleep(50_000_000)
@@ -156,13 +164,19 @@ def bench_batch(dm, b, args):
         torch.cuda.synchronize()
         h = ids.cpu().numpy()
         distinct += [len(np.unique(h[li])) for li in range(dm.spec.n_layers)]
+        for li in range(dm.spec.n_layers):  # the expert groups of <= 16 tokens the grouped launches run
+            counts = np.bincount(h[li].ravel(), minlength=N_EXPERT)
+            sizes = [min(16, c - g) for c in counts if c > 0 for g in range(0, int(c), 16)]
+            groups.append(len(sizes))
+            sets8.append(sum((n + 7) // 8 for n in sizes))
     stats = be.kernelStats()
     be.profileKernels(False)
     dm.desc.ids_out = None
     del dec, graph
     torch.cuda.empty_cache()
     return dict(ms=ms, wall_ms=wall / args.steps * 1e3, tok_s=b * 1e3 / ms, stats=stats,
-                distinct=float(np.mean(distinct)), prof_steps=prof_steps)
+                distinct=float(np.mean(distinct)), groups=float(np.mean(groups)), sets8=float(np.mean(sets8)),
+                prof_steps=prof_steps)
 
 
 N_HEADS, HD = 32, 128
@@ -271,6 +285,67 @@ def roofline(r, b, ctx, layers):
         if prof:
             roof["chain"]["frac_rocprof"] = round(floor_s / (prof / 1e6), 4)
     return roof, per_kernel
+
+
+def mfma_issued_measured(kernel):
+    """int8 MFMA ops per launch of a kernel as the committed rocprofv3 PMC
+    summary counted them (SQ_INSTS_VALU_MFMA_MOPS_I8 x 512), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "mfma_per_launch.json")) as f:
+            return json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def moe_gemm(r, b, ctx):
+    """The grouped expert matmuls of one MoE layer at b tokens on the int8
+    matrix cores: useful ops (a multiply and an add per weight per routed
+    token: 2 x pairs x rows x cols per matrix) per event-timed launch, against
+    the bf16 and int8 dense peaks and against the attainable min(int8 peak,
+    AI x HBM peak), AI = useful ops / the launch's algorithmic bytes.  Issued
+    = the MFMAs the kernels run for this layer's groups (experts' tokens in
+    groups of up to 16): gate/up per (group, 16-row tile, super-block) one
+    set of 8 MFMAs per matrix per 8 tokens (4 dot + 4 mins, A rows = (token,
+    group)), down 16 per (group, 16-row tile, super-block) (one per 16-value
+    run); beside it the count rocprofv3 measured, and the same rates over
+    the committed rocprof duration."""
+    pairs = b * TOP_K
+    out = {}
+    for tag, kern in MOE_GEMM_KERNELS.items():
+        s = r["stats"].get(tag)
+        if not s:
+            continue
+        avg_s = s["ms"] / s["count"] / 1e3
+        useful = (2 if tag == "gate_up" else 1) * 2 * pairs * FFN * DIM
+        if tag == "gate_up":
+            issued = r["sets8"] * 2 * 8 * (FFN // 16) * (DIM // 256) * MFMA_I8_OPS
+        else:
+            issued = r["groups"] * 16 * (DIM // 16) * (FFN // 256) * MFMA_I8_OPS
+        byts = per_launch_bytes(tag, b, ctx, r["distinct"])
+        ai = useful / byts
+        attain = min(PEAK_INT8_OPS, ai * HBM_PEAK_GBS * 1e9)
+        ach = useful / avg_s
+        e = {"kernel": kern, "useful_ops": int(useful), "issued_ops_est": int(issued),
+             "issued_over_useful": round(issued / useful, 2), "bytes": int(byts), "ai_ops_per_byte": round(ai, 1),
+             "avg_launch_us": round(avg_s * 1e6, 2), "achieved_Tops": round(ach / 1e12, 1),
+             "frac_bf16_peak": round(ach / PEAK_BF16_OPS, 4), "frac_int8_peak": round(ach / PEAK_INT8_OPS, 4),
+             "attainable_Tops": round(attain / 1e12, 1), "frac_attainable": round(ach / attain, 4),
+             "hbm_GBs": round(byts / avg_s / 1e9, 1)}
+        meas = mfma_issued_measured(kern)
+        if meas:
+            e["issued_ops_rocprof"] = meas
+        try:
+            with open(os.path.join(ROOT, "profiles", "kernel_durations.json")) as f:
+                prof = json.load(f).get(kern, {}).get("n1")
+        except (OSError, ValueError):
+            prof = None
+        if prof:
+            achp = useful / (prof / 1e6)
+            e.update({"rocprof_avg_us": prof, "achieved_Tops_rocprof": round(achp / 1e12, 1),
+                      "frac_attainable_rocprof": round(achp / attain, 4),
+                      "frac_int8_peak_rocprof": round(achp / PEAK_INT8_OPS, 4)})
+        out[tag] = e
+    return out
 
 
 def step_bytes(b, ctx, distinct, layers):
@@ -1069,6 +1144,8 @@ def main():
                              "distinct_experts_per_layer": round(rb["distinct"], 2),
                              "roofline": rb["roofline"], "step_roofline": step_roof(rb),
                              "kernels": rb["per_kernel"]}
+        if b >= 16:  # the grouped expert matmuls run on the matrix cores
+            line[f"batch{b}"]["moe_gemm"] = moe_gemm(rb, b, args.ctx)
     if "fast" in modes and hmode != "fast":
         # FAST numerics do not hold north_star's 2e-3 at this context: reported
         # beside the headline with the bound the tests measure for them

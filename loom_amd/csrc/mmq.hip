@@ -96,8 +96,8 @@ __device__ __forceinline__ void q4k_tile(const Q4kTile &w, int q4, const mmq_i4 
             const mmq_i4 db = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[mt][p], wb, z, 0, 0, 0);
             msum[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[mt][p], mrep, msum[mt], 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                isum[mt][i] += sc[2 * p] * da[i] + sc[2 * p + 1] * db[i];
+            for (int i = 0; i < 4; i++) // 24-bit products (|dot| < 2^16, sc <= 63): full rate, exact
+                isum[mt][i] += __mul24(sc[2 * p], da[i]) + __mul24(sc[2 * p + 1], db[i]);
         }
     }
 #pragma unroll
@@ -171,8 +171,8 @@ __device__ __forceinline__ void q6k_tile(const Q6kTile &w, int q4, const mmq_i4 
             for (int mt = 0; mt < MT; mt++) {
                 const mmq_i4 dq = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[mt][h], bq, z, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    isum[mt][i] += sc * dq[i];
+                for (int i = 0; i < 4; i++) // 24-bit products (|dot| < 2^16, |sc| <= 128): full rate, exact
+                    isum[mt][i] += __mul24(sc, dq[i]);
             }
         }
     }
