@@ -141,7 +141,7 @@ __device__ __forceinline__ float decode_gates(const DecodeParams &p, int my_id,
             if ((my_id >> 6) == i)
                 l = v;
         }
-        g = p.gating == 2 ? 1.0f / (1.0f + exp_f32(-l)) : l;
+        g = p.gating == 2 ? 1.0f / (1.0f + exp_f32_poly(-l)) : l;
     } else {
         float mx = -INFINITY;
 #pragma unroll
@@ -150,7 +150,7 @@ __device__ __forceinline__ float decode_gates(const DecodeParams &p, int my_id,
         mx = wave_max(mx);
 #pragma unroll
         for (int i = 0; i < NI; i++)
-            sc[lane + 64 * i] = exp_f32(lv[i] - mx);
+            sc[lane + 64 * i] = exp_f32_poly(lv[i] - mx);
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         const float inv = 1.0f / lds_seq_sum(sc, p.n_expert);

@@ -233,7 +233,7 @@ template <> struct Fmt<LH_Q4_0> {
 
 // silu(g) * u with silu(x) = x / (1 + exp(-x))  (src/core/tensor.zig:30-57)
 __device__ inline float swiglu1(float g, float u) {
-    const float e = exp_f32(-g);
+    const float e = exp_f32_poly(-g);
     const float s = g / (1.0f + e);
     return s * u;
 }

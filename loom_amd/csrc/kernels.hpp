@@ -107,8 +107,7 @@ struct MoeBuckets {
     int *iota;        // [n*k] identity
     DmmvGroup *groups; // [max_groups]
     int *n_groups;    // [1]; null = route only, no bucketing
-    int max_groups;   // with group_src: its rows ([max_groups][nt]) receive each group's
-    int *group_src;   // pairs' tokens (the last repeated to nt), or null
+    int *group_src;   // [groups made][nt]: each group's pairs' tokens (the last repeated to nt), or null
 };
 int moe_max_groups(int n, int k, int n_expert, int nt);
 

@@ -199,7 +199,8 @@ __device__ int block_excl_scan(int v, int *total) {
 // order is deterministic.
 __device__ void bucket_block(const GateParams &p) {
     __shared__ uint32_t mask[MAX_E][MAX_TOK / 32];
-    __shared__ int off[MAX_E];
+    __shared__ int off[MAX_E], goff[MAX_E], cnt[MAX_E];
+    __shared__ uint8_t eid[MAX_TOK * MAX_K]; // each pair's expert, read from ids once
     const int tid = threadIdx.x, n = p.n, K = p.k, E = p.n_expert, nt = p.nt;
     const int W = (n + 31) / 32;
     for (int i = tid; i < E * W; i += GT_THREADS)
@@ -208,6 +209,7 @@ __device__ void bucket_block(const GateParams &p) {
     const int P = n * K;
     for (int q = tid; q < P; q += GT_THREADS) {
         const int t = q / K, e = min((int)ld_dev(p.ids + q), E - 1);
+        eid[q] = (uint8_t)e; // E <= MAX_E = 256
         atomicOr(&mask[e][t >> 5], 1u << (t & 31));
     }
     __syncthreads();
@@ -219,13 +221,16 @@ __device__ void bucket_block(const GateParams &p) {
     const int o = block_excl_scan(c, &tot);
     const int ng = (c + nt - 1) / nt;
     const int go = block_excl_scan(ng, &gtot);
-    if (tid < E)
+    if (tid < E) {
         off[tid] = o;
+        goff[tid] = go;
+        cnt[tid] = c;
+    }
     if (tid == 0)
         *p.b.n_groups = gtot;
     __syncthreads();
     for (int q = tid; q < P; q += GT_THREADS) {
-        const int t = q / K, e = min((int)ld_dev(p.ids + q), E - 1);
+        const int t = q / K, e = eid[q];
         int rank = 0;
         for (int w = 0; w < (t >> 5); w++)
             rank += __popc(mask[e][w]);
@@ -234,6 +239,15 @@ __device__ void bucket_block(const GateParams &p) {
         p.b.pair_tok[pos] = t;
         p.b.pair_of[q] = pos;
         p.b.iota[q] = q;
+        if (p.b.group_src) {
+            // each group's tokens in pair order, the group's last one repeated
+            // to nt (read by the expert kernels at the group's index)
+            int *row = p.b.group_src + (size_t)(goff[e] + rank / nt) * nt;
+            const int i0 = rank % nt;
+            const int i1 = rank == cnt[e] - 1 ? nt : i0 + 1;
+            for (int i = i0; i < i1; i++)
+                row[i] = t;
+        }
     }
     if (tid < E)
         for (int gi = 0; gi * nt < c; gi++) {
@@ -243,20 +257,6 @@ __device__ void bucket_block(const GateParams &p) {
             g.n = (c - gi * nt) < nt ? (c - gi * nt) : nt;
             p.b.groups[go + gi] = g;
         }
-    if (!p.b.group_src)
-        return;
-    // each group's tokens in pair order (the last one repeated to nt; 0 past
-    // the groups made), read by the expert kernels at the group's index
-    __syncthreads(); // this work group's groups and pair_tok stores are visible to it
-    for (int i = tid; i < p.b.max_groups * nt; i += GT_THREADS) {
-        const int g = i / nt, t = i % nt;
-        int src = 0;
-        if (g < gtot) {
-            const DmmvGroup gr = p.b.groups[g];
-            src = p.b.pair_tok[gr.first + min(t, gr.n - 1)];
-        }
-        p.b.group_src[i] = src;
-    }
 }
 
 __global__ __launch_bounds__(GT_THREADS) void moe_gate_kernel(GateParams p) {

@@ -314,7 +314,6 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     b.iota = (int *)(base + o_iota);
     b.groups = (DmmvGroup *)(base + o_groups);
     b.n_groups = (int *)(base + o_ng);
-    b.max_groups = mq ? maxg : 0;
     b.group_src = mq ? (int *)(base + o_gsrc) : nullptr;
     float *y = (float *)(base + o_y);
     gp.b = b;
