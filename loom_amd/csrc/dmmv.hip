@@ -14,6 +14,7 @@
 // each output row is summed over its blocks sequentially in block order --
 // the reference's `acc += r` -- so the result is bit-identical to the CPU.
 #include "fmt.hpp"
+#include "frame.hpp"
 
 namespace lh {
 
@@ -194,6 +195,90 @@ __global__ __launch_bounds__(256) void dmmv_seg_kernel(DmmvSegParams sp) {
         dmmv_tile<LH_Q4_0, NT, false>(p, bx, blockIdx.y, lds, vec);
         break;
     }
+}
+
+// ---- the attention rmsnorm fused into q, k and v (PARITY, one vector) -----------
+// Every work group normalises x itself (the reference's sequential sum of the
+// squares, 4 waves) and quantizes the row for the segments' activation block
+// into LDS, then runs dmmv_seg_kernel's tile against that LDS copy: the norm
+// launch, its HBM round trip of the int8 row and one launch gap leave the
+// layer.  Same values as norm_quant_kernel<QB, true> followed by
+// dmmv_seg_kernel<1>.
+constexpr int NSEG_MAX_DIM = 4096;
+constexpr int NSEG_XV = norm_xv(NSEG_MAX_DIM, 4);
+
+__global__ __launch_bounds__(256) void norm_seg_kernel(DmmvSegParams sp, const float *__restrict__ x,
+                                                       const float *__restrict__ nw, float eps) {
+    extern __shared__ float lds[];
+    __shared__ int vec[1];
+    __shared__ __align__(16) float xn[NSEG_MAX_DIM];
+    __shared__ SeqSumLds seq;
+    __shared__ __align__(16) int8_t aq[NSEG_MAX_DIM];
+    __shared__ float ad[NSEG_MAX_DIM / 32];
+    __shared__ int32_t as[NSEG_MAX_DIM / 16];
+    const int dim = sp.base.cols;
+    float4 xv[NSEG_XV], wv[NSEG_XV];
+    norm_exact_load<4, NSEG_XV>(x, nw, dim, xv, wv);
+    norm_exact_block<4, NSEG_XV>(xv, wv, dim, eps, xn, seq);
+    // the row for the segments' weight type (they share its activation block)
+    const int qt = sp.seg[0].t;
+    const int items = quant_items(qt, dim);
+    for (int it = (int)threadIdx.x >> 6; it < items; it += 4)
+        quant_item_wave(qt, xn, dim, 0, it, QAct{aq, ad, as});
+    lds_barrier();
+    int s = 0, bx = blockIdx.x;
+    while (s + 1 < sp.n_seg && bx >= sp.seg[s].tiles) {
+        bx -= sp.seg[s].tiles;
+        s++;
+    }
+    DmmvParams p = sp.base;
+    p.w = sp.seg[s].w;
+    p.rows = sp.seg[s].rows;
+    p.rpw = sp.seg[s].rpw;
+    p.out = sp.seg[s].out;
+    p.out_stride = sp.seg[s].rows;
+    p.xq = aq;
+    p.xd = ad;
+    p.xs = as;
+    switch (sp.seg[s].t) {
+    case LH_Q4_K:
+        dmmv_tile<LH_Q4_K, 1, false>(p, bx, 0, lds, vec);
+        break;
+    case LH_Q6_K:
+        dmmv_tile<LH_Q6_K, 1, false>(p, bx, 0, lds, vec);
+        break;
+    case LH_Q8_0:
+        dmmv_tile<LH_Q8_0, 1, false>(p, bx, 0, lds, vec);
+        break;
+    default:
+        dmmv_tile<LH_Q4_0, 1, false>(p, bx, 0, lds, vec);
+        break;
+    }
+}
+
+// One vector (sp.base: n_groups 1, identity pairs): false = not served (the
+// caller normalises and runs launch_dmmv_seg instead).
+bool launch_norm_seg(DmmvSegParams sp, const float *x, const float *norm_w, float eps, hipStream_t st) {
+    const int dim = sp.base.cols;
+    if (dim > NSEG_MAX_DIM || dim % 256 || sp.base.n_groups != 1 || sp.n_seg < 1)
+        return false;
+    size_t lds = 0;
+    int tiles = 0;
+    for (int i = 0; i < sp.n_seg; i++) {
+        DmmvSeg &g = sp.seg[i];
+        if (act_block(g.t) != act_block(sp.seg[0].t))
+            return false;
+        g.rpw = dmmv_pick_rpw(g.t, dim, g.rows, 1, 1, false);
+        g.tiles = (g.rows + WAVES * g.rpw - 1) / (WAVES * g.rpw);
+        tiles += g.tiles;
+        const size_t l = dmmv_lds_bytes(g.t, dim, 1, false, g.rpw);
+        lds = l > lds ? l : lds;
+    }
+    if (lds > 64 * 1024)
+        return false;
+    hipLaunchKernelGGL(norm_seg_kernel, dim3(tiles), dim3(256), lds, st, sp, x, norm_w, eps);
+    note_launch();
+    return true;
 }
 
 bool launch_dmmv_seg(int nt, DmmvSegParams sp, hipStream_t st) {

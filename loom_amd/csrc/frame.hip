@@ -1037,8 +1037,12 @@ static bool frame_matvec(int t, const void *wt, int rows, int cols, const FrameW
     return ok;
 }
 
-// q, k and v of one layer against the normalised input, one launch.
-static bool frame_qkv(const loomhip_layer &l, const FrameDims &D, const FrameWs &w, size_t n, hipStream_t st) {
+// q, k and v of one layer against the normalised input, one launch.  With
+// fused: one lane in PARITY, the launch normalises x itself (the exact sum)
+// and true means both steps ran; false with *fused cleared: not served, the
+// caller normalises and calls again without.
+static bool frame_qkv(const loomhip_layer &l, const FrameDims &D, const FrameWs &w, size_t n, hipStream_t st,
+                      bool *fused = nullptr) {
     DmmvSegParams sp{};
     DmmvParams &p = sp.base;
     p.cols = D.dim;
@@ -1053,6 +1057,15 @@ static bool frame_qkv(const loomhip_layer &l, const FrameDims &D, const FrameWs 
     sp.seg[1] = DmmvSeg{(const uint8_t *)l.wk, l.wk_t, D.kvd, w.k, 0, 0};
     sp.seg[2] = DmmvSeg{(const uint8_t *)l.wv, l.wv_t, D.kvd, w.v, 0, 0};
     sp.n_seg = 3;
+    if (fused) { // one lane only, before any other path
+        *fused = false;
+        if (n != 1)
+            return false;
+        const int ph = prof_begin(LOOMHIP_KT_QKV, st);
+        *fused = launch_norm_seg(sp, w.x, l.attn_norm, D.eps, st);
+        prof_end(ph, st);
+        return *fused;
+    }
     // from MMQ_MIN_TOK lanes: the matrix cores, the three matrices in one
     // launch, lanes in groups of 16
     if (use_mmq(l.wq_t, D.dim, (int)n, 32, false) && use_mmq(l.wk_t, D.dim, (int)n, 32, false) &&
@@ -1216,10 +1229,14 @@ int frame_layer(const FrameCall &c, const loomhip_layer &l, size_t li, uint32_t 
     const bool parity = c.parity;
     hipStream_t st = c.st;
     // attention block (llama.zig:1127-1201)
-    // layer 0 normalises the embedding row: exact sum in either mode
-    launch_norm(act_block(l.wq_t), w.x, D.dim, l.attn_norm, D.eps, w.qa_dim, nullptr, n, st, parity || li == 0);
-    if (!frame_qkv(l, D, w, n, st))
-        return fail(LOOMHIP_ERR_ARG, "token_frame: q/k/v matvec declined");
+    // layer 0 normalises the embedding row: exact sum in either mode; one
+    // lane in PARITY: the q/k/v launch normalises its input itself
+    bool fused = false;
+    if (!(parity && frame_qkv(l, D, w, n, st, &fused))) {
+        launch_norm(act_block(l.wq_t), w.x, D.dim, l.attn_norm, D.eps, w.qa_dim, nullptr, n, st, parity || li == 0);
+        if (!frame_qkv(l, D, w, n, st))
+            return fail(LOOMHIP_ERR_ARG, "token_frame: q/k/v matvec declined");
+    }
     // few lanes: norm/rope/append inside the attention launch; more lanes:
     // once per head in their own launch (the attention is then
     // throughput-bound and the fused prologue would repeat per chunk)

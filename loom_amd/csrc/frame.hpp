@@ -324,6 +324,63 @@ __device__ __forceinline__ void softmax_exps(const float (&sv)[NV], float m, int
     }
 }
 
+// ---- rmsnorm with the reference's sum, computed by a whole work group ----------
+// (tensor.zig:9-15) for a kernel that normalises its own input: x and the
+// norm weights in registers -- float4 k of thread tid holds values
+// 4 tid + 256 NW k, XV of them cover the largest dim served -- then the
+// squares in order, zero-padded to whole 64s, summed sequentially
+// (seq_sum_nonneg), then xn = (x * scale) * w in LDS.
+__host__ __device__ constexpr int norm_xv(int max_dim, int nw) { return (max_dim + 256 * nw - 1) / (256 * nw); }
+
+template <int NW, int XV>
+__device__ __forceinline__ void norm_exact_load(const float *__restrict__ x, const float *__restrict__ w, int dim,
+                                                float4 (&xv)[XV], float4 (&wv)[XV]) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < XV; k++) {
+        const int i = 4 * tid + 4 * 64 * NW * k;
+        xv[k] = wv[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < dim) { // dim is a multiple of 32
+            xv[k] = *(const float4 *)(x + i);
+            wv[k] = *(const float4 *)(w + i);
+        }
+    }
+}
+
+template <int NW, int XV>
+__device__ __forceinline__ void norm_exact_block(const float4 (&xv)[XV], const float4 (&wv)[XV], int dim,
+                                                 float eps, float *xn, SeqSumLds &seq) {
+    const int tid = threadIdx.x, n64 = (dim + 63) & ~63;
+#pragma unroll
+    for (int k = 0; k < XV; k++) {
+        const int i = 4 * tid + 4 * 64 * NW * k;
+        if (i < n64) {
+            float4 q;
+            q.x = xv[k].x * xv[k].x;
+            q.y = xv[k].y * xv[k].y;
+            q.z = xv[k].z * xv[k].z;
+            q.w = xv[k].w * xv[k].w;
+            *(float4 *)(xn + i) = q;
+        }
+    }
+    lds_barrier();
+    const float total = seq_sum_nonneg<NW>(xn, dim, seq); // ends with a barrier: xn is free again
+    const float scale = 1.0f / sqrtf(total / (float)dim + eps);
+#pragma unroll
+    for (int k = 0; k < XV; k++) {
+        const int i = 4 * tid + 4 * 64 * NW * k;
+        if (i < dim) {
+            float4 o;
+            o.x = (xv[k].x * scale) * wv[k].x;
+            o.y = (xv[k].y * scale) * wv[k].y;
+            o.z = (xv[k].z * scale) * wv[k].z;
+            o.w = (xv[k].w * scale) * wv[k].w;
+            *(float4 *)(xn + i) = o;
+        }
+    }
+    lds_barrier();
+}
+
 // ---- the reference-order attention (attn_exact.hip), PARITY numerics --------
 // Scores, softmax and P.V of llama.zig:1162-1192 in the reference's own
 // evaluation order over any context: one launch of scores per 64 positions,

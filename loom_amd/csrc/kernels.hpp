@@ -62,6 +62,9 @@ struct DmmvSegParams {
     int n_seg;
 };
 bool launch_dmmv_seg(int nt, DmmvSegParams sp, hipStream_t st);
+// The same for one vector with the PARITY rmsnorm of x (norm weights norm_w)
+// computed by the launch itself; false = not served.
+bool launch_norm_seg(DmmvSegParams sp, const float *x, const float *norm_w, float eps, hipStream_t st);
 
 void note_launch();
 // Event timing around tagged launches (LOOMHIP_KT_*); -1 when disabled.

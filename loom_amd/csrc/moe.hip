@@ -548,60 +548,7 @@ __global__ __launch_bounds__(64) void router_small_kernel(GateParams p) {
 constexpr int RX_WAVES = 8;
 constexpr int RX_MAX_DIM = 7936; // the squares, then the normed row, in LDS
 
-// x and the norm weights in registers: float4 k of thread tid holds values
-// 4 tid + 4 NT k (RX_XV of them cover RX_MAX_DIM)
-constexpr int RX_XV = (RX_MAX_DIM + 4 * 64 * RX_WAVES - 1) / (4 * 64 * RX_WAVES);
-
-template <int NW>
-__device__ __forceinline__ void norm_exact_load(const float *__restrict__ x, const float *__restrict__ w, int dim,
-                                                float4 (&xv)[RX_XV], float4 (&wv)[RX_XV]) {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int k = 0; k < RX_XV; k++) {
-        const int i = 4 * tid + 4 * 64 * NW * k;
-        xv[k] = wv[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (i < dim) { // dim is a multiple of 32
-            xv[k] = *(const float4 *)(x + i);
-            wv[k] = *(const float4 *)(w + i);
-        }
-    }
-}
-
-// xn = rmsnorm(x) (tensor.zig:9-15): the squares in order, zero-padded to
-// whole 64s, summed sequentially, then (x * scale) * w.
-template <int NW>
-__device__ __forceinline__ void norm_exact_block(const float4 (&xv)[RX_XV], const float4 (&wv)[RX_XV], int dim,
-                                                 float eps, float *xn, SeqSumLds &seq) {
-    const int tid = threadIdx.x, n64 = (dim + 63) & ~63;
-#pragma unroll
-    for (int k = 0; k < RX_XV; k++) {
-        const int i = 4 * tid + 4 * 64 * NW * k;
-        if (i < n64) {
-            float4 q;
-            q.x = xv[k].x * xv[k].x;
-            q.y = xv[k].y * xv[k].y;
-            q.z = xv[k].z * xv[k].z;
-            q.w = xv[k].w * xv[k].w;
-            *(float4 *)(xn + i) = q;
-        }
-    }
-    __syncthreads();
-    const float total = seq_sum_nonneg<NW>(xn, dim, seq); // ends with a barrier: xn is free again
-    const float scale = 1.0f / sqrtf(total / (float)dim + eps);
-#pragma unroll
-    for (int k = 0; k < RX_XV; k++) {
-        const int i = 4 * tid + 4 * 64 * NW * k;
-        if (i < dim) {
-            float4 o;
-            o.x = (xv[k].x * scale) * wv[k].x;
-            o.y = (xv[k].y * scale) * wv[k].y;
-            o.z = (xv[k].z * scale) * wv[k].z;
-            o.w = (xv[k].w * scale) * wv[k].w;
-            *(float4 *)(xn + i) = o;
-        }
-    }
-    __syncthreads();
-}
+constexpr int RX_XV = norm_xv(RX_MAX_DIM, RX_WAVES);
 
 __global__ __launch_bounds__(64 * RX_WAVES) void router_exact_kernel(GateParams p) {
     __shared__ __align__(16) float xn[RX_MAX_DIM];
@@ -615,14 +562,14 @@ __global__ __launch_bounds__(64 * RX_WAVES) void router_exact_kernel(GateParams 
     const bool one_pass = n32 <= RS_STEPS;
     // x and the norm weights first: the router rows' loads queue behind them
     float4 xv[RX_XV], wv[RX_XV];
-    norm_exact_load<RX_WAVES>(p.x, p.norm_w, dim, xv, wv);
+    norm_exact_load<RX_WAVES, RX_XV>(p.x, p.norm_w, dim, xv, wv);
     float wpre[RS_STEPS];
     if (gemv && one_pass) {
 #pragma unroll
         for (int u = 0; u < RS_STEPS; u++)
             wpre[u] = row[32 * min(u, n32 - 1) + P];
     }
-    norm_exact_block<RX_WAVES>(xv, wv, dim, p.norm_eps, xn, seq);
+    norm_exact_block<RX_WAVES, RX_XV>(xv, wv, dim, p.norm_eps, xn, seq);
     if (gemv) {
         if (dim == 32 * RS_STEPS)
             router_row_dot<true>(p, e, valid, row, xn, 0, one_pass, wpre);
