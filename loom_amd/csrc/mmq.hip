@@ -1,7 +1,8 @@
-// mmq.hip -- grouped int8 matrix-core matmul for Q4_K / Q6_K weights against
-// int8 activations, bit-identical to the reference CPU kernels
-// (src/gguf/ggml.zig:1002-1059 kBlockDot / matvecK256 / matmulK256) and so
-// to dmmv.hip.
+// mmq.hip -- grouped int8 matrix-core matmul for Q4_K / Q6_K (and, from the
+// 32-value-block section below, Q8_0 / Q4_0) weights against int8
+// activations, bit-identical to the reference CPU kernels
+// (src/gguf/ggml.zig:1002-1059 kBlockDot / matvecK256 / matmulK256,
+// 1196-1222 matvecQ40Int, 1277-1294 matvecQ80Int) and so to dmmv.hip.
 //
 // The integer part of every block dot runs on the int8 MFMAs: the activations
 // of 16 tokens are the A rows, 16 weight rows the B columns (Q4_K:
@@ -882,7 +883,193 @@ static bool mmq_shape(int rows, int cols, int mt, bool fused, int &rg, int &ks, 
     return mmq_lds_bytes(cols, mt, rg, fused) <= 64 * 1024;
 }
 
+// ---- Q8_0 / Q4_0 (32-value blocks) on the int8 matrix cores ----------------------
+// A work group of MQ32_W waves per (16-row tile, 16 tokens of a group: a group
+// of up to 32 takes two, along z); wave w takes the w-th share of the rows'
+// 64-value spans.  Per span
+// (blocks 2s and 2s + 1) lane quarter q4 holds 16 values of block 2s + q4/2
+// -- A: token r16's activations, B: row r16's quants (Q4_0 as nibble - 8) --
+// and two MFMAs over the span, each with the other block's quarters of the
+// weights zeroed, give each block's integer dot for the 16 tokens: Q8_0
+// sum w*x; Q4_0 sum (q - 8)*x, which is the reference's sum q*x - 8*sum x as
+// one exact integer.  Each block's f32 tail (d * xd) * f32(isum)
+// (ggml.zig:1212-1218, 1289-1290) goes to LDS; then every output sums its
+// blocks in block order from +0 -- the reference's acc += r -- one thread
+// per output.  A wave's loads run MQ32_AHEAD spans ahead; the tokens' block
+// scales are staged in LDS once.
+constexpr int MQ32_AHEAD = 4;
+constexpr int MQ32_W = 8;         // waves per work group (span shares)
+constexpr int MQ32_MAXS = 8;      // spans per wave: cols <= 4096
+constexpr int MQ32_PART = 32768;  // LDS floats of block values: nb * 256
+
+template <int T>
+__global__ __launch_bounds__(64 * MQ32_W) void mmq32_kernel(DmmvParams p) {
+    constexpr int MT = 1;
+    static_assert(T == LH_Q8_0 || T == LH_Q4_0, "32-value blocks");
+    constexpr int QB = T == LH_Q8_0 ? 32 : 16; // quant bytes per block
+    constexpr int NO = 256 * MT;               // outputs per work group: (token, row)
+    constexpr int MAXNB = 64 * MQ32_W * MQ32_MAXS / 32;
+    __shared__ __align__(16) float part[MQ32_PART];      // [block][token * 16 + row]
+    __shared__ __align__(16) float xds[16 * MT][MAXNB];  // the tokens' block scales
+    const int ln = threadIdx.x & 63, r16 = ln & 15, q4 = ln >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const bool ident = p.ident_n > 0;
+    DmmvGroup grp;
+    if (ident) {
+        grp.plane = 0;
+        grp.first = (int)blockIdx.y * 16;
+        grp.n = min(16, p.ident_n - grp.first);
+    } else {
+        const int ng = p.n_groups_dev ? *p.n_groups_dev : p.n_groups;
+        if ((int)blockIdx.y >= ng)
+            return;
+        grp = p.groups[blockIdx.y];
+        // tokens 16 z .. of the group (pairs first + 16 z ..)
+        grp.first += 16 * (int)blockIdx.z;
+        grp.n = min(16, grp.n - 16 * (int)blockIdx.z);
+        if (grp.n <= 0)
+            return;
+    }
+    const int n = grp.n, cols = p.cols, nb = cols / 32, ns = cols / 64;
+    const int s_lo = wave * ns / MQ32_W, cnt = (wave + 1) * ns / MQ32_W - s_lo; // this wave's spans
+    const int row0 = (int)blockIdx.x * 16;
+    const int row = min(row0 + r16, p.rows - 1);
+    const size_t U = (size_t)p.rows * nb;
+    const uint8_t *wb = p.w + (size_t)grp.plane * p.plane_bytes;
+    // A row r16 of token tile mt carries a vector (tokens past n repeat the
+    // last; their outputs are never stored); this lane's outputs are tokens
+    // 16 mt + 4 q4 + i of row r16
+    const int8_t *xr[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const int tk = min(16 * mt + r16, n - 1);
+        const int vrow = ident ? grp.first + tk : p.pair_src[grp.first + tk];
+        xr[mt] = p.xq + (size_t)vrow * cols + 16 * q4;
+    }
+    // the group's block scales, bound for LDS (row tk of xds: token tk's nb
+    // scales; tokens past n repeat the last): thread (tk, part) loads blocks
+    // xpart + TPT u of token tk, unconditionally from clamped indices, first;
+    // they are stored after the first spans' loads are out, so that store
+    // waits for these loads alone
+    constexpr int TPT = 64 * MQ32_W / (16 * MT); // threads per token
+    constexpr int XU = (MAXNB + TPT - 1) / TPT;  // scales per thread (at most)
+    const int xtk = (int)threadIdx.x / TPT, xpart = (int)threadIdx.x % TPT;
+    const float *xdr;
+    {
+        const int tc = min(xtk, n - 1);
+        xdr = p.xd + (size_t)(ident ? grp.first + tc : p.pair_src[grp.first + tc]) * nb;
+    }
+    float xe[XU];
+#pragma unroll
+    for (int u = 0; u < XU; u++)
+        xe[u] = xdr[min(xpart + TPT * u, nb - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    // block 2s + q4/2 of the lane's row: its 16 quant bytes (Q8_0: half q4 & 1;
+    // Q4_0: all 16, the nibble half picked below) and the (d, d) pair of blocks 2s, 2s + 1
+    const uint8_t *wq = wb + ((size_t)row * nb + (q4 >> 1)) * QB + (T == LH_Q8_0 ? 16 * (q4 & 1) : 0);
+    const uint32_t *wd = (const uint32_t *)(wb + U * QB + (size_t)row * nb * 2);
+    struct Span {
+        mmq_i4 a[MT], w;
+        uint32_t d;
+    };
+    // span j of this wave (past its last: the last, loaded and not used)
+    auto load = [&](int j, Span &o) {
+        const int sc = s_lo + min(j, cnt - 1);
+        o.w = *(const mmq_i4 *)(wq + (size_t)2 * sc * QB);
+        o.d = wd[sc];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+            o.a[mt] = *(const mmq_i4 *)(xr[mt] + 64 * sc);
+    };
+    const mmq_i4 z = {0, 0, 0, 0};
+    const bool lo = q4 < 2;
+    auto span = [&](const Span &o, int sc) {
+        mmq_i4 wv = o.w;
+        if constexpr (T == LH_Q4_0) {
+            // the lane's nibble half, then q - 8 per byte: (q + 0x78) ^ 0x80
+            const uint32_t sh = 4 * (q4 & 1);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                wv[e] = (int)((((uint32_t)wv[e] >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ (int)0x80808080u;
+        }
+        const mmq_i4 wa = lo ? wv : z, wbk = lo ? z : wv;
+        const float dwa = half_bits_to_float(o.d & 0xffffu), dwb = half_bits_to_float(o.d >> 16);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const mmq_i4 da = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a[mt], wa, z, 0, 0, 0);
+            const mmq_i4 db = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a[mt], wbk, z, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tk = 16 * mt + 4 * q4 + i;
+                const float2 xd = *(const float2 *)&xds[tk][2 * sc];
+                const float sa = dwa * xd.x;
+                part[(size_t)(2 * sc) * NO + tk * 16 + r16] = sa * (float)da[i];
+                const float sb = dwb * xd.y;
+                part[(size_t)(2 * sc + 1) * NO + tk * 16 + r16] = sb * (float)db[i];
+            }
+        }
+    };
+    // each span's loads are issued as a unit, in span order (the fences keep
+    // them there), so a span's wait leaves the later spans' loads in flight
+    Span ring[MQ32_AHEAD];
+#pragma unroll
+    for (int j = 0; j < MQ32_AHEAD; j++) {
+        load(j, ring[j]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int u = 0; u < XU; u++)
+        if (xpart + TPT * u < nb)
+            xds[xtk][xpart + TPT * u] = xe[u];
+    lds_barrier(); // the scales
+#pragma unroll
+    for (int j = 0; j < MQ32_MAXS; j++) {
+        if (j < cnt)
+            span(ring[j % MQ32_AHEAD], s_lo + j);
+        __builtin_amdgcn_sched_barrier(0);
+        if (j + MQ32_AHEAD < MQ32_MAXS)
+            load(j + MQ32_AHEAD, ring[j % MQ32_AHEAD]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_barrier(); // every block's values
+    // output o = (token o / 16, row o % 16): its blocks in order from +0
+    for (int o = (int)threadIdx.x; o < NO; o += 64 * MQ32_W) {
+        const int tk = o >> 4, rr = o & 15;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int bl = 0; bl < nb; bl++)
+            acc = acc + part[(size_t)bl * NO + o];
+        if (tk < n && row0 + rr < p.rows) {
+            const int dst = ident ? grp.first + tk : p.pair_dst[grp.first + tk];
+            float *out = p.out + (size_t)dst * p.out_stride + row0 + rr;
+            *out = p.accumulate ? *out + acc : acc;
+        }
+    }
+}
+
+static bool mmq32_supported(int t, int cols, int max_tok, bool fused) {
+    // the block values of a work group fill (cols / 32) * 256 floats of LDS
+    return (t == LH_Q8_0 || t == LH_Q4_0) && !fused && cols % 64 == 0 && cols >= 64 * MQ32_W &&
+           cols <= 64 * MQ32_W * MQ32_MAXS && max_tok >= 1 && max_tok <= 32 &&
+           (size_t)(cols / 32) * 256 <= (size_t)MQ32_PART;
+}
+
+// Identity pairs go in groups of 16 tokens; a caller's groups of up to 32
+// take two work groups each (z).
+static bool launch_mmq32(int t, int max_tok, const DmmvParams &p, hipStream_t st) {
+    const bool ident = p.ident_n > 0;
+    const int groups = ident ? (p.ident_n + 15) / 16 : p.n_groups;
+    const dim3 grid((p.rows + 15) / 16, groups, ident || max_tok <= 16 ? 1 : 2), block(64 * MQ32_W);
+    if (t == LH_Q8_0)
+        hipLaunchKernelGGL(mmq32_kernel<LH_Q8_0>, grid, block, 0, st, p);
+    else
+        hipLaunchKernelGGL(mmq32_kernel<LH_Q4_0>, grid, block, 0, st, p);
+    return true;
+}
+
 bool mmq_supported(int t, int cols, int max_tok, bool fused) {
+    if (t == LH_Q8_0 || t == LH_Q4_0)
+        return mmq32_supported(t, cols, max_tok, fused);
     if ((t != LH_Q4_K && t != LH_Q6_K) || cols % 256 || cols < 256 || max_tok < 1 || max_tok > 32)
         return false;
     if (fused && t != LH_Q4_K) // a fused pair is gate/up: Q4_K only here
@@ -965,6 +1152,11 @@ bool launch_mmq_seg(DmmvSegParams sp, hipStream_t st) {
 bool launch_mmq(int t, int max_tok, bool fused, const DmmvParams &p, hipStream_t st) {
     if (!mmq_supported(t, p.cols, max_tok, fused) || p.rows < 1)
         return false;
+    if (t == LH_Q8_0 || t == LH_Q4_0) {
+        launch_mmq32(t, max_tok, p, st);
+        note_launch();
+        return true;
+    }
     const int mt = max_tok > 16 ? 2 : 1;
     int rg, ks, sbw;
     if (!mmq_shape(p.rows, p.cols, mt, fused, rg, ks, sbw))

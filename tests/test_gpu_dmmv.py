@@ -129,12 +129,14 @@ def test_matmul_bit_exact_to_per_vector_oracle(be, oracle, t):
         assert np.array_equal(_bits(got), _bits(want)), n
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("t", [Q4_K, Q6_K, Q8_0, Q4_0])
 @pytest.mark.parametrize("rows,cols", [(37, 768), (300, 4096), (64, 256), (130, 2048)])
 def test_matmul_matrix_cores_bit_exact(be, oracle, t, rows, cols):
     """From 16 vectors on, Q4_K / Q6_K matmuls run on the int8 matrix cores
-    (mmq.hip, groups of 32): bit-identical to per-vector oracle matvecs,
-    including ragged row tiles and groups."""
+    (mmq.hip, groups of 32), and so do Q8_0 / Q4_0 over whole 64-value spans
+    (mmq32_kernel: a wave per 16-row tile walks the blocks in order, 16 vectors
+    a group): bit-identical to per-vector oracle matvecs, including ragged row
+    tiles and groups."""
     rng = np.random.default_rng(77 + t + rows)
     raw = npref.pinned_scale_blocks(t, rows, cols, rng)
     for n in (16, 17, 32, 45):
