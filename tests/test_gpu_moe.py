@@ -258,6 +258,37 @@ def test_moe_layer_dev_gatings_and_down_types(be, oracle, down_t, ffn, gi, n):
     _same_bits(out.cpu().numpy(), want, f"gating {gating} down {down_t} n={n}")
 
 
+@pytest.mark.parametrize("down_t,ffn", [(Q8_0, 512), (Q4_0, 768), (Q8_0, 4096)])
+@pytest.mark.parametrize("n", [16, 32])
+def test_moe_layer_dev_matrix_core_32_block_downs(be, oracle, down_t, ffn, n):
+    """From 16 tokens the batched path runs the expert matmuls on the int8
+    matrix cores: the fused Q4_K gate/up on mmq.hip's K-quant kernels and a
+    Q8_0 / Q4_0 down on mmq32_kernel in its grouped form (expert planes, the
+    groups' pair sources and destinations; ffn 4096 is its widest span
+    count).  8 experts top-4, so at 32 tokens the busiest experts take more
+    than one group of 16.  Ids, gates and the layer's output bits against
+    lo_moe_batch_union."""
+    import torch
+
+    dim, E, k = 512, 8, 4
+    w = make_layer(oracle, dim, ffn, E, k, seed=90 + ffn + n, gate_t=Q4_K, down_t=down_t)
+    layer = _dev_layer(be, w)
+    xs = np.stack([oracle.normal(dim, 700 + i, 0.0, 1.0) for i in range(n)])
+    normed = torch.from_numpy(xs).cuda()
+    ids = torch.empty((n, k), dtype=torch.int32, device="cuda")
+    gates = torch.empty((n, k), dtype=torch.float32, device="cuda")
+    resid = np.stack([oracle.normal(dim, 900 + i, 0.0, 1.0) for i in range(n)])
+    out = torch.from_numpy(resid.copy()).cuda()
+    layer(normed, out, combine=be.COMBINE_EXPERT_ASC, ids=ids, gates=gates)
+    want, wid, wg = oracle.moe_batch_union(w, xs, resid)
+    torch.cuda.synchronize()
+    got_ids = ids.cpu().numpy().astype(np.uint32)
+    assert np.array_equal(got_ids, wid)
+    assert np.bincount(got_ids.ravel(), minlength=E).max() > 16 or n < 32  # some expert spans two groups
+    assert np.all(np.abs(gates.cpu().numpy() - wg) <= 1e-5)
+    _same_bits(out.cpu().numpy(), want, f"down {down_t} ffn {ffn} n={n}")
+
+
 # ---- config 5's block: the shared expert, and moeFfnBlock -------------------------
 
 
