@@ -242,6 +242,26 @@ def test_llama_frame_batch_head_layouts(lh, oracle, heads):
     assert same
 
 
+@pytest.mark.parametrize("wt", [2, 8])  # Q4_0, Q8_0
+@pytest.mark.parametrize("n", [16, 32])
+def test_llama_frame_batch_32_block_matrix_cores(lh, oracle, wt, n):
+    """A llama-architecture model 512 wide in Q4_0 or Q8_0 throughout (q, k,
+    v, wo, the FFN and the head): from 16 lanes every one of its matmuls runs
+    on mmq32_kernel (whole 64-value spans, 512 to 4096 columns) through the
+    frame.  PARITY per-lane logits against lo_decode_batch over 3 steps on
+    identical state, identical greedy tokens."""
+    import dataclasses
+
+    spec = dataclasses.replace(lh.stories15m(ctx_len=160), dim=512, n_layers=2, vocab=2048, n_heads=8,
+                               n_kv_heads=4, head_dim=64, rope_dim=64, ffn=1024, embed_t=wt, output_t=wt,
+                               wq_t=wt, wk_t=wt, wv_t=wt, wo_t=wt, ffn_gate_t=wt, ffn_down_t=wt)
+    dm = lh.DeviceModel.synth(spec, seed=31 + wt, keep_ggml=True)
+    om = OracleModel(oracle, dm)
+    rels, same = _batch_steps(lh, om, dm, n, 3, 140, seed=wt + n)
+    _check(rels, "parity")
+    assert same
+
+
 @pytest.mark.parametrize("numerics", ["parity", "fast"])
 @pytest.mark.parametrize("n", [1, 32])
 def test_qwen3moe_frame_4096_context(lh, oracle, n, numerics):
