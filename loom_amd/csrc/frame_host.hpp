@@ -49,8 +49,12 @@ int frame_setup(const loomhip_model *m, size_t n, size_t ffn_max, float scale, i
 // One layer (llama.zig:1127-1224): attention with the K/V append at pos,
 // x += wo . attn, then the FFN and its residual add, on c.w.x.  ids (device,
 // [n][n_used]) receives a MoE layer's routed ids, or is NULL.
-int frame_layer(const FrameCall &c, const loomhip_layer &l, size_t li, uint32_t *ids);
+// next (optional): the rmsnorm the residual row meets after this layer; on
+// the batched MoE path the combine forms it and sets *next_done.
+// prenormed: the previous layer's combine formed this layer's attention norm.
+int frame_layer(const FrameCall &c, const loomhip_layer &l, size_t li, uint32_t *ids, const NextNorm *next = nullptr,
+                bool *next_done = nullptr, bool prenormed = false);
 // The output norm and head (llama.zig:1225-1227) into logits [n][vocab].
-int frame_head(const FrameCall &c, const loomhip_model *m, float *logits);
+int frame_head(const FrameCall &c, const loomhip_model *m, float *logits, bool prenormed = false);
 
 } // namespace lh

@@ -174,6 +174,21 @@ bool launch_moe_decode(int gate_t, int down_t, const DecodeParams &p, int n, hip
                        int prof_gu, int prof_dn);
 void launch_combine(const float *y, const float *gates, const uint32_t *ids, const int *pair_of,
                     int n, int k, int dim, int mode, float *out, hipStream_t st);
+// The rmsnorm the next consumer of the residual row applies (the next
+// layer's attention, or the output head): weights, eps, the activation
+// block of the weight it feeds (32 or 256), the int8 target, exact sum.
+struct NextNorm {
+    const float *w;
+    float eps;
+    int qb;
+    QAct qa;
+    bool exact;
+};
+// The batched combine (ascending expert, mode 1) with the next rmsnorm in the
+// same launch; false: not served (a tree-summed norm, dim), the caller
+// launches them apart.
+bool launch_combine_norm(const float *y, const float *gates, const uint32_t *ids, const int *pair_of, int n,
+                         int k, int dim, float *out, const NextNorm &nx, hipStream_t st);
 
 // Sync-buffer size (ints): the gate kernel's completion counters.
 constexpr int SYNC_INTS = 1024;

@@ -51,6 +51,8 @@ struct MoeRun {
     float norm_eps = 0.0f;
     bool norm_exact = false;       // ... with the squares summed in the reference's order (one token)
     DenseFfn sh{}; // the shared expert (sh.gate null: none)
+    const NextNorm *next = nullptr; // batched path: the next rmsnorm in the combine's launch
+    bool *next_done = nullptr;      // ... set when it ran there
 };
 
 static size_t qbytes(size_t nvec, size_t cols) {
@@ -372,6 +374,12 @@ static int moe_run(const MoeRun &m, const float *normed, const float *logits_in,
     if (!launched)
         return fail(LOOMHIP_ERR_ARG, "moe: down partials exceed LDS");
 
+    if (m.next && combine == LOOMHIP_COMBINE_EXPERT_ASC && !m.sh.gate &&
+        launch_combine_norm(y, gates, ids, b.pair_of, (int)n, (int)m.k, (int)m.dim, out, *m.next, st)) {
+        if (m.next_done)
+            *m.next_done = true;
+        return LOOMHIP_OK;
+    }
     launch_combine(y, gates, ids, b.pair_of, (int)n, (int)m.k, (int)m.dim, combine, out, st);
     return m.sh.gate ? dense_ffn_add(m.sh, normed, n, m.dim, out, st, true) : LOOMHIP_OK;
 }
@@ -407,6 +415,17 @@ int moe_layer_fused_norm(const loomhip_moe_layer *L, const float *x, const float
     m.norm_eps = eps;
     m.norm_exact = exact;
     return moe_run(m, x, nullptr, n_tok, combine, out, ids_out, nullptr, st);
+}
+
+int moe_layer_next_norm(const loomhip_moe_layer *L, const float *normed, size_t n_tok, int combine, float *out,
+                        uint32_t *ids_out, const NextNorm *next, bool *next_done, hipStream_t st) {
+    MoeRun m{L->dim, L->ffn, L->n_expert, L->n_used, L->gating, L->weights_norm, L->weights_scale,
+             L->router, L->router_bias, L->sel_bias, L->gate_t, L->up_t, L->down_t, L->gate,
+             L->up, L->down};
+    m.sh = shexp_of(L);
+    m.next = next;
+    m.next_done = next_done;
+    return moe_run(m, normed, nullptr, n_tok, combine, out, ids_out, nullptr, st);
 }
 
 bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok, bool exact) {

@@ -75,6 +75,10 @@ int moe_noalloc_setup(int device);
 int moe_layer_fused_norm(const loomhip_moe_layer *L, const float *x, const float *norm_w, float eps, size_t n_tok,
                          int combine, float *out, uint32_t *ids_out, bool exact, hipStream_t st);
 bool moe_decode_fusable(const loomhip_moe_layer *L, size_t n_tok, bool exact);
+// loomhip_moe_layer_dev with, on the batched path, the next rmsnorm of the
+// residual row (next) formed in the combine's launch; *next_done says it ran.
+int moe_layer_next_norm(const loomhip_moe_layer *L, const float *normed, size_t n_tok, int combine, float *out,
+                        uint32_t *ids_out, const NextNorm *next, bool *next_done, hipStream_t st);
 // What the MoE layer would decline at n tokens, checked before any launch.
 int moe_frame_check(const loomhip_moe_layer *L, size_t n);
 // The same checks for a caller that forms acc = routed + shared itself
