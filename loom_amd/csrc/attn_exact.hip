@@ -269,7 +269,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void at
 // with the VALU close behind (v_fma_mix issues at about half the rate of an
 // f32 multiply); p by v_readlane, p broadcast by the matrix cores
 // (v_mfma_f32_32x32x1f32 against 1.0), two heads per lane, and the values as
-// f32 with v_mul all measured slower.
+// f32 with v_mul all measured slower, as did f32 values with p read once per
+// 32 positions and turned into scalar operands by 32 v_readlane issued ahead
+// of the group's products (76 us against 58: readlane + v_mul + add per
+// position costs more than v_fma_mix + add, whatever it saves the LDS).
 constexpr int PVM_TJ = 128;        // positions per tile
 constexpr int PVM_Q = PVM_TJ / 4;  // position quads per tile
 constexpr int PVM_RS = 2 * 64 + 4; // dwords per quad row (64 columns x 2, padded)
