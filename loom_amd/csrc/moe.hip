@@ -22,6 +22,7 @@ constexpr int GT_ROWS = GT_THREADS / 32; // router rows per workgroup (a half-wa
 constexpr int GT_TOK = 4;                // tokens per chunk = tokens per half-wave pass
 constexpr int GT_UNROLL = 64; // router elements in flight per lane (dim 2048: one chunk)
 constexpr int GT_COLS = 32 * GT_UNROLL; // columns per staged chunk
+static_assert(GT_TOK == 4, "a staged column's tokens are one float4");
 
 // Router GEMV for up to GT_TOK tokens in dotF32 order (src/gguf/ggml.zig:
 // 198-217): lane L of a half-wave accumulates row[32i + L] * x[32i + L] over
@@ -30,7 +31,8 @@ constexpr int GT_COLS = 32 * GT_UNROLL; // columns per staged chunk
 // one row (e < n_expert: valid); the whole work group calls this.  A chunk of
 // GT_COLS columns is processed at a time: the half-wave's row loads (64 per
 // lane) are issued together, and the tokens' matching x columns are staged
-// in LDS (xs, [GT_TOK][GT_COLS]) by the whole work group.
+// in LDS by the whole work group as [GT_COLS][GT_TOK] (a column's four
+// token values in one 16-byte read).
 __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int nt, int hw, int L,
                             float (*part)[GT_TOK][32], float *xs) {
     const int dim = p.dim;
@@ -44,15 +46,17 @@ __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int 
         const int ccols = (main_end - c0) < GT_COLS ? (main_end - c0) : GT_COLS;
         const int cnt = ccols / 32;
         // the tokens' x columns are requested first, then the row, so one
-        // round trip covers both; the barriers below wait on LDS only
-        constexpr int XPT = GT_TOK * GT_COLS / 4 / GT_THREADS;
-        float4 xv[XPT];
+        // round trip covers both; the barriers below wait on LDS only.
+        // Thread item q: the column quad 4 (tid + q GT_THREADS) of every token.
+        constexpr int XPT = GT_COLS / 4 / GT_THREADS;
+        float4 xv[XPT][GT_TOK];
 #pragma unroll
         for (int q = 0; q < XPT; q++) {
-            const int idx = 4 * ((int)threadIdx.x + q * GT_THREADS);
-            const int k = idx / ccols, col = idx % ccols;
-            xv[q] = k < nt ? *(const float4 *)(p.x + (size_t)(t0 + k) * dim + c0 + col)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int col = 4 * ((int)threadIdx.x + q * GT_THREADS);
+#pragma unroll
+            for (int k = 0; k < GT_TOK; k++)
+                xv[q][k] = k < nt && col < ccols ? *(const float4 *)(p.x + (size_t)(t0 + k) * dim + c0 + col)
+                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
         }
         // unconditional loads (steps past cnt re-read the chunk's last step,
         // their products are never added), so they all go out together
@@ -64,13 +68,19 @@ __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int 
             lds_barrier(); // the previous chunk's readers are done with xs
 #pragma unroll
         for (int q = 0; q < XPT; q++) {
-            const int idx = 4 * ((int)threadIdx.x + q * GT_THREADS);
-            const int k = idx / ccols, col = idx % ccols;
-            if (k < nt)
-                *(float4 *)(xs + k * GT_COLS + col) = xv[q];
+            const int col = 4 * ((int)threadIdx.x + q * GT_THREADS);
+            if (col < ccols) {
+#pragma unroll
+                for (int k = 0; k < GT_TOK; k++) {
+                    xs[4 * (col + 0) + k] = xv[q][k].x;
+                    xs[4 * (col + 1) + k] = xv[q][k].y;
+                    xs[4 * (col + 2) + k] = xv[q][k].z;
+                    xs[4 * (col + 3) + k] = xv[q][k].w;
+                }
+            }
         }
         lds_barrier();
-        // tokens past nt compute on stale LDS and are not stored.  A full
+        // tokens past nt compute on zeros and are not stored.  A full
         // chunk has no per-step guard, so its LDS reads issue back to back
         // (a guard per step compiles to a branch around each read).
         if (cnt == GT_UNROLL) {
@@ -78,9 +88,11 @@ __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int 
             // column order
 #pragma unroll
             for (int u = 0; u < GT_UNROLL; u++) {
+                const float4 xq = *(const float4 *)(xs + 4 * (32 * u + L));
+                const float xk[GT_TOK] = {xq.x, xq.y, xq.z, xq.w};
 #pragma unroll
                 for (int k = 0; k < GT_TOK; k++) {
-                    const float pr = wv[u] * xs[k * GT_COLS + 32 * u + L];
+                    const float pr = wv[u] * xk[k];
                     acc[k] = acc[k] + pr;
                 }
             }
@@ -91,7 +103,7 @@ __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int 
             for (int k = 0; k < GT_TOK; k++) {
 #pragma unroll
                 for (int u = 0; u < GT_UNROLL; u++) {
-                    const float xv = xs[k * GT_COLS + 32 * min(u, cnt - 1) + L];
+                    const float xv = xs[4 * (32 * min(u, cnt - 1) + L) + k];
                     const float pr = u < cnt ? wv[u] * xv : 0.0f;
                     acc[k] = acc[k] + pr;
                 }
@@ -142,24 +154,19 @@ __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int 
 }
 
 // Route one token with one wave and publish ids (read by the bucketing work
-// group of this launch) and gates.
-__device__ void route_token_wave(const GateParams &p, int t, RouteLds<1> &L) {
+// group of this launch) and gates.  The logits are read with device-coherent
+// loads either way: written by this launch's other work groups, or by an
+// earlier launch (where such a load is merely a plain one).
+__device__ __forceinline__ void route_token_wave(const GateParams &p, int t, RouteLds<1> &L) {
     const int lane = threadIdx.x & 63;
     const int E = p.n_expert, K = p.k;
-    const bool coh = p.logits_in == nullptr; // logits from this launch's other work groups
-    const float *lg = coh ? p.logits + (size_t)t * E : p.logits_in + (size_t)t * E;
-    if (coh)
-        route_rank<1, true>(lg, p.sel_bias, E, K, p.gating, L);
-    else
-        route_rank<1, false>(lg, p.sel_bias, E, K, p.gating, L);
+    const float *lg = (p.logits_in ? p.logits_in : p.logits) + (size_t)t * E;
+    route_rank<1, true>(lg, p.sel_bias, E, K, p.gating, L);
     bool redo;
     float g = route_finish<1>(L, E, K, p.gating, route_is_exact(p.gating, p.sel_bias),
                               p.weights_norm, p.weights_scale, redo);
     if (redo) {
-        if (coh)
-            route_exact_wave<1, true>(lg, p.sel_bias, E, K, p.gating, L);
-        else
-            route_exact_wave<1, false>(lg, p.sel_bias, E, K, p.gating, L);
+        route_exact_wave<1, true>(lg, p.sel_bias, E, K, p.gating, L);
         g = route_finish<1>(L, E, K, p.gating, true, p.weights_norm, p.weights_scale, redo);
     }
     if (lane < K) {
