@@ -282,7 +282,7 @@ __device__ inline void lds_barrier() {
 // Offsets (ints) inside the library's zero-initialised sync buffer.  Every
 // counter is reset to zero by the arrival that completes it, so the buffer
 // is all zeros between launches.
-constexpr int SYNC_GATE_CHUNK = 0;   // [MAX_TOK / GT_TOK]
+constexpr int SYNC_GATE_CHUNK = 0;   // [MAX_TOK / GT_TOK]: a counter per token chunk
 constexpr int SYNC_GATE_FINAL = 128; // [1]
 constexpr int SYNC_PV_QUANT = 256;   // [4 lanes][64 items]: P.V groups of one 256-column item
 //

@@ -19,10 +19,22 @@ namespace lh {
 
 constexpr int GT_THREADS = 256;
 constexpr int GT_ROWS = GT_THREADS / 32; // router rows per workgroup (a half-wave each)
-constexpr int GT_TOK = 4;                // tokens per chunk = tokens per half-wave pass
+constexpr int GT_TOK = 2;                // tokens per chunk = tokens per half-wave pass
 constexpr int GT_UNROLL = 64; // router elements in flight per lane (dim 2048: one chunk)
 constexpr int GT_COLS = 32 * GT_UNROLL; // columns per staged chunk
-static_assert(GT_TOK == 4, "a staged column's tokens are one float4");
+static_assert(GT_TOK == 2 || GT_TOK == 4, "a staged column's tokens are one float2 or float4");
+static_assert(SYNC_GATE_CHUNK + MAX_TOK / GT_TOK <= SYNC_GATE_FINAL, "a completion counter per token chunk");
+
+// A staged column's GT_TOK token values, one 8- or 16-byte LDS read.
+__device__ __forceinline__ void xs_tokens(const float *src, float (&o)[GT_TOK]) {
+    if constexpr (GT_TOK == 4) {
+        const float4 v = *(const float4 *)src;
+        o[0] = v.x, o[1] = v.y, o[2] = v.z, o[3] = v.w;
+    } else {
+        const float2 v = *(const float2 *)src;
+        o[0] = v.x, o[1] = v.y;
+    }
+}
 
 // Router GEMV for up to GT_TOK tokens in dotF32 order (src/gguf/ggml.zig:
 // 198-217): lane L of a half-wave accumulates row[32i + L] * x[32i + L] over
@@ -31,8 +43,8 @@ static_assert(GT_TOK == 4, "a staged column's tokens are one float4");
 // one row (e < n_expert: valid); the whole work group calls this.  A chunk of
 // GT_COLS columns is processed at a time: the half-wave's row loads (64 per
 // lane) are issued together, and the tokens' matching x columns are staged
-// in LDS by the whole work group as [GT_COLS][GT_TOK] (a column's four
-// token values in one 16-byte read).
+// in LDS by the whole work group as [GT_COLS][GT_TOK] (a column's token
+// values in one read).
 __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int nt, int hw, int L,
                             float (*part)[GT_TOK][32], float *xs) {
     const int dim = p.dim;
@@ -72,10 +84,10 @@ __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int 
             if (col < ccols) {
 #pragma unroll
                 for (int k = 0; k < GT_TOK; k++) {
-                    xs[4 * (col + 0) + k] = xv[q][k].x;
-                    xs[4 * (col + 1) + k] = xv[q][k].y;
-                    xs[4 * (col + 2) + k] = xv[q][k].z;
-                    xs[4 * (col + 3) + k] = xv[q][k].w;
+                    xs[GT_TOK * (col + 0) + k] = xv[q][k].x;
+                    xs[GT_TOK * (col + 1) + k] = xv[q][k].y;
+                    xs[GT_TOK * (col + 2) + k] = xv[q][k].z;
+                    xs[GT_TOK * (col + 3) + k] = xv[q][k].w;
                 }
             }
         }
@@ -88,8 +100,8 @@ __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int 
             // column order
 #pragma unroll
             for (int u = 0; u < GT_UNROLL; u++) {
-                const float4 xq = *(const float4 *)(xs + 4 * (32 * u + L));
-                const float xk[GT_TOK] = {xq.x, xq.y, xq.z, xq.w};
+                float xk[GT_TOK];
+                xs_tokens(xs + GT_TOK * (32 * u + L), xk);
 #pragma unroll
                 for (int k = 0; k < GT_TOK; k++) {
                     const float pr = wv[u] * xk[k];
@@ -103,7 +115,7 @@ __device__ void router_rows(const GateParams &p, int e, bool valid, int t0, int 
             for (int k = 0; k < GT_TOK; k++) {
 #pragma unroll
                 for (int u = 0; u < GT_UNROLL; u++) {
-                    const float xv = xs[4 * (32 * min(u, cnt - 1) + L) + k];
+                    const float xv = xs[GT_TOK * (32 * min(u, cnt - 1) + L) + k];
                     const float pr = u < cnt ? wv[u] * xv : 0.0f;
                     acc[k] = acc[k] + pr;
                 }
